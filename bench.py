@@ -1,0 +1,267 @@
+#!/usr/bin/env python3
+"""Benchmark: decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s on one MI355X.
+
+Headline (``value``): the cb4 codebook GEMV of the decode path, M=1, K=2048,
+N=6144, cb4-g64 weights (4-bit indices, a 16-entry fp16 codebook per
+64-group), bf16 activations, f32 output -- algorithmic bytes (weights +
+activations + outputs, each once) per second over the timed steps.
+
+A "step" is one GEMV launch over one of ``copies`` distinct device-resident
+weight copies (together > 2x the 256 MB Infinity Cache), so every step reads
+its weights from HBM.  Steps are captured once in a HIP graph and replayed;
+the timed region is one replay of ``--steps`` launches bracketed by
+``torch.cuda.synchronize()``.  HIP events on the launch stream give the
+per-launch kernel time used for ``roofline``.
+
+Other configurations are reported under ``"secondary"`` (Q8 GEMV config 0,
+the Q8 small-M sweep, prefill GEMM, decode stack).  ``cpu_baseline`` times the
+C restatement of the reference CPU GEMV (oracle/) on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0       # dense bf16 / fp16 MFMA
+MALL_BYTES = 256 << 20          # Infinity Cache
+METRIC = "decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s, 1×MI355X"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# --------------------------------------------------------------------------
+# algorithmic bytes per call
+# --------------------------------------------------------------------------
+
+def weight_bytes(m) -> int:
+    k = m.kind
+    if k == "g64":
+        return m.rows * m.padded_cols // 2 + m.rows * (m.padded_cols // 64) * 32
+    if k == "q8":
+        return m.rows * m.blocks_per_row * 34
+    return (m.rows * m.padded_cols // 2 + m.rows * (m.padded_cols // 128) * 2
+            + (m.rows + 1) * 4 + m.outliers_packed.size * 4)
+
+
+def call_bytes(m, M: int, x_elem: int, y_elem: int) -> int:
+    return weight_bytes(m) + M * m.cols * x_elem + M * m.rows * y_elem
+
+
+# --------------------------------------------------------------------------
+# GPU timing
+# --------------------------------------------------------------------------
+
+class GraphTimer:
+    """Capture `steps` launches in one HIP graph and time a replay."""
+
+    def __init__(self, torch, enqueue, steps: int, warmup: int):
+        self.torch = torch
+        self.enqueue = enqueue
+        self.steps = steps
+        self.warmup = warmup
+
+    def run(self):
+        torch = self.torch
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            for i in range(max(self.warmup, 1)):      # eager warm-up (also JIT-free)
+                self.enqueue(i, s.cuda_stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(self.steps):
+                self.enqueue(i, s.cuda_stream)
+        torch.cuda.synchronize()
+        g.replay()                                    # warm replay
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        with torch.cuda.stream(s):
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        ev_ms = e0.elapsed_time(e1)
+        del g
+        return (t1 - t0), ev_ms
+
+
+def bench_gemv(torch, eng, m, M: int, x_dtype: str, y_dtype: str, steps: int, warmup: int,
+               seed: int = 0):
+    """GB/s of y = W x over rotating weight copies. Returns a result dict."""
+    from vxg_amd import engine, synth
+    wb = weight_bytes(m)
+    n_copies = max(2, math.ceil(2.5 * MALL_BYTES / wb))
+    base = eng.upload_packed(m)
+    copies = [base] + [base.clone() for _ in range(n_copies - 1)]
+    if x_dtype == "bf16":
+        xh = synth.make_x_bf16(M, m.cols, seed=seed)
+        xd = torch.from_numpy(xh.view(np.int16).copy()).cuda()
+        xdt, xel = engine.DTYPE_BF16, 2
+    else:
+        xh = synth.make_x_f32(M, m.cols, seed=seed)
+        xd = torch.from_numpy(xh).cuda()
+        xdt, xel = engine.DTYPE_F32, 4
+    if y_dtype == "bf16":
+        yd = torch.empty((M, m.rows), dtype=torch.bfloat16, device="cuda")
+        ydt, yel = engine.DTYPE_BF16, 2
+    else:
+        yd = torch.empty((M, m.rows), dtype=torch.float32, device="cuda")
+        ydt, yel = engine.DTYPE_F32, 4
+    xp, yp = xd.data_ptr(), yd.data_ptr()
+
+    def enqueue(i, stream):
+        eng.matmul_dev(copies[i % n_copies], xp, xdt, M, yp, ydt, stream)
+
+    wall_s, ev_ms = GraphTimer(torch, enqueue, steps, warmup).run()
+    nbytes = call_bytes(m, M, xel, yel)
+    for c in copies:
+        c.free()
+    kern_ms = ev_ms / steps
+    return {
+        "bytes_per_call": nbytes, "weight_copies": n_copies, "steps": steps,
+        "wall_ms_per_step": wall_s * 1e3 / steps, "kernel_ms": kern_ms,
+        "GBps": nbytes * steps / wall_s / 1e9, "kernel_GBps": nbytes / (kern_ms * 1e-3) / 1e9,
+        "flops_per_call": 2 * M * m.rows * m.cols,
+    }
+
+
+# --------------------------------------------------------------------------
+# CPU baseline (reference CPU path, C restatement in oracle/)
+# --------------------------------------------------------------------------
+
+def cpu_baseline(m, budget_s: float = 10.0):
+    import oracle
+    from vxg_amd import synth
+    threads = oracle.hardware_threads()
+    xh = synth.make_x_bf16(1, m.cols, seed=0)
+    from vxg_amd.formats import bf16_bits_to_f32
+    x = bf16_bits_to_f32(xh)[0]
+    oracle.gemv(m, x, threads)                 # warm call (bench.rs:317-318)
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.gemv(m, x, threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    per_call = el / n
+    return {
+        "value": call_bytes(m, 1, 2, 4) / per_call / 1e9, "unit": "GB/s", "cores": threads,
+        "kind": "port", "ms_per_call": per_call * 1e3,
+        "sample": f"{n} calls of the g64 GEMV (M=1, K={m.cols}, N={m.rows}) in {el:.1f} s, "
+                  f"one warm call first, threads spawned per call (codebook.rs:357-369)",
+    }
+
+
+# --------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
+              f"multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vxg_amd import engine, synth
+
+    eng = engine.HipEngine()
+    log(f"device {eng.device_name}")
+
+    # headline: config 1
+    m = synth.make_g64(6144, 2048, seed=1)
+    log("config 1: cb4-g64 GEMV M=1 K=2048 N=6144")
+    r = bench_gemv(torch, eng, m, 1, "bf16", "f32", args.steps, args.warmup, seed=0)
+    log(f"  {r['GBps']:.1f} GB/s wall, kernel {r['kernel_ms']*1e3:.2f} us "
+        f"({r['kernel_GBps']:.1f} GB/s)")
+
+    secondary = []
+    if not args.quick:
+        m0 = synth.make_q8(4096, 4096, seed=0)
+        log("config 0: Q8 GEMV M=1 K=N=4096 x f32")
+        r0 = bench_gemv(torch, eng, m0, 1, "f32", "f32", args.steps, args.warmup, seed=0)
+        secondary.append({"config": "0: q8 gemv M=1 K=4096 N=4096 x=f32 y=f32",
+                          "GBps": round(r0["GBps"], 1), "kernel_us": round(r0["kernel_ms"] * 1e3, 3),
+                          "kernel_GBps": round(r0["kernel_GBps"], 1),
+                          "frac_hbm": round(r0["kernel_GBps"] / HBM_PEAK_GBS, 4)})
+        log(f"  {r0['GBps']:.1f} GB/s wall, kernel {r0['kernel_ms']*1e3:.2f} us")
+        for (K, N) in [(2048, 2048), (2048, 6144), (6144, 2048), (2048, 151936)]:
+            mq = synth.make_q8(N, K, seed=2)
+            for M in (1, 2, 4, 8):
+                st = max(20, min(args.steps, int(2e9 / weight_bytes(mq))))
+                rq = bench_gemv(torch, eng, mq, M, "bf16", "f32", st, min(args.warmup, 5), seed=M)
+                secondary.append({"config": f"2: q8 gemv M={M} K={K} N={N}",
+                                  "GBps": round(rq["GBps"], 1),
+                                  "kernel_us": round(rq["kernel_ms"] * 1e3, 3),
+                                  "kernel_GBps": round(rq["kernel_GBps"], 1),
+                                  "frac_hbm": round(rq["kernel_GBps"] / HBM_PEAK_GBS, 4)})
+                log(f"  config 2 M={M} K={K} N={N}: {rq['kernel_GBps']:.1f} GB/s kernel")
+            del mq
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle g64 GEMV)")
+        cpu = cpu_baseline(m, args.cpu_seconds)
+        log(f"  {cpu['value']:.2f} GB/s on {cpu['cores']} threads")
+
+    achieved = r["kernel_GBps"]
+    out = {
+        "metric": METRIC,
+        "value": round(r["GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["wall_ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4 idx + f16 codebook -> f32 acc (bf16 x)",
+        "data": "synthetic: seeded cb4-g64 weights (uniform 4-bit indices, sorted N(0,0.02) "
+                "fp16 codebooks), bf16 N(0,1) activations",
+        "config": {"workload": "config 1: cb4-g64 decode GEMV", "M": 1, "K": 2048, "N": 6144,
+                   "x_dtype": "bf16", "y_dtype": "f32", "weight_copies": r["weight_copies"],
+                   "mall_defeat": "rotate weight copies totalling > 2x 256 MB MALL",
+                   "timing": "HIP graph of `steps` launches, one replay"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "vxt::gemv_kernel<9,1,..> (g64, M=1)",
+                     "bytes_per_launch": r["bytes_per_call"],
+                     "kernel_us": round(r["kernel_ms"] * 1e3, 3)},
+        "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)
+                                                  for k, v in cpu.items() if k != "ms_per_call"},
+        "secondary": secondary,
+    }
+    eng.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

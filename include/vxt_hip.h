@@ -1,0 +1,186 @@
+/*
+ * vxt_hip.h -- C ABI of the MI355X (gfx950) compressed-weight matmul engine.
+ *
+ * Drop-in for vxg-tensor's GPU matmul boundary: the same create / upload /
+ * run / free life cycle, opaque handles, caller-provided error buffers and
+ * synchronous semantics as the reference's Metal bridge
+ * (crates/vxg-tensor/src/metal_ffi.rs:27-49, native/metal_gemv.mm:258-475),
+ * with a HIP engine behind it.  Plain pointers and sizes only.
+ *
+ * Conventions (kept from the reference):
+ *   - constructors return an opaque pointer, NULL on failure, with a
+ *     NUL-terminated message in (err, err_cap) (metal_gemv.mm:49-52);
+ *   - every other call returns VXT_OK (0) or a negative VXT_E_* code and
+ *     writes a message; no C++ exception crosses this boundary;
+ *   - uploads COPY the host planes (host memory is not retained after return);
+ *     device memory is released by vxt_hip_free_tensor / vxt_hip_destroy;
+ *   - host-pointer entry points are synchronous: outputs are in host memory
+ *     when they return (metal_gemv.mm:444-472);
+ *   - one context is used by one thread at a time (metal_ffi.rs:96); tensors
+ *     may be shared between threads.
+ *
+ * Layout conventions: rows = N (output features), cols = K (reduction axis),
+ * batch_m = M (tokens).  y[m*rows + r] = sum_c W[r,c] * x[m*cols + c].
+ */
+#ifndef VXT_HIP_H
+#define VXT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define VXT_API __attribute__((visibility("default")))
+#else
+#define VXT_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define VXT_OK 0
+#define VXT_E_ARG (-1)         /* null handle or pointer, bad enum value      */
+#define VXT_E_SHAPE (-2)       /* sizes do not match the tensor / each other  */
+#define VXT_E_FORMAT (-3)      /* corrupt planes (lengths, CSR indices)       */
+#define VXT_E_DEVICE (-4)      /* HIP runtime error (message carries it)      */
+#define VXT_E_UNSUPPORTED (-5) /* valid request this build does not support   */
+
+/* ---- element types for activations / outputs --------------------------- */
+#define VXT_DTYPE_F32 0u
+#define VXT_DTYPE_BF16 1u
+
+/* ---- tensor kinds (kind 2 = codebook, as VxtMetalOp.kind in
+ *      native/metal_internal.h:14) ---------------------------------------- */
+#define VXT_KIND_CB4 2u     /* CodebookMatrix, bits = 4 (codebook.rs:9-24)   */
+#define VXT_KIND_Q8_0 8u    /* GGUF Q8_0 / KvQ8Block rows (llm_prefill.rs:17) */
+#define VXT_KIND_CB4_G64 9u /* cb4 with a per-64-group fp16 codebook         */
+
+/* Borrowed view of a CodebookMatrix (codebook.rs:9-24), bits = 4.
+ * Mirrors the sub-matrix descriptor the reference passes to its device packer
+ * (metal_cb4_fast_ffi.rs:38-85).  Plane lengths are validated as the archive
+ * reader does (format.rs:423-440, :565-574). */
+typedef struct VxtCb4View {
+    uint32_t bits;         /* must be 4                                     */
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t padded_cols;  /* multiple of 128, >= cols                      */
+    const float* centroids;          /* [16]                                */
+    const uint16_t* scales_f16;      /* [rows * padded_cols/128]            */
+    size_t n_scales;
+    const uint32_t* packed_words;    /* [rows * padded_cols/8]              */
+    size_t n_words;
+    const uint32_t* outlier_row_ptr; /* [rows + 1]                          */
+    size_t n_row_ptr;
+    const uint32_t* outliers_packed; /* [n_outliers], col | f16 << 16       */
+    size_t n_outliers;
+} VxtCb4View;
+
+/* Borrowed view of a cb4-g64 matrix: idx[r*padded_cols/2 + c/2] >> 4*(c%2)
+ * is column c's index, lut_f16[(r*padded_cols/64 + c/64)*16 + q] its value. */
+typedef struct VxtCb4G64View {
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t padded_cols;  /* multiple of 64, >= cols                       */
+    uint32_t reserved;
+    const uint8_t* idx;              /* [rows * padded_cols/2]              */
+    size_t n_idx;
+    const uint16_t* lut_f16;         /* [rows * padded_cols/64 * 16]        */
+    size_t n_lut;
+} VxtCb4G64View;
+
+/* One GEMV job of vxt_hip_run_multi: a tensor and its host output
+ * (the (&GpuPackedTensor, &mut [f32]) pairs of metal.rs:466-481). */
+typedef struct VxtHipJob {
+    void* tensor;
+    float* y;              /* host, [rows]                                  */
+} VxtHipJob;
+
+/* ---- context ------------------------------------------------------------ */
+
+/* Replaces vxt_metal_create (metal_ffi.rs:28-33).  device < 0 selects the
+ * current HIP device.  Writes the device name into dev_name. */
+VXT_API void* vxt_hip_create(int32_t device, char* dev_name, size_t dev_name_cap, char* err,
+                     size_t err_cap);
+
+/* Replaces vxt_metal_destroy (metal_ffi.rs:34).  Frees every tensor the
+ * context still owns. NULL is a no-op. */
+VXT_API void vxt_hip_destroy(void* ctx);
+
+/* ---- weights: upload with device-residency re-layout -------------------- */
+
+/* Replaces GpuPackedInner::upload_codebook (metal.rs:162-177) over
+ * vxt_metal_upload (metal_ffi.rs:35). Returns a tensor handle or NULL. */
+VXT_API void* vxt_hip_upload_cb4(void* ctx, const VxtCb4View* view, char* err, size_t err_cap);
+
+/* cb4-g64 upload (no reference counterpart: the decode-benchmark layout). */
+VXT_API void* vxt_hip_upload_cb4_g64(void* ctx, const VxtCb4G64View* view, char* err,
+                             size_t err_cap);
+
+/* Raw GGUF Q8_0 bytes as GgufView::tensor_bytes returns them
+ * (gguf.rs:160-172): rows * ceil(cols/32) blocks of 34 bytes.  Replaces the
+ * reference's load-time f32 expansion (gguf.rs:223-229, llm.rs:164). */
+VXT_API void* vxt_hip_upload_q8_0(void* ctx, uint32_t rows, uint32_t cols, const uint8_t* blocks,
+                          size_t n_bytes, char* err, size_t err_cap);
+
+/* Device-to-device copy of an uploaded tensor (same layout, new memory). */
+VXT_API void* vxt_hip_clone_tensor(void* tensor, char* err, size_t err_cap);
+
+/* Replaces vxt_metal_free_buffer (metal_ffi.rs:36). NULL is a no-op. */
+VXT_API void vxt_hip_free_tensor(void* tensor);
+
+/* kind (VXT_KIND_*), rows, cols, and device bytes of the resident layout. */
+VXT_API int vxt_hip_tensor_info(void* tensor, uint32_t* kind, uint32_t* rows, uint32_t* cols,
+                        uint64_t* device_bytes);
+
+/* ---- host-pointer entry points (synchronous) ---------------------------- */
+
+/* Replaces vxt_metal_run_multi (metal_ffi.rs:38-48): every job's GEMV over the
+ * same f32 x (x_elems >= every job's cols; extra elements are ignored), run
+ * `iters` times; gpu_ms (may be NULL) receives the summed kernel time.  Used by
+ * MetalEngine::run_multi_same_x (metal.rs:466) and run_gemv (metal.rs:535). */
+VXT_API int vxt_hip_run_multi(void* ctx, const float* x, uint32_t x_elems, const VxtHipJob* jobs,
+                      uint32_t n_jobs, uint32_t iters, double* gpu_ms, char* err,
+                      size_t err_cap);
+
+/* Replaces PackedTensor::gemm_cpu (llm_prefill.rs:160): y_batch[batch_m*rows]
+ * = x_batch[batch_m*cols] times W^T, f32 in and out; batch_m == 1 is the
+ * GEMV (llm_prefill.rs:168-171). */
+VXT_API int vxt_hip_gemm(void* ctx, void* tensor, const float* x_batch, uint32_t batch_m,
+                 float* y_batch, double* gpu_ms, char* err, size_t err_cap);
+
+/* Bit-exact dequantised rows [row0, row0+nrows) x cols, f32, host output.
+ * Same values as CodebookMatrix::decode_row (codebook.rs:285-337), the Q8_0
+ * expansion (gguf.rs:223-229), and the g64 table lookup. */
+VXT_API int vxt_hip_dequant_rows(void* ctx, void* tensor, uint32_t row0, uint32_t nrows, float* out,
+                         char* err, size_t err_cap);
+
+/* ---- device-pointer entry points (asynchronous on `stream`) ------------- */
+/* x, y, out are device pointers; stream is a hipStream_t (NULL = default).
+ * Nothing is copied to or from the host.  These are what the decode loop and
+ * the benchmarks call with activations already resident in HBM. */
+
+/* y[batch_m * rows] (y_dtype) = W x for x[batch_m * cols] (x_dtype).
+ * batch_m 1..8 runs the GEMV kernels; larger batch_m the GEMM kernels. */
+VXT_API int vxt_hip_matmul_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype,
+                       uint32_t batch_m, void* y, uint32_t y_dtype, void* stream, char* err,
+                       size_t err_cap);
+
+/* Several tensors sharing one x (forward_multi, llm_cpu.rs:51-71): tensors[i]
+ * writes ys[i].  All tensors must have the same cols. */
+VXT_API int vxt_hip_matmul_multi_dev(void* ctx, void* const* tensors, uint32_t n, const void* x,
+                             uint32_t x_dtype, uint32_t batch_m, void* const* ys,
+                             uint32_t y_dtype, void* stream, char* err, size_t err_cap);
+
+/* Device-side bit-exact dequant of rows [row0, row0+nrows) into out (f32). */
+VXT_API int vxt_hip_dequant_rows_dev(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
+                             float* out, void* stream, char* err, size_t err_cap);
+
+/* Kernel time of the last synchronous call, in ms (hipEvent pair). */
+VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VXT_HIP_H */

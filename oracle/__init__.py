@@ -1,0 +1,242 @@
+"""CPU parity oracle for the compressed-weight matmul path -- TEST INFRASTRUCTURE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may import this package, and only as the checker or the timed CPU
+baseline.  The product (``vxg_amd``) never imports it.
+
+The arithmetic lives in ``oracle/vxt_oracle.c`` (built by ``oracle/Makefile``
+into ``oracle/liboracle_vxt.so``); each C function cites the reference
+(``crates/vxg-tensor``) lines it restates.  This module only marshals numpy
+arrays through ctypes.
+
+Parity status of every function, and the checks that pin it, are listed in
+``tests/test_oracle_pinning.py``'s module docstring.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle_vxt.so")
+
+KIND_CB4, KIND_G64, KIND_Q8 = 1, 2, 3
+
+_lib = None
+
+
+def build(force: bool = False) -> str:
+    """Compile the oracle with its Makefile (gcc; runs where gcc exists)."""
+    if force and os.path.exists(LIB_PATH):
+        os.remove(LIB_PATH)
+    subprocess.run(["make", "-s", "-C", _HERE, "liboracle_vxt.so"], check=True)
+    return LIB_PATH
+
+
+class _Cb4(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("padded_cols", C.c_uint32),
+                ("centroids", C.c_void_p), ("scales_f16", C.c_void_p),
+                ("packed_words", C.c_void_p), ("outlier_row_ptr", C.c_void_p),
+                ("outliers_packed", C.c_void_p)]
+
+
+class _G64(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("padded_cols", C.c_uint32),
+                ("idx", C.c_void_p), ("lut_f16", C.c_void_p)]
+
+
+class _Q8(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("blocks", C.c_void_p)]
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = C.CDLL(LIB_PATH)
+        vp, sz, i32 = C.c_void_p, C.c_size_t, C.c_int
+        L.vxo_f16_to_f32.restype = C.c_float
+        L.vxo_f16_to_f32.argtypes = [C.c_uint16]
+        L.vxo_f32_to_f16.restype = C.c_uint16
+        L.vxo_f32_to_f16.argtypes = [C.c_float]
+        L.vxo_f32_to_bf16.restype = C.c_uint16
+        L.vxo_f32_to_bf16.argtypes = [C.c_float]
+        for n in ("vxo_f16_to_f32_n", "vxo_f32_to_f16_n", "vxo_bf16_to_f32_n", "vxo_f32_to_bf16_n"):
+            getattr(L, n).argtypes = [vp, vp, sz]
+            getattr(L, n).restype = None
+        for n in ("vxo_cb4_decode_row", "vxo_g64_decode_row", "vxo_q8_decode_row"):
+            getattr(L, n).argtypes = [vp, sz, vp]
+            getattr(L, n).restype = None
+        for n in ("vxo_cb4_gemv", "vxo_g64_gemv", "vxo_q8_gemv"):
+            getattr(L, n).argtypes = [vp, vp, vp, i32]
+            getattr(L, n).restype = None
+        L.vxo_q8_quantize.argtypes = [vp, vp]
+        L.vxo_q8_quantize.restype = None
+        L.vxo_q8_dot_f32.argtypes = [vp, vp]
+        L.vxo_q8_dot_f32.restype = C.c_float
+        L.vxo_q8_axpy_f32.argtypes = [vp, C.c_float, vp]
+        L.vxo_q8_axpy_f32.restype = None
+        L.vxo_q8_dequant.argtypes = [vp, sz, vp]
+        L.vxo_q8_dequant.restype = None
+        L.vxo_gemm.argtypes = [i32, vp, vp, sz, vp, i32]
+        L.vxo_gemm.restype = None
+        L.vxo_gemv_any.argtypes = [i32, vp, vp, vp, i32]
+        L.vxo_gemv_any.restype = None
+        L.vxo_hardware_threads.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def hardware_threads() -> int:
+    return int(lib().vxo_hardware_threads())
+
+
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+# --------------------------------------------------------------------------
+# conversions
+# --------------------------------------------------------------------------
+
+def f16_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().vxo_f16_to_f32_n(_ptr(b), _ptr(out), b.size)
+    return out
+
+
+def f32_to_f16(vals) -> np.ndarray:
+    v = np.ascontiguousarray(vals, dtype=np.float32)
+    out = np.empty(v.shape, dtype=np.uint16)
+    lib().vxo_f32_to_f16_n(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(b.shape, dtype=np.float32)
+    lib().vxo_bf16_to_f32_n(_ptr(b), _ptr(out), b.size)
+    return out
+
+
+def f32_to_bf16(vals) -> np.ndarray:
+    v = np.ascontiguousarray(vals, dtype=np.float32)
+    out = np.empty(v.shape, dtype=np.uint16)
+    lib().vxo_f32_to_bf16_n(_ptr(v), _ptr(out), v.size)
+    return out
+
+
+# --------------------------------------------------------------------------
+# matrix views (the arrays are kept alive on the returned object)
+# --------------------------------------------------------------------------
+
+class _View:
+    def __init__(self, kind, struct, keep):
+        self.kind = kind
+        self.struct = struct
+        self._keep = keep
+
+    @property
+    def ptr(self):
+        return C.addressof(self.struct)
+
+
+def view(m) -> _View:
+    k = m.kind
+    if k == "cb4":
+        arrs = [np.ascontiguousarray(m.centroids, dtype=np.float32),
+                np.ascontiguousarray(m.scales_f16, dtype=np.uint16),
+                np.ascontiguousarray(m.packed_words, dtype=np.uint32),
+                np.ascontiguousarray(m.outlier_row_ptr, dtype=np.uint32),
+                np.ascontiguousarray(m.outliers_packed, dtype=np.uint32)]
+        if arrs[4].size == 0:
+            arrs[4] = np.zeros(1, dtype=np.uint32)
+        s = _Cb4(m.rows, m.cols, m.padded_cols, *[_ptr(a) for a in arrs])
+        return _View(KIND_CB4, s, arrs)
+    if k == "g64":
+        arrs = [np.ascontiguousarray(m.idx, dtype=np.uint8),
+                np.ascontiguousarray(m.lut_f16, dtype=np.uint16)]
+        s = _G64(m.rows, m.cols, m.padded_cols, *[_ptr(a) for a in arrs])
+        return _View(KIND_G64, s, arrs)
+    if k == "q8":
+        arrs = [np.ascontiguousarray(m.blocks, dtype=np.uint8)]
+        s = _Q8(m.rows, m.cols, _ptr(arrs[0]))
+        return _View(KIND_Q8, s, arrs)
+    raise TypeError(f"unknown matrix kind {k!r}")
+
+
+_DECODE = {KIND_CB4: "vxo_cb4_decode_row", KIND_G64: "vxo_g64_decode_row",
+           KIND_Q8: "vxo_q8_decode_row"}
+
+
+def decode_rows(m, row0: int = 0, nrows: int | None = None) -> np.ndarray:
+    """Dequantised rows [nrows, cols] (``decode_row`` per row)."""
+    v = view(m)
+    nrows = m.rows - row0 if nrows is None else nrows
+    out = np.zeros((nrows, m.cols), dtype=np.float32)
+    fn = getattr(lib(), _DECODE[v.kind])
+    for i in range(nrows):
+        fn(v.ptr, row0 + i, out[i].ctypes.data)
+    return out
+
+
+def gemv(m, x, threads: int = 1) -> np.ndarray:
+    """y[rows] = W x for f32 x[cols] (the reference GEMV of that kind)."""
+    v = view(m)
+    xx = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    assert xx.size == m.cols
+    y = np.empty(m.rows, dtype=np.float32)
+    lib().vxo_gemv_any(v.kind, v.ptr, _ptr(xx), _ptr(y), int(threads))
+    return y
+
+
+def gemv_batch(m, X, threads: int = 1) -> np.ndarray:
+    """Per-token GEMV: Y[M, rows] with row m = gemv(W, X[m])."""
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, m.cols)
+    return np.stack([gemv(m, X[i], threads) for i in range(X.shape[0])])
+
+
+def gemm(m, X, threads: int = 1) -> np.ndarray:
+    """``PackedTensor::gemm_cpu`` for batch_m >= 2: Y[M, rows] (f32)."""
+    v = view(m)
+    X = np.ascontiguousarray(X, dtype=np.float32).reshape(-1, m.cols)
+    Y = np.empty((X.shape[0], m.rows), dtype=np.float32)
+    lib().vxo_gemm(v.kind, v.ptr, _ptr(X), X.shape[0], _ptr(Y), int(threads))
+    return Y
+
+
+# --------------------------------------------------------------------------
+# Q8 block primitives
+# --------------------------------------------------------------------------
+
+def q8_quantize(src32) -> np.ndarray:
+    s = np.ascontiguousarray(src32, dtype=np.float32).reshape(32)
+    blk = np.empty(34, dtype=np.uint8)
+    lib().vxo_q8_quantize(_ptr(s), _ptr(blk))
+    return blk
+
+
+def q8_dot(blk, x32) -> float:
+    b = np.ascontiguousarray(blk, dtype=np.uint8).reshape(34)
+    x = np.ascontiguousarray(x32, dtype=np.float32).reshape(32)
+    return float(np.float32(lib().vxo_q8_dot_f32(_ptr(b), _ptr(x))))
+
+
+def q8_axpy(blk, weight: float, out32) -> np.ndarray:
+    b = np.ascontiguousarray(blk, dtype=np.uint8).reshape(34)
+    o = np.array(out32, dtype=np.float32).reshape(32)
+    lib().vxo_q8_axpy_f32(_ptr(b), float(weight), _ptr(o))
+    return o
+
+
+def q8_dequant(blocks) -> np.ndarray:
+    b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)
+    assert b.size % 34 == 0
+    out = np.empty(b.size // 34 * 32, dtype=np.float32)
+    lib().vxo_q8_dequant(_ptr(b), b.size // 34, _ptr(out))
+    return out

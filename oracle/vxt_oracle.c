@@ -1,0 +1,517 @@
+/*
+ * vxt_oracle.c -- CPU restatement of vxg-tensor's compressed-weight matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the parity oracle and the CPU
+ * baseline: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.  The product library (vxg_amd/libvxt_hip.so) never links
+ * or calls it.
+ *
+ * Every function restates one reference function (Rust, crates/vxg-tensor),
+ * keeping its loop order, accumulator interleave and summation order.  Rust
+ * never contracts a*b+c, and `mul_add` is a single-rounding fused multiply-add,
+ * so this file is compiled with -ffp-contract=off and every reference
+ * `mul_add` is written as fmaf().
+ *
+ * Pinning (how each function is checked independently of its own formula)
+ * lives in tests/test_oracle_*.py; the header of each function names the
+ * reference lines it follows.
+ *
+ * Layout conventions (reference `rows x cols`, BASELINE `N x K`):
+ *   rows = N (output features), cols = K (reduction), batch_m = M (tokens).
+ */
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#define VXO_API __attribute__((visibility("default")))
+
+/* ------------------------------------------------------------------------- */
+/* fp16 / bf16 conversions                                                    */
+/* ------------------------------------------------------------------------- */
+
+static inline float bits_to_f32(uint32_t b) { float f; memcpy(&f, &b, 4); return f; }
+static inline uint32_t f32_to_bits(float f) { uint32_t b; memcpy(&b, &f, 4); return b; }
+
+/* fp16.rs:6-29 f16_to_f32: exact widening, subnormals normalised. */
+VXO_API float vxo_f16_to_f32(uint16_t bits) {
+    uint32_t sign = ((uint32_t)(bits & 0x8000u)) << 16;
+    uint32_t exp = (bits >> 10) & 0x1fu;
+    uint32_t mant = bits & 0x03ffu;
+    if (exp == 0) {
+        if (mant == 0) return bits_to_f32(sign);
+        uint32_t m = mant, e = 127u - 14u;
+        while ((m & 0x0400u) == 0) { m <<= 1; e -= 1; }
+        m &= 0x03ffu;
+        return bits_to_f32(sign | (e << 23) | (m << 13));
+    } else if (exp == 31) {
+        return bits_to_f32(sign | 0x7f800000u | (mant << 13));
+    }
+    return bits_to_f32(sign | ((exp + 112u) << 23) | (mant << 13));
+}
+
+/* fp16.rs:33-77 f32_to_f16: round-to-nearest-even including subnormals. */
+VXO_API uint16_t vxo_f32_to_f16(float val) {
+    uint32_t b = f32_to_bits(val);
+    uint16_t sign = (uint16_t)((b >> 16) & 0x8000u);
+    int32_t exp = (int32_t)((b >> 23) & 0xffu);
+    uint32_t mant = b & 0x007fffffu;
+    if (exp == 255) {
+        if (mant != 0) return (uint16_t)(sign | 0x7e00u | (uint16_t)(mant >> 13));
+        return (uint16_t)(sign | 0x7c00u);
+    }
+    int32_t unbiased = exp - 127;
+    if (unbiased > 15) return (uint16_t)(sign | 0x7c00u);
+    if (unbiased < -25) return sign;
+    if (unbiased < -14) {
+        uint32_t shift = (uint32_t)(-14 - unbiased);
+        uint32_t full_mant = mant | 0x00800000u;
+        uint32_t round_shift = 13u + shift;
+        uint32_t half = 1u << (round_shift - 1);
+        uint32_t mask = (1u << round_shift) - 1u;
+        uint32_t rem = full_mant & mask;
+        uint16_t m16 = (uint16_t)(full_mant >> round_shift);
+        if (rem > half || (rem == half && (m16 & 1u) != 0)) m16 += 1;
+        return (uint16_t)(sign | m16);
+    }
+    uint16_t e16 = (uint16_t)(((uint32_t)(unbiased + 15)) << 10);
+    uint32_t rem = mant & 0x1fffu;
+    uint16_t m16 = (uint16_t)(mant >> 13);
+    if (rem > 0x1000u || (rem == 0x1000u && (m16 & 1u) != 0)) {
+        m16 += 1;
+        if (m16 == 0x0400u) return (uint16_t)(sign | (uint16_t)(e16 + 0x0400u));
+    }
+    return (uint16_t)(sign | e16 | m16);
+}
+
+/* fp16.rs:81-83 bf16_to_f32. */
+VXO_API float vxo_bf16_to_f32(uint16_t bits) { return bits_to_f32(((uint32_t)bits) << 16); }
+
+/* fp16.rs:113-120 f32_to_bf16: RNE via 0x7fff + lsb bias; NaN keeps a quiet bit. */
+VXO_API uint16_t vxo_f32_to_bf16(float val) {
+    uint32_t b = f32_to_bits(val);
+    if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu) != 0)
+        return (uint16_t)((b >> 16) | 0x0040u);
+    uint32_t lsb = (b >> 16) & 1u;
+    uint32_t bias = 0x7fffu + lsb;
+    return (uint16_t)((b + bias) >> 16);
+}
+
+/* Bulk wrappers so the Python side can check all 65,536 patterns at once. */
+VXO_API void vxo_f16_to_f32_n(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = vxo_f16_to_f32(src[i]);
+}
+VXO_API void vxo_f32_to_f16_n(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = vxo_f32_to_f16(src[i]);
+}
+VXO_API void vxo_bf16_to_f32_n(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = vxo_bf16_to_f32(src[i]);
+}
+VXO_API void vxo_f32_to_bf16_n(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = vxo_f32_to_bf16(src[i]);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Row-parallel driver shared by the GEMVs                                    */
+/* ------------------------------------------------------------------------- */
+
+typedef void (*vxo_rows_fn)(const void* mat, const float* x_pad, float* y, size_t r0, size_t r1);
+
+typedef struct {
+    vxo_rows_fn fn;
+    const void* mat;
+    const float* x_pad;
+    float* y;
+    size_t r0, r1;
+} vxo_rows_job;
+
+static void* vxo_rows_thread(void* p) {
+    vxo_rows_job* j = (vxo_rows_job*)p;
+    j->fn(j->mat, j->x_pad, j->y, j->r0, j->r1);
+    return NULL;
+}
+
+/* codebook.rs:357-369: workers = clamp(threads,1,256).min(rows.max(1)); one
+ * thread when workers <= 1 or rows < 16; otherwise contiguous chunks of
+ * ceil(rows/workers) rows, threads spawned per call. */
+static void vxo_run_rows(vxo_rows_fn fn, const void* mat, const float* x_pad, float* y,
+                         size_t rows, int threads) {
+    size_t t = threads < 1 ? 1 : (threads > 256 ? 256 : (size_t)threads);
+    size_t workers = t < (rows > 0 ? rows : 1) ? t : (rows > 0 ? rows : 1);
+    if (workers <= 1 || rows < 16) {
+        fn(mat, x_pad, y, 0, rows);
+        return;
+    }
+    size_t chunk = (rows + workers - 1) / workers;
+    size_t n = (rows + chunk - 1) / chunk;
+    pthread_t* tid = (pthread_t*)calloc(n, sizeof(pthread_t));
+    vxo_rows_job* jobs = (vxo_rows_job*)calloc(n, sizeof(vxo_rows_job));
+    for (size_t i = 0; i < n; ++i) {
+        jobs[i].fn = fn; jobs[i].mat = mat; jobs[i].x_pad = x_pad; jobs[i].y = y;
+        jobs[i].r0 = i * chunk;
+        jobs[i].r1 = (i + 1) * chunk < rows ? (i + 1) * chunk : rows;
+        pthread_create(&tid[i], NULL, vxo_rows_thread, &jobs[i]);
+    }
+    for (size_t i = 0; i < n; ++i) pthread_join(tid[i], NULL);
+    free(tid);
+    free(jobs);
+}
+
+/* ------------------------------------------------------------------------- */
+/* cb4 reference layout: CodebookMatrix with bits = 4 (codebook.rs:9-24)      */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    uint32_t rows, cols, padded_cols;   /* padded_cols % 128 == 0, >= cols */
+    const float* centroids;             /* [16] */
+    const uint16_t* scales_f16;         /* [rows * padded_cols/128] */
+    const uint32_t* packed_words;       /* [rows * padded_cols/8], nibble c%8 of word c/8 */
+    const uint32_t* outlier_row_ptr;    /* [rows + 1] */
+    const uint32_t* outliers_packed;    /* col | f16_residual << 16 */
+} vxo_cb4;
+
+/* codebook.rs:285-306 + :329-336 decode_row (4-bit branch): dst[c] = sc*cent[q]
+ * (one f32 rounding), then CSR residuals added in order for col < cols. */
+VXO_API void vxo_cb4_decode_row(const vxo_cb4* m, size_t r, float* dst) {
+    size_t gpr = m->padded_cols / 128;
+    for (size_t g = 0; g < gpr; ++g) {
+        size_t g_idx = r * gpr + g;
+        float sc = vxo_f16_to_f32(m->scales_f16[g_idx]);
+        for (size_t sub = 0; sub < 4; ++sub) {
+            size_t col_base = g * 128 + sub * 32;
+            if (col_base >= m->cols) break;
+            size_t valid = m->cols - col_base < 32 ? m->cols - col_base : 32;
+            const uint32_t* cw = m->packed_words + (g_idx * 4 + sub) * 4;
+            for (size_t l = 0; l < valid; ++l) {
+                uint32_t q = (cw[l / 8] >> ((l % 8) * 4)) & 0x0fu;
+                dst[col_base + l] = sc * m->centroids[q];
+            }
+        }
+    }
+    uint32_t os = m->outlier_row_ptr[r], oe = m->outlier_row_ptr[r + 1];
+    for (uint32_t i = os; i < oe; ++i) {
+        uint32_t packed = m->outliers_packed[i];
+        uint32_t col = packed & 0xffffu;
+        if (col < m->cols) dst[col] += vxo_f16_to_f32((uint16_t)(packed >> 16));
+    }
+}
+
+/* codebook.rs:372-417 gemv_rows_range (4-bit branch). */
+static void vxo_cb4_rows(const void* mp, const float* x_pad, float* y, size_t r0, size_t r1) {
+    const vxo_cb4* m = (const vxo_cb4*)mp;
+    size_t gpr = m->padded_cols / 128;
+    for (size_t r = r0; r < r1; ++r) {
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        for (size_t g = 0; g < gpr; ++g) {
+            size_t g_idx = r * gpr + g;
+            float sc = vxo_f16_to_f32(m->scales_f16[g_idx]);
+            if (sc == 0.0f) continue;
+            float slut[16];
+            for (int k = 0; k < 16; ++k) slut[k] = sc * m->centroids[k];
+            for (size_t sub = 0; sub < 4; ++sub) {
+                const uint32_t* cw = m->packed_words + (g_idx * 4 + sub) * 4;
+                size_t base_x = g * 128 + sub * 32;
+                for (size_t w = 0; w < 4; ++w) {
+                    uint32_t word = cw[w];
+                    const float* xv = x_pad + base_x + w * 8;
+                    acc0 = fmaf(slut[word & 0x0f], xv[0], acc0);
+                    acc1 = fmaf(slut[(word >> 4) & 0x0f], xv[1], acc1);
+                    acc2 = fmaf(slut[(word >> 8) & 0x0f], xv[2], acc2);
+                    acc3 = fmaf(slut[(word >> 12) & 0x0f], xv[3], acc3);
+                    acc0 = fmaf(slut[(word >> 16) & 0x0f], xv[4], acc0);
+                    acc1 = fmaf(slut[(word >> 20) & 0x0f], xv[5], acc1);
+                    acc2 = fmaf(slut[(word >> 24) & 0x0f], xv[6], acc2);
+                    acc3 = fmaf(slut[(word >> 28) & 0x0f], xv[7], acc3);
+                }
+            }
+        }
+        float sum = (acc0 + acc1) + (acc2 + acc3);
+        uint32_t os = m->outlier_row_ptr[r], oe = m->outlier_row_ptr[r + 1];
+        for (uint32_t i = os; i < oe; ++i) {
+            uint32_t packed = m->outliers_packed[i];
+            float val = vxo_f16_to_f32((uint16_t)(packed >> 16));
+            sum = fmaf(val, x_pad[packed & 0xffffu], sum);
+        }
+        y[r] = sum;
+    }
+}
+
+/* codebook.rs:350-370 gemv_cpu: x zero-padded to padded_cols, row-parallel. */
+VXO_API void vxo_cb4_gemv(const vxo_cb4* m, const float* x, float* y, int threads) {
+    float* x_pad = (float*)calloc(m->padded_cols ? m->padded_cols : 1, sizeof(float));
+    memcpy(x_pad, x, (size_t)m->cols * sizeof(float));
+    vxo_run_rows(vxo_cb4_rows, m, x_pad, y, m->rows, threads);
+    free(x_pad);
+}
+
+/* ------------------------------------------------------------------------- */
+/* cb4-g64: the BASELINE decode layout (groups of 64 along K, one 16-entry    */
+/* fp16 codebook per group, no scale, no outliers).  Not a reference type;    */
+/* its GEMV follows the reference cb4 kernel's loop shape (codebook.rs:376-417)*/
+/* with the per-group table in place of sc*centroid.                          */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    uint32_t rows, cols, padded_cols;   /* padded_cols = roundup(cols, 64) */
+    const uint8_t* idx;                 /* [rows * padded_cols/2], low nibble = even col */
+    const uint16_t* lut_f16;            /* [rows * padded_cols/64 * 16] */
+} vxo_g64;
+
+VXO_API void vxo_g64_decode_row(const vxo_g64* m, size_t r, float* dst) {
+    size_t gpr = m->padded_cols / 64;
+    const uint8_t* row = m->idx + r * (m->padded_cols / 2);
+    for (size_t c = 0; c < m->cols; ++c) {
+        uint32_t q = (row[c / 2] >> ((c & 1) * 4)) & 0x0fu;
+        dst[c] = vxo_f16_to_f32(m->lut_f16[(r * gpr + c / 64) * 16 + q]);
+    }
+}
+
+static void vxo_g64_rows(const void* mp, const float* x_pad, float* y, size_t r0, size_t r1) {
+    const vxo_g64* m = (const vxo_g64*)mp;
+    size_t gpr = m->padded_cols / 64;
+    for (size_t r = r0; r < r1; ++r) {
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
+        const uint8_t* row = m->idx + r * (m->padded_cols / 2);
+        for (size_t g = 0; g < gpr; ++g) {
+            float lut[16];
+            for (int k = 0; k < 16; ++k) lut[k] = vxo_f16_to_f32(m->lut_f16[(r * gpr + g) * 16 + k]);
+            for (size_t w = 0; w < 8; ++w) {
+                uint32_t word;
+                memcpy(&word, row + g * 32 + w * 4, 4);
+                const float* xv = x_pad + g * 64 + w * 8;
+                acc0 = fmaf(lut[word & 0x0f], xv[0], acc0);
+                acc1 = fmaf(lut[(word >> 4) & 0x0f], xv[1], acc1);
+                acc2 = fmaf(lut[(word >> 8) & 0x0f], xv[2], acc2);
+                acc3 = fmaf(lut[(word >> 12) & 0x0f], xv[3], acc3);
+                acc0 = fmaf(lut[(word >> 16) & 0x0f], xv[4], acc0);
+                acc1 = fmaf(lut[(word >> 20) & 0x0f], xv[5], acc1);
+                acc2 = fmaf(lut[(word >> 24) & 0x0f], xv[6], acc2);
+                acc3 = fmaf(lut[(word >> 28) & 0x0f], xv[7], acc3);
+            }
+        }
+        y[r] = (acc0 + acc1) + (acc2 + acc3);
+    }
+}
+
+VXO_API void vxo_g64_gemv(const vxo_g64* m, const float* x, float* y, int threads) {
+    float* x_pad = (float*)calloc(m->padded_cols ? m->padded_cols : 1, sizeof(float));
+    memcpy(x_pad, x, (size_t)m->cols * sizeof(float));
+    vxo_run_rows(vxo_g64_rows, m, x_pad, y, m->rows, threads);
+    free(x_pad);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Q8: the 34-byte {f16 d; i8 qs[32]} block (llm_prefill.rs:17-24, identical   */
+/* to GGUF Q8_0 bytes at gguf.rs:224-228).  A Q8 weight matrix is rows x       */
+/* ceil(cols/32) such blocks, row-major, as GgufView::tensor_bytes returns.   */
+/* ------------------------------------------------------------------------- */
+
+static inline uint16_t load_u16le(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* llm_prefill.rs:28-42 KvQ8Block::quantize. */
+VXO_API void vxo_q8_quantize(const float* src, uint8_t* blk) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; ++i) {
+        float a = fabsf(src[i]);
+        /* Rust f32::max ignores a NaN operand. */
+        if (!isnan(a) && (isnan(amax) || a > amax)) amax = a;
+    }
+    uint16_t dh = vxo_f32_to_f16(amax / 127.0f);
+    float df = vxo_f16_to_f32(dh);
+    float inv = df > 0.0f ? 1.0f / df : 0.0f;
+    blk[0] = (uint8_t)(dh & 0xff);
+    blk[1] = (uint8_t)(dh >> 8);
+    for (int i = 0; i < 32; ++i) {
+        float v = rintf(src[i] * inv);            /* round_ties_even (default FE mode) */
+        int8_t q;
+        if (isnan(v)) q = 0;                       /* `as i8` maps NaN to 0 */
+        else if (v < -127.0f) q = -127;
+        else if (v > 127.0f) q = 127;
+        else q = (int8_t)v;
+        blk[2 + i] = (uint8_t)q;
+    }
+}
+
+/* llm_prefill.rs:45-54 KvQ8Block::dot_f32: two interleaved FMA chains, then *d. */
+VXO_API float vxo_q8_dot_f32(const uint8_t* blk, const float* q) {
+    float sc = vxo_f16_to_f32(load_u16le(blk));
+    const int8_t* qs = (const int8_t*)(blk + 2);
+    float s0 = 0.0f, s1 = 0.0f;
+    for (int i = 0; i < 16; ++i) {
+        s0 = fmaf((float)qs[2 * i], q[2 * i], s0);
+        s1 = fmaf((float)qs[2 * i + 1], q[2 * i + 1], s1);
+    }
+    return (s0 + s1) * sc;
+}
+
+/* llm_prefill.rs:56-62 KvQ8Block::axpy_f32. */
+VXO_API void vxo_q8_axpy_f32(const uint8_t* blk, float weight, float* out) {
+    float ws = weight * vxo_f16_to_f32(load_u16le(blk));
+    const int8_t* qs = (const int8_t*)(blk + 2);
+    for (int i = 0; i < 32; ++i) out[i] = fmaf((float)qs[i], ws, out[i]);
+}
+
+/* gguf.rs:223-229 Q8_0 dequant: w = (q as i8 as f32) * f16_to_f32(d) (exact). */
+VXO_API void vxo_q8_dequant(const uint8_t* blocks, size_t nblocks, float* out) {
+    for (size_t b = 0; b < nblocks; ++b) {
+        const uint8_t* blk = blocks + b * 34;
+        float d = vxo_f16_to_f32(load_u16le(blk));
+        for (int i = 0; i < 32; ++i) out[b * 32 + i] = (float)(int8_t)blk[2 + i] * d;
+    }
+}
+
+typedef struct {
+    uint32_t rows, cols;                /* blocks per row = ceil(cols/32) */
+    const uint8_t* blocks;              /* [rows * ceil(cols/32) * 34] */
+} vxo_q8;
+
+/* Q8 row dequant: gguf.rs:223-229 applied to one row, truncated to cols. */
+VXO_API void vxo_q8_decode_row(const vxo_q8* m, size_t r, float* dst) {
+    size_t kb = ((size_t)m->cols + 31) / 32;
+    const uint8_t* row = m->blocks + r * kb * 34;
+    for (size_t b = 0; b < kb; ++b) {
+        float d = vxo_f16_to_f32(load_u16le(row + b * 34));
+        for (size_t i = 0; i < 32 && b * 32 + i < m->cols; ++i)
+            dst[b * 32 + i] = (float)(int8_t)row[b * 34 + 2 + i] * d;
+    }
+}
+
+/* Q8 GEMV = the reference's block-dot composition (llm_prefill.rs:336-340:
+ * `dot += kb[b].dot_f32(..)`, starting from 0.0, blocks in order). */
+static void vxo_q8_rows(const void* mp, const float* x_pad, float* y, size_t r0, size_t r1) {
+    const vxo_q8* m = (const vxo_q8*)mp;
+    size_t kb = ((size_t)m->cols + 31) / 32;
+    for (size_t r = r0; r < r1; ++r) {
+        const uint8_t* row = m->blocks + r * kb * 34;
+        float dot = 0.0f;
+        for (size_t b = 0; b < kb; ++b) dot += vxo_q8_dot_f32(row + b * 34, x_pad + b * 32);
+        y[r] = dot;
+    }
+}
+
+VXO_API void vxo_q8_gemv(const vxo_q8* m, const float* x, float* y, int threads) {
+    size_t kp = ((size_t)m->cols + 31) / 32 * 32;
+    float* x_pad = (float*)calloc(kp ? kp : 1, sizeof(float));
+    memcpy(x_pad, x, (size_t)m->cols * sizeof(float));
+    vxo_run_rows(vxo_q8_rows, m, x_pad, y, m->rows, threads);
+    free(x_pad);
+}
+
+/* ------------------------------------------------------------------------- */
+/* Prefill GEMM: PackedTensor::gemm_cpu (llm_prefill.rs:156-255) with the      */
+/* scalar dense_tile_gemm (llm_prefill.rs:139-153).                           */
+/* ------------------------------------------------------------------------- */
+
+enum { VXO_KIND_CB4 = 1, VXO_KIND_G64 = 2, VXO_KIND_Q8 = 3 };
+
+static void vxo_decode_row_any(int kind, const void* m, size_t r, float* dst) {
+    if (kind == VXO_KIND_CB4) vxo_cb4_decode_row((const vxo_cb4*)m, r, dst);
+    else if (kind == VXO_KIND_G64) vxo_g64_decode_row((const vxo_g64*)m, r, dst);
+    else vxo_q8_decode_row((const vxo_q8*)m, r, dst);
+}
+
+static void vxo_dims(int kind, const void* m, size_t* rows, size_t* cols) {
+    if (kind == VXO_KIND_CB4) { *rows = ((const vxo_cb4*)m)->rows; *cols = ((const vxo_cb4*)m)->cols; }
+    else if (kind == VXO_KIND_G64) { *rows = ((const vxo_g64*)m)->rows; *cols = ((const vxo_g64*)m)->cols; }
+    else { *rows = ((const vxo_q8*)m)->rows; *cols = ((const vxo_q8*)m)->cols; }
+}
+
+/* llm_prefill.rs:139-153 (non-mac branch): y[m*ldc + r_off + r] = FMA chain. */
+static void vxo_dense_tile_gemm(const float* x_batch, size_t batch_m, size_t cols,
+                                const float* w_tile, size_t br, float* y_dst, size_t ldc,
+                                size_t r_off) {
+    for (size_t m = 0; m < batch_m; ++m) {
+        const float* xm = x_batch + m * cols;
+        float* ym = y_dst + m * ldc + r_off;
+        for (size_t r = 0; r < br; ++r) {
+            const float* wr = w_tile + r * cols;
+            float s = 0.0f;
+            for (size_t c = 0; c < cols; ++c) s = fmaf(wr[c], xm[c], s);
+            ym[r] = s;
+        }
+    }
+}
+
+typedef struct {
+    int kind;
+    const void* m;
+    const float* x_batch;
+    size_t batch_m, cols, r_beg, w_rows;
+    float* part_y;
+} vxo_gemm_job;
+
+#define VXO_TILE_R 32
+
+static void* vxo_gemm_thread(void* p) {
+    vxo_gemm_job* j = (vxo_gemm_job*)p;
+    size_t tile_rows = j->w_rows < VXO_TILE_R ? j->w_rows : VXO_TILE_R;
+    float* w_tile = (float*)malloc((tile_rows ? tile_rows : 1) * j->cols * sizeof(float));
+    for (size_t loc_r = 0; loc_r < j->w_rows;) {
+        size_t br = j->w_rows - loc_r < VXO_TILE_R ? j->w_rows - loc_r : VXO_TILE_R;
+        for (size_t dr = 0; dr < br; ++dr)
+            vxo_decode_row_any(j->kind, j->m, j->r_beg + loc_r + dr, w_tile + dr * j->cols);
+        vxo_dense_tile_gemm(j->x_batch, j->batch_m, j->cols, w_tile, br, j->part_y, j->w_rows,
+                            loc_r);
+        loc_r += br;
+    }
+    free(w_tile);
+    return NULL;
+}
+
+/* gemm_cpu for batch_m >= 2 (batch_m == 1 dispatches to the GEMV, :168-171,
+ * which is the caller's job here).  workers = clamp(threads,1,16) capped at the
+ * number of 32-row tiles; each worker decodes its tiles and writes a private
+ * [batch_m x w_rows] block that is copied into y_batch afterwards (:202-254). */
+VXO_API void vxo_gemm(int kind, const void* m, const float* x_batch, size_t batch_m,
+                      float* y_batch, int threads) {
+    size_t rows, cols;
+    vxo_dims(kind, m, &rows, &cols);
+    if (batch_m == 0 || rows == 0) return;
+    size_t t = threads < 1 ? 1 : (threads > 16 ? 16 : (size_t)threads);
+    size_t tiles_total = (rows + VXO_TILE_R - 1) / VXO_TILE_R;
+    size_t workers = t < tiles_total ? t : tiles_total;
+    if (workers < 1) workers = 1;
+    size_t tiles_per_worker = (tiles_total + workers - 1) / workers;
+    size_t rows_per_worker = tiles_per_worker * VXO_TILE_R;
+    size_t n = 0;
+    vxo_gemm_job* jobs = (vxo_gemm_job*)calloc(workers, sizeof(vxo_gemm_job));
+    pthread_t* tid = (pthread_t*)calloc(workers, sizeof(pthread_t));
+    for (size_t wi = 0; wi < workers; ++wi) {
+        size_t r_beg = wi * rows_per_worker;
+        if (r_beg >= rows) break;
+        size_t w_rows = rows - r_beg < rows_per_worker ? rows - r_beg : rows_per_worker;
+        jobs[n].kind = kind; jobs[n].m = m; jobs[n].x_batch = x_batch;
+        jobs[n].batch_m = batch_m; jobs[n].cols = cols; jobs[n].r_beg = r_beg;
+        jobs[n].w_rows = w_rows;
+        jobs[n].part_y = (float*)calloc(batch_m * w_rows, sizeof(float));
+        ++n;
+    }
+    if (n == 1) {
+        vxo_gemm_thread(&jobs[0]);
+    } else {
+        for (size_t i = 0; i < n; ++i) pthread_create(&tid[i], NULL, vxo_gemm_thread, &jobs[i]);
+        for (size_t i = 0; i < n; ++i) pthread_join(tid[i], NULL);
+    }
+    for (size_t i = 0; i < n; ++i) {
+        for (size_t mm = 0; mm < batch_m; ++mm)
+            memcpy(y_batch + mm * rows + jobs[i].r_beg, jobs[i].part_y + mm * jobs[i].w_rows,
+                   jobs[i].w_rows * sizeof(float));
+        free(jobs[i].part_y);
+    }
+    free(jobs);
+    free(tid);
+}
+
+/* The GEMV entry used by gemm_cpu's batch_m == 1 branch, for any kind. */
+VXO_API void vxo_gemv_any(int kind, const void* m, const float* x, float* y, int threads) {
+    if (kind == VXO_KIND_CB4) vxo_cb4_gemv((const vxo_cb4*)m, x, y, threads);
+    else if (kind == VXO_KIND_G64) vxo_g64_gemv((const vxo_g64*)m, x, y, threads);
+    else vxo_q8_gemv((const vxo_q8*)m, x, y, threads);
+}
+
+VXO_API int vxo_hardware_threads(void) {
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    return n > 0 ? (int)n : 1;
+}

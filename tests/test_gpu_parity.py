@@ -1,0 +1,328 @@
+"""GPU parity: the HIP path against the CPU oracle, through the C ABI.
+
+Bars (written into each check):
+  * dequant: bit-exact (NaN patterns compared as NaN);
+  * GEMV / GEMM, f32 out: max relative error <= 1e-3, where the error of an
+    output is measured against max(|y_ref|, 2^-10 * sum_c |w_c x_c|) so that
+    outputs that cancel to near zero are judged on the scale of their terms;
+  * bf16 out: within 1 bf16 ulp of f32_to_bf16(y_ref) (or inside the same
+    near-zero floor);
+  * the reference's own GPU-vs-CPU bar, max |err| < 2e-4 at rows=197,
+    cols=544 (tensor_roundtrip_gemv.rs:273-279), is checked as written;
+  * run-to-run and launch-grouping bit identity (llm_gpu_cpu_parity.rs:697).
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from vxg_amd import engine, synth
+from vxg_amd.formats import (CodebookMatrix, bf16_bits_to_f32, f32_to_bf16_bits,
+                             f32_to_f16_bits)
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(os.cpu_count() or 1, 16)
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = engine.HipEngine()
+    print(f"device: {e.device_name}", flush=True)
+    yield e
+    e.close()
+
+
+@pytest.fixture(scope="module")
+def torch_cuda():
+    torch = pytest.importorskip("torch")
+    assert torch.cuda.is_available()
+    return torch
+
+
+def make(kind, rows, cols, seed):
+    if kind == "q8":
+        return synth.make_q8(rows, cols, seed=seed)
+    if kind == "g64":
+        return synth.make_g64(rows, cols, seed=seed)
+    return synth.make_cb4(rows, cols, seed=seed, outlier_frac=0.0074)
+
+
+def floor_scale(W, X):
+    """2^-10 * sum_c |w_rc x_mc| as [M, rows]."""
+    return 2.0 ** -10 * (np.abs(X.astype(np.float64)) @ np.abs(W.astype(np.float64)).T)
+
+
+def q8_floor(m, x):
+    """2^-10 * sum_c |w_rc x_c| for a Q8 matrix, computed in row chunks."""
+    kb = m.blocks_per_row
+    xa = np.zeros(kb * 32, np.float32)
+    xa[: m.cols] = np.abs(x)
+    xa = xa.reshape(kb, 32)
+    d = np.abs(m.scales_f16().view(np.float16).astype(np.float32)).reshape(m.rows, kb)
+    qs = m.qs().reshape(m.rows, kb, 32)
+    out = np.empty(m.rows, np.float64)
+    for r0 in range(0, m.rows, 8192):
+        q = np.abs(qs[r0:r0 + 8192].astype(np.float32))
+        out[r0:r0 + 8192] = ((q * xa[None]).sum(-1) * d[r0:r0 + 8192]).sum(-1)
+    return 2.0 ** -10 * out
+
+
+def max_rel(y, yref, floor):
+    y = np.asarray(y, np.float64)
+    yref = np.asarray(yref, np.float64)
+    return float(np.max(np.abs(y - yref) / np.maximum(np.abs(yref), floor)))
+
+
+def assert_bf16_close(y_bits, yref, floor):
+    a = y_bits.astype(np.int32)
+    b = f32_to_bf16_bits(yref.astype(np.float32)).astype(np.int32)
+    # map sign-magnitude bf16 to a monotone integer line
+    a = np.where(a & 0x8000, -(a & 0x7FFF), a)
+    b = np.where(b & 0x8000, -(b & 0x7FFF), b)
+    ulps = np.abs(a - b)
+    near_zero = np.abs(bf16_bits_to_f32(y_bits) - yref) <= 1e-3 * floor
+    assert np.all((ulps <= 1) | near_zero), int(ulps.max())
+
+
+def assert_bits_equal(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    assert np.array_equal(a.view(np.uint32)[~nan], b.view(np.uint32)[~nan])
+
+
+# ---------------------------------------------------------------- dequant
+
+def closed_form(rows, cols, packed_fn):
+    padded = (cols + 127) // 128 * 128
+    groups = padded // 128
+    cent = ((np.arange(16, dtype=np.float32) - np.float32(7.5)) * np.float32(0.1234567)).astype(np.float32)
+    scales = f32_to_f16_bits(np.float32(0.125) + (np.arange(rows * groups) % 11).astype(np.float32) * np.float32(0.25))
+    rot = np.array([((0x76543210 << s) | (0x76543210 >> (32 - s))) & 0xFFFFFFFF if s else 0x76543210
+                    for s in range(0, 32, 4)], dtype=np.uint64).astype(np.uint32)
+    words = rot[np.arange(rows * groups * 16) % 8]
+    packed = np.array([x for _ in range(rows) for x in packed_fn(cols)], np.uint32)
+    row_ptr = np.arange(0, packed.size + 1, packed.size // rows if rows else 1, dtype=np.uint32)
+    return CodebookMatrix(rows, cols, padded, cent, scales, words, row_ptr, packed)
+
+
+def f16b(v):
+    return int(f32_to_f16_bits(np.array([v], np.float32))[0])
+
+
+@pytest.mark.parametrize("cols", [1, 129, 257, 385])
+def test_dequant_closed_form_fixture(eng, cols):
+    """metal_llm_tests.rs:31-58 (+ :135-139): exact GPU cb4 row dequant."""
+    m = closed_form(515, cols, lambda c: [(f16b(v) << 16) | (c - 1)
+                                          for v in (0.33325195, -0.125, 0.0009765625)])
+    t = eng.upload_packed(m)
+    got = eng.dequant_rows(t)
+    gold = np.load(os.path.join(GOLD, "cb4_closed_form.npz"))
+    for i, r in enumerate(gold[f"c{cols}_rows"]):
+        assert_bits_equal(got[r], gold[f"c{cols}_expected"][i])
+    assert_bits_equal(got, oracle.decode_rows(m))
+    # a row window (the embedding-row probe): rows 513..514
+    assert_bits_equal(eng.dequant_rows(t, 513, 2), got[513:515])
+
+
+@pytest.mark.parametrize("rows", [1, 3, 4, 5, 7, 9, 17])
+@pytest.mark.parametrize("cols", [1, 129, 257, 513])
+def test_dequant_duplicate_column_outliers(eng, rows, cols):
+    m = closed_form(rows, cols, lambda c: [f16b(0.25) << 16, f16b(-0.125) << 16,
+                                           (f16b(0.5) << 16) | (c - 1)])
+    gold = np.load(os.path.join(GOLD, "cb4_dup_outlier.npz"))
+    got = eng.dequant_rows(eng.upload_packed(m))
+    assert_bits_equal(got, gold[f"r{rows}_c{cols}"])
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 33), (197, 544), (512, 2048), (64, 6144)])
+def test_dequant_random_bit_exact(eng, kind, rows, cols):
+    m = make(kind, rows, cols, seed=rows + cols)
+    got = eng.dequant_rows(eng.upload_packed(m))
+    assert_bits_equal(got, oracle.decode_rows(m))
+
+
+def test_dequant_special_values(eng):
+    """Subnormal, zero, inf and NaN scales / table entries dequantise exactly."""
+    m = synth.make_g64(4, 128, seed=1)
+    lut = m.lut_f16.copy()
+    lut[:8] = [0x0000, 0x8000, 0x0001, 0x83FF, 0x7C00, 0xFC00, 0x7E01, 0x7C01]
+    m.lut_f16 = lut
+    m.idx = np.arange(m.idx.size, dtype=np.uint32).astype(np.uint8)
+    got = eng.dequant_rows(eng.upload_packed(m))
+    assert_bits_equal(got, oracle.decode_rows(m))
+    q = synth.make_q8(2, 64, seed=2)
+    b = q.blocks.copy().reshape(-1, 34)
+    b[0, 0:2] = np.array([0x0001], np.uint16).view(np.uint8)   # subnormal d
+    b[1, 0:2] = np.array([0x7C00], np.uint16).view(np.uint8)   # inf d
+    q.blocks = b.reshape(-1)
+    got = eng.dequant_rows(eng.upload_packed(q))
+    assert_bits_equal(got, oracle.decode_rows(q))
+
+
+# ---------------------------------------------------------------- GEMV
+
+def gemv_ref(m, X):
+    return np.stack([oracle.gemv(m, X[i], threads=THREADS) for i in range(X.shape[0])])
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("cols", [1, 129, 257, 513, 544])
+def test_gemv_tail_shapes_host_api(eng, kind, cols):
+    for rows in (1, 3, 5, 7, 9, 17):
+        m = make(kind, rows, cols, seed=rows * 7 + cols)
+        t = eng.upload_packed(m)
+        x = synth.make_x_f32(1, cols, seed=cols)[0]
+        y = np.full(rows, np.nan, np.float32)
+        t.run_gemv(eng, x, y)
+        W = oracle.decode_rows(m)
+        yref = oracle.gemv(m, x)
+        assert max_rel(y, yref, floor_scale(W, x[None])[0]) <= 1e-3, (rows, cols)
+
+
+def test_gemv_reference_bar_197x544(eng):
+    """tensor_roundtrip_gemv.rs:188-279: GPU vs CPU max_abs_err < 2e-4."""
+    for kind in ("cb4", "g64", "q8"):
+        m = make(kind, 197, 544, seed=11)
+        x = synth.make_x_f32(1, 544, seed=999)[0] * np.float32(0.1)
+        y = np.empty(197, np.float32)
+        eng.upload_packed(m).run_gemv(eng, x, y)
+        assert np.max(np.abs(y - oracle.gemv(m, x, threads=4))) < 2e-4, kind
+
+
+BASELINE_SHAPES = [(2048, 2048), (2048, 6144), (6144, 2048), (4096, 4096)]
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("K,N", BASELINE_SHAPES)
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_gemv_baseline_shapes_bf16(eng, torch_cuda, kind, K, N, M):
+    torch = torch_cuda
+    m = make(kind, N, K, seed=K + N + M)
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(M, K, seed=M)
+    X = bf16_bits_to_f32(xb).reshape(M, K)
+    xd = torch.from_numpy(xb.view(np.int16).copy()).cuda()
+    yf = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    yb = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_BF16, M, yf.data_ptr(), engine.DTYPE_F32, s)
+    eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_BF16, M, yb.data_ptr(), engine.DTYPE_BF16, s)
+    torch.cuda.synchronize()
+    yref = gemv_ref(m, X)
+    W = oracle.decode_rows(m)
+    fl = floor_scale(W, X)
+    assert max_rel(yf.cpu().numpy(), yref, fl) <= 1e-3
+    assert_bf16_close(yb.view(torch.int16).cpu().numpy().view(np.uint16), yref, fl)
+
+
+def test_gemv_q8_config0_f32(eng, torch_cuda):
+    """Config 0: Q8, M=1, K=N=4096, x f32 N(0,1), y f32, seed 0."""
+    torch = torch_cuda
+    m = synth.make_q8(4096, 4096, seed=0)
+    x = synth.make_x_f32(1, 4096, seed=0)
+    t = eng.upload_packed(m)
+    xd = torch.from_numpy(x).cuda()
+    yd = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
+    eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_F32, 1, yd.data_ptr(), engine.DTYPE_F32,
+                   torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    yref = oracle.gemv(m, x[0], threads=THREADS)
+    assert max_rel(yd.cpu().numpy()[0], yref, floor_scale(oracle.decode_rows(m), x)[0]) <= 1e-3
+
+
+def test_gemv_lm_head_q8(eng, torch_cuda):
+    """Q8 LM head 151936 x 2048 at M = 1 and 8 against the oracle."""
+    torch = torch_cuda
+    m = synth.make_q8(151936, 2048, seed=5)
+    t = eng.upload_packed(m)
+    for M in (1, 8):
+        xb = synth.make_x_bf16(M, 2048, seed=M)
+        X = bf16_bits_to_f32(xb).reshape(M, 2048)
+        xd = torch.from_numpy(xb.view(np.int16).copy()).cuda()
+        yd = torch.empty((M, 151936), dtype=torch.float32, device="cuda")
+        eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_BF16, M, yd.data_ptr(), engine.DTYPE_F32,
+                       torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        y = yd.cpu().numpy()
+        for i in range(M):
+            yref = oracle.gemv(m, X[i], threads=THREADS)
+            assert max_rel(y[i], yref, q8_floor(m, X[i])) <= 1e-3
+
+
+def test_gemv_deterministic_and_grouping_invariant(eng):
+    for kind in ("cb4", "g64", "q8"):
+        m = make(kind, 17, 513, seed=3)
+        x = synth.make_x_f32(1, 513, seed=4)[0]
+        t = eng.upload_packed(m)
+        y1 = np.empty(17, np.float32)
+        y2 = np.empty(17, np.float32)
+        t.run_gemv(eng, x, y1)
+        t.run_gemv(eng, x, y2)
+        assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+        # the first 5 rows as their own matrix give the same bits
+        if kind == "q8":
+            sub = synth.make_q8(17, 513, seed=3)
+            sub.rows, sub.blocks = 5, sub.blocks[: 5 * sub.blocks_per_row * 34]
+        elif kind == "g64":
+            sub = synth.make_g64(17, 513, seed=3)
+            sub.rows = 5
+            sub.idx = sub.idx[: 5 * sub.padded_cols // 2]
+            sub.lut_f16 = sub.lut_f16[: 5 * sub.padded_cols // 64 * 16]
+        else:
+            sub = synth.make_cb4(17, 513, seed=3)
+            sub.rows = 5
+            sub.scales_f16 = sub.scales_f16[: 5 * sub.padded_cols // 128]
+            sub.packed_words = sub.packed_words[: 5 * sub.padded_cols // 8]
+            sub.outlier_row_ptr = sub.outlier_row_ptr[:6]
+            sub.outliers_packed = sub.outliers_packed[: int(sub.outlier_row_ptr[5])]
+        y5 = np.empty(5, np.float32)
+        eng.upload_packed(sub).run_gemv(eng, x, y5)
+        assert np.array_equal(y5.view(np.uint32), y1[:5].view(np.uint32)), kind
+
+
+def test_run_multi_same_x(eng):
+    """metal.rs:466 / tensor_roundtrip_gemv.rs:284-300: one x, several tensors."""
+    ms = [make(k, 97, 640, seed=i) for i, k in enumerate(["cb4", "g64", "q8", "cb4"])]
+    ts = [eng.upload_packed(m) for m in ms]
+    x = synth.make_x_f32(1, 640, seed=9)[0]
+    ys = [np.empty(97, np.float32) for _ in ts]
+    eng.run_multi_same_x(x, list(zip(ts, ys)))
+    for m, t, y in zip(ms, ts, ys):
+        y1 = np.empty(97, np.float32)
+        t.run_gemv(eng, x, y1)
+        assert np.array_equal(y.view(np.uint32), y1.view(np.uint32))
+
+
+def test_clone_and_free(eng):
+    m = make("g64", 64, 256, seed=1)
+    t = eng.upload_packed(m)
+    c = t.clone()
+    x = synth.make_x_f32(1, 256, seed=1)[0]
+    y1, y2 = np.empty(64, np.float32), np.empty(64, np.float32)
+    t.run_gemv(eng, x, y1)
+    t.free()
+    c.run_gemv(eng, x, y2)
+    assert np.array_equal(y1, y2)
+
+
+def test_error_paths(eng):
+    m = make("q8", 8, 64, seed=1)
+    t = eng.upload_packed(m)
+    with pytest.raises(engine.BackendError) as ei:
+        eng.run_multi_same_x(np.zeros(32, np.float32), [(t, np.empty(8, np.float32))])
+    assert ei.value.code == engine.VXT_E_SHAPE
+    bad = synth.make_cb4(4, 256, seed=1)
+    bad.packed_words = bad.packed_words[:-1]
+    with pytest.raises(engine.BackendError) as ei:
+        eng.upload_packed(bad)
+    assert ei.value.code == engine.VXT_E_FORMAT
+    with pytest.raises(engine.BackendError):
+        eng.dequant_rows(t, 7, 2)
+    with pytest.raises(engine.BackendError) as ei:
+        eng.matmul_dev(t, 0, engine.DTYPE_F32, 1, 0, engine.DTYPE_F32)
+    assert ei.value.code == engine.VXT_E_ARG

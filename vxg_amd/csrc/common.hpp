@@ -1,0 +1,95 @@
+// common.hpp -- device-side descriptors and helpers shared by the kernels.
+//
+// Device-resident layouts (built by vxt_hip.hip at upload time):
+//
+//   Q8_0   qs    int8  [rows][kp]        kp = 32 * ceil(cols/32), 16-B rows
+//          d     f16   [rows][kp/32]
+//   CB4    words u32   [rows][kp/8]      nibble c%8 of word c/8 (as uploaded)
+//          sc    f16   [rows][kp/128]
+//          cent  f32   [16]              (kernel argument)
+//          CSR   row_ptr u32[rows+1], outliers u32[nnz] (col | f16 << 16)
+//   G64    idx   u8    [rows][kp/2]      low nibble = even column
+//          lut   f16   [rows][kp/64][16]
+//
+// Every plane starts 256-byte aligned inside one arena allocation per tensor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vxt {
+
+enum Kind : uint32_t { KIND_CB4 = 2u, KIND_Q8 = 8u, KIND_G64 = 9u };
+
+struct DevTensor {
+  uint32_t kind;
+  uint32_t rows;
+  uint32_t cols;
+  uint32_t kp;          // padded cols of the resident layout
+  const void* p0;       // Q8: qs      CB4: words     G64: idx
+  const uint16_t* p1;   // Q8: d       CB4: scales    G64: lut
+  const uint32_t* row_ptr;   // CB4 only
+  const uint32_t* outliers;  // CB4 only
+  float cent[16];            // CB4 only
+};
+
+// ---- memory ----------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (weights are read once per call: non-temporal hint).
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  u32x4 v = __builtin_nontemporal_load(static_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---- conversions ---------------------------------------------------------
+
+// Exact f16 -> f32 in integer arithmetic: the reference's rule
+// (fp16.rs:6-29), including its NaN payload (sign | 0x7f800000 | mant << 13).
+__device__ __forceinline__ float f16_to_f32_exact(uint32_t h) {
+  uint32_t sign = (h & 0x8000u) << 16;
+  uint32_t e = (h >> 10) & 0x1fu;
+  uint32_t m = h & 0x3ffu;
+  uint32_t out;
+  if (e == 0u) {
+    if (m == 0u) {
+      out = sign;
+    } else {
+      uint32_t sh = (uint32_t)__clz((int)m) - 21u;  // shifts until bit 10 is set
+      out = sign | ((113u - sh) << 23) | (((m << sh) & 0x3ffu) << 13);
+    }
+  } else if (e == 31u) {
+    out = sign | 0x7f800000u | (m << 13);
+  } else {
+    out = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  return __uint_as_float(out);
+}
+
+// Hardware f16 -> f32 (v_cvt_f32_f16); identical to the exact rule for every
+// non-NaN input.  Used on the compute paths.
+__device__ __forceinline__ float f16_to_f32(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// f32 -> bf16 with the reference's rule (fp16.rs:113-120).
+__device__ __forceinline__ uint16_t f32_to_bf16(float v) {
+  uint32_t b = __float_as_uint(v);
+  if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu) != 0u)
+    return (uint16_t)((b >> 16) | 0x0040u);
+  return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+}
+
+// ---- wave64 reductions ----------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+}  // namespace vxt

@@ -1,0 +1,70 @@
+// dequant.hip -- bit-exact dequantisation of resident weights to f32 rows.
+//
+// The probe the reference uses to prove GPU dequant matches decode_row bit
+// for bit (vxt_embedding_cb4_exact, vxt_llm_ops.metal:547-567, checked by
+// metal_llm_tests.rs:95-139).  Values:
+//   CB4: dst[c] = f32(sc) * cent[q] (one f32 rounding, no contraction), then
+//        the row's CSR residuals added in CSR order for col < cols
+//        (codebook.rs:285-337);
+//   Q8:  dst[c] = (float)q * f32(d)                (gguf.rs:223-229, exact);
+//   G64: dst[c] = f32(lut[q])                      (exact).
+// f16 scales and tables are widened with the integer rule of fp16.rs:6-29 so
+// NaN payloads match as well.
+#include "common.hpp"
+
+namespace vxt {
+
+#pragma clang fp contract(off)
+
+__global__ __launch_bounds__(256) void dequant_dense_kernel(DevTensor t, uint32_t row0, uint32_t nrows,
+                                                           float* __restrict__ out) {
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t rr = blockIdx.y;
+  if (c >= t.cols || rr >= nrows) return;
+  const size_t row = (size_t)row0 + rr;
+  float v;
+  if (t.kind == KIND_Q8) {
+    const int8_t q = static_cast<const int8_t*>(t.p0)[row * t.kp + c];
+    v = (float)q * f16_to_f32_exact(t.p1[row * (t.kp / 32) + c / 32]);
+  } else if (t.kind == KIND_CB4) {
+    const uint32_t w = static_cast<const uint32_t*>(t.p0)[row * (t.kp / 8) + c / 8];
+    const uint32_t q = (w >> ((c % 8) * 4)) & 0xfu;
+    const float sc = f16_to_f32_exact(t.p1[row * (t.kp / 128) + c / 128]);
+    v = sc * t.cent[q];
+  } else {
+    const uint8_t b = static_cast<const uint8_t*>(t.p0)[row * (t.kp / 2) + c / 2];
+    const uint32_t q = (b >> ((c & 1) * 4)) & 0xfu;
+    v = f16_to_f32_exact(t.p1[(row * (t.kp / 64) + c / 64) * 16 + q]);
+  }
+  out[(size_t)rr * t.cols + c] = v;
+}
+
+// One thread per row walks that row's CSR range in order, so duplicate
+// columns accumulate in the reference's order.
+__global__ __launch_bounds__(256) void dequant_outlier_kernel(DevTensor t, uint32_t row0,
+                                                             uint32_t nrows, float* __restrict__ out) {
+  const uint32_t rr = blockIdx.x * 256 + threadIdx.x;
+  if (rr >= nrows) return;
+  const uint32_t row = row0 + rr;
+  const uint32_t os = t.row_ptr[row], oe = t.row_ptr[row + 1];
+  float* dst = out + (size_t)rr * t.cols;
+  for (uint32_t i = os; i < oe; ++i) {
+    const uint32_t pk = t.outliers[i];
+    const uint32_t col = pk & 0xffffu;
+    if (col < t.cols) dst[col] = dst[col] + f16_to_f32_exact(pk >> 16);
+  }
+}
+
+hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
+                          hipStream_t s) {
+  if (nrows == 0) return hipSuccess;
+  dim3 grid((t.cols + 255) / 256, nrows);
+  hipLaunchKernelGGL(dequant_dense_kernel, grid, dim3(256), 0, s, t, row0, nrows, out);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || t.kind != KIND_CB4) return e;
+  hipLaunchKernelGGL(dequant_outlier_kernel, dim3((nrows + 255) / 256), dim3(256), 0, s, t, row0,
+                     nrows, out);
+  return hipGetLastError();
+}
+
+}  // namespace vxt

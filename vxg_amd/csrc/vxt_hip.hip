@@ -1,0 +1,582 @@
+// vxt_hip.hip -- C ABI, context, upload (device-residency re-layout) and
+// dispatch for the compressed-weight matmul engine.  See include/vxt_hip.h.
+//
+// Reference boundary mirrored here: vxt_metal_create / upload / run_multi /
+// free_buffer / destroy (crates/vxg-tensor/src/metal_ffi.rs:27-49,
+// native/metal_gemv.mm:258-475) and the engine calls built on them
+// (metal.rs:393-557).  Errors are reported as negative codes plus a message in
+// the caller's buffer; nothing throws across the boundary.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../../include/vxt_hip.h"
+#include "common.hpp"
+
+namespace vxt {
+hipError_t launch_gemv(const DevTensor& t, const void* x, bool x_bf16, bool x_vec, uint32_t m,
+                       void* y, bool y_bf16, hipStream_t s);
+hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y,
+                       bool y_bf16, hipStream_t s);
+hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
+                          hipStream_t s);
+}  // namespace vxt
+
+namespace {
+
+using vxt::DevTensor;
+
+struct Ctx;
+
+struct Tensor {
+  Ctx* ctx = nullptr;
+  uint32_t kind = 0, rows = 0, cols = 0, kp = 0;
+  void* arena = nullptr;
+  size_t bytes = 0;
+  size_t off_p0 = 0, off_p1 = 0, off_rp = 0, off_out = 0;
+  uint32_t nnz = 0;
+  float cent[16] = {};
+
+  DevTensor dev() const {
+    DevTensor d{};
+    const char* base = static_cast<const char*>(arena);
+    d.kind = kind;
+    d.rows = rows;
+    d.cols = cols;
+    d.kp = kp;
+    d.p0 = base + off_p0;
+    d.p1 = reinterpret_cast<const uint16_t*>(base + off_p1);
+    if (kind == VXT_KIND_CB4) {
+      d.row_ptr = reinterpret_cast<const uint32_t*>(base + off_rp);
+      d.outliers = reinterpret_cast<const uint32_t*>(base + off_out);
+      std::memcpy(d.cent, cent, sizeof(cent));
+    }
+    return d;
+  }
+};
+
+struct Ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipEvent_t ev0 = nullptr, ev1 = nullptr;
+  double last_ms = 0.0;
+  void* d_x = nullptr;
+  size_t d_x_cap = 0;
+  void* d_y = nullptr;
+  size_t d_y_cap = 0;
+  std::mutex mu;
+  std::set<Tensor*> tensors;
+};
+
+// ---- error plumbing ---------------------------------------------------------
+
+void set_err(char* err, size_t cap, const char* fmt, ...) {
+  if (!err || cap == 0) return;
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(err, cap, fmt, ap);
+  va_end(ap);
+}
+
+void clear_err(char* err, size_t cap) {
+  if (err && cap) err[0] = '\0';
+}
+
+struct Fail {
+  int code;
+  std::string msg;
+};
+
+#define VXT_HIP_CHECK(expr)                                                                   \
+  do {                                                                                        \
+    hipError_t e_ = (expr);                                                                   \
+    if (e_ != hipSuccess)                                                                     \
+      throw Fail{VXT_E_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)};            \
+  } while (0)
+
+[[noreturn]] void fail(int code, const std::string& msg) { throw Fail{code, msg}; }
+
+template <typename F>
+int guarded(char* err, size_t cap, F&& f) {
+  clear_err(err, cap);
+  try {
+    f();
+    return VXT_OK;
+  } catch (const Fail& e) {
+    set_err(err, cap, "%s", e.msg.c_str());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_err(err, cap, "host allocation failed");
+    return VXT_E_DEVICE;
+  } catch (...) {
+    set_err(err, cap, "unexpected internal error");
+    return VXT_E_DEVICE;
+  }
+}
+
+size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+void use_device(Ctx* c) { VXT_HIP_CHECK(hipSetDevice(c->device)); }
+
+void ensure(void** buf, size_t* cap, size_t need) {
+  if (*cap >= need) return;
+  if (*buf) VXT_HIP_CHECK(hipFree(*buf));
+  *buf = nullptr;
+  *cap = 0;
+  size_t n = std::max<size_t>(need, 1 << 20);
+  VXT_HIP_CHECK(hipMalloc(buf, n));
+  *cap = n;
+}
+
+Tensor* new_tensor(Ctx* c, uint32_t kind, uint32_t rows, uint32_t cols, uint32_t kp,
+                   const std::vector<char>& host_arena) {
+  Tensor* t = new Tensor();
+  t->ctx = c;
+  t->kind = kind;
+  t->rows = rows;
+  t->cols = cols;
+  t->kp = kp;
+  t->bytes = host_arena.size();
+  hipError_t e = hipMalloc(&t->arena, t->bytes);
+  if (e != hipSuccess) {
+    delete t;
+    fail(VXT_E_DEVICE, std::string("hipMalloc of weight arena failed: ") + hipGetErrorString(e));
+  }
+  e = hipMemcpy(t->arena, host_arena.data(), t->bytes, hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    (void)hipFree(t->arena);
+    delete t;
+    fail(VXT_E_DEVICE, std::string("weight upload failed: ") + hipGetErrorString(e));
+  }
+  return t;
+}
+
+void register_tensor(Ctx* c, Tensor* t) {
+  std::lock_guard<std::mutex> g(c->mu);
+  c->tensors.insert(t);
+}
+
+Tensor* as_tensor(void* p) {
+  if (!p) fail(VXT_E_ARG, "null tensor handle");
+  return static_cast<Tensor*>(p);
+}
+
+Ctx* as_ctx(void* p) {
+  if (!p) fail(VXT_E_ARG, "null context handle");
+  return static_cast<Ctx*>(p);
+}
+
+bool dtype_ok(uint32_t d) { return d == VXT_DTYPE_F32 || d == VXT_DTYPE_BF16; }
+
+// Shared argument checks for the device matmul entry points.
+void check_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, const void* y,
+                  uint32_t y_dtype) {
+  if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+  if (!x || !y) fail(VXT_E_ARG, "null activation or output pointer");
+  if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) fail(VXT_E_ARG, "unknown dtype");
+  if (m == 0) fail(VXT_E_SHAPE, "batch_m must be >= 1");
+}
+
+void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, void* y,
+                uint32_t y_dtype, hipStream_t s) {
+  const DevTensor d = t->dev();
+  const bool xb = x_dtype == VXT_DTYPE_BF16;
+  const bool yb = y_dtype == VXT_DTYPE_BF16;
+  hipError_t e;
+  if (m <= 8) {
+    const size_t esz = xb ? 2 : 4;
+    const bool x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t->cols * esz) % 16 == 0;
+    e = vxt::launch_gemv(d, x, xb, x_vec, m, y, yb, s);
+  } else {
+    e = vxt::launch_gemm(d, x, xb, m, y, yb, s);
+  }
+  if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
+  if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e));
+  (void)c;
+}
+
+}  // namespace
+
+// ============================================================================
+// C ABI
+// ============================================================================
+
+extern "C" {
+
+void* vxt_hip_create(int32_t device, char* dev_name, size_t dev_name_cap, char* err,
+                     size_t err_cap) {
+  Ctx* c = nullptr;
+  int rc = guarded(err, err_cap, [&] {
+    int n = 0;
+    VXT_HIP_CHECK(hipGetDeviceCount(&n));
+    if (n <= 0) fail(VXT_E_DEVICE, "no HIP device");
+    int dev = device;
+    if (dev < 0) VXT_HIP_CHECK(hipGetDevice(&dev));
+    if (dev >= n) fail(VXT_E_ARG, "device index out of range");
+    hipDeviceProp_t prop;
+    VXT_HIP_CHECK(hipGetDeviceProperties(&prop, dev));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+      fail(VXT_E_UNSUPPORTED, std::string("kernels are built for gfx950, device is ") + prop.gcnArchName);
+    c = new Ctx();
+    c->device = dev;
+    try {
+      VXT_HIP_CHECK(hipSetDevice(dev));
+      VXT_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
+      VXT_HIP_CHECK(hipEventCreate(&c->ev0));
+      VXT_HIP_CHECK(hipEventCreate(&c->ev1));
+    } catch (...) {
+      if (c->ev1) (void)hipEventDestroy(c->ev1);
+      if (c->ev0) (void)hipEventDestroy(c->ev0);
+      if (c->stream) (void)hipStreamDestroy(c->stream);
+      delete c;
+      c = nullptr;
+      throw;
+    }
+    if (dev_name && dev_name_cap)
+      std::snprintf(dev_name, dev_name_cap, "%s (%s)", prop.name, prop.gcnArchName);
+  });
+  if (rc != VXT_OK) return nullptr;
+  return c;
+}
+
+void vxt_hip_destroy(void* ctx) {
+  if (!ctx) return;
+  Ctx* c = static_cast<Ctx*>(ctx);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  {
+    std::lock_guard<std::mutex> g(c->mu);
+    for (Tensor* t : c->tensors) {
+      (void)hipFree(t->arena);
+      delete t;
+    }
+    c->tensors.clear();
+  }
+  if (c->d_x) (void)hipFree(c->d_x);
+  if (c->d_y) (void)hipFree(c->d_y);
+  (void)hipEventDestroy(c->ev0);
+  (void)hipEventDestroy(c->ev1);
+  (void)hipStreamDestroy(c->stream);
+  delete c;
+}
+
+void* vxt_hip_upload_q8_0(void* ctx, uint32_t rows, uint32_t cols, const uint8_t* blocks,
+                          size_t n_bytes, char* err, size_t err_cap) {
+  Tensor* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!blocks) fail(VXT_E_ARG, "null Q8_0 byte pointer");
+    if (rows == 0 || cols == 0) fail(VXT_E_SHAPE, "rows and cols must be positive");
+    const size_t kb = (cols + 31u) / 32u;
+    if (n_bytes != (size_t)rows * kb * 34u)
+      fail(VXT_E_FORMAT, "Q8_0 byte length != rows * ceil(cols/32) * 34");
+    const uint32_t kp = (uint32_t)(kb * 32u);
+    // Split each 34-byte block into an int8 plane and an f16 scale plane so
+    // every lane's 16-byte load is aligned and contiguous.
+    const size_t qs_bytes = align256((size_t)rows * kp);
+    const size_t d_bytes = align256((size_t)rows * kb * 2u);
+    std::vector<char> h(qs_bytes + d_bytes, 0);
+    int8_t* qs = reinterpret_cast<int8_t*>(h.data());
+    uint16_t* d = reinterpret_cast<uint16_t*>(h.data() + qs_bytes);
+    for (size_t r = 0; r < rows; ++r) {
+      for (size_t b = 0; b < kb; ++b) {
+        const uint8_t* blk = blocks + (r * kb + b) * 34u;
+        d[r * kb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+        std::memcpy(qs + r * kp + b * 32u, blk + 2, 32);
+      }
+    }
+    use_device(c);
+    Tensor* t = new_tensor(c, VXT_KIND_Q8_0, rows, cols, kp, h);
+    t->off_p0 = 0;
+    t->off_p1 = qs_bytes;
+    register_tensor(c, t);
+    out = t;
+  });
+  return out;
+}
+
+void* vxt_hip_upload_cb4(void* ctx, const VxtCb4View* v, char* err, size_t err_cap) {
+  Tensor* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!v) fail(VXT_E_ARG, "null codebook view");
+    if (v->bits != 4) fail(VXT_E_UNSUPPORTED, "only 4-bit codebooks run on the device");
+    if (v->rows == 0 || v->cols == 0) fail(VXT_E_SHAPE, "rows and cols must be positive");
+    if (v->padded_cols < v->cols || v->padded_cols % 128u != 0)
+      fail(VXT_E_FORMAT, "invalid codebook padded_cols");
+    if (v->cols > 65536u && v->n_outliers != 0)
+      fail(VXT_E_FORMAT, "outliers need cols <= 65536");
+    if (!v->centroids || !v->scales_f16 || !v->packed_words || !v->outlier_row_ptr ||
+        (v->n_outliers && !v->outliers_packed))
+      fail(VXT_E_ARG, "null codebook plane");
+    const size_t groups = (size_t)v->rows * (v->padded_cols / 128u);
+    // format.rs:432-439
+    if (v->n_scales != groups || v->n_words != groups * 16u || v->n_row_ptr != (size_t)v->rows + 1u ||
+        v->outlier_row_ptr[v->rows] != v->n_outliers)
+      fail(VXT_E_FORMAT, "corrupt VXT codebook plane lengths");
+    // format.rs:565-574
+    if (v->outlier_row_ptr[0] != 0) fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
+    for (size_t r = 0; r < v->rows; ++r)
+      if (v->outlier_row_ptr[r] > v->outlier_row_ptr[r + 1] || v->outlier_row_ptr[r + 1] > v->n_outliers)
+        fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
+    for (size_t i = 0; i < v->n_outliers; ++i)
+      if ((v->outliers_packed[i] & 0xffffu) >= v->cols) fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
+
+    const size_t w_bytes = align256(v->n_words * 4u);
+    const size_t s_bytes = align256(v->n_scales * 2u);
+    const size_t rp_bytes = align256(v->n_row_ptr * 4u);
+    const size_t o_bytes = align256(std::max<size_t>(v->n_outliers, 1) * 4u);
+    std::vector<char> h(w_bytes + s_bytes + rp_bytes + o_bytes, 0);
+    std::memcpy(h.data(), v->packed_words, v->n_words * 4u);
+    std::memcpy(h.data() + w_bytes, v->scales_f16, v->n_scales * 2u);
+    std::memcpy(h.data() + w_bytes + s_bytes, v->outlier_row_ptr, v->n_row_ptr * 4u);
+    if (v->n_outliers)
+      std::memcpy(h.data() + w_bytes + s_bytes + rp_bytes, v->outliers_packed, v->n_outliers * 4u);
+    use_device(c);
+    Tensor* t = new_tensor(c, VXT_KIND_CB4, v->rows, v->cols, v->padded_cols, h);
+    t->off_p0 = 0;
+    t->off_p1 = w_bytes;
+    t->off_rp = w_bytes + s_bytes;
+    t->off_out = w_bytes + s_bytes + rp_bytes;
+    t->nnz = (uint32_t)v->n_outliers;
+    std::memcpy(t->cent, v->centroids, sizeof(t->cent));
+    register_tensor(c, t);
+    out = t;
+  });
+  return out;
+}
+
+void* vxt_hip_upload_cb4_g64(void* ctx, const VxtCb4G64View* v, char* err, size_t err_cap) {
+  Tensor* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!v) fail(VXT_E_ARG, "null g64 view");
+    if (!v->idx || !v->lut_f16) fail(VXT_E_ARG, "null g64 plane");
+    if (v->rows == 0 || v->cols == 0) fail(VXT_E_SHAPE, "rows and cols must be positive");
+    if (v->padded_cols < v->cols || v->padded_cols % 64u != 0) fail(VXT_E_FORMAT, "invalid g64 padded_cols");
+    const size_t n_idx = (size_t)v->rows * v->padded_cols / 2u;
+    const size_t n_lut = (size_t)v->rows * (v->padded_cols / 64u) * 16u;
+    if (v->n_idx != n_idx || v->n_lut != n_lut) fail(VXT_E_FORMAT, "corrupt g64 plane lengths");
+    const size_t i_bytes = align256(n_idx);
+    const size_t l_bytes = align256(n_lut * 2u);
+    std::vector<char> h(i_bytes + l_bytes, 0);
+    std::memcpy(h.data(), v->idx, n_idx);
+    std::memcpy(h.data() + i_bytes, v->lut_f16, n_lut * 2u);
+    use_device(c);
+    Tensor* t = new_tensor(c, VXT_KIND_CB4_G64, v->rows, v->cols, v->padded_cols, h);
+    t->off_p0 = 0;
+    t->off_p1 = i_bytes;
+    register_tensor(c, t);
+    out = t;
+  });
+  return out;
+}
+
+void* vxt_hip_clone_tensor(void* tensor, char* err, size_t err_cap) {
+  Tensor* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Tensor* s = as_tensor(tensor);
+    Ctx* c = s->ctx;
+    use_device(c);
+    Tensor* t = new Tensor(*s);
+    t->arena = nullptr;
+    hipError_t e = hipMalloc(&t->arena, t->bytes);
+    if (e != hipSuccess) {
+      delete t;
+      fail(VXT_E_DEVICE, std::string("hipMalloc for clone failed: ") + hipGetErrorString(e));
+    }
+    e = hipMemcpy(t->arena, s->arena, t->bytes, hipMemcpyDeviceToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(t->arena);
+      delete t;
+      fail(VXT_E_DEVICE, std::string("clone copy failed: ") + hipGetErrorString(e));
+    }
+    register_tensor(c, t);
+    out = t;
+  });
+  return out;
+}
+
+void vxt_hip_free_tensor(void* tensor) {
+  if (!tensor) return;
+  Tensor* t = static_cast<Tensor*>(tensor);
+  Ctx* c = t->ctx;
+  (void)hipSetDevice(c->device);
+  // Work queued on the context stream may still read the arena.
+  (void)hipStreamSynchronize(c->stream);
+  {
+    std::lock_guard<std::mutex> g(c->mu);
+    c->tensors.erase(t);
+  }
+  (void)hipFree(t->arena);
+  delete t;
+}
+
+int vxt_hip_tensor_info(void* tensor, uint32_t* kind, uint32_t* rows, uint32_t* cols,
+                        uint64_t* device_bytes) {
+  if (!tensor) return VXT_E_ARG;
+  Tensor* t = static_cast<Tensor*>(tensor);
+  if (kind) *kind = t->kind;
+  if (rows) *rows = t->rows;
+  if (cols) *cols = t->cols;
+  if (device_bytes) *device_bytes = t->bytes;
+  return VXT_OK;
+}
+
+int vxt_hip_matmul_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype, uint32_t batch_m,
+                       void* y, uint32_t y_dtype, void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    check_matmul(c, t, x, x_dtype, batch_m, y, y_dtype);
+    run_matmul(c, t, x, x_dtype, batch_m, y, y_dtype, static_cast<hipStream_t>(stream));
+  });
+}
+
+int vxt_hip_matmul_multi_dev(void* ctx, void* const* tensors, uint32_t n, const void* x,
+                             uint32_t x_dtype, uint32_t batch_m, void* const* ys, uint32_t y_dtype,
+                             void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!tensors || !ys) fail(VXT_E_ARG, "null tensor or output array");
+    uint32_t cols = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+      Tensor* t = as_tensor(tensors[i]);
+      check_matmul(c, t, x, x_dtype, batch_m, ys[i], y_dtype);
+      if (i == 0) cols = t->cols;
+      if (t->cols != cols) fail(VXT_E_SHAPE, "tensors sharing x must have equal cols");
+    }
+    for (uint32_t i = 0; i < n; ++i)
+      run_matmul(c, static_cast<Tensor*>(tensors[i]), x, x_dtype, batch_m, ys[i], y_dtype,
+                 static_cast<hipStream_t>(stream));
+  });
+}
+
+int vxt_hip_run_multi(void* ctx, const float* x, uint32_t x_elems, const VxtHipJob* jobs,
+                      uint32_t n_jobs, uint32_t iters, double* gpu_ms, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (gpu_ms) *gpu_ms = 0.0;
+    if (n_jobs == 0) return;
+    if (!x || !jobs) fail(VXT_E_ARG, "null x or job array");
+    size_t y_total = 0;
+    for (uint32_t i = 0; i < n_jobs; ++i) {
+      Tensor* t = as_tensor(jobs[i].tensor);
+      if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+      if (!jobs[i].y) fail(VXT_E_ARG, "null job output");
+      if (x_elems < t->cols) fail(VXT_E_SHAPE, "x shorter than a job's cols");
+      y_total += align256((size_t)t->rows * 4u);
+    }
+    use_device(c);
+    ensure(&c->d_x, &c->d_x_cap, (size_t)x_elems * 4u);
+    ensure(&c->d_y, &c->d_y_cap, y_total);
+    VXT_HIP_CHECK(hipMemcpyAsync(c->d_x, x, (size_t)x_elems * 4u, hipMemcpyHostToDevice, c->stream));
+    const uint32_t runs = std::max<uint32_t>(iters, 1u);
+    VXT_HIP_CHECK(hipEventRecord(c->ev0, c->stream));
+    for (uint32_t it = 0; it < runs; ++it) {
+      size_t off = 0;
+      for (uint32_t i = 0; i < n_jobs; ++i) {
+        Tensor* t = static_cast<Tensor*>(jobs[i].tensor);
+        run_matmul(c, t, c->d_x, VXT_DTYPE_F32, 1, static_cast<char*>(c->d_y) + off, VXT_DTYPE_F32,
+                   c->stream);
+        off += align256((size_t)t->rows * 4u);
+      }
+    }
+    VXT_HIP_CHECK(hipEventRecord(c->ev1, c->stream));
+    size_t off = 0;
+    for (uint32_t i = 0; i < n_jobs; ++i) {
+      Tensor* t = static_cast<Tensor*>(jobs[i].tensor);
+      VXT_HIP_CHECK(hipMemcpyAsync(jobs[i].y, static_cast<char*>(c->d_y) + off, (size_t)t->rows * 4u,
+                                   hipMemcpyDeviceToHost, c->stream));
+      off += align256((size_t)t->rows * 4u);
+    }
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+    float ms = 0.0f;
+    VXT_HIP_CHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    c->last_ms = ms;
+    if (gpu_ms) *gpu_ms = ms;
+  });
+}
+
+int vxt_hip_gemm(void* ctx, void* tensor, const float* x_batch, uint32_t batch_m, float* y_batch,
+                 double* gpu_ms, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    if (gpu_ms) *gpu_ms = 0.0;
+    if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+    if (batch_m == 0) return;  // llm_prefill.rs:163-165
+    if (!x_batch || !y_batch) fail(VXT_E_ARG, "null x_batch or y_batch");
+    use_device(c);
+    const size_t xb = (size_t)batch_m * t->cols * 4u;
+    const size_t yb = (size_t)batch_m * t->rows * 4u;
+    ensure(&c->d_x, &c->d_x_cap, xb);
+    ensure(&c->d_y, &c->d_y_cap, yb);
+    VXT_HIP_CHECK(hipMemcpyAsync(c->d_x, x_batch, xb, hipMemcpyHostToDevice, c->stream));
+    VXT_HIP_CHECK(hipEventRecord(c->ev0, c->stream));
+    run_matmul(c, t, c->d_x, VXT_DTYPE_F32, batch_m, c->d_y, VXT_DTYPE_F32, c->stream);
+    VXT_HIP_CHECK(hipEventRecord(c->ev1, c->stream));
+    VXT_HIP_CHECK(hipMemcpyAsync(y_batch, c->d_y, yb, hipMemcpyDeviceToHost, c->stream));
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+    float ms = 0.0f;
+    VXT_HIP_CHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    c->last_ms = ms;
+    if (gpu_ms) *gpu_ms = ms;
+  });
+}
+
+int vxt_hip_dequant_rows_dev(void* ctx, void* tensor, uint32_t row0, uint32_t nrows, float* out,
+                             void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+    if (!out && nrows) fail(VXT_E_ARG, "null output");
+    if ((uint64_t)row0 + nrows > t->rows) fail(VXT_E_SHAPE, "row range outside the tensor");
+    const DevTensor d = t->dev();
+    for (uint32_t done = 0; done < nrows;) {
+      const uint32_t n = std::min<uint32_t>(nrows - done, 32768u);
+      hipError_t e = vxt::launch_dequant(d, row0 + done, n, out + (size_t)done * t->cols,
+                                         static_cast<hipStream_t>(stream));
+      if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("dequant launch failed: ") + hipGetErrorString(e));
+      done += n;
+    }
+  });
+}
+
+int vxt_hip_dequant_rows(void* ctx, void* tensor, uint32_t row0, uint32_t nrows, float* out,
+                         char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+    if (!out && nrows) fail(VXT_E_ARG, "null output");
+    if ((uint64_t)row0 + nrows > t->rows) fail(VXT_E_SHAPE, "row range outside the tensor");
+    if (nrows == 0) return;
+    use_device(c);
+    const size_t ob = (size_t)nrows * t->cols * 4u;
+    ensure(&c->d_y, &c->d_y_cap, ob);
+    char e2[256];
+    int rc = vxt_hip_dequant_rows_dev(ctx, tensor, row0, nrows, static_cast<float*>(c->d_y), c->stream,
+                                      e2, sizeof(e2));
+    if (rc != VXT_OK) fail(rc, e2);
+    VXT_HIP_CHECK(hipMemcpyAsync(out, c->d_y, ob, hipMemcpyDeviceToHost, c->stream));
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int vxt_hip_last_kernel_ms(void* ctx, double* ms) {
+  if (!ctx || !ms) return VXT_E_ARG;
+  *ms = static_cast<Ctx*>(ctx)->last_ms;
+  return VXT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,312 @@
+"""Python mirror of the reference's GPU matmul engine API over the HIP C ABI.
+
+Shape of the API follows ``MetalEngine`` / ``GpuPackedTensor``
+(``crates/vxg-tensor/src/metal.rs:393-557``) and the weight dispatch seam
+``MatWeight::forward`` / ``forward_multi`` (``llm_cpu.rs:15-71``):
+
+=============================================  ================================
+reference (Rust)                               here
+=============================================  ================================
+``MetalEngine::new()``                         ``HipEngine(device=-1)``
+``MetalEngine::device_name()``                 ``HipEngine.device_name``
+``MetalEngine::upload_packed(&PackedTensor)``  ``HipEngine.upload_packed(m)``
+``MetalEngine::run_multi_same_x(x, jobs)``     ``HipEngine.run_multi_same_x``
+``GpuPackedTensor::run_gemv(eng, x, y, it)``   ``GpuPackedTensor.run_gemv``
+``PackedTensor::gemm_cpu(x, m, y, threads)``   ``HipEngine.gemm(t, X)``
+``CodebookMatrix::decode_row``                 ``HipEngine.dequant_rows``
+``Error::Backend(String)``                     :class:`BackendError`
+``Error::Unsupported``                         :class:`UnsupportedError`
+=============================================  ================================
+
+Device-pointer calls (``matmul_dev`` / ``matmul_multi_dev`` /
+``dequant_rows_dev``) take raw device addresses and a ``hipStream_t``; callers
+that manage device memory with PyTorch pass ``tensor.data_ptr()`` and
+``torch.cuda.current_stream().cuda_stream``.
+
+There is no CPU fallback: if ``libvxt_hip.so`` is missing or no gfx950 device
+is present, construction raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+from typing import Iterable, Sequence
+
+import numpy as np
+
+from .formats import Cb4G64Matrix, CodebookMatrix, Q8Matrix
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvxt_hip.so")
+
+VXT_OK = 0
+VXT_E_ARG, VXT_E_SHAPE, VXT_E_FORMAT, VXT_E_DEVICE, VXT_E_UNSUPPORTED = -1, -2, -3, -4, -5
+DTYPE_F32, DTYPE_BF16 = 0, 1
+KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
+
+ABI_SYMBOLS = (
+    "vxt_hip_create", "vxt_hip_destroy", "vxt_hip_upload_cb4", "vxt_hip_upload_cb4_g64",
+    "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
+    "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
+    "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev",
+    "vxt_hip_last_kernel_ms",
+)
+
+
+class BackendError(RuntimeError):
+    """A failed engine call (the reference's ``Error::Backend(String)``)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class UnsupportedError(BackendError):
+    """A valid request this build does not support (``Error::Unsupported``)."""
+
+
+class Cb4View(C.Structure):
+    _fields_ = [("bits", C.c_uint32), ("rows", C.c_uint32), ("cols", C.c_uint32),
+                ("padded_cols", C.c_uint32),
+                ("centroids", C.c_void_p),
+                ("scales_f16", C.c_void_p), ("n_scales", C.c_size_t),
+                ("packed_words", C.c_void_p), ("n_words", C.c_size_t),
+                ("outlier_row_ptr", C.c_void_p), ("n_row_ptr", C.c_size_t),
+                ("outliers_packed", C.c_void_p), ("n_outliers", C.c_size_t)]
+
+
+class Cb4G64View(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("padded_cols", C.c_uint32),
+                ("reserved", C.c_uint32),
+                ("idx", C.c_void_p), ("n_idx", C.c_size_t),
+                ("lut_f16", C.c_void_p), ("n_lut", C.c_size_t)]
+
+
+class HipJob(C.Structure):
+    _fields_ = [("tensor", C.c_void_p), ("y", C.c_void_p)]
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH):
+    """Load and type the C ABI.  Raises if the library is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is not built; run `python -m vxg_amd.build` first")
+    L = C.CDLL(path)
+    vp, sz, u32, i32 = C.c_void_p, C.c_size_t, C.c_uint32, C.c_int32
+    cp = C.c_char_p
+    L.vxt_hip_create.restype = vp
+    L.vxt_hip_create.argtypes = [i32, cp, sz, cp, sz]
+    L.vxt_hip_destroy.restype = None
+    L.vxt_hip_destroy.argtypes = [vp]
+    L.vxt_hip_upload_cb4.restype = vp
+    L.vxt_hip_upload_cb4.argtypes = [vp, C.POINTER(Cb4View), cp, sz]
+    L.vxt_hip_upload_cb4_g64.restype = vp
+    L.vxt_hip_upload_cb4_g64.argtypes = [vp, C.POINTER(Cb4G64View), cp, sz]
+    L.vxt_hip_upload_q8_0.restype = vp
+    L.vxt_hip_upload_q8_0.argtypes = [vp, u32, u32, vp, sz, cp, sz]
+    L.vxt_hip_clone_tensor.restype = vp
+    L.vxt_hip_clone_tensor.argtypes = [vp, cp, sz]
+    L.vxt_hip_free_tensor.restype = None
+    L.vxt_hip_free_tensor.argtypes = [vp]
+    L.vxt_hip_tensor_info.restype = C.c_int
+    L.vxt_hip_tensor_info.argtypes = [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(u32),
+                                      C.POINTER(C.c_uint64)]
+    L.vxt_hip_run_multi.restype = C.c_int
+    L.vxt_hip_run_multi.argtypes = [vp, vp, u32, C.POINTER(HipJob), u32, u32,
+                                    C.POINTER(C.c_double), cp, sz]
+    L.vxt_hip_gemm.restype = C.c_int
+    L.vxt_hip_gemm.argtypes = [vp, vp, vp, u32, vp, C.POINTER(C.c_double), cp, sz]
+    L.vxt_hip_dequant_rows.restype = C.c_int
+    L.vxt_hip_dequant_rows.argtypes = [vp, vp, u32, u32, vp, cp, sz]
+    L.vxt_hip_matmul_dev.restype = C.c_int
+    L.vxt_hip_matmul_dev.argtypes = [vp, vp, vp, u32, u32, vp, u32, vp, cp, sz]
+    L.vxt_hip_matmul_multi_dev.restype = C.c_int
+    L.vxt_hip_matmul_multi_dev.argtypes = [vp, C.POINTER(vp), u32, vp, u32, u32, C.POINTER(vp),
+                                           u32, vp, cp, sz]
+    L.vxt_hip_dequant_rows_dev.restype = C.c_int
+    L.vxt_hip_dequant_rows_dev.argtypes = [vp, vp, u32, u32, vp, vp, cp, sz]
+    L.vxt_hip_last_kernel_ms.restype = C.c_int
+    L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
+    _lib = L
+    return L
+
+
+def _errbuf():
+    return C.create_string_buffer(512)
+
+
+def _raise(code: int, buf) -> None:
+    msg = buf.value.decode("utf-8", "replace")
+    if code == VXT_E_UNSUPPORTED:
+        raise UnsupportedError(code, msg)
+    raise BackendError(code, msg)
+
+
+def _check(code: int, buf) -> None:
+    if code != VXT_OK:
+        _raise(code, buf)
+
+
+class GpuPackedTensor:
+    """A device-resident weight matrix (``GpuPackedTensor``, metal.rs:527-557)."""
+
+    def __init__(self, engine: "HipEngine", handle: int):
+        self._engine = engine
+        self.handle = handle
+        k, r, c, b = C.c_uint32(), C.c_uint32(), C.c_uint32(), C.c_uint64()
+        load_library().vxt_hip_tensor_info(handle, C.byref(k), C.byref(r), C.byref(c), C.byref(b))
+        self.kind, self.rows, self.cols, self.device_bytes = k.value, r.value, c.value, b.value
+
+    def run_gemv(self, engine: "HipEngine", x, y: np.ndarray, iters: int = 1) -> float:
+        """``y = W x`` (f32, host), ``iters`` times; returns mean kernel ms."""
+        return engine.run_multi_same_x(x, [(self, y)], iters=iters)
+
+    def clone(self) -> "GpuPackedTensor":
+        buf = _errbuf()
+        h = load_library().vxt_hip_clone_tensor(self.handle, buf, len(buf))
+        if not h:
+            _raise(VXT_E_DEVICE, buf)
+        return GpuPackedTensor(self._engine, h)
+
+    def free(self) -> None:
+        if self.handle:
+            load_library().vxt_hip_free_tensor(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            if self.handle and self._engine.ctx:
+                self.free()
+        except Exception:
+            pass
+
+
+class HipEngine:
+    """HIP compute engine for fused compressed-domain GEMV / GEMM (one GPU)."""
+
+    def __init__(self, device: int = -1):
+        L = load_library()
+        name = C.create_string_buffer(256)
+        buf = _errbuf()
+        ctx = L.vxt_hip_create(int(device), name, len(name), buf, len(buf))
+        if not ctx:
+            _raise(VXT_E_DEVICE, buf)
+        self.ctx = ctx
+        self.device_name = name.value.decode()
+
+    # -- lifetime -----------------------------------------------------------
+    def close(self) -> None:
+        if getattr(self, "ctx", None):
+            load_library().vxt_hip_destroy(self.ctx)
+            self.ctx = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # -- upload --------------------------------------------------------------
+    def upload_packed(self, m) -> GpuPackedTensor:
+        """Copy a host weight matrix to HBM in its device-resident layout."""
+        L = load_library()
+        buf = _errbuf()
+        if isinstance(m, CodebookMatrix):
+            keep = [np.ascontiguousarray(m.centroids, np.float32),
+                    np.ascontiguousarray(m.scales_f16, np.uint16),
+                    np.ascontiguousarray(m.packed_words, np.uint32),
+                    np.ascontiguousarray(m.outlier_row_ptr, np.uint32),
+                    np.ascontiguousarray(m.outliers_packed, np.uint32)]
+            v = Cb4View(m.bits, m.rows, m.cols, m.padded_cols, keep[0].ctypes.data,
+                        keep[1].ctypes.data, keep[1].size, keep[2].ctypes.data, keep[2].size,
+                        keep[3].ctypes.data, keep[3].size,
+                        keep[4].ctypes.data if keep[4].size else None, keep[4].size)
+            h = L.vxt_hip_upload_cb4(self.ctx, C.byref(v), buf, len(buf))
+        elif isinstance(m, Cb4G64Matrix):
+            keep = [np.ascontiguousarray(m.idx, np.uint8), np.ascontiguousarray(m.lut_f16, np.uint16)]
+            v = Cb4G64View(m.rows, m.cols, m.padded_cols, 0, keep[0].ctypes.data, keep[0].size,
+                           keep[1].ctypes.data, keep[1].size)
+            h = L.vxt_hip_upload_cb4_g64(self.ctx, C.byref(v), buf, len(buf))
+        elif isinstance(m, Q8Matrix):
+            b = np.ascontiguousarray(m.blocks, np.uint8)
+            h = L.vxt_hip_upload_q8_0(self.ctx, m.rows, m.cols, b.ctypes.data, b.size, buf, len(buf))
+        else:
+            raise UnsupportedError(VXT_E_UNSUPPORTED, f"no device path for {type(m).__name__}")
+        if not h:
+            code = VXT_E_FORMAT if b"corrupt" in buf.value or b"invalid" in buf.value else VXT_E_DEVICE
+            _raise(code, buf)
+        return GpuPackedTensor(self, h)
+
+    # -- host-pointer calls (synchronous) ------------------------------------
+    def run_multi_same_x(self, x, jobs: Sequence, iters: int = 1) -> float:
+        """All ``(tensor, y)`` GEMVs over one f32 x; returns mean kernel ms."""
+        xx = np.ascontiguousarray(x, np.float32).reshape(-1)
+        arr = (HipJob * len(jobs))()
+        for i, (t, y) in enumerate(jobs):
+            if not (isinstance(y, np.ndarray) and y.dtype == np.float32 and y.flags.c_contiguous
+                    and y.size == t.rows):
+                raise BackendError(VXT_E_SHAPE, "y must be a contiguous f32 array of rows")
+            arr[i].tensor = t.handle
+            arr[i].y = y.ctypes.data
+        ms = C.c_double()
+        buf = _errbuf()
+        _check(load_library().vxt_hip_run_multi(self.ctx, xx.ctypes.data, xx.size, arr, len(jobs),
+                                                max(int(iters), 1), C.byref(ms), buf, len(buf)), buf)
+        return ms.value / max(int(iters), 1)
+
+    def gemm(self, t: GpuPackedTensor, X) -> np.ndarray:
+        """``Y[M, rows] = X[M, cols] W^T`` with f32 host arrays."""
+        X = np.ascontiguousarray(X, np.float32).reshape(-1, t.cols)
+        Y = np.empty((X.shape[0], t.rows), np.float32)
+        ms = C.c_double()
+        buf = _errbuf()
+        _check(load_library().vxt_hip_gemm(self.ctx, t.handle, X.ctypes.data, X.shape[0],
+                                           Y.ctypes.data, C.byref(ms), buf, len(buf)), buf)
+        return Y
+
+    def dequant_rows(self, t: GpuPackedTensor, row0: int = 0, nrows: int | None = None) -> np.ndarray:
+        nrows = t.rows - row0 if nrows is None else nrows
+        out = np.empty((nrows, t.cols), np.float32)
+        buf = _errbuf()
+        _check(load_library().vxt_hip_dequant_rows(self.ctx, t.handle, row0, nrows,
+                                                   out.ctypes.data, buf, len(buf)), buf)
+        return out
+
+    def last_kernel_ms(self) -> float:
+        ms = C.c_double()
+        load_library().vxt_hip_last_kernel_ms(self.ctx, C.byref(ms))
+        return ms.value
+
+    # -- device-pointer calls (asynchronous on `stream`) ----------------------
+    def matmul_dev(self, t: GpuPackedTensor, x_ptr: int, x_dtype: int, batch_m: int, y_ptr: int,
+                   y_dtype: int, stream: int = 0) -> None:
+        buf = _errbuf()
+        _check(load_library().vxt_hip_matmul_dev(self.ctx, t.handle, x_ptr, x_dtype, batch_m,
+                                                 y_ptr, y_dtype, stream or None, buf, len(buf)), buf)
+
+    def matmul_multi_dev(self, ts: Sequence[GpuPackedTensor], x_ptr: int, x_dtype: int,
+                         batch_m: int, y_ptrs: Iterable[int], y_dtype: int, stream: int = 0) -> None:
+        ys = list(y_ptrs)
+        ta = (C.c_void_p * len(ts))(*[t.handle for t in ts])
+        ya = (C.c_void_p * len(ys))(*ys)
+        buf = _errbuf()
+        _check(load_library().vxt_hip_matmul_multi_dev(self.ctx, ta, len(ts), x_ptr, x_dtype,
+                                                       batch_m, ya, y_dtype, stream or None, buf,
+                                                       len(buf)), buf)
+
+    def dequant_rows_dev(self, t: GpuPackedTensor, row0: int, nrows: int, out_ptr: int,
+                         stream: int = 0) -> None:
+        buf = _errbuf()
+        _check(load_library().vxt_hip_dequant_rows_dev(self.ctx, t.handle, row0, nrows, out_ptr,
+                                                       stream or None, buf, len(buf)), buf)
