@@ -9,9 +9,9 @@ activations + outputs, each once) per second over the timed steps.
 A "step" is one GEMV launch over one of ``copies`` distinct device-resident
 weight copies (together > 2x the 256 MB Infinity Cache), so every step reads
 its weights from HBM.  Steps are captured once in a HIP graph and replayed;
-the timed region is one replay of ``--steps`` launches bracketed by
-``torch.cuda.synchronize()``.  HIP events on the launch stream give the
-per-launch kernel time used for ``roofline``.
+the timed region is one replay of ``--steps`` launches, waited for on both
+sides (stream synchronize).  A hipEvent pair recorded on the launch
+stream around the replay gives the per-launch GPU time used for ``roofline``.
 
 Other configurations are reported under ``"secondary"`` (Q8 GEMV config 0,
 the Q8 small-M sweep, prefill GEMM, decode stack).  ``cpu_baseline`` times the
@@ -65,45 +65,26 @@ def call_bytes(m, M: int, x_elem: int, y_elem: int) -> int:
 # GPU timing
 # --------------------------------------------------------------------------
 
-class GraphTimer:
-    """Capture `steps` launches in one HIP graph and time a replay."""
+def time_graph(eng, enqueue, steps: int, warmup: int):
+    """Capture `steps` launches into one HIP graph; time one replay.
 
-    def __init__(self, torch, enqueue, steps: int, warmup: int):
-        self.torch = torch
-        self.enqueue = enqueue
-        self.steps = steps
-        self.warmup = warmup
-
-    def run(self):
-        torch = self.torch
-        s = torch.cuda.Stream()
-        with torch.cuda.stream(s):
-            for i in range(max(self.warmup, 1)):      # eager warm-up (also JIT-free)
-                self.enqueue(i, s.cuda_stream)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=s):
-            for i in range(self.steps):
-                self.enqueue(i, s.cuda_stream)
-        torch.cuda.synchronize()
-        g.replay()                                    # warm replay
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        with torch.cuda.stream(s):
-            e0.record(s)
-            g.replay()
-            e1.record(s)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        ev_ms = e0.elapsed_time(e1)
-        del g
-        return (t1 - t0), ev_ms
+    Returns (wall seconds, GPU ms from the hipEvent pair on the launch stream).
+    """
+    s = eng.stream
+    for i in range(max(warmup, 1)):                   # eager warm-up
+        enqueue(i, s)
+    eng.synchronize()
+    g = eng.capture(lambda st: [enqueue(i, st) for i in range(steps)])
+    g.launch(1)                                       # warm replay
+    eng.synchronize()
+    t0 = time.perf_counter()
+    ev_ms = g.launch(1)                               # records events, waits
+    t1 = time.perf_counter()
+    g.free()
+    return (t1 - t0), ev_ms
 
 
-def bench_gemv(torch, eng, m, M: int, x_dtype: str, y_dtype: str, steps: int, warmup: int,
+def bench_gemv(eng, m, M: int, x_dtype: str, y_dtype: str, steps: int, warmup: int,
                seed: int = 0):
     """GB/s of y = W x over rotating weight copies. Returns a result dict."""
     from vxg_amd import engine, synth
@@ -112,28 +93,26 @@ def bench_gemv(torch, eng, m, M: int, x_dtype: str, y_dtype: str, steps: int, wa
     base = eng.upload_packed(m)
     copies = [base] + [base.clone() for _ in range(n_copies - 1)]
     if x_dtype == "bf16":
-        xh = synth.make_x_bf16(M, m.cols, seed=seed)
-        xd = torch.from_numpy(xh.view(np.int16).copy()).cuda()
+        xd = eng.to_device(synth.make_x_bf16(M, m.cols, seed=seed))
         xdt, xel = engine.DTYPE_BF16, 2
     else:
-        xh = synth.make_x_f32(M, m.cols, seed=seed)
-        xd = torch.from_numpy(xh).cuda()
+        xd = eng.to_device(synth.make_x_f32(M, m.cols, seed=seed))
         xdt, xel = engine.DTYPE_F32, 4
     if y_dtype == "bf16":
-        yd = torch.empty((M, m.rows), dtype=torch.bfloat16, device="cuda")
         ydt, yel = engine.DTYPE_BF16, 2
     else:
-        yd = torch.empty((M, m.rows), dtype=torch.float32, device="cuda")
         ydt, yel = engine.DTYPE_F32, 4
-    xp, yp = xd.data_ptr(), yd.data_ptr()
+    yd = eng.alloc(M * m.rows * yel)
 
     def enqueue(i, stream):
-        eng.matmul_dev(copies[i % n_copies], xp, xdt, M, yp, ydt, stream)
+        eng.matmul_dev(copies[i % n_copies], xd.ptr, xdt, M, yd.ptr, ydt, stream)
 
-    wall_s, ev_ms = GraphTimer(torch, enqueue, steps, warmup).run()
+    wall_s, ev_ms = time_graph(eng, enqueue, steps, warmup)
     nbytes = call_bytes(m, M, xel, yel)
     for c in copies:
         c.free()
+    xd.free()
+    yd.free()
     kern_ms = ev_ms / steps
     return {
         "bytes_per_call": nbytes, "weight_copies": n_copies, "steps": steps,
@@ -189,7 +168,6 @@ def main():
               f"multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
-    import torch
     from vxg_amd import engine, synth
 
     eng = engine.HipEngine()
@@ -198,7 +176,7 @@ def main():
     # headline: config 1
     m = synth.make_g64(6144, 2048, seed=1)
     log("config 1: cb4-g64 GEMV M=1 K=2048 N=6144")
-    r = bench_gemv(torch, eng, m, 1, "bf16", "f32", args.steps, args.warmup, seed=0)
+    r = bench_gemv(eng, m, 1, "bf16", "f32", args.steps, args.warmup, seed=0)
     log(f"  {r['GBps']:.1f} GB/s wall, kernel {r['kernel_ms']*1e3:.2f} us "
         f"({r['kernel_GBps']:.1f} GB/s)")
 
@@ -206,7 +184,7 @@ def main():
     if not args.quick:
         m0 = synth.make_q8(4096, 4096, seed=0)
         log("config 0: Q8 GEMV M=1 K=N=4096 x f32")
-        r0 = bench_gemv(torch, eng, m0, 1, "f32", "f32", args.steps, args.warmup, seed=0)
+        r0 = bench_gemv(eng, m0, 1, "f32", "f32", args.steps, args.warmup, seed=0)
         secondary.append({"config": "0: q8 gemv M=1 K=4096 N=4096 x=f32 y=f32",
                           "GBps": round(r0["GBps"], 1), "kernel_us": round(r0["kernel_ms"] * 1e3, 3),
                           "kernel_GBps": round(r0["kernel_GBps"], 1),
@@ -216,7 +194,7 @@ def main():
             mq = synth.make_q8(N, K, seed=2)
             for M in (1, 2, 4, 8):
                 st = max(20, min(args.steps, int(2e9 / weight_bytes(mq))))
-                rq = bench_gemv(torch, eng, mq, M, "bf16", "f32", st, min(args.warmup, 5), seed=M)
+                rq = bench_gemv(eng, mq, M, "bf16", "f32", st, min(args.warmup, 5), seed=M)
                 secondary.append({"config": f"2: q8 gemv M={M} K={K} N={N}",
                                   "GBps": round(rq["GBps"], 1),
                                   "kernel_us": round(rq["kernel_ms"] * 1e3, 3),

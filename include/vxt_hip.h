@@ -176,6 +176,40 @@ VXT_API int vxt_hip_matmul_multi_dev(void* ctx, void* const* tensors, uint32_t n
 VXT_API int vxt_hip_dequant_rows_dev(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
                              float* out, void* stream, char* err, size_t err_cap);
 
+/* ---- device memory, stream and graphs ---------------------------------- */
+/* What a host without another GPU runtime (the Rust engine, C callers) needs
+ * to keep activations resident and to replay a decode loop without per-launch
+ * CPU overhead.  No reference counterpart: the Metal bridge keeps x and y in
+ * unified memory (metal_gemv.mm:350-351) and records one command buffer per
+ * call (metal_gemv.mm:369-445). */
+
+/* hipMalloc'd device buffer owned by the context (freed by destroy). */
+VXT_API void* vxt_hip_device_alloc(void* ctx, size_t bytes, char* err, size_t err_cap);
+VXT_API void vxt_hip_device_free(void* ctx, void* dev_ptr);
+
+/* Synchronous copy on the context stream; kind: 0 host->device,
+ * 1 device->host, 2 device->device. */
+VXT_API int vxt_hip_memcpy(void* ctx, void* dst, const void* src, size_t bytes, uint32_t kind,
+                           char* err, size_t err_cap);
+
+/* The context's hipStream_t, for the *_dev entry points. */
+VXT_API void* vxt_hip_stream(void* ctx);
+
+/* Wait for all work queued on the context stream. */
+VXT_API int vxt_hip_synchronize(void* ctx, char* err, size_t err_cap);
+
+/* Start capturing the context stream into a HIP graph; enqueue *_dev calls
+ * with stream = vxt_hip_stream(ctx); vxt_hip_capture_end returns the
+ * instantiated graph (NULL on failure). */
+VXT_API int vxt_hip_capture_begin(void* ctx, char* err, size_t err_cap);
+VXT_API void* vxt_hip_capture_end(void* ctx, char* err, size_t err_cap);
+
+/* Launch a captured graph `replays` times back to back on the context
+ * stream, wait, and report the GPU time of all replays (hipEvent pair). */
+VXT_API int vxt_hip_graph_launch(void* ctx, void* graph, uint32_t replays, double* gpu_ms,
+                                 char* err, size_t err_cap);
+VXT_API void vxt_hip_graph_free(void* graph);
+
 /* Kernel time of the last synchronous call, in ms (hipEvent pair). */
 VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
 

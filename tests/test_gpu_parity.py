@@ -35,11 +35,17 @@ def eng():
     e.close()
 
 
-@pytest.fixture(scope="module")
-def torch_cuda():
-    torch = pytest.importorskip("torch")
-    assert torch.cuda.is_available()
-    return torch
+def run_dev(eng, t, x_host, x_dtype, M, y_dtype):
+    """matmul_dev with engine-owned device buffers; returns the host result."""
+    xd = eng.to_device(x_host)
+    ybytes = M * t.rows * (4 if y_dtype == engine.DTYPE_F32 else 2)
+    yd = eng.alloc(ybytes)
+    eng.matmul_dev(t, xd.ptr, x_dtype, M, yd.ptr, y_dtype, eng.stream)
+    eng.synchronize()
+    out = yd.download(np.float32 if y_dtype == engine.DTYPE_F32 else np.uint16, (M, t.rows))
+    xd.free()
+    yd.free()
+    return out
 
 
 def make(kind, rows, cols, seed):
@@ -200,55 +206,38 @@ BASELINE_SHAPES = [(2048, 2048), (2048, 6144), (6144, 2048), (4096, 4096)]
 @pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
 @pytest.mark.parametrize("K,N", BASELINE_SHAPES)
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
-def test_gemv_baseline_shapes_bf16(eng, torch_cuda, kind, K, N, M):
-    torch = torch_cuda
+def test_gemv_baseline_shapes_bf16(eng, kind, K, N, M):
     m = make(kind, N, K, seed=K + N + M)
     t = eng.upload_packed(m)
     xb = synth.make_x_bf16(M, K, seed=M)
     X = bf16_bits_to_f32(xb).reshape(M, K)
-    xd = torch.from_numpy(xb.view(np.int16).copy()).cuda()
-    yf = torch.empty((M, N), dtype=torch.float32, device="cuda")
-    yb = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    s = torch.cuda.current_stream().cuda_stream
-    eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_BF16, M, yf.data_ptr(), engine.DTYPE_F32, s)
-    eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_BF16, M, yb.data_ptr(), engine.DTYPE_BF16, s)
-    torch.cuda.synchronize()
+    yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
     yref = gemv_ref(m, X)
     W = oracle.decode_rows(m)
     fl = floor_scale(W, X)
-    assert max_rel(yf.cpu().numpy(), yref, fl) <= 1e-3
-    assert_bf16_close(yb.view(torch.int16).cpu().numpy().view(np.uint16), yref, fl)
+    assert max_rel(yf, yref, fl) <= 1e-3
+    assert_bf16_close(yb, yref, fl)
 
 
-def test_gemv_q8_config0_f32(eng, torch_cuda):
+def test_gemv_q8_config0_f32(eng):
     """Config 0: Q8, M=1, K=N=4096, x f32 N(0,1), y f32, seed 0."""
-    torch = torch_cuda
     m = synth.make_q8(4096, 4096, seed=0)
     x = synth.make_x_f32(1, 4096, seed=0)
     t = eng.upload_packed(m)
-    xd = torch.from_numpy(x).cuda()
-    yd = torch.empty((1, 4096), dtype=torch.float32, device="cuda")
-    eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_F32, 1, yd.data_ptr(), engine.DTYPE_F32,
-                   torch.cuda.current_stream().cuda_stream)
-    torch.cuda.synchronize()
+    y = run_dev(eng, t, x, engine.DTYPE_F32, 1, engine.DTYPE_F32)
     yref = oracle.gemv(m, x[0], threads=THREADS)
-    assert max_rel(yd.cpu().numpy()[0], yref, floor_scale(oracle.decode_rows(m), x)[0]) <= 1e-3
+    assert max_rel(y[0], yref, floor_scale(oracle.decode_rows(m), x)[0]) <= 1e-3
 
 
-def test_gemv_lm_head_q8(eng, torch_cuda):
+def test_gemv_lm_head_q8(eng):
     """Q8 LM head 151936 x 2048 at M = 1 and 8 against the oracle."""
-    torch = torch_cuda
     m = synth.make_q8(151936, 2048, seed=5)
     t = eng.upload_packed(m)
     for M in (1, 8):
         xb = synth.make_x_bf16(M, 2048, seed=M)
         X = bf16_bits_to_f32(xb).reshape(M, 2048)
-        xd = torch.from_numpy(xb.view(np.int16).copy()).cuda()
-        yd = torch.empty((M, 151936), dtype=torch.float32, device="cuda")
-        eng.matmul_dev(t, xd.data_ptr(), engine.DTYPE_BF16, M, yd.data_ptr(), engine.DTYPE_F32,
-                       torch.cuda.current_stream().cuda_stream)
-        torch.cuda.synchronize()
-        y = yd.cpu().numpy()
+        y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
         for i in range(M):
             yref = oracle.gemv(m, X[i], threads=THREADS)
             assert max_rel(y[i], yref, q8_floor(m, X[i])) <= 1e-3
@@ -326,3 +315,80 @@ def test_error_paths(eng):
     with pytest.raises(engine.BackendError) as ei:
         eng.matmul_dev(t, 0, engine.DTYPE_F32, 1, 0, engine.DTYPE_F32)
     assert ei.value.code == engine.VXT_E_ARG
+
+
+def test_graph_replays_match_eager(eng):
+    """Captured GEMVs replayed several times, with eager work in between."""
+    m = make("g64", 2048, 2048, seed=2)
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(1, 2048, seed=2)
+    xd = eng.to_device(xb)
+    yd = eng.alloc(2048 * 4)
+    eng.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 1, yd.ptr, engine.DTYPE_F32, eng.stream)
+    eng.synchronize()
+    ref = yd.download(np.float32, 2048)
+    g = eng.capture(lambda s: [eng.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 1, yd.ptr,
+                                              engine.DTYPE_F32, s) for _ in range(3)])
+    other = eng.alloc(2048 * 4)
+    for rep in range(4):
+        yd.upload(np.full(2048, np.nan, np.float32))
+        eng.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 1, other.ptr, engine.DTYPE_F32, eng.stream)
+        g.launch(1 + rep)
+        assert np.array_equal(yd.download(np.float32, 2048).view(np.uint32), ref.view(np.uint32)), rep
+    g.free()
+
+
+# ---------------------------------------------------------------- GEMM
+
+def gemm_check(y, yref, W, X, bf16):
+    fl = floor_scale(W, X)
+    if bf16:
+        assert_bf16_close(y, yref, fl)
+    else:
+        assert max_rel(y, yref, fl) <= 1e-3
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (5, 33), (97, 130), (130, 257), (257, 544)])
+@pytest.mark.parametrize("M", [9, 11, 64, 129])
+def test_gemm_tail_shapes_host_api(eng, kind, rows, cols, M):
+    m = make(kind, rows, cols, seed=rows + cols + M)
+    t = eng.upload_packed(m)
+    X = synth.make_x_f32(M, cols, seed=M)
+    Y = eng.gemm(t, X)
+    gemm_check(Y, oracle.gemm(m, X, threads=THREADS), oracle.decode_rows(m), X, False)
+
+
+def test_gemm_matches_per_token_gemv_96x256x11(eng):
+    """vxt_roadmap_steps.rs:210-230 on the device: gemm vs per-token gemv."""
+    for kind in ("cb4", "g64", "q8"):
+        m = make(kind, 96, 256, seed=901)
+        t = eng.upload_packed(m)
+        X = synth.make_x_f32(11, 256, seed=902)
+        Yg = eng.gemm(t, X)
+        Yv = np.stack([np.empty(96, np.float32) for _ in range(11)])
+        for i in range(11):
+            t.run_gemv(eng, X[i], Yv[i])
+        a, b = Yg.astype(np.float64).ravel(), Yv.astype(np.float64).ravel()
+        assert a @ b / (np.linalg.norm(a) * np.linalg.norm(b)) > 0.999999, kind
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
+@pytest.mark.parametrize("M", [128, 512, 2048])
+def test_gemm_prefill_shapes_bf16(eng, kind, K, N, M):
+    """Config 3: bf16 activations, fp32 accumulate, bf16 output (and f32)."""
+    m = make(kind, N, K, seed=K + M)
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(M, K, seed=M)
+    X = bf16_bits_to_f32(xb).reshape(M, K)
+    yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+    yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    # oracle on a token sample (tokens are independent rows of the product)
+    sel = np.unique(np.r_[0, M - 1, np.random.default_rng(M).choice(M, 14, replace=False)])
+    W = oracle.decode_rows(m)
+    yref = oracle.gemm(m, X[sel], threads=THREADS)
+    gemm_check(yb[sel], yref, W, X[sel], True)
+    gemm_check(yf[sel], yref, W, X[sel], False)
+    # every token: bf16 output is the rounding of the f32 output
+    assert np.array_equal(yb, f32_to_bf16_bits(yf))

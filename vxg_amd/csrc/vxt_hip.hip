@@ -74,6 +74,14 @@ struct Ctx {
   size_t d_y_cap = 0;
   std::mutex mu;
   std::set<Tensor*> tensors;
+  std::set<void*> buffers;
+  bool capturing = false;
+};
+
+struct Graph {
+  Ctx* ctx = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
 };
 
 // ---- error plumbing ---------------------------------------------------------
@@ -259,6 +267,8 @@ void vxt_hip_destroy(void* ctx) {
       delete t;
     }
     c->tensors.clear();
+    for (void* b : c->buffers) (void)hipFree(b);
+    c->buffers.clear();
   }
   if (c->d_x) (void)hipFree(c->d_x);
   if (c->d_y) (void)hipFree(c->d_y);
@@ -571,6 +581,121 @@ int vxt_hip_dequant_rows(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
     VXT_HIP_CHECK(hipMemcpyAsync(out, c->d_y, ob, hipMemcpyDeviceToHost, c->stream));
     VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
   });
+}
+
+void* vxt_hip_device_alloc(void* ctx, size_t bytes, char* err, size_t err_cap) {
+  void* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    use_device(c);
+    void* p = nullptr;
+    VXT_HIP_CHECK(hipMalloc(&p, std::max<size_t>(bytes, 256)));
+    std::lock_guard<std::mutex> g(c->mu);
+    c->buffers.insert(p);
+    out = p;
+  });
+  return out;
+}
+
+void vxt_hip_device_free(void* ctx, void* dev_ptr) {
+  if (!ctx || !dev_ptr) return;
+  Ctx* c = static_cast<Ctx*>(ctx);
+  (void)hipSetDevice(c->device);
+  (void)hipStreamSynchronize(c->stream);
+  std::lock_guard<std::mutex> g(c->mu);
+  if (c->buffers.erase(dev_ptr)) (void)hipFree(dev_ptr);
+}
+
+int vxt_hip_memcpy(void* ctx, void* dst, const void* src, size_t bytes, uint32_t kind, char* err,
+                   size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (bytes == 0) return;
+    if (!dst || !src) fail(VXT_E_ARG, "null copy pointer");
+    hipMemcpyKind k;
+    switch (kind) {
+      case 0: k = hipMemcpyHostToDevice; break;
+      case 1: k = hipMemcpyDeviceToHost; break;
+      case 2: k = hipMemcpyDeviceToDevice; break;
+      default: fail(VXT_E_ARG, "unknown copy kind");
+    }
+    use_device(c);
+    VXT_HIP_CHECK(hipMemcpyAsync(dst, src, bytes, k, c->stream));
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+void* vxt_hip_stream(void* ctx) {
+  if (!ctx) return nullptr;
+  return static_cast<Ctx*>(ctx)->stream;
+}
+
+int vxt_hip_synchronize(void* ctx, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    use_device(c);
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int vxt_hip_capture_begin(void* ctx, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (c->capturing) fail(VXT_E_ARG, "capture already in progress");
+    use_device(c);
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+    VXT_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+  });
+}
+
+void* vxt_hip_capture_end(void* ctx, char* err, size_t err_cap) {
+  Graph* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!c->capturing) fail(VXT_E_ARG, "no capture in progress");
+    use_device(c);
+    c->capturing = false;
+    hipGraph_t g = nullptr;
+    VXT_HIP_CHECK(hipStreamEndCapture(c->stream, &g));
+    hipGraphExec_t ex = nullptr;
+    hipError_t e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+      (void)hipGraphDestroy(g);
+      fail(VXT_E_DEVICE, std::string("hipGraphInstantiate failed: ") + hipGetErrorString(e));
+    }
+    out = new Graph{c, g, ex};
+  });
+  return out;
+}
+
+int vxt_hip_graph_launch(void* ctx, void* graph, uint32_t replays, double* gpu_ms, char* err,
+                         size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!graph) fail(VXT_E_ARG, "null graph");
+    Graph* g = static_cast<Graph*>(graph);
+    if (g->ctx != c) fail(VXT_E_ARG, "graph belongs to another context");
+    use_device(c);
+    VXT_HIP_CHECK(hipEventRecord(c->ev0, c->stream));
+    for (uint32_t i = 0; i < replays; ++i) VXT_HIP_CHECK(hipGraphLaunch(g->exec, c->stream));
+    VXT_HIP_CHECK(hipEventRecord(c->ev1, c->stream));
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+    float ms = 0.0f;
+    VXT_HIP_CHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
+    c->last_ms = ms;
+    if (gpu_ms) *gpu_ms = ms;
+  });
+}
+
+void vxt_hip_graph_free(void* graph) {
+  if (!graph) return;
+  Graph* g = static_cast<Graph*>(graph);
+  (void)hipSetDevice(g->ctx->device);
+  (void)hipStreamSynchronize(g->ctx->stream);
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  delete g;
 }
 
 int vxt_hip_last_kernel_ms(void* ctx, double* ms) {

@@ -19,9 +19,13 @@ reference (Rust)                               here
 =============================================  ================================
 
 Device-pointer calls (``matmul_dev`` / ``matmul_multi_dev`` /
-``dequant_rows_dev``) take raw device addresses and a ``hipStream_t``; callers
-that manage device memory with PyTorch pass ``tensor.data_ptr()`` and
-``torch.cuda.current_stream().cuda_stream``.
+``dequant_rows_dev``) take raw device addresses and a ``hipStream_t``.  The
+engine owns what they need -- :meth:`HipEngine.alloc` / :class:`DeviceBuffer`,
+the context stream (:attr:`HipEngine.stream`) and HIP-graph capture
+(:meth:`HipEngine.capture`) -- so no other GPU runtime has to be loaded.  (A
+process that also uses PyTorch must import torch first: torch ships its own
+copy of the HIP runtime under the same soname, and the first one loaded is the
+one both use.)
 
 There is no CPU fallback: if ``libvxt_hip.so`` is missing or no gfx950 device
 is present, construction raises.
@@ -49,7 +53,9 @@ ABI_SYMBOLS = (
     "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev",
-    "vxt_hip_last_kernel_ms",
+    "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
+    "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
+    "vxt_hip_graph_launch", "vxt_hip_graph_free",
 )
 
 
@@ -132,6 +138,24 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_dequant_rows_dev.argtypes = [vp, vp, u32, u32, vp, vp, cp, sz]
     L.vxt_hip_last_kernel_ms.restype = C.c_int
     L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
+    L.vxt_hip_device_alloc.restype = vp
+    L.vxt_hip_device_alloc.argtypes = [vp, sz, cp, sz]
+    L.vxt_hip_device_free.restype = None
+    L.vxt_hip_device_free.argtypes = [vp, vp]
+    L.vxt_hip_memcpy.restype = C.c_int
+    L.vxt_hip_memcpy.argtypes = [vp, vp, vp, sz, u32, cp, sz]
+    L.vxt_hip_stream.restype = vp
+    L.vxt_hip_stream.argtypes = [vp]
+    L.vxt_hip_synchronize.restype = C.c_int
+    L.vxt_hip_synchronize.argtypes = [vp, cp, sz]
+    L.vxt_hip_capture_begin.restype = C.c_int
+    L.vxt_hip_capture_begin.argtypes = [vp, cp, sz]
+    L.vxt_hip_capture_end.restype = vp
+    L.vxt_hip_capture_end.argtypes = [vp, cp, sz]
+    L.vxt_hip_graph_launch.restype = C.c_int
+    L.vxt_hip_graph_launch.argtypes = [vp, vp, u32, C.POINTER(C.c_double), cp, sz]
+    L.vxt_hip_graph_free.restype = None
+    L.vxt_hip_graph_free.argtypes = [vp]
     _lib = L
     return L
 
@@ -184,6 +208,63 @@ class GpuPackedTensor:
                 self.free()
         except Exception:
             pass
+
+
+class DeviceBuffer:
+    """A device allocation owned by the engine (``vxt_hip_device_alloc``)."""
+
+    def __init__(self, engine: "HipEngine", nbytes: int):
+        buf = _errbuf()
+        p = load_library().vxt_hip_device_alloc(engine.ctx, int(nbytes), buf, len(buf))
+        if not p:
+            _raise(VXT_E_DEVICE, buf)
+        self._engine = engine
+        self.ptr = p
+        self.nbytes = int(nbytes)
+
+    def upload(self, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        if a.nbytes > self.nbytes:
+            raise BackendError(VXT_E_SHAPE, "array larger than the buffer")
+        buf = _errbuf()
+        _check(load_library().vxt_hip_memcpy(self._engine.ctx, self.ptr, a.ctypes.data, a.nbytes, 0,
+                                             buf, len(buf)), buf)
+        return self
+
+    def download(self, dtype, shape) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        if out.nbytes > self.nbytes:
+            raise BackendError(VXT_E_SHAPE, "requested more bytes than the buffer holds")
+        buf = _errbuf()
+        _check(load_library().vxt_hip_memcpy(self._engine.ctx, out.ctypes.data, self.ptr, out.nbytes,
+                                             1, buf, len(buf)), buf)
+        return out
+
+    def free(self) -> None:
+        if self.ptr and self._engine.ctx:
+            load_library().vxt_hip_device_free(self._engine.ctx, self.ptr)
+        self.ptr = None
+
+
+class Graph:
+    """An instantiated HIP graph captured from the engine stream."""
+
+    def __init__(self, engine: "HipEngine", handle: int):
+        self._engine = engine
+        self.handle = handle
+
+    def launch(self, replays: int = 1) -> float:
+        """Replay back to back, wait, return total GPU ms of all replays."""
+        ms = C.c_double()
+        buf = _errbuf()
+        _check(load_library().vxt_hip_graph_launch(self._engine.ctx, self.handle, int(replays),
+                                                   C.byref(ms), buf, len(buf)), buf)
+        return ms.value
+
+    def free(self) -> None:
+        if self.handle:
+            load_library().vxt_hip_graph_free(self.handle)
+            self.handle = None
 
 
 class HipEngine:
@@ -287,6 +368,35 @@ class HipEngine:
         ms = C.c_double()
         load_library().vxt_hip_last_kernel_ms(self.ctx, C.byref(ms))
         return ms.value
+
+    # -- device memory, stream, graphs ---------------------------------------
+    def alloc(self, nbytes: int) -> DeviceBuffer:
+        return DeviceBuffer(self, nbytes)
+
+    def to_device(self, a: np.ndarray) -> DeviceBuffer:
+        a = np.ascontiguousarray(a)
+        return DeviceBuffer(self, a.nbytes).upload(a)
+
+    @property
+    def stream(self) -> int:
+        return load_library().vxt_hip_stream(self.ctx) or 0
+
+    def synchronize(self) -> None:
+        buf = _errbuf()
+        _check(load_library().vxt_hip_synchronize(self.ctx, buf, len(buf)), buf)
+
+    def capture(self, enqueue) -> Graph:
+        """Record ``enqueue(stream)`` (which issues *_dev calls) into a graph."""
+        L = load_library()
+        buf = _errbuf()
+        _check(L.vxt_hip_capture_begin(self.ctx, buf, len(buf)), buf)
+        try:
+            enqueue(self.stream)
+        finally:
+            h = L.vxt_hip_capture_end(self.ctx, buf, len(buf))
+        if not h:
+            _raise(VXT_E_DEVICE, buf)
+        return Graph(self, h)
 
     # -- device-pointer calls (asynchronous on `stream`) ----------------------
     def matmul_dev(self, t: GpuPackedTensor, x_ptr: int, x_dtype: int, batch_m: int, y_ptr: int,
