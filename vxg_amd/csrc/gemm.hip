@@ -9,11 +9,13 @@
 // Exactness of the MFMA operands (products are then exact in fp32):
 //   * X (bf16) is converted to f16 while it is staged; exact for |x| in the
 //     f16 normal range [2^-14, 65504] (values below lose only bits under
-//     2^-24 absolute);
+//     2^-24 absolute).  f32 X is split like the weights, hi + lo in f16
+//     (22 significant bits), with one more MFMA (lo * lo is dropped);
 //   * g64 weights ARE f16 table entries: exact, one MFMA per step;
 //   * Q8 weights q*d (<= 18 significant bits) and cb4 weights f32(sc*cent)
-//     are split into hi = f16(w), lo = f16(w - hi); hi + lo is exact for Q8
-//     and within 2^-22 relative for cb4, at the price of a second MFMA;
+//     are split into hi = f16(w) and lo = f16((w - hi) * 2^11); hi + lo*2^-11
+//     is exact for Q8 and within 2^-22 relative for cb4.  lo products go to a
+//     second fp32 accumulator scaled by 2^-11 at the end (a second MFMA);
 //   * cb4 CSR residuals are added in the epilogue as res * x[col] before the
 //     output is rounded.
 //
@@ -29,6 +31,10 @@ namespace gemm {
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int LDK = BK + 8;          // padded LDS row (halves) against bank conflicts
 constexpr int THREADS = 256;
+// lo halves are stored as f16((v - hi) * 2^11) so they stay out of the f16
+// subnormal range; their products accumulate separately and are scaled back.
+constexpr float kLoScale = 2048.0f;
+constexpr float kLoInv = 1.0f / 2048.0f;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
@@ -40,7 +46,8 @@ __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
 // Per-thread staging registers for one K tile.  Thread t owns row t/2 of both
 // the A tile and the B tile, K half (t%2)*32 .. +32.
 struct Stage {
-  uint32_t a[16];      // 32 activations as f16 pairs
+  uint32_t a[16];      // 32 activations as f16 pairs (hi)
+  uint32_t al[16];     // 32 activations (lo) as f16 pairs (f32 inputs)
   uint32_t bh[16];     // 32 weights (hi) as f16 pairs
   uint32_t bl[16];     // 32 weights (lo) as f16 pairs (split kinds)
 };
@@ -48,7 +55,7 @@ struct Stage {
 // A: X[m, k0 + h*32 .. +32] -> f16 (zero outside [0,M) x [0,K)).
 template <bool XBF16>
 __device__ __forceinline__ void load_a(const void* __restrict__ x, uint32_t M, uint32_t K, uint32_t m,
-                                       uint32_t kb, bool vec, uint32_t (&a)[16]) {
+                                       uint32_t kb, bool vec, uint32_t (&a)[16], uint32_t (&al)[16]) {
   float v[32];
   if (m < M && vec && kb + 32 <= K) {
     if constexpr (XBF16) {
@@ -85,15 +92,27 @@ __device__ __forceinline__ void load_a(const void* __restrict__ x, uint32_t M, u
       v[j] = f;
     }
   }
+  if constexpr (XBF16) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) a[j] = pack_h2((_Float16)v[2 * j], (_Float16)v[2 * j + 1]);
+    for (int j = 0; j < 16; ++j) a[j] = pack_h2((_Float16)v[2 * j], (_Float16)v[2 * j + 1]);
+  } else {
+    // f32 activations: x = hi + lo with both halves f16 (22 significant bits)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
+      a[j] = pack_h2(h0, h1);
+      al[j] = pack_h2((_Float16)((v[2 * j] - (float)h0) * kLoScale),
+                      (_Float16)((v[2 * j + 1] - (float)h1) * kLoScale));
+    }
+  }
 }
 
 __device__ __forceinline__ void split_store(const float (&w)[32], uint32_t (&bh)[16], uint32_t (&bl)[16]) {
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const _Float16 h0 = (_Float16)w[2 * j], h1 = (_Float16)w[2 * j + 1];
-    const _Float16 l0 = (_Float16)(w[2 * j] - (float)h0), l1 = (_Float16)(w[2 * j + 1] - (float)h1);
+    const _Float16 l0 = (_Float16)((w[2 * j] - (float)h0) * kLoScale);
+    const _Float16 l1 = (_Float16)((w[2 * j + 1] - (float)h1) * kLoScale);
     bh[j] = pack_h2(h0, h1);
     bl[j] = pack_h2(l0, l1);
   }
@@ -106,9 +125,11 @@ __device__ __forceinline__ void load_b(const DevTensor& t, uint32_t n, uint32_t 
   const bool live = n < t.rows && kb < t.cols;
   if constexpr (KIND == KIND_G64) {
     // group = kb/64 (BK == 64 so a 32-wide half never straddles groups)
+    // Both threads of a row share one LDS table slot, so both load the table
+    // whenever the 64-group is live, even if their own 32-column half is not.
     uint4 u = make_uint4(0, 0, 0, 0), l0 = u, l1 = u;
-    if (live) {
-      u = load_nt16(static_cast<const uint8_t*>(t.p0) + (size_t)n * (t.kp / 2) + kb / 2);
+    if (live) u = load_nt16(static_cast<const uint8_t*>(t.p0) + (size_t)n * (t.kp / 2) + kb / 2);
+    if (n < t.rows && (kb & ~63u) < t.cols) {
       const uint16_t* lp = t.p1 + ((size_t)n * (t.kp / 64) + kb / 64) * 16;
       l0 = load_nt16(lp);
       l1 = load_nt16(lp + 8);
@@ -168,8 +189,10 @@ __device__ __forceinline__ void load_b(const DevTensor& t, uint32_t n, uint32_t 
 template <uint32_t KIND, bool XBF16>
 __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* __restrict__ x, uint32_t M,
                                                        void* __restrict__ y, uint32_t y_bf16, uint32_t x_vec) {
-  constexpr bool SPLIT = KIND != KIND_G64;
+  constexpr bool SPLIT = KIND != KIND_G64;   // weights as hi + lo
+  constexpr bool SPLIT_A = !XBF16;            // activations as hi + lo
   __shared__ __attribute__((aligned(16))) _Float16 sA[BM * LDK];
+  __shared__ __attribute__((aligned(16))) _Float16 sAl[SPLIT_A ? BM * LDK : 8];
   __shared__ __attribute__((aligned(16))) _Float16 sB[BN * LDK];
   __shared__ __attribute__((aligned(16))) _Float16 sBl[SPLIT ? BN * LDK : 8];
   __shared__ float s_cent[16];
@@ -189,17 +212,20 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* 
   // staging ownership: row tid/2, K half tid%2
   const uint32_t srow = tid >> 1, shalf = tid & 1;
 
-  float16v acc[2][2];
+  float16v acc[2][2], accl[2][2];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+        accl[i][j][r] = 0.0f;
+      }
 
   Stage st;
   const uint32_t ktiles = (K + BK - 1) / BK;
-  load_a<XBF16>(x, M, K, m0 + srow, shalf * 32, x_vec != 0, st.a);
+  load_a<XBF16>(x, M, K, m0 + srow, shalf * 32, x_vec != 0, st.a, st.al);
   load_b<KIND>(t, n0 + srow, shalf * 32, s_cent, s_lut, st);
 
   for (uint32_t kt = 0; kt < ktiles; ++kt) {
@@ -212,6 +238,12 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* 
         da[i] = make_uint4(st.a[4 * i], st.a[4 * i + 1], st.a[4 * i + 2], st.a[4 * i + 3]);
         db[i] = make_uint4(st.bh[4 * i], st.bh[4 * i + 1], st.bh[4 * i + 2], st.bh[4 * i + 3]);
       }
+      if constexpr (SPLIT_A) {
+        uint4* dal = reinterpret_cast<uint4*>(sAl + srow * LDK + shalf * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          dal[i] = make_uint4(st.al[4 * i], st.al[4 * i + 1], st.al[4 * i + 2], st.al[4 * i + 3]);
+      }
       if constexpr (SPLIT) {
         uint4* dl = reinterpret_cast<uint4*>(sBl + srow * LDK + shalf * 32);
 #pragma unroll
@@ -223,17 +255,18 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* 
     // prefetch the next K tile into registers while multiplying this one
     if (kt + 1 < ktiles) {
       const uint32_t kb = (kt + 1) * BK + shalf * 32;
-      load_a<XBF16>(x, M, K, m0 + srow, kb, x_vec != 0, st.a);
+      load_a<XBF16>(x, M, K, m0 + srow, kb, x_vec != 0, st.a, st.al);
       load_b<KIND>(t, n0 + srow, kb, s_cent, s_lut, st);
     }
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      half8 af[2], bf[2], bfl[2];
+      half8 af[2], afl[2], bf[2], bfl[2];
       const uint32_t kofs = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const uint32_t ar = wm * 64 + i * 32 + (lane & 31);
         af[i] = *reinterpret_cast<const half8*>(sA + ar * LDK + kofs);
+        if constexpr (SPLIT_A) afl[i] = *reinterpret_cast<const half8*>(sAl + ar * LDK + kofs);
         const uint32_t br = wn * 64 + i * 32 + (lane & 31);
         bf[i] = *reinterpret_cast<const half8*>(sB + br * LDK + kofs);
         if constexpr (SPLIT) bfl[i] = *reinterpret_cast<const half8*>(sBl + br * LDK + kofs);
@@ -244,10 +277,21 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* 
         for (int j = 0; j < 2; ++j) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
           if constexpr (SPLIT)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], acc[i][j], 0, 0, 0);
+            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], accl[i][j], 0, 0, 0);
+          if constexpr (SPLIT_A)   // lo * lo is below 2^-22 relative and dropped
+            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], accl[i][j], 0, 0, 0);
         }
     }
     __syncthreads();
+  }
+
+  if constexpr (SPLIT || SPLIT_A) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(accl[i][j][r], kLoInv, acc[i][j][r]);
   }
 
   // epilogue: lane owns column n = n0 + wn*64 + j*32 + lane%32 of tile (i, j),

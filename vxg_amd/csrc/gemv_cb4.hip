@@ -1,0 +1,12 @@
+// gemv_cb4.hip -- instantiates the decode GEMV (gemv_impl.hpp) for one
+// weight kind, so the kinds compile in parallel.
+#include "gemv_impl.hpp"
+
+namespace vxt {
+
+hipError_t launch_gemv_cb4(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y,
+                        bool y_bf16, hipStream_t s) {
+  return gv::launch_kind<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, s);
+}
+
+}  // namespace vxt

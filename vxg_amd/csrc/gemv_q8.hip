@@ -1,0 +1,12 @@
+// gemv_q8.hip -- instantiates the decode GEMV (gemv_impl.hpp) for one
+// weight kind, so the kinds compile in parallel.
+#include "gemv_impl.hpp"
+
+namespace vxt {
+
+hipError_t launch_gemv_q8(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y,
+                        bool y_bf16, hipStream_t s) {
+  return gv::launch_kind<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, s);
+}
+
+}  // namespace vxt
