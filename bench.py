@@ -38,6 +38,11 @@ BF16_PEAK_TFLOPS = 2500.0       # dense bf16 / fp16 MFMA
 MALL_BYTES = 256 << 20          # Infinity Cache
 METRIC = "decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s, 1×MI355X"
 
+# HBM bytes per launch of the headline kernel, from two rocprofv3 --pmc runs
+# (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
+# device-to-device copy of known size; see profiles/gemv_g64_config1.md.
+MEASURED_TRAFFIC_BYTES = {"config1": 12712110}
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -122,6 +127,31 @@ def bench_gemv(eng, m, M: int, x_dtype: str, y_dtype: str, steps: int, warmup: i
     }
 
 
+def bench_gemm(eng, m, M: int, steps: int, warmup: int, seed: int = 0):
+    """TFLOP/s of the prefill dequant+GEMM (bf16 x, bf16 out) over weight copies."""
+    from vxg_amd import engine, synth
+    wb = weight_bytes(m)
+    n_copies = max(2, math.ceil(2.5 * MALL_BYTES / wb))
+    base = eng.upload_packed(m)
+    copies = [base] + [base.clone() for _ in range(n_copies - 1)]
+    xd = eng.to_device(synth.make_x_bf16(M, m.cols, seed=seed))
+    yd = eng.alloc(M * m.rows * 2)
+
+    def enqueue(i, stream):
+        eng.matmul_dev(copies[i % n_copies], xd.ptr, engine.DTYPE_BF16, M, yd.ptr, engine.DTYPE_BF16, stream)
+
+    wall_s, ev_ms = time_graph(eng, enqueue, steps, warmup)
+    for c in copies:
+        c.free()
+    xd.free()
+    yd.free()
+    flops = 2.0 * M * m.rows * m.cols
+    kern_ms = ev_ms / steps
+    return {"kernel_ms": kern_ms, "TFLOPs": flops / (kern_ms * 1e-3) / 1e12,
+            "wall_TFLOPs": flops * steps / wall_s / 1e12,
+            "bytes_per_call": call_bytes(m, M, 2, 2)}
+
+
 # --------------------------------------------------------------------------
 # CPU baseline (reference CPU path, C restatement in oracle/)
 # --------------------------------------------------------------------------
@@ -202,6 +232,17 @@ def main():
                                   "frac_hbm": round(rq["kernel_GBps"] / HBM_PEAK_GBS, 4)})
                 log(f"  config 2 M={M} K={K} N={N}: {rq['kernel_GBps']:.1f} GB/s kernel")
             del mq
+        for kind in ("g64", "q8", "cb4"):
+            for (K, N) in [(2048, 6144), (6144, 2048)]:
+                mk = {"g64": synth.make_g64, "q8": synth.make_q8, "cb4": synth.make_cb4}[kind](N, K, seed=3)
+                for M in (128, 512, 2048):
+                    st = max(10, min(100, int(4e12 / (2.0 * M * N * K))))
+                    rg = bench_gemm(eng, mk, M, st, 3, seed=M)
+                    secondary.append({"config": f"3: {kind} gemm M={M} K={K} N={N} bf16->bf16",
+                                      "TFLOPs": round(rg["TFLOPs"], 1),
+                                      "kernel_us": round(rg["kernel_ms"] * 1e3, 2),
+                                      "frac_mfma": round(rg["TFLOPs"] / BF16_PEAK_TFLOPS, 4)})
+                    log(f"  config 3 {kind} M={M} K={K} N={N}: {rg['TFLOPs']:.1f} TFLOP/s")
 
     cpu = None
     if not args.no_cpu:
@@ -229,7 +270,8 @@ def main():
                    "mall_defeat": "rotate weight copies totalling > 2x 256 MB MALL",
                    "timing": "HIP graph of `steps` launches, one replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": MEASURED_TRAFFIC_BYTES["config1"],
                      "kernel": "vxt::gemv_kernel<9,1,..> (g64, M=1)",
                      "bytes_per_launch": r["bytes_per_call"],
                      "kernel_us": round(r["kernel_ms"] * 1e3, 3)},
