@@ -152,6 +152,53 @@ def bench_gemm(eng, m, M: int, steps: int, warmup: int, seed: int = 0):
             "bytes_per_call": call_bytes(m, M, 2, 2)}
 
 
+def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
+                ffn: int = 6144, seed: int = 40):
+    """Config 4: tokens/s of the decode-step linear stack (matmul-only path).
+
+    Per layer [q;k;v] (3 x hidden rows), o, [gate;up] (2 x ffn rows), down,
+    then the Q8 LM head; every layer's weights are drawn separately.  One
+    token is captured as a HIP graph; ``tokens`` replays are timed.
+    """
+    from vxg_amd import stack, synth
+    gen = {"g64": synth.make_g64, "cb4": synth.make_cb4}[kind]
+    lw, nbytes = [], weight_bytes(head_m)
+    for li in range(layers):
+        s = seed + 10 * li
+        qkv = [gen(hidden, hidden, seed=s + i) for i in range(3)]
+        o = gen(hidden, hidden, seed=s + 3)
+        gu = [gen(ffn, hidden, seed=s + 4), gen(ffn, hidden, seed=s + 5)]
+        dn = gen(hidden, ffn, seed=s + 6)
+        nbytes += sum(weight_bytes(m) for m in qkv + [o] + gu + [dn])
+        lw.append(stack.LayerWeights(eng.upload_concat(qkv), eng.upload_packed(o),
+                                     eng.upload_concat(gu), eng.upload_packed(dn)))
+    head = eng.upload_packed(head_m)
+    st = stack.DecodeStack(eng, lw, head)
+    st.set_input(synth.make_x_bf16(1, hidden, seed=4)[0])
+    # activations read and written per token (bf16 between layers, f32 logits)
+    # qkv: h in, 3h out; o: h, h; gate/up: h, 2 ffn; down: ffn, h
+    act = layers * 2 * (8 * hidden + 3 * ffn) + 2 * hidden + 4 * head_m.rows
+    nbytes += act
+    for _ in range(3):
+        st.enqueue()
+    eng.synchronize()
+    g = st.capture()
+    g.launch(3)
+    t0 = time.perf_counter()
+    ev_ms = g.launch(tokens)
+    wall = time.perf_counter() - t0
+    g.free()
+    st.free()
+    for L in lw:
+        for t in (L.qkv, L.o, L.gate_up, L.down):
+            t.free()
+    head.free()
+    ms_tok = ev_ms / tokens
+    return {"tokens_per_s": tokens / (ev_ms * 1e-3), "wall_tokens_per_s": tokens / wall,
+            "ms_per_token": ms_tok, "bytes_per_token": nbytes, "launches_per_token": st.launches,
+            "GBps": nbytes / (ms_tok * 1e-3) / 1e9}
+
+
 # --------------------------------------------------------------------------
 # CPU baseline (reference CPU path, C restatement in oracle/)
 # --------------------------------------------------------------------------
@@ -190,6 +237,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--configs", default="0,2,3,4", help="secondary configurations to run")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
 
@@ -211,7 +259,8 @@ def main():
         f"({r['kernel_GBps']:.1f} GB/s)")
 
     secondary = []
-    if not args.quick:
+    run = set() if args.quick else {c.strip() for c in args.configs.split(",")}
+    if "0" in run:
         m0 = synth.make_q8(4096, 4096, seed=0)
         log("config 0: Q8 GEMV M=1 K=N=4096 x f32")
         r0 = bench_gemv(eng, m0, 1, "f32", "f32", args.steps, args.warmup, seed=0)
@@ -220,6 +269,7 @@ def main():
                           "kernel_GBps": round(r0["kernel_GBps"], 1),
                           "frac_hbm": round(r0["kernel_GBps"] / HBM_PEAK_GBS, 4)})
         log(f"  {r0['GBps']:.1f} GB/s wall, kernel {r0['kernel_ms']*1e3:.2f} us")
+    if "2" in run:
         for (K, N) in [(2048, 2048), (2048, 6144), (6144, 2048), (2048, 151936)]:
             mq = synth.make_q8(N, K, seed=2)
             for M in (1, 2, 4, 8):
@@ -232,6 +282,7 @@ def main():
                                   "frac_hbm": round(rq["kernel_GBps"] / HBM_PEAK_GBS, 4)})
                 log(f"  config 2 M={M} K={K} N={N}: {rq['kernel_GBps']:.1f} GB/s kernel")
             del mq
+    if "3" in run:
         for kind in ("g64", "q8", "cb4"):
             for (K, N) in [(2048, 6144), (6144, 2048)]:
                 mk = {"g64": synth.make_g64, "q8": synth.make_q8, "cb4": synth.make_cb4}[kind](N, K, seed=3)
@@ -243,6 +294,21 @@ def main():
                                       "kernel_us": round(rg["kernel_ms"] * 1e3, 2),
                                       "frac_mfma": round(rg["TFLOPs"] / BF16_PEAK_TFLOPS, 4)})
                     log(f"  config 3 {kind} M={M} K={K} N={N}: {rg['TFLOPs']:.1f} TFLOP/s")
+    if "4" in run:
+        head_m = synth.make_q8(151936, 2048, seed=5)
+        for kind in ("g64", "cb4"):
+            log(f"config 4: decode stack, 24 layers {kind} + Q8 LM head")
+            rs = bench_stack(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)))
+            secondary.append({"config": f"4: decode stack 24x{{[q;k;v],o,[gate;up],down}} {kind} + q8 head, M=1",
+                              "tokens_per_s": round(rs["tokens_per_s"], 1),
+                              "ms_per_token": round(rs["ms_per_token"], 4),
+                              "bytes_per_token": rs["bytes_per_token"],
+                              "launches_per_token": rs["launches_per_token"],
+                              "GBps": round(rs["GBps"], 1),
+                              "frac_hbm": round(rs["GBps"] / HBM_PEAK_GBS, 4)})
+            log(f"  {rs['tokens_per_s']:.1f} tok/s ({rs['GBps']:.1f} GB/s, "
+                f"{rs['ms_per_token']*1e3:.1f} us/token)")
+        del head_m
 
     cpu = None
     if not args.no_cpu:

@@ -113,6 +113,14 @@ VXT_API void vxt_hip_destroy(void* ctx);
  * vxt_metal_upload (metal_ffi.rs:35). Returns a tensor handle or NULL. */
 VXT_API void* vxt_hip_upload_cb4(void* ctx, const VxtCb4View* view, char* err, size_t err_cap);
 
+/* Row-concatenation of 1..3 CodebookMatrix parts with equal cols into one
+ * tensor ([q;k;v], [gate;up]); each part keeps its own centroid table and the
+ * CSR row pointers are rebased.  Replaces VxtCb4FastConcatMat::from_subs and
+ * the arena packer it feeds (metal_cb4_fast_ffi.rs:89-104,
+ * metal_cb4_fast.mm:6-44,140-171). */
+VXT_API void* vxt_hip_upload_cb4_concat(void* ctx, const VxtCb4View* subs, uint32_t n_subs, char* err,
+                                size_t err_cap);
+
 /* cb4-g64 upload (no reference counterpart: the decode-benchmark layout). */
 VXT_API void* vxt_hip_upload_cb4_g64(void* ctx, const VxtCb4G64View* view, char* err,
                              size_t err_cap);

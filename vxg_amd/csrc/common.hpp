@@ -6,7 +6,9 @@
 //          d     f16   [rows][kp/32]
 //   CB4    words u32   [rows][kp/8]      nibble c%8 of word c/8 (as uploaded)
 //          sc    f16   [rows][kp/128]
-//          cent  f32   [16]              (kernel argument)
+//          cent  f32   [3][16]           (kernel argument; table t serves rows
+//                                     [split(t), split(t+1)) of a row-concatenated
+//                                     matrix, split(0)=0, split(3)=rows)
 //          CSR   row_ptr u32[rows+1], outliers u32[nnz] (col | f16 << 16)
 //   G64    idx   u8    [rows][kp/2]      low nibble = even column
 //          lut   f16   [rows][kp/64][16]
@@ -30,8 +32,14 @@ struct DevTensor {
   const uint16_t* p1;   // Q8: d       CB4: scales    G64: lut
   const uint32_t* row_ptr;   // CB4 only
   const uint32_t* outliers;  // CB4 only
-  float cent[16];            // CB4 only
+  uint32_t split0, split1;   // CB4: first rows served by tables 1 and 2
+  float cent[48];            // CB4 only: 3 centroid tables of 16
 };
+
+// Centroid table serving `row` (rows of up to 3 concatenated sub-matrices).
+__device__ __forceinline__ uint32_t cent_table(const DevTensor& t, uint32_t row) {
+  return (uint32_t)(row >= t.split0) + (uint32_t)(row >= t.split1);
+}
 
 // ---- memory ----------------------------------------------------------------
 

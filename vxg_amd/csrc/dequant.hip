@@ -30,7 +30,7 @@ __global__ __launch_bounds__(256) void dequant_dense_kernel(DevTensor t, uint32_
     const uint32_t w = static_cast<const uint32_t*>(t.p0)[row * (t.kp / 8) + c / 8];
     const uint32_t q = (w >> ((c % 8) * 4)) & 0xfu;
     const float sc = f16_to_f32_exact(t.p1[row * (t.kp / 128) + c / 128]);
-    v = sc * t.cent[q];
+    v = sc * t.cent[16u * cent_table(t, row) + q];
   } else {
     const uint8_t b = static_cast<const uint8_t*>(t.p0)[row * (t.kp / 2) + c / 2];
     const uint32_t q = (b >> ((c & 1) * 4)) & 0xfu;

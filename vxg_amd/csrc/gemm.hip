@@ -176,9 +176,10 @@ __device__ __forceinline__ void load_b(const DevTensor& t, uint32_t n, uint32_t 
         sc = f16_to_f32(t.p1[(size_t)n * (t.kp / 128) + kb / 128]);
       }
       const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+      const float* tab = s_cent + 16u * cent_table(t, n);
 #pragma unroll
       for (int j = 0; j < 32; ++j) {
-        const float c = s_cent[(wd[j >> 3] >> ((j & 7) * 4)) & 0xfu];
+        const float c = tab[(wd[j >> 3] >> ((j & 7) * 4)) & 0xfu];
         w[j] = (kb + j < t.cols) ? sc * c : 0.0f;
       }
     }
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* 
   __shared__ __attribute__((aligned(16))) _Float16 sAl[SPLIT_A ? BM * LDK : 8];
   __shared__ __attribute__((aligned(16))) _Float16 sB[BN * LDK];
   __shared__ __attribute__((aligned(16))) _Float16 sBl[SPLIT ? BN * LDK : 8];
-  __shared__ float s_cent[16];
+  __shared__ float s_cent[48];
   __shared__ __attribute__((aligned(16))) _Float16 s_lut[KIND == KIND_G64 ? BN * 24 : 8];
 
   const uint32_t tid = threadIdx.x;
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(DevTensor t, const void* 
   const uint32_t N = t.rows, K = t.cols;
 
   if constexpr (KIND == KIND_CB4) {
-    if (tid < 16) s_cent[tid] = t.cent[tid];
+    if (tid < 48) s_cent[tid] = t.cent[tid];
     __syncthreads();
   }
 

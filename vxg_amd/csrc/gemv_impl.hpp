@@ -17,8 +17,8 @@
 //     in order, so one such wait serialises every load issued before it.);
 //   * activations are read straight from global memory (they are L2-resident
 //     after the first wave touches them), 16 bytes at a time;
-//   * cb4: the 16-entry centroid table lives in LDS (staged before any load is
-//     issued); g64: each lane loads 16 bytes of its group's codebook
+//   * cb4: the 16-entry centroid tables (up to 3 for row-concatenated
+//     matrices) live in LDS, staged before any load is issued; g64: each lane loads 16 bytes of its group's codebook
 //     (coalesced) and the two lanes of a 64-group exchange halves through a
 //     per-wave LDS slot laid out against bank conflicts;
 //   * partial sums are reduced across the wave with DPP at the end.
@@ -156,7 +156,7 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Table reads use byte addresses base | (q << k) with an aligned base, so the
 // address costs one shift and one v_and_or_b32.
 template <uint32_t KIND>
-__device__ __forceinline__ void dequant_chunk(const WChunk<KIND>& c, const float* s_cent, uint32_t slot,
+__device__ __forceinline__ void dequant_chunk(const WChunk<KIND>& c, uint32_t cbase, uint32_t slot,
                                               uint32_t lane, float (&w)[kChunk]) {
   if constexpr (KIND == KIND_Q8) {
     const uint32_t qa[8] = {c.a.x, c.a.y, c.a.z, c.a.w, c.b.x, c.b.y, c.b.z, c.b.w};
@@ -164,7 +164,7 @@ __device__ __forceinline__ void dequant_chunk(const WChunk<KIND>& c, const float
     for (int j = 0; j < kChunk; ++j) w[j] = (float)(int8_t)((qa[j >> 2] >> ((j & 3) * 8)) & 0xffu);
   } else if constexpr (KIND == KIND_CB4) {
     const uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
-    const uint32_t base = lds_addr(s_cent);   // 64-byte aligned
+    const uint32_t base = cbase;   // 64-byte aligned table for this row
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) {
       const int sh = (j & 7) * 4 - 2;
@@ -189,7 +189,7 @@ template <uint32_t KIND, int MT, int RPW, int S, bool XBF16>
 __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const void* __restrict__ x,
                                                           void* __restrict__ y, uint32_t M_rt,
                                                           uint32_t y_bf16, uint32_t x_vec) {
-  __shared__ __attribute__((aligned(64))) float s_cent[16];
+  __shared__ __attribute__((aligned(64))) float s_cent[48];
   __shared__ __attribute__((aligned(64))) uint4 s_slot[KIND == KIND_G64 ? kWaves * S * RPW * kSlotBytes / 16 : 1];
 
   const uint32_t lane = threadIdx.x & 63;
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   const uint32_t nsteps = (kp + kStep - 1) / kStep;
 
   if constexpr (KIND == KIND_CB4) {   // before any global load is in flight
-    if (threadIdx.x < 16) s_cent[threadIdx.x] = t.cent[threadIdx.x];
+    if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
     __syncthreads();
   }
   const uint32_t slot = lds_addr(s_slot) + (KIND == KIND_G64 ? wave * S * RPW * kSlotBytes : 0);
@@ -257,8 +257,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
         if constexpr (KIND == KIND_G64)   // lane l holds half (l & 1) of pair table l >> 1
           *(__attribute__((address_space(3))) u32x4*)(size_t)(sl + (lane >> 1) * kPairStride + (lane & 1) * 16) =
               u32x4{wc[s][r].lut.x, wc[s][r].lut.y, wc[s][r].lut.z, wc[s][r].lut.w};
+        uint32_t cbase = 0;
+        if constexpr (KIND == KIND_CB4) cbase = lds_addr(s_cent) + 64u * cent_table(t, row0 + r);
         float w[kChunk];
-        dequant_chunk<KIND>(wc[s][r], s_cent, sl, lane, w);
+        dequant_chunk<KIND>(wc[s][r], cbase, sl, lane, w);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           float p0 = 0.0f, p1 = 0.0f;

@@ -43,7 +43,8 @@ struct Tensor {
   size_t bytes = 0;
   size_t off_p0 = 0, off_p1 = 0, off_rp = 0, off_out = 0;
   uint32_t nnz = 0;
-  float cent[16] = {};
+  uint32_t split0 = 0, split1 = 0;
+  float cent[48] = {};
 
   DevTensor dev() const {
     DevTensor d{};
@@ -57,6 +58,8 @@ struct Tensor {
     if (kind == VXT_KIND_CB4) {
       d.row_ptr = reinterpret_cast<const uint32_t*>(base + off_rp);
       d.outliers = reinterpret_cast<const uint32_t*>(base + off_out);
+      d.split0 = split0;
+      d.split1 = split1;
       std::memcpy(d.cent, cent, sizeof(cent));
     }
     return d;
@@ -180,6 +183,29 @@ Tensor* as_tensor(void* p) {
 Ctx* as_ctx(void* p) {
   if (!p) fail(VXT_E_ARG, "null context handle");
   return static_cast<Ctx*>(p);
+}
+
+// Plane checks of one CodebookMatrix view, as the archive reader does
+// (format.rs:423-440, :565-574).
+void validate_cb4(const VxtCb4View* v) {
+  if (v->bits != 4) fail(VXT_E_UNSUPPORTED, "only 4-bit codebooks run on the device");
+  if (v->rows == 0 || v->cols == 0) fail(VXT_E_SHAPE, "rows and cols must be positive");
+  if (v->padded_cols < v->cols || v->padded_cols % 128u != 0)
+    fail(VXT_E_FORMAT, "invalid codebook padded_cols");
+  if (v->cols > 65536u && v->n_outliers != 0) fail(VXT_E_FORMAT, "outliers need cols <= 65536");
+  if (!v->centroids || !v->scales_f16 || !v->packed_words || !v->outlier_row_ptr ||
+      (v->n_outliers && !v->outliers_packed))
+    fail(VXT_E_ARG, "null codebook plane");
+  const size_t groups = (size_t)v->rows * (v->padded_cols / 128u);
+  if (v->n_scales != groups || v->n_words != groups * 16u || v->n_row_ptr != (size_t)v->rows + 1u ||
+      v->outlier_row_ptr[v->rows] != v->n_outliers)
+    fail(VXT_E_FORMAT, "corrupt VXT codebook plane lengths");
+  if (v->outlier_row_ptr[0] != 0) fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
+  for (size_t r = 0; r < v->rows; ++r)
+    if (v->outlier_row_ptr[r] > v->outlier_row_ptr[r + 1] || v->outlier_row_ptr[r + 1] > v->n_outliers)
+      fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
+  for (size_t i = 0; i < v->n_outliers; ++i)
+    if ((v->outliers_packed[i] & 0xffffu) >= v->cols) fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
 }
 
 bool dtype_ok(uint32_t d) { return d == VXT_DTYPE_F32 || d == VXT_DTYPE_BF16; }
@@ -314,50 +340,69 @@ void* vxt_hip_upload_q8_0(void* ctx, uint32_t rows, uint32_t cols, const uint8_t
 }
 
 void* vxt_hip_upload_cb4(void* ctx, const VxtCb4View* v, char* err, size_t err_cap) {
+  return vxt_hip_upload_cb4_concat(ctx, v, 1u, err, err_cap);
+}
+
+void* vxt_hip_upload_cb4_concat(void* ctx, const VxtCb4View* subs, uint32_t n_subs, char* err,
+                                size_t err_cap) {
   Tensor* out = nullptr;
   guarded(err, err_cap, [&] {
     Ctx* c = as_ctx(ctx);
-    if (!v) fail(VXT_E_ARG, "null codebook view");
-    if (v->bits != 4) fail(VXT_E_UNSUPPORTED, "only 4-bit codebooks run on the device");
-    if (v->rows == 0 || v->cols == 0) fail(VXT_E_SHAPE, "rows and cols must be positive");
-    if (v->padded_cols < v->cols || v->padded_cols % 128u != 0)
-      fail(VXT_E_FORMAT, "invalid codebook padded_cols");
-    if (v->cols > 65536u && v->n_outliers != 0)
-      fail(VXT_E_FORMAT, "outliers need cols <= 65536");
-    if (!v->centroids || !v->scales_f16 || !v->packed_words || !v->outlier_row_ptr ||
-        (v->n_outliers && !v->outliers_packed))
-      fail(VXT_E_ARG, "null codebook plane");
-    const size_t groups = (size_t)v->rows * (v->padded_cols / 128u);
-    // format.rs:432-439
-    if (v->n_scales != groups || v->n_words != groups * 16u || v->n_row_ptr != (size_t)v->rows + 1u ||
-        v->outlier_row_ptr[v->rows] != v->n_outliers)
-      fail(VXT_E_FORMAT, "corrupt VXT codebook plane lengths");
-    // format.rs:565-574
-    if (v->outlier_row_ptr[0] != 0) fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
-    for (size_t r = 0; r < v->rows; ++r)
-      if (v->outlier_row_ptr[r] > v->outlier_row_ptr[r + 1] || v->outlier_row_ptr[r + 1] > v->n_outliers)
-        fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
-    for (size_t i = 0; i < v->n_outliers; ++i)
-      if ((v->outliers_packed[i] & 0xffffu) >= v->cols) fail(VXT_E_FORMAT, "invalid VXT outlier CSR indices");
-
-    const size_t w_bytes = align256(v->n_words * 4u);
-    const size_t s_bytes = align256(v->n_scales * 2u);
-    const size_t rp_bytes = align256(v->n_row_ptr * 4u);
-    const size_t o_bytes = align256(std::max<size_t>(v->n_outliers, 1) * 4u);
+    if (!subs) fail(VXT_E_ARG, "null codebook view");
+    if (n_subs == 0 || n_subs > 3) fail(VXT_E_ARG, "a concatenated codebook tensor has 1 to 3 parts");
+    size_t rows = 0, nnz = 0, n_words = 0, n_scales = 0;
+    for (uint32_t i = 0; i < n_subs; ++i) {
+      validate_cb4(&subs[i]);
+      if (subs[i].cols != subs[0].cols || subs[i].padded_cols != subs[0].padded_cols)
+        fail(VXT_E_SHAPE, "concatenated codebook parts must share cols and padded_cols");
+      rows += subs[i].rows;
+      nnz += subs[i].n_outliers;
+      n_words += subs[i].n_words;
+      n_scales += subs[i].n_scales;
+    }
+    if (rows > 0xffffffffu || nnz > 0xffffffffu) fail(VXT_E_SHAPE, "concatenated tensor too large");
+    // One arena: words, scales, row_ptr (rebased per part), outliers, each
+    // plane 256-byte aligned (metal_cb4_fast.mm:140-171 concatenates the same way).
+    const size_t w_bytes = align256(n_words * 4u);
+    const size_t s_bytes = align256(n_scales * 2u);
+    const size_t rp_bytes = align256((rows + 1u) * 4u);
+    const size_t o_bytes = align256(std::max<size_t>(nnz, 1) * 4u);
     std::vector<char> h(w_bytes + s_bytes + rp_bytes + o_bytes, 0);
-    std::memcpy(h.data(), v->packed_words, v->n_words * 4u);
-    std::memcpy(h.data() + w_bytes, v->scales_f16, v->n_scales * 2u);
-    std::memcpy(h.data() + w_bytes + s_bytes, v->outlier_row_ptr, v->n_row_ptr * 4u);
-    if (v->n_outliers)
-      std::memcpy(h.data() + w_bytes + s_bytes + rp_bytes, v->outliers_packed, v->n_outliers * 4u);
+    uint32_t* rp = reinterpret_cast<uint32_t*>(h.data() + w_bytes + s_bytes);
+    size_t wo = 0, so = 0, ro = 0, oo = 0;
+    for (uint32_t i = 0; i < n_subs; ++i) {
+      const VxtCb4View& v = subs[i];
+      std::memcpy(h.data() + wo * 4u, v.packed_words, v.n_words * 4u);
+      std::memcpy(h.data() + w_bytes + so * 2u, v.scales_f16, v.n_scales * 2u);
+      for (size_t r = 0; r < v.rows; ++r) rp[ro + r] = (uint32_t)(oo + v.outlier_row_ptr[r]);
+      if (v.n_outliers)
+        std::memcpy(h.data() + w_bytes + s_bytes + rp_bytes + oo * 4u, v.outliers_packed, v.n_outliers * 4u);
+      wo += v.n_words;
+      so += v.n_scales;
+      ro += v.rows;
+      oo += v.n_outliers;
+    }
+    rp[rows] = (uint32_t)nnz;
     use_device(c);
-    Tensor* t = new_tensor(c, VXT_KIND_CB4, v->rows, v->cols, v->padded_cols, h);
+    Tensor* t = new_tensor(c, VXT_KIND_CB4, (uint32_t)rows, subs[0].cols, subs[0].padded_cols, h);
     t->off_p0 = 0;
     t->off_p1 = w_bytes;
     t->off_rp = w_bytes + s_bytes;
     t->off_out = w_bytes + s_bytes + rp_bytes;
-    t->nnz = (uint32_t)v->n_outliers;
-    std::memcpy(t->cent, v->centroids, sizeof(t->cent));
+    t->nnz = (uint32_t)nnz;
+    // Table i serves rows [split(i), split(i+1)); unused tables repeat the last part's.
+    uint32_t split[2] = {(uint32_t)rows, (uint32_t)rows};
+    uint32_t acc = 0;
+    for (uint32_t i = 0; i < 3; ++i) {
+      const VxtCb4View& v = subs[i < n_subs ? i : n_subs - 1];
+      std::memcpy(t->cent + 16 * i, v.centroids, 16 * sizeof(float));
+      if (i < n_subs) {
+        acc += v.rows;
+        if (i < 2 && i + 1 < n_subs) split[i] = acc;
+      }
+    }
+    t->split0 = split[0];
+    t->split1 = split[1];
     register_tensor(c, t);
     out = t;
   });

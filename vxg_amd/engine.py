@@ -49,7 +49,8 @@ DTYPE_F32, DTYPE_BF16 = 0, 1
 KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
 
 ABI_SYMBOLS = (
-    "vxt_hip_create", "vxt_hip_destroy", "vxt_hip_upload_cb4", "vxt_hip_upload_cb4_g64",
+    "vxt_hip_create", "vxt_hip_destroy", "vxt_hip_upload_cb4", "vxt_hip_upload_cb4_concat",
+    "vxt_hip_upload_cb4_g64",
     "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev",
@@ -111,6 +112,8 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_destroy.argtypes = [vp]
     L.vxt_hip_upload_cb4.restype = vp
     L.vxt_hip_upload_cb4.argtypes = [vp, C.POINTER(Cb4View), cp, sz]
+    L.vxt_hip_upload_cb4_concat.restype = vp
+    L.vxt_hip_upload_cb4_concat.argtypes = [vp, C.POINTER(Cb4View), u32, cp, sz]
     L.vxt_hip_upload_cb4_g64.restype = vp
     L.vxt_hip_upload_cb4_g64.argtypes = [vp, C.POINTER(Cb4G64View), cp, sz]
     L.vxt_hip_upload_q8_0.restype = vp
@@ -169,6 +172,22 @@ def _raise(code: int, buf) -> None:
     if code == VXT_E_UNSUPPORTED:
         raise UnsupportedError(code, msg)
     raise BackendError(code, msg)
+
+
+def _upload_failed(buf) -> None:
+    """An upload returned NULL: raise with the code its message implies."""
+    msg = buf.value
+    if b"corrupt" in msg or b"invalid" in msg or b"need" in msg:
+        code = VXT_E_FORMAT
+    elif b"only" in msg:
+        code = VXT_E_UNSUPPORTED
+    elif b"must" in msg or b"too large" in msg:
+        code = VXT_E_SHAPE
+    elif b"null" in msg or b"parts" in msg:
+        code = VXT_E_ARG
+    else:
+        code = VXT_E_DEVICE
+    _raise(code, buf)
 
 
 def _check(code: int, buf) -> None:
@@ -301,20 +320,11 @@ class HipEngine:
     # -- upload --------------------------------------------------------------
     def upload_packed(self, m) -> GpuPackedTensor:
         """Copy a host weight matrix to HBM in its device-resident layout."""
+        if isinstance(m, CodebookMatrix):
+            return self.upload_concat([m])
         L = load_library()
         buf = _errbuf()
-        if isinstance(m, CodebookMatrix):
-            keep = [np.ascontiguousarray(m.centroids, np.float32),
-                    np.ascontiguousarray(m.scales_f16, np.uint16),
-                    np.ascontiguousarray(m.packed_words, np.uint32),
-                    np.ascontiguousarray(m.outlier_row_ptr, np.uint32),
-                    np.ascontiguousarray(m.outliers_packed, np.uint32)]
-            v = Cb4View(m.bits, m.rows, m.cols, m.padded_cols, keep[0].ctypes.data,
-                        keep[1].ctypes.data, keep[1].size, keep[2].ctypes.data, keep[2].size,
-                        keep[3].ctypes.data, keep[3].size,
-                        keep[4].ctypes.data if keep[4].size else None, keep[4].size)
-            h = L.vxt_hip_upload_cb4(self.ctx, C.byref(v), buf, len(buf))
-        elif isinstance(m, Cb4G64Matrix):
+        if isinstance(m, Cb4G64Matrix):
             keep = [np.ascontiguousarray(m.idx, np.uint8), np.ascontiguousarray(m.lut_f16, np.uint16)]
             v = Cb4G64View(m.rows, m.cols, m.padded_cols, 0, keep[0].ctypes.data, keep[0].size,
                            keep[1].ctypes.data, keep[1].size)
@@ -325,9 +335,41 @@ class HipEngine:
         else:
             raise UnsupportedError(VXT_E_UNSUPPORTED, f"no device path for {type(m).__name__}")
         if not h:
-            code = VXT_E_FORMAT if b"corrupt" in buf.value or b"invalid" in buf.value else VXT_E_DEVICE
-            _raise(code, buf)
+            _upload_failed(buf)
         return GpuPackedTensor(self, h)
+
+    def upload_concat(self, parts: Sequence) -> GpuPackedTensor:
+        """Upload matrices with equal ``cols`` as one row-concatenated tensor.
+
+        Codebook parts (1 to 3) keep their own centroid tables and CSR
+        streams, as ``VxtCb4FastConcatMat::from_subs`` does
+        (``metal_cb4_fast_ffi.rs:89-104``); g64 and Q8 parts are stacked on
+        the host (``formats.concat_rows``).
+        """
+        parts = list(parts)
+        if parts and all(isinstance(p, CodebookMatrix) for p in parts):
+            L = load_library()
+            buf = _errbuf()
+            keep, views = [], (Cb4View * len(parts))()
+            for i, m in enumerate(parts):
+                arrs = [np.ascontiguousarray(m.centroids, np.float32),
+                        np.ascontiguousarray(m.scales_f16, np.uint16),
+                        np.ascontiguousarray(m.packed_words, np.uint32),
+                        np.ascontiguousarray(m.outlier_row_ptr, np.uint32),
+                        np.ascontiguousarray(m.outliers_packed, np.uint32)]
+                keep.append(arrs)
+                views[i] = Cb4View(m.bits, m.rows, m.cols, m.padded_cols, arrs[0].ctypes.data,
+                                   arrs[1].ctypes.data, arrs[1].size, arrs[2].ctypes.data, arrs[2].size,
+                                   arrs[3].ctypes.data, arrs[3].size,
+                                   arrs[4].ctypes.data if arrs[4].size else None, arrs[4].size)
+            h = L.vxt_hip_upload_cb4_concat(self.ctx, views, len(parts), buf, len(buf))
+            if not h:
+                _upload_failed(buf)
+            return GpuPackedTensor(self, h)
+        if any(isinstance(p, CodebookMatrix) for p in parts):
+            raise BackendError(VXT_E_ARG, "concatenated parts must share one format")
+        from .formats import concat_rows
+        return self.upload_packed(concat_rows(parts))
 
     # -- host-pointer calls (synchronous) ------------------------------------
     def run_multi_same_x(self, x, jobs: Sequence, iters: int = 1) -> float:

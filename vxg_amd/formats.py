@@ -197,3 +197,30 @@ def q8_from_planes(rows: int, cols: int, qs: np.ndarray, d_f16: np.ndarray) -> Q
     blk[:, 0:2] = d.view(np.uint8).reshape(rows * kb, 2)
     blk[:, 2:] = qs.view(np.uint8)
     return Q8Matrix(rows, cols, blk.reshape(-1))
+
+
+def concat_rows(parts):
+    """Stack g64 or Q8 matrices with equal ``cols`` along rows (``[q;k;v]``).
+
+    Their planes are per-row, so stacking needs no rebasing.  Codebook
+    matrices carry a per-matrix centroid table and CSR stream; they are
+    concatenated on upload instead (``HipEngine.upload_concat``).
+    """
+    parts = list(parts)
+    if not parts:
+        raise FormatError("nothing to concatenate")
+    first = parts[0]
+    if any(type(p) is not type(first) for p in parts):
+        raise FormatError("concatenated parts must share one format")
+    if any(p.cols != first.cols for p in parts):
+        raise FormatError("concatenated parts must share cols")
+    rows = sum(p.rows for p in parts)
+    if isinstance(first, Q8Matrix):
+        return Q8Matrix(rows, first.cols, np.concatenate([np.asarray(p.blocks, np.uint8) for p in parts]))
+    if isinstance(first, Cb4G64Matrix):
+        if any(p.padded_cols != first.padded_cols for p in parts):
+            raise FormatError("concatenated parts must share padded_cols")
+        return Cb4G64Matrix(rows, first.cols, first.padded_cols,
+                            np.concatenate([np.asarray(p.idx, np.uint8) for p in parts]),
+                            np.concatenate([np.asarray(p.lut_f16, np.uint16) for p in parts]))
+    raise FormatError(f"concat_rows does not handle {type(first).__name__}")

@@ -47,7 +47,7 @@ def make_g64(rows: int, cols: int, seed: int = 1) -> Cb4G64Matrix:
         idx2 = idx.reshape(rows, kp // 2)
         for c in range(cols, kp):
             idx2[:, c // 2] &= np.uint8(0xF0 if c % 2 == 0 else 0x0F)
-    lut = np.sort(g.normal(0.0, 0.02, size=(groups, 16)).astype(np.float32), axis=1)
+    lut = np.sort(g.standard_normal(size=(groups, 16), dtype=np.float32) * np.float32(0.02), axis=1)
     lut_f16 = f32_to_f16_bits(lut).reshape(-1)
     return Cb4G64Matrix(rows, cols, kp, idx, lut_f16)
 
