@@ -160,16 +160,60 @@ def test_gemv_q8_config0_f32(eng):
 
 
 def test_gemv_lm_head_q8(eng):
-    """Q8 LM head 151936 x 2048 at M = 1 and 8 against the oracle."""
+    """Q8 LM head 151936 x 2048 at M = 1, 2, 4 and 8 against the oracle."""
     m = synth.make_q8(151936, 2048, seed=5)
     t = eng.upload_packed(m)
-    for M in (1, 8):
+    for M in (1, 2, 4, 8):
         xb = synth.make_x_bf16(M, 2048, seed=M)
         X = bf16_bits_to_f32(xb).reshape(M, 2048)
         y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
         for i in range(M):
             yref = oracle.gemv(m, X[i], threads=THREADS)
             assert max_rel(y[i], yref, q8_floor(m, X[i])) <= 1e-3
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("M", [2, 3, 5, 8])
+def test_gemv_small_batch_tails_bf16(eng, kind, M):
+    """M = 2..8 with bf16 x at ragged shapes (cols % 8 != 0 takes the element-wise x path)."""
+    for rows, cols in [(1, 1), (7, 129), (33, 257), (5, 544), (9, 2050)]:
+        m = make(kind, rows, cols, seed=rows + cols + M)
+        t = eng.upload_packed(m)
+        xb = synth.make_x_bf16(M, cols, seed=cols + M)
+        X = bf16_bits_to_f32(xb).reshape(M, cols)
+        yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+        yref = gemv_ref(m, X)
+        fl = floor_scale(oracle.decode_rows(m), X)
+        assert max_rel(yf, yref, fl) <= 1e-3, (rows, cols)
+        assert_bf16_close(yb, yref, fl)
+        yf2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        assert np.array_equal(yf.view(np.uint32), yf2.view(np.uint32)), "run-to-run bits"
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("M", [4, 8])
+def test_gemv_small_batch_f32_x(eng, kind, M):
+    for rows, cols in [(3, 100), (64, 2048), (16, 6144)]:
+        m = make(kind, rows, cols, seed=rows * cols + M)
+        t = eng.upload_packed(m)
+        X = synth.make_x_f32(M, cols, seed=M)
+        y = run_dev(eng, t, X, engine.DTYPE_F32, M, engine.DTYPE_F32)
+        assert max_rel(y, gemv_ref(m, X), floor_scale(oracle.decode_rows(m), X)) <= 1e-3, (rows, cols)
+
+
+@pytest.mark.parametrize("cols", [100, 2048])
+def test_gemv_q8_many_rows_small_batch(eng, cols):
+    """Row counts >= 65536 with M = 2..8 take the LDS-staged persistent kernel."""
+    m = synth.make_q8(65541, cols, seed=cols)
+    t = eng.upload_packed(m)
+    for M in (2, 3, 4, 8):
+        xb = synth.make_x_bf16(M, cols, seed=M)
+        X = bf16_bits_to_f32(xb).reshape(M, cols)
+        y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        for i in range(M):
+            yref = oracle.gemv(m, X[i], threads=THREADS)
+            assert max_rel(y[i], yref, q8_floor(m, X[i])) <= 1e-3, (M, i)
 
 
 def test_gemv_deterministic_and_grouping_invariant(eng):

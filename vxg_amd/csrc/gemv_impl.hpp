@@ -25,6 +25,8 @@
 // Sums are fp32; the order differs from the CPU reference, so results agree
 // to fp32 rounding (the parity bar is relative error, not bits).
 #pragma once
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace vxt {
@@ -197,6 +199,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   const uint32_t row0 = (blockIdx.x * kWaves + wave) * RPW;
   const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
   const uint32_t nsteps = (kp + kStep - 1) / kStep;
+  constexpr bool kLateX = MT >= 4;
 
   if constexpr (KIND == KIND_CB4) {   // before any global load is in flight
     if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
@@ -213,14 +216,15 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   for (uint32_t s0 = 0; s0 < nsteps; s0 += S) {
     const uint32_t ns = nsteps - s0 < (uint32_t)S ? nsteps - s0 : (uint32_t)S;   // uniform
     // ---- issue: activations, then weights, for every step of the batch
-    XChunk<XBF16> xc[S][MT];
+    XChunk<XBF16> xc[kLateX ? 1 : S][kLateX ? 1 : MT];
     WChunk<KIND> wc[S][RPW];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      if ((uint32_t)s < ns && x_vec) {
+      if (!kLateX && (uint32_t)s < ns && x_vec) {
         const uint32_t k0 = (s0 + s) * kStep + lane * kChunk;
 #pragma unroll
-        for (int m = 0; m < MT; ++m) load_x<XBF16>(x, cols, (uint32_t)m < M_rt ? m : 0, k0, xc[s][m]);
+        for (int m = 0; m < MT; ++m)
+          load_x<XBF16>(x, cols, (uint32_t)m < M_rt ? m : 0, k0, xc[kLateX ? 0 : s][kLateX ? 0 : m]);
       }
     }
 #pragma unroll
@@ -243,13 +247,18 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
       if ((uint32_t)s >= ns) break;
       const uint32_t k0 = (s0 + s) * kStep + lane * kChunk;
       const bool kin = k0 < kp;
-      float xv[MT][kChunk];
+      // Early x: every token unpacked once per step.  Late x (MT >= 4): each
+      // token is loaded and unpacked where it is used, so the registers hold
+      // one token's 32 values at a time.
+      float xv[kLateX ? 1 : MT][kChunk];
+      if constexpr (!kLateX) {
 #pragma unroll
-      for (int m = 0; m < MT; ++m) {
-        if (x_vec)
-          unpack_x<XBF16>(xc[s][m], xv[m]);
-        else
-          load_x_scalar<XBF16>(x, cols, (uint32_t)m < M_rt ? m : 0, k0, xv[m]);
+        for (int m = 0; m < MT; ++m) {
+          if (x_vec)
+            unpack_x<XBF16>(xc[s][m], xv[m]);
+          else
+            load_x_scalar<XBF16>(x, cols, (uint32_t)m < M_rt ? m : 0, k0, xv[m]);
+        }
       }
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
@@ -263,11 +272,22 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
         dequant_chunk<KIND>(wc[s][r], cbase, sl, lane, w);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
+          const float* xm = xv[kLateX ? 0 : m];
+          if constexpr (kLateX) {
+            const uint32_t mm = (uint32_t)m < M_rt ? m : 0;
+            if (x_vec) {
+              XChunk<XBF16> c;
+              load_x<XBF16>(x, cols, mm, k0, c);
+              unpack_x<XBF16>(c, xv[0]);
+            } else {
+              load_x_scalar<XBF16>(x, cols, mm, k0, xv[0]);
+            }
+          }
           float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
           for (int j = 0; j < kChunk; j += 2) {
-            p0 = __builtin_fmaf(w[j], xv[m][j], p0);
-            p1 = __builtin_fmaf(w[j + 1], xv[m][j + 1], p1);
+            p0 = __builtin_fmaf(w[j], xm[j], p0);
+            p1 = __builtin_fmaf(w[j + 1], xm[j + 1], p1);
           }
           float p = p0 + p1;
           if constexpr (KIND == KIND_Q8) {
@@ -325,6 +345,307 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q8 weights x bf16 activations: packed bf16 dot products.
+//
+// An int8 weight is exact in bf16 (at most 8 significant bits), and bf16 x
+// needs no conversion, so each pair of columns costs one v_dot2_f32_bf16 per
+// token (the products are exact, the sum is fp32) instead of two FMAs plus
+// two unpacks.  Weights are converted once per row-step (int8 -> f32 via
+// SDWA, then the high halves of two f32 packed by one v_perm), and x stays in
+// its packed bf16 form in registers.  Block scale, masking and the final
+// wave reduction are as in gemv_kernel.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c,
+                                         false);
+}
+
+// Columns (2j, 2j+1) of a Q8 chunk as a packed bf16 pair (low half = even column).
+__device__ __forceinline__ void q8_pairs(const WChunk<KIND_Q8>& c, uint32_t (&qp)[kChunk / 2]) {
+  const uint32_t wd[8] = {c.a.x, c.a.y, c.a.z, c.a.w, c.b.x, c.b.y, c.b.z, c.b.w};
+#pragma unroll
+  for (int j = 0; j < kChunk / 2; ++j) {
+    const uint32_t w = wd[j >> 1];
+    const int sh = (j & 1) * 16;
+    const float lo = (float)(int8_t)((w >> sh) & 0xffu);
+    const float hi = (float)(int8_t)((w >> (sh + 8)) & 0xffu);
+    qp[j] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+  }
+}
+
+// One token's 32 bf16 activations at k0 as 16 packed pairs, zero outside
+// [0, cols).  The token's row is a raw buffer (base and byte size in SGPRs):
+// offsets are 32-bit per lane, and the hardware returns zeros for any part
+// of a load at or past the row's end, so no clamping or masking is needed.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_row_rsrc(const uint16_t* x, uint32_t cols, uint32_t m) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x + (size_t)m * cols), (short)0,
+                                           (int)(cols * 2u), 0x00020000);
+}
+
+__device__ __forceinline__ void load_x_pairs(__amdgpu_buffer_rsrc_t r, uint32_t k0, uint32_t x_vec,
+                                             uint32_t (&xp)[kChunk / 2]) {
+  if (x_vec) {   // cols % 8 == 0: each 16-byte piece is wholly inside or outside the row
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, (k0 + 8u * i) * 2u, 0, 0);
+      xp[4 * i + 0] = v.x;
+      xp[4 * i + 1] = v.y;
+      xp[4 * i + 2] = v.z;
+      xp[4 * i + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < kChunk / 2; ++j) {
+      const uint32_t v0 = __builtin_amdgcn_raw_buffer_load_b16(r, (k0 + 2u * j) * 2u, 0, 0);
+      const uint32_t v1 = __builtin_amdgcn_raw_buffer_load_b16(r, (k0 + 2u * j + 1u) * 2u, 0, 0);
+      xp[j] = (v0 & 0xffffu) | (v1 << 16);
+    }
+  }
+}
+
+template <int MT, int RPW, int S>
+__global__ __launch_bounds__(kWaves * 64) void gemv_q8_dot2_kernel(DevTensor t, const uint16_t* __restrict__ x,
+                                                                  void* __restrict__ y, uint32_t M_rt,
+                                                                  uint32_t y_bf16, uint32_t x_vec) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t row0 = (blockIdx.x * kWaves + wave) * RPW;
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t nsteps = (kp + kStep - 1) / kStep;
+
+  float acc[RPW][MT];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+
+  for (uint32_t s0 = 0; s0 < nsteps; s0 += S) {
+    const uint32_t ns = nsteps - s0 < (uint32_t)S ? nsteps - s0 : (uint32_t)S;   // uniform
+    // Per step: the activations, then the weights, so that consuming step s
+    // waits only for loads issued up to step s (the memory counter drains in
+    // issue order).
+    uint32_t xp[S][MT][kChunk / 2];
+    WChunk<KIND_Q8> wc[S][RPW];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if ((uint32_t)s < ns) {
+        const uint32_t k0 = (s0 + s) * kStep + lane * kChunk;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) load_x_pairs(x_row_rsrc(x, cols, (uint32_t)m < M_rt ? m : 0), k0, x_vec, xp[s][m]);
+        const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const uint32_t row = row0 + r < rows ? row0 + r : rows - 1;
+          load_chunk<KIND_Q8>(t, row, k0c, 0, 0, wc[s][r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      if ((uint32_t)s >= ns) break;
+      const bool kin = (s0 + s) * kStep + lane * kChunk < kp;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        uint32_t qp[kChunk / 2];
+        q8_pairs(wc[s][r], qp);
+        const float d = f16_to_f32(wc[s][r].d);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+          for (int j = 0; j < kChunk / 2; j += 2) {
+            p0 = dot2_bf16(qp[j], xp[s][m][j], p0);
+            p1 = dot2_bf16(qp[j + 1], xp[s][m][j + 1], p1);
+          }
+          acc[r][m] += kin ? (p0 + p1) * d : 0.0f;
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint32_t row = row0 + r;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float v = wave_sum(acc[r][m]);
+      if (lane == 0 && row < rows && (uint32_t)m < M_rt) {
+        if (y_bf16)
+          static_cast<uint16_t*>(y)[(size_t)m * rows + row] = f32_to_bf16(v);
+        else
+          static_cast<float*>(y)[(size_t)m * rows + row] = v;
+      }
+    }
+  }
+}
+
+// Larger batches (M >= 4): the same dot2 arithmetic with the activations
+// staged in LDS once per workgroup.  Reading x straight from L2 costs
+// M * K * 2 bytes per wave, which at M = 8 is four times the weight bytes a
+// wave streams, and L2 bandwidth, not HBM, sets the time.  Workgroups are
+// persistent: each stages x (all M tokens, all of K: kp <= 3 * kStep) once and
+// then walks row blocks with a stride of the grid size.
+template <int MT, int RPW, int WAVES, int NS>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q8_lds_kernel(DevTensor t, const uint16_t* __restrict__ x,
+                                                                void* __restrict__ y, uint32_t M_rt,
+                                                                uint32_t y_bf16, uint32_t x_vec) {
+  extern __shared__ __attribute__((aligned(16))) uint32_t s_x[];   // [MT][kp / 2] packed bf16 pairs
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t kpw = kp / 2;
+  const uint32_t nblocks = (rows + WAVES * RPW - 1) / (WAVES * RPW);
+
+  // First row block's weights go out before the activations are staged.
+  WChunk<KIND_Q8> wc[NS][RPW];
+  auto issue = [&](uint32_t b) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint32_t k0 = s * kStep + lane * kChunk;
+      const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const uint32_t row = (b * WAVES + wave) * RPW + r;
+        load_chunk<KIND_Q8>(t, row < rows ? row : rows - 1, k0c, 0, 0, wc[s][r]);
+      }
+    }
+  };
+  if (blockIdx.x < nblocks) issue(blockIdx.x);
+
+  // Stage x: 8-column pieces, zero outside [0, cols) (raw-buffer bounds).
+  const uint32_t ppr = kp / 8;   // pieces per token row
+  for (uint32_t p = tid; p < MT * ppr; p += WAVES * 64) {
+    const uint32_t m = p / ppr, pc = p - m * ppr;
+    const __amdgpu_buffer_rsrc_t r = x_row_rsrc(x, cols, m < M_rt ? m : 0);
+    u32x4 v;
+    if (x_vec) {
+      v = __builtin_amdgcn_raw_buffer_load_b128(r, pc * 16u, 0, 0);
+    } else {
+      uint32_t h[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) h[j] = __builtin_amdgcn_raw_buffer_load_b16(r, (pc * 8u + j) * 2u, 0, 0) & 0xffffu;
+      v = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    }
+    *reinterpret_cast<u32x4*>(&s_x[m * kpw + pc * 4]) = v;
+  }
+  __syncthreads();
+
+  for (uint32_t b = blockIdx.x; b < nblocks; b += gridDim.x) {
+    float acc[RPW][MT];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      const uint32_t k0 = s * kStep + lane * kChunk;
+      const bool kin = k0 < kp;
+      const uint32_t k0c = kin ? k0 : kp - kChunk;
+      uint32_t qp[RPW][kChunk / 2];
+      float d[RPW];
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        q8_pairs(wc[s][r], qp[r]);
+        d[r] = f16_to_f32(wc[s][r].d);
+      }
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        uint32_t xp[kChunk / 2];
+        const u32x4* src = reinterpret_cast<const u32x4*>(&s_x[m * kpw + k0c / 2]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4 v = src[i];
+          xp[4 * i] = v.x;
+          xp[4 * i + 1] = v.y;
+          xp[4 * i + 2] = v.z;
+          xp[4 * i + 3] = v.w;
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+          for (int j = 0; j < kChunk / 2; j += 2) {
+            p0 = dot2_bf16(qp[r][j], xp[j], p0);
+            p1 = dot2_bf16(qp[r][j + 1], xp[j + 1], p1);
+          }
+          acc[r][m] += kin ? (p0 + p1) * d[r] : 0.0f;
+        }
+      }
+    }
+    const uint32_t row0 = (b * WAVES + wave) * RPW;
+    if (b + gridDim.x < nblocks) issue(b + gridDim.x);   // next block's weights in flight during the reduction
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const uint32_t row = row0 + r;
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_sum(acc[r][m]);
+        if (lane == 0 && row < rows && (uint32_t)m < M_rt) {
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * rows + row] = f32_to_bf16(v);
+          else
+            static_cast<float*>(y)[(size_t)m * rows + row] = v;
+        }
+      }
+    }
+  }
+}
+
+// Grid for the persistent kernel: enough workgroups to fill every CU at the
+// occupancy the LDS footprint allows, never more than there are row blocks.
+template <int MT, int RPW, int WAVES, int NS>
+hipError_t launch_q8_lds_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s,
+                           uint32_t per_cu = 0) {
+  // Dynamic LDS above 64 KiB must be allowed per kernel, once.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&gemv_q8_lds_kernel<MT, RPW, WAVES, NS>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  const size_t lds = (size_t)MT * t.kp * 2;
+  if (lds > 160u * 1024u || (t.kp + kStep - 1) / kStep != (uint32_t)NS) return hipErrorInvalidValue;
+  const uint32_t nblocks = (t.rows + WAVES * RPW - 1) / (WAVES * RPW);
+  uint32_t occ = per_cu ? per_cu : (uint32_t)std::min<size_t>(160u * 1024u / lds, 16u / WAVES * 2u);
+  if (occ == 0) occ = 1;
+  const uint32_t grid = std::min<uint32_t>(nblocks, 256u * occ);
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && t.cols % 8 == 0;
+  hipLaunchKernelGGL((gemv_q8_lds_kernel<MT, RPW, WAVES, NS>), dim3(grid), dim3(WAVES * 64), lds, s, t,
+                     static_cast<const uint16_t*>(x), y, m, (uint32_t)(y_bf16 ? 1u : 0u), x_vec);
+  return hipGetLastError();
+}
+
+template <int MT, int RPW, int S>
+hipError_t launch_q8_dot2_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  const uint32_t rows_per_block = kWaves * RPW;
+  const dim3 grid((t.rows + rows_per_block - 1) / rows_per_block);
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && t.cols % 8 == 0;
+  hipLaunchKernelGGL((gemv_q8_dot2_kernel<MT, RPW, S>), grid, dim3(kWaves * 64), 0, s, t,
+                     static_cast<const uint16_t*>(x), y, m, (uint32_t)(y_bf16 ? 1u : 0u), x_vec);
+  return hipGetLastError();
+}
+
+// Shape choices for Q8 x bf16 at M = 2..8, from measurements over the
+// decode shapes (K x N in {2048, 6144} x {2048, 6144}, and the 151936-row LM
+// head): the LDS-staged persistent kernel wins only when there are many more
+// row blocks than CUs; otherwise the direct kernel with two rows per wave.
+template <int MT>
+hipError_t launch_q8_dot2_m(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (t.rows >= 65536 && nsteps == 1) {
+    if constexpr (MT >= 8) return launch_q8_lds_t<MT, 1, 4, 1>(t, x, m, y, y_bf16, s);
+    return launch_q8_lds_t<MT, 2, 8, 1>(t, x, m, y, y_bf16, s);
+  }
+  if constexpr (MT == 2) {
+    if (nsteps == 3) return launch_q8_dot2_t<2, 1, 1>(t, x, m, y, y_bf16, s);
+    if (nsteps >= 2) return launch_q8_dot2_t<2, 2, 2>(t, x, m, y, y_bf16, s);
+    return launch_q8_dot2_t<2, 2, 1>(t, x, m, y, y_bf16, s);
+  } else if constexpr (MT == 4) {
+    if (nsteps >= 2) return launch_q8_dot2_t<4, 2, 2>(t, x, m, y, y_bf16, s);
+    return launch_q8_dot2_t<4, 2, 1>(t, x, m, y, y_bf16, s);
+  }
+  return launch_q8_dot2_t<MT, 2, 1>(t, x, m, y, y_bf16, s);
+}
+
 template <uint32_t KIND, int MT, int RPW, int S, bool XBF16>
 hipError_t launch_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
   const uint32_t rows_per_block = kWaves * RPW;
@@ -358,6 +679,14 @@ hipError_t launch_r(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, 
 template <uint32_t KIND>
 hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16,
                        hipStream_t s) {
+  if constexpr (KIND == KIND_Q8) {
+    if (x_bf16 && m >= 2) {
+      if (m == 2) return launch_q8_dot2_m<2>(t, x, m, y, y_bf16, s);
+      if (m <= 4) return launch_q8_dot2_m<4>(t, x, m, y, y_bf16, s);
+      if (m <= 8) return launch_q8_dot2_m<8>(t, x, m, y, y_bf16, s);
+      return hipErrorInvalidValue;
+    }
+  }
   if (m == 1) {
     if (t.rows >= 65536) return launch_r<KIND, 1, 4>(t, x, x_bf16, m, y, y_bf16, s);
     if (t.rows >= 4096) return launch_r<KIND, 1, 2>(t, x, x_bf16, m, y, y_bf16, s);
