@@ -365,3 +365,65 @@ def test_gemm_prefill_shapes_bf16(eng, kind, K, N, M):
     gemm_check(yf[sel], yref, W, X[sel], False)
     # every token: bf16 output is the rounding of the f32 output
     assert np.array_equal(yb, f32_to_bf16_bits(yf))
+
+
+def test_gemm_extreme_weight_magnitudes(eng):
+    """Weights far outside the f16 range (and subnormal scales) keep the GEMM bar:
+    each panel row carries its own power-of-two scale."""
+    q = synth.make_q8(70, 320, seed=3)
+    b = q.blocks.copy().reshape(-1, 34)
+    b[0::3, 0:2] = np.array([0x7800], np.uint16).view(np.uint8)   # d = 32768: |w| up to 4.2e6
+    b[1::7, 0:2] = np.array([0x0001], np.uint16).view(np.uint8)   # subnormal d
+    q.blocks = b.reshape(-1)
+    c = synth.make_cb4(70, 320, seed=4, outlier_frac=0.02)
+    c.scales_f16 = np.where(np.arange(c.scales_f16.size) % 2 == 0, np.uint16(0x7800), c.scales_f16)
+    c.centroids = c.centroids * np.float32(500.0)
+    for m in (q, c):
+        t = eng.upload_packed(m)
+        xb = synth.make_x_bf16(24, 320, seed=5)
+        X = bf16_bits_to_f32(xb).reshape(24, 320)
+        yref = oracle.gemm(m, X, threads=THREADS)
+        W = oracle.decode_rows(m)
+        gemm_check(run_dev(eng, t, xb, engine.DTYPE_BF16, 24, engine.DTYPE_F32), yref, W, X, False)
+        gemm_check(run_dev(eng, t, xb, engine.DTYPE_BF16, 24, engine.DTYPE_BF16), yref, W, X, True)
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("M,N,K", [(16, 64, 4096), (40, 300, 3000), (9, 2048, 6144)])
+def test_gemm_split_k(eng, kind, M, N, K):
+    """Small M x N grids split K across workgroups; partial sums are added in a fixed order."""
+    m = make(kind, N, K, seed=M + N)
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(M, K, seed=K)
+    X = bf16_bits_to_f32(xb).reshape(M, K)
+    yref = oracle.gemm(m, X, threads=THREADS)
+    y1 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    gemm_check(y1, yref, oracle.decode_rows(m), X, False)
+    y2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
+
+
+def test_gemm_in_captured_graph():
+    """A GEMM records into a graph once its workspace is sized by an eager call."""
+    e = engine.HipEngine()
+    try:
+        m = synth.make_q8(512, 1024, seed=8)
+        t = e.upload_packed(m)
+        xd = e.to_device(synth.make_x_bf16(64, 1024, seed=8))
+        yd = e.alloc(64 * 512 * 4)
+        with pytest.raises(engine.BackendError) as ei:
+            e.capture(lambda s: e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 64, yd.ptr, engine.DTYPE_F32, s))
+        assert ei.value.code == engine.VXT_E_ARG
+        e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 64, yd.ptr, engine.DTYPE_F32, e.stream)
+        e.synchronize()
+        ref = yd.download(np.float32, (64, 512))
+        g = e.capture(lambda s: e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 64, yd.ptr, engine.DTYPE_F32, s))
+        for rep in range(3):
+            yd.upload(np.full((64, 512), np.nan, np.float32))
+            g.launch(1)
+            assert np.array_equal(yd.download(np.float32, (64, 512)).view(np.uint32), ref.view(np.uint32)), rep
+            e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 64, yd.ptr, engine.DTYPE_F32, e.stream)
+            e.synchronize()
+        g.free()
+    finally:
+        e.close()

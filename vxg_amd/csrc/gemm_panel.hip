@@ -1,0 +1,541 @@
+// gemm_panel.hip -- prefill GEMM (batch_m > 8) in two phases on one stream.
+//
+// Reference behaviour: PackedTensor::gemm_cpu (llm_prefill.rs:156-255) decodes
+// 32-row weight tiles to f32 with CodebookMatrix::decode_row and multiplies
+// them densely.  The same split, laid out for CDNA4:
+//
+//   1. panel_kernel: every weight row is decoded bit-exactly (the values
+//      decode_row / the Q8_0 and g64 rules produce, cb4 CSR residuals applied
+//      in CSR order) and written once to an f16 panel in HBM, K-contiguous
+//      rows padded to a multiple of 64 with zeros:
+//        * g64: the f16 table entry itself (exact), one plane;
+//        * Q8 and cb4: w * s = hi + lo * 2^-11 with hi = f16(w s),
+//          lo = f16((w s - hi) * 2^11), where s = 2^e per row keeps the
+//          row's largest magnitude in [2^14, 2^15) (no f16 overflow, lo out
+//          of the subnormal range).  hi + lo carries 22 significant bits:
+//          exact for Q8 (q * d has <= 18), within 2^-22 relative for cb4.
+//   2. dense_kernel: Y = X * W^T on v_mfma_f32_32x32x16_f16 from LDS tiles,
+//      fp32 accumulation; lo products go to a second accumulator folded in
+//      as acc + accl * 2^-11, then scaled by 1/s.  bf16 X becomes f16 while it
+//      is staged (exact for |x| in the f16 normal range); f32 X is split into
+//      hi + lo like the weights, with one more MFMA (lo * lo dropped).
+//      Small M*N grids split K across workgroups; reduce_kernel then adds the
+//      partial sums in a fixed order (results do not depend on timing).
+//
+// The panel costs one pass over the packed weights plus one f16 (or 2 x f16)
+// write; the fused alternative re-decodes every weight tile once per M tile
+// and adds cb4 residuals from scattered activation reads per output.
+#include <algorithm>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace vxt {
+
+namespace gp {
+
+constexpr int BK = 64;
+constexpr int LDK = BK + 8;   // padded LDS row (halves): conflict-light fragment reads
+constexpr int THREADS = 256;
+constexpr float kLoScale = 2048.0f;
+constexpr float kLoInv = 1.0f / 2048.0f;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+struct Panel {
+  uint16_t* hi;     // [N][kp] f16
+  uint16_t* lo;     // [N][kp] f16 (split kinds)
+  float* inv;       // [N] 1 / s
+  uint32_t kp;      // K rounded up to BK
+};
+
+__host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+__device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// s = 2^e with bound * s in [2^14, 2^15); 1 for zero or non-finite bounds.
+__device__ __forceinline__ float row_scale(float bound) {
+  if (!(bound > 0.0f) || !(bound < 3.0e38f)) return 1.0f;
+  const int e = 14 - ilogbf(bound);
+  return ldexpf(1.0f, e);
+}
+
+__device__ __forceinline__ void split_write(float w, float s, uint16_t* hi, uint16_t* lo, size_t i) {
+  const float ws = w * s;                              // exact: s is a power of two
+  const _Float16 h = (_Float16)ws;
+  hi[i] = __builtin_bit_cast(uint16_t, h);
+  lo[i] = __builtin_bit_cast(uint16_t, (_Float16)((ws - (float)h) * kLoScale));
+}
+
+// ---- phase 1: activations and panel -----------------------------------------
+
+// X [M][K] (bf16 or f32) -> A [M][kp] f16, zero for k >= K; f32 X also gets
+// the lo plane (x - hi) * 2^11.  One thread per 8 columns.
+template <bool XBF16>
+__global__ __launch_bounds__(THREADS) void xconv_kernel(const void* __restrict__ x, uint32_t M, uint32_t K, uint32_t kp,
+                                                        uint16_t* __restrict__ ah, uint16_t* __restrict__ al,
+                                                        uint32_t x_vec) {
+  const uint32_t ppr = kp / 8;
+  const size_t pieces = (size_t)M * ppr;
+  for (size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x; i < pieces; i += (size_t)gridDim.x * THREADS) {
+    const uint32_t m = (uint32_t)(i / ppr), k = (uint32_t)(i % ppr) * 8;
+    float v[8];
+    if (x_vec && k + 8 <= K) {
+      if constexpr (XBF16) {
+        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + (size_t)m * K + k);
+        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[2 * j] = __uint_as_float(w[j] << 16);
+          v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+      } else {
+        const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + (size_t)m * K + k);
+        const float4 f0 = f[0], f1 = f[1];
+        v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+        v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float f = 0.0f;
+        if (k + j < K) {
+          if constexpr (XBF16)
+            f = bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k + j]);
+          else
+            f = static_cast<const float*>(x)[(size_t)m * K + k + j];
+        }
+        v[j] = f;
+      }
+    }
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
+      h[j] = pack_h2(h0, h1);
+      if constexpr (!XBF16)
+        l[j] = pack_h2((_Float16)((v[2 * j] - (float)h0) * kLoScale), (_Float16)((v[2 * j + 1] - (float)h1) * kLoScale));
+    }
+    *reinterpret_cast<uint4*>(ah + (size_t)m * kp + k) = make_uint4(h[0], h[1], h[2], h[3]);
+    if constexpr (!XBF16) *reinterpret_cast<uint4*>(al + (size_t)m * kp + k) = make_uint4(l[0], l[1], l[2], l[3]);
+  }
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_add(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// 32 consecutive f32 weights -> hi (and lo) f16 pieces at column k0 of the row.
+template <bool SPLIT>
+__device__ __forceinline__ void store32(const float (&w)[32], float s, uint16_t* hi, uint16_t* lo, uint32_t k0) {
+  uint32_t h[16], l[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const float a = w[2 * j] * s, b = w[2 * j + 1] * s;   // exact: s is a power of two
+    const _Float16 ha = (_Float16)a, hb = (_Float16)b;
+    h[j] = pack_h2(ha, hb);
+    if constexpr (SPLIT) l[j] = pack_h2((_Float16)((a - (float)ha) * kLoScale), (_Float16)((b - (float)hb) * kLoScale));
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    *reinterpret_cast<uint4*>(hi + k0 + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+    if constexpr (SPLIT)
+      *reinterpret_cast<uint4*>(lo + k0 + 8 * i) = make_uint4(l[4 * i], l[4 * i + 1], l[4 * i + 2], l[4 * i + 3]);
+  }
+}
+
+// One wave per weight row (grid-stride over rows); a lane decodes 32
+// consecutive columns per 2048-column segment with 16-byte loads, as the
+// GEMV does, and writes them as 16-byte f16 pieces.
+template <uint32_t KIND>
+__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p) {
+  constexpr uint32_t kPair = 48;   // g64 pair-table stride (bytes) in the per-wave slot
+  __shared__ __attribute__((aligned(64))) uint32_t s_slot[KIND == KIND_G64 ? 4 * 32 * kPair / 4 : 1];
+  __shared__ __attribute__((aligned(64))) float s_cent[48];
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t N = t.rows, K = t.cols, kp = t.kp, KP = p.kp;
+  if constexpr (KIND == KIND_CB4) {
+    if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
+    __syncthreads();
+  }
+  for (uint32_t n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {
+    uint16_t* hi = p.hi + (size_t)n * KP;
+    uint16_t* lo = p.lo + (size_t)n * KP;
+    float s = 1.0f;
+    if constexpr (KIND == KIND_Q8) {
+      const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
+      float dm = 0.0f;
+      for (uint32_t b = lane; b < kp / 32; b += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[b])));
+      s = row_scale(127.0f * wave_max(dm));
+    } else if constexpr (KIND == KIND_CB4) {
+      const uint16_t* sp = t.p1 + (size_t)n * (kp / 128);
+      const float* cent = s_cent + 16u * cent_table(t, n);
+      float sm = 0.0f, rs = 0.0f, cm = 0.0f;
+      for (uint32_t g = lane; g < kp / 128; g += 64) sm = fmaxf(sm, fabsf(f16_to_f32_exact(sp[g])));
+      for (uint32_t o = t.row_ptr[n] + lane; o < t.row_ptr[n + 1]; o += 64)
+        rs += fabsf(f16_to_f32_exact(t.outliers[o] >> 16));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) cm = fmaxf(cm, fabsf(cent[i]));
+      s = row_scale(wave_max(sm) * cm + wave_add(rs));
+    }
+    for (uint32_t seg = 0; seg < KP; seg += 64 * 32) {
+      const uint32_t k0 = seg + lane * 32;
+      if (k0 >= KP) break;   // KP % 64 == 0: a lane pair is wholly inside or outside
+      float w[32];
+      if constexpr (KIND == KIND_G64) {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2) + k0 / 2);
+        const uint4 lt = *reinterpret_cast<const uint4*>(t.p1 + ((size_t)n * (kp / 64) + k0 / 64) * 16 + (lane & 1) * 8);
+        const uint32_t slot = wave * 32 * kPair + (lane >> 1) * kPair;   // bytes
+        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_slot) + slot + (lane & 1) * 16) = lt;
+        const uint16_t* tab = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(s_slot) + slot);
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+        uint32_t h[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const uint32_t c0 = 2 * j, c1 = c0 + 1;
+          const uint32_t e0 = k0 + c0 < K ? tab[(wd[c0 >> 3] >> ((c0 & 7) * 4)) & 0xfu] : 0u;
+          const uint32_t e1 = k0 + c1 < K ? tab[(wd[c1 >> 3] >> ((c1 & 7) * 4)) & 0xfu] : 0u;
+          h[j] = e0 | (e1 << 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          *reinterpret_cast<uint4*>(hi + k0 + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+        continue;
+      } else if constexpr (KIND == KIND_Q8) {
+        const uint32_t kc = k0 < kp ? k0 : kp - 32;   // kp may be 32 short of KP
+        const int8_t* qp = static_cast<const int8_t*>(t.p0) + (size_t)n * kp + kc;
+        const uint4 a = *reinterpret_cast<const uint4*>(qp), b = *reinterpret_cast<const uint4*>(qp + 16);
+        const float d = f16_to_f32_exact(t.p1[(size_t)n * (kp / 32) + kc / 32]);
+        const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 32; ++j)
+          w[j] = k0 + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d : 0.0f;   // gguf.rs:223-229
+      } else {
+        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint32_t*>(t.p0) + (size_t)n * (kp / 8) + k0 / 8);
+        const float sc = f16_to_f32_exact(t.p1[(size_t)n * (kp / 128) + k0 / 128]);
+        const float* cent = s_cent + 16u * cent_table(t, n);
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 32; ++j) w[j] = k0 + j < K ? sc * cent[(wd[j >> 3] >> ((j & 7) * 4)) & 0xfu] : 0.0f;
+      }
+      store32<true>(w, s, hi, lo, k0);
+    }
+    if constexpr (KIND == KIND_CB4) {
+      // CSR residuals (codebook.rs:316-333): the lane holding a column's first
+      // entry rebuilds that column from sc * cent[q] and adds the column's
+      // residuals in CSR order, then overwrites the two halves written above.
+      const uint32_t os = t.row_ptr[n], oe = t.row_ptr[n + 1];
+      if (oe > os) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // the dense stores above land first
+        const float* cent = s_cent + 16u * cent_table(t, n);
+        for (uint32_t i = os + lane; i < oe; i += 64) {
+          const uint32_t c = t.outliers[i] & 0xffffu;
+          bool first = c < K;
+          for (uint32_t j = os; j < i && first; ++j) first = (t.outliers[j] & 0xffffu) != c;
+          if (!first) continue;
+          const uint32_t wd = static_cast<const uint32_t*>(t.p0)[(size_t)n * (kp / 8) + c / 8];
+          float v = f16_to_f32_exact(t.p1[(size_t)n * (kp / 128) + c / 128]) * cent[(wd >> ((c % 8) * 4)) & 0xfu];
+          for (uint32_t j = i; j < oe; ++j) {
+            const uint32_t pk = t.outliers[j];
+            if ((pk & 0xffffu) == c) v += f16_to_f32_exact(pk >> 16);
+          }
+          split_write(v, s, hi, lo, c);
+        }
+      }
+    }
+    if (lane == 0) p.inv[n] = 1.0f / s;
+  }
+}
+
+// ---- phase 2: dense GEMM -----------------------------------------------------
+
+// 16-byte pieces of one operand tile: piece p of the thread covers row
+// r0 + p/8 (clamped to the last row: rows past the end are never stored),
+// columns kb + (p%8)*8 .. +8.
+template <int NP, bool LO>
+__device__ __forceinline__ void fetch_tile(const uint16_t* __restrict__ hi, const uint16_t* __restrict__ lo,
+                                           uint32_t r0, uint32_t rows, uint32_t kp, uint32_t kb, u32x4 (&h)[NP],
+                                           u32x4 (&l)[LO ? NP : 1]) {
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const uint32_t piece = threadIdx.x + THREADS * i;
+    const uint32_t r = std::min(r0 + piece / 8, rows - 1);
+    const size_t off = (size_t)r * kp + kb + (piece % 8) * 8;
+    h[i] = *reinterpret_cast<const u32x4*>(hi + off);
+    if constexpr (LO) l[i] = *reinterpret_cast<const u32x4*>(lo + off);
+  }
+}
+
+template <int NP, bool LO>
+__device__ __forceinline__ void commit_tile(_Float16* sh, _Float16* sl, uint32_t st, uint32_t stage_halves,
+                                            const u32x4 (&h)[NP], const u32x4 (&l)[LO ? NP : 1]) {
+#pragma unroll
+  for (int i = 0; i < NP; ++i) {
+    const uint32_t piece = threadIdx.x + THREADS * i;
+    const uint32_t o = st * stage_halves + (piece / 8) * LDK + (piece % 8) * 8;
+    *reinterpret_cast<u32x4*>(sh + o) = h[i];
+    if constexpr (LO) *reinterpret_cast<u32x4*>(sl + o) = l[i];
+  }
+}
+
+// Block tile BM x BN, 2 x 2 waves of (BM/2) x (BN/2) with 32x32x16 f16 MFMA
+// fragments.  Operands are f16 rows of length kp (A: activations, B: panel);
+// LDS holds two stages, so one barrier per K tile: tile k+1 is fetched into
+// registers while tile k is multiplied, then written to the other stage.
+// blockIdx.y selects a K range; with gridDim.y > 1 the block writes fp32
+// partial sums (hi + lo combined, unscaled) to `partial` [z][M][N].
+template <int BM, int BN, bool SPLIT, bool SPLIT_A>
+__global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t* __restrict__ ah,
+                                                        const uint16_t* __restrict__ al, uint32_t M, uint32_t N,
+                                                        void* __restrict__ y, uint32_t y_bf16,
+                                                        float* __restrict__ partial, uint32_t kt_per_split,
+                                                        uint32_t tiles_m) {
+  constexpr int FI = BM / 64, FJ = BN / 64;
+  constexpr int PA = BM * 8 / THREADS, PB = BN * 8 / THREADS;   // 16-byte pieces per thread
+  constexpr int SA = BM * LDK, SB = BN * LDK;                   // halves per stage
+  extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+  _Float16* sA = smem;
+  _Float16* sB = sA + 2 * SA;
+  _Float16* sAl = sB + 2 * SB;
+  _Float16* sBl = sAl + (SPLIT_A ? 2 * SA : 0);
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  const uint32_t tm = blockIdx.x % tiles_m, tn = blockIdx.x / tiles_m;
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint32_t kp = p.kp, ktiles = kp / BK;
+  const uint32_t kt0 = blockIdx.y * kt_per_split;
+  const uint32_t kt1 = std::min(ktiles, kt0 + kt_per_split);
+
+  float16v acc[FI][FJ], accl[FI][FJ];
+#pragma unroll
+  for (int i = 0; i < FI; ++i)
+#pragma unroll
+    for (int j = 0; j < FJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+        accl[i][j][r] = 0.0f;
+      }
+
+  u32x4 ra[PA], ral[SPLIT_A ? PA : 1], rb[PB], rbl[SPLIT ? PB : 1];
+
+  if (kt0 < kt1) {
+    fetch_tile<PA, SPLIT_A>(ah, al, m0, M, kp, kt0 * BK, ra, ral);
+    fetch_tile<PB, SPLIT>(p.hi, p.lo, n0, N, kp, kt0 * BK, rb, rbl);
+    commit_tile<PA, SPLIT_A>(sA, sAl, 0, SA, ra, ral);
+    commit_tile<PB, SPLIT>(sB, sBl, 0, SB, rb, rbl);
+  }
+  __syncthreads();
+  for (uint32_t kt = kt0; kt < kt1; ++kt) {
+    const uint32_t st = (kt - kt0) & 1;
+    if (kt + 1 < kt1) {
+      fetch_tile<PA, SPLIT_A>(ah, al, m0, M, kp, (kt + 1) * BK, ra, ral);
+      fetch_tile<PB, SPLIT>(p.hi, p.lo, n0, N, kp, (kt + 1) * BK, rb, rbl);
+    }
+    const _Float16* a_st = sA + st * SA;
+    const _Float16* b_st = sB + st * SB;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      half8 af[FI], afl[SPLIT_A ? FI : 1], bf[FJ], bfl[SPLIT ? FJ : 1];
+      const uint32_t kofs = ks * 16 + (lane >> 5) * 8;
+#pragma unroll
+      for (int i = 0; i < FI; ++i) {
+        const uint32_t ar = (wm * (BM / 2) + i * 32 + (lane & 31)) * LDK + kofs;
+        af[i] = *reinterpret_cast<const half8*>(a_st + ar);
+        if constexpr (SPLIT_A) afl[i] = *reinterpret_cast<const half8*>(sAl + st * SA + ar);
+      }
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        const uint32_t br = (wn * (BN / 2) + j * 32 + (lane & 31)) * LDK + kofs;
+        bf[j] = *reinterpret_cast<const half8*>(b_st + br);
+        if constexpr (SPLIT) bfl[j] = *reinterpret_cast<const half8*>(sBl + st * SB + br);
+      }
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j) {
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+          if constexpr (SPLIT)
+            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], accl[i][j], 0, 0, 0);
+          if constexpr (SPLIT_A)   // lo * lo is below 2^-22 relative and dropped
+            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], accl[i][j], 0, 0, 0);
+        }
+    }
+    if (kt + 1 < kt1) {
+      commit_tile<PA, SPLIT_A>(sA, sAl, st ^ 1u, SA, ra, ral);
+      commit_tile<PB, SPLIT>(sB, sBl, st ^ 1u, SB, rb, rbl);
+    }
+    __syncthreads();
+  }
+
+  // Lane owns column n = n0 + wn*(BN/2) + j*32 + lane%32 of fragment (i, j),
+  // rows m = m0 + wm*(BM/2) + i*32 + (lane/32)*4 + 8*(r/4) + r%4.
+  const bool to_partial = gridDim.y > 1;
+#pragma unroll
+  for (int j = 0; j < FJ; ++j) {
+    const uint32_t n = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
+    if (n >= N) continue;
+    const float inv = p.inv[n];
+#pragma unroll
+    for (int i = 0; i < FI; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t m = m0 + wm * (BM / 2) + i * 32 + (lane >> 5) * 4 + 8 * (r >> 2) + (r & 3);
+        if (m >= M) continue;
+        float v = acc[i][j][r];
+        if constexpr (SPLIT || SPLIT_A) v = __builtin_fmaf(accl[i][j][r], kLoInv, v);
+        if (to_partial) {
+          partial[((size_t)blockIdx.y * M + m) * N + n] = v;
+        } else {
+          v *= inv;
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(v);
+          else
+            static_cast<float*>(y)[(size_t)m * N + n] = v;
+        }
+      }
+  }
+}
+
+// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n].
+__global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict__ partial, uint32_t splits,
+                                                         const float* __restrict__ inv, uint32_t M, uint32_t N,
+                                                         void* __restrict__ y, uint32_t y_bf16) {
+  const size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x;
+  const size_t total = (size_t)M * N;
+  if (i >= total) return;
+  float v = 0.0f;
+  for (uint32_t z = 0; z < splits; ++z) v += partial[(size_t)z * total + i];
+  v *= inv[i % N];
+  if (y_bf16)
+    static_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
+  else
+    static_cast<float*>(y)[i] = v;
+}
+
+// ---- planning ------------------------------------------------------------------
+
+struct Plan {
+  int bm, bn;
+  uint32_t kp, splits, kt_per_split;
+  size_t panel_plane, panel_bytes, a_plane, a_bytes, partial_bytes;
+};
+
+inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16) {
+  Plan pl{};
+  const bool split_w = t.kind != KIND_G64;
+  pl.kp = (t.cols + BK - 1) / BK * BK;
+  const uint32_t ktiles = pl.kp / BK;
+  pl.bm = m >= 256 ? 128 : 64;
+  pl.bn = pl.bm;
+  const uint32_t tiles = ((m + pl.bm - 1) / pl.bm) * ((t.rows + pl.bn - 1) / pl.bn);
+  // Split K until the grid covers the 256 CUs, keeping >= 4 K tiles per split.
+  uint32_t splits = 1;
+  while (tiles * splits < 256 && ktiles / (splits * 2) >= 4) splits *= 2;
+  pl.kt_per_split = (ktiles + splits - 1) / splits;
+  pl.splits = (ktiles + pl.kt_per_split - 1) / pl.kt_per_split;
+  pl.panel_plane = al256((size_t)t.rows * pl.kp * 2);
+  pl.panel_bytes = pl.panel_plane * (split_w ? 2 : 1) + al256((size_t)t.rows * 4);
+  pl.a_plane = al256((size_t)m * pl.kp * 2);
+  pl.a_bytes = pl.a_plane * (x_bf16 ? 1 : 2);
+  pl.partial_bytes = pl.splits > 1 ? al256((size_t)pl.splits * m * t.rows * 4) : 0;
+  return pl;
+}
+
+template <int BM, int BN, bool SPLIT, bool SPLIT_A>
+hipError_t launch_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, uint32_t m, uint32_t n, void* y,
+                        bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
+  constexpr size_t lds = (size_t)(2 * BM * LDK + 2 * BN * LDK + (SPLIT_A ? 2 * BM * LDK : 0) +
+                                  (SPLIT ? 2 * BN * LDK : 0)) * 2;
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&dense_kernel<BM, BN, SPLIT, SPLIT_A>), hipFuncAttributeMaxDynamicSharedMemorySize,
+      (int)lds);
+  if (attr != hipSuccess) return attr;
+  const uint32_t tiles_m = (m + BM - 1) / BM;
+  const dim3 grid(tiles_m * ((n + BN - 1) / BN), pl.splits);
+  hipLaunchKernelGGL((dense_kernel<BM, BN, SPLIT, SPLIT_A>), grid, dim3(THREADS), lds, s, p, ah, al, m, n, y,
+                     (uint32_t)y_bf16, partial, pl.kt_per_split, tiles_m);
+  return hipGetLastError();
+}
+
+template <int BM, bool SPLIT>
+hipError_t launch_dense_x(const Panel& p, const uint16_t* ah, const uint16_t* al, bool x_bf16, uint32_t m,
+                          uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
+  if (x_bf16) return launch_dense<BM, BM, SPLIT, false>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+  return launch_dense<BM, BM, SPLIT, true>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+}
+
+template <uint32_t KIND>
+hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
+               size_t ws_bytes, hipStream_t s) {
+  constexpr bool SPLIT = KIND != KIND_G64;
+  const Plan pl = plan(t, m, x_bf16);
+  if (ws_bytes < pl.panel_bytes + pl.a_bytes + pl.partial_bytes) return hipErrorInvalidValue;
+  char* base = static_cast<char*>(ws);
+  Panel p;
+  p.hi = reinterpret_cast<uint16_t*>(base);
+  p.lo = reinterpret_cast<uint16_t*>(base + (SPLIT ? pl.panel_plane : 0));
+  p.inv = reinterpret_cast<float*>(base + pl.panel_plane * (SPLIT ? 2 : 1));
+  p.kp = pl.kp;
+  uint16_t* ah = reinterpret_cast<uint16_t*>(base + pl.panel_bytes);
+  uint16_t* al = reinterpret_cast<uint16_t*>(base + pl.panel_bytes + (x_bf16 ? 0 : pl.a_plane));
+  float* partial = reinterpret_cast<float*>(base + pl.panel_bytes + pl.a_bytes);
+
+  const size_t esz = x_bf16 ? 2 : 4;
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t.cols * esz) % 16 == 0;
+  const size_t pieces = (size_t)m * (pl.kp / 8);
+  const uint32_t xgrid = (uint32_t)std::min<size_t>((pieces + THREADS - 1) / THREADS, 2048);
+  if (x_bf16)
+    hipLaunchKernelGGL((xconv_kernel<true>), dim3(xgrid), dim3(THREADS), 0, s, x, m, t.cols, pl.kp, ah, al, x_vec);
+  else
+    hipLaunchKernelGGL((xconv_kernel<false>), dim3(xgrid), dim3(THREADS), 0, s, x, m, t.cols, pl.kp, ah, al, x_vec);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const uint32_t pgrid = std::min<uint32_t>((t.rows + 3) / 4, 2048);
+  hipLaunchKernelGGL((panel_kernel<KIND>), dim3(pgrid), dim3(THREADS), 0, s, t, p);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (pl.bm == 128)
+    e = launch_dense_x<128, SPLIT>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+  else
+    e = launch_dense_x<64, SPLIT>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+  if (e != hipSuccess || pl.splits == 1) return e;
+  const size_t total = (size_t)m * t.rows;
+  hipLaunchKernelGGL(reduce_kernel, dim3((uint32_t)((total + THREADS - 1) / THREADS)), dim3(THREADS), 0, s, partial,
+                     pl.splits, p.inv, m, t.rows, y, (uint32_t)y_bf16);
+  return hipGetLastError();
+}
+
+}  // namespace gp
+
+size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16) {
+  const gp::Plan pl = gp::plan(t, m, x_bf16);
+  return pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
+}
+
+hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
+                       size_t ws_bytes, hipStream_t s) {
+  if (m == 0 || (size_t)m * t.rows > (size_t)1 << 40) return hipErrorInvalidValue;
+  switch (t.kind) {
+    case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
+    case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
+    case KIND_CB4: return gp::run<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace vxt

@@ -24,8 +24,9 @@
 namespace vxt {
 hipError_t launch_gemv(const DevTensor& t, const void* x, bool x_bf16, bool x_vec, uint32_t m,
                        void* y, bool y_bf16, hipStream_t s);
-hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y,
-                       bool y_bf16, hipStream_t s);
+size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16);
+hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
+                       size_t ws_bytes, hipStream_t s);
 hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
                           hipStream_t s);
 }  // namespace vxt
@@ -75,6 +76,8 @@ struct Ctx {
   size_t d_x_cap = 0;
   void* d_y = nullptr;
   size_t d_y_cap = 0;
+  void* ws = nullptr;      // GEMM workspace: weight panel + split-K partial sums
+  size_t ws_cap = 0;
   std::mutex mu;
   std::set<Tensor*> tensors;
   std::set<void*> buffers;
@@ -230,7 +233,21 @@ void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, 
     const bool x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t->cols * esz) % 16 == 0;
     e = vxt::launch_gemv(d, x, xb, x_vec, m, y, yb, s);
   } else {
-    e = vxt::launch_gemm(d, x, xb, m, y, yb, s);
+    // The panel workspace is shared by every GEMM of this context (calls are
+    // ordered on one stream, or the caller orders them).  It only grows
+    // outside a capture: a captured graph keeps the pointer it recorded.
+    const size_t need = vxt::gemm_workspace_bytes(d, m, xb);
+    if (need > c->ws_cap) {
+      if (c->capturing)
+        fail(VXT_E_ARG, "GEMM workspace too small inside a capture: run this shape once before capturing");
+      VXT_HIP_CHECK(hipDeviceSynchronize());   // earlier GEMMs may still read the old workspace
+      if (c->ws) VXT_HIP_CHECK(hipFree(c->ws));
+      c->ws = nullptr;
+      c->ws_cap = 0;
+      VXT_HIP_CHECK(hipMalloc(&c->ws, need));
+      c->ws_cap = need;
+    }
+    e = vxt::launch_gemm(d, x, xb, m, y, yb, c->ws, c->ws_cap, s);
   }
   if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
   if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e));
@@ -298,6 +315,7 @@ void vxt_hip_destroy(void* ctx) {
   }
   if (c->d_x) (void)hipFree(c->d_x);
   if (c->d_y) (void)hipFree(c->d_y);
+  if (c->ws) (void)hipFree(c->ws);
   (void)hipEventDestroy(c->ev0);
   (void)hipEventDestroy(c->ev1);
   (void)hipStreamDestroy(c->stream);
