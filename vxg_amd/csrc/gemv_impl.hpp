@@ -207,6 +207,19 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   }
   const uint32_t slot = lds_addr(s_slot) + (KIND == KIND_G64 ? wave * S * RPW * kSlotBytes : 0);
 
+  // cb4 residuals: each row's CSR bounds are requested before anything else
+  // and each lane's first entry right after the first batch of weights, so
+  // only the activation read of the residual is left after the last weight.
+  uint32_t os[RPW], oe[RPW], pk0[RPW];
+  if constexpr (KIND == KIND_CB4) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const uint32_t row = row0 + r < rows ? row0 + r : rows - 1;
+      os[r] = t.row_ptr[row];
+      oe[r] = t.row_ptr[row + 1];
+    }
+  }
+
   float acc[RPW][MT];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -238,6 +251,16 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
         for (int r = 0; r < RPW; ++r) {
           const uint32_t row = row0 + r < rows ? row0 + r : rows - 1;
           load_chunk<KIND>(t, row, k0c, g < gmax ? g : gmax, lane & 1, wc[s][r]);
+        }
+      }
+    }
+    if constexpr (KIND == KIND_CB4) {
+      if (s0 == 0) {   // clamped, unconditional (the CSR stream holds at least one word)
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+          const uint32_t i = os[r] + lane;
+          const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
+          pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
         }
       }
     }
@@ -304,14 +327,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   }
 
   if constexpr (KIND == KIND_CB4) {
-    // CSR residuals (codebook.rs:409-415): y += f16(res) * x[col].
+    // CSR residuals (codebook.rs:409-415): y += f16(res) * x[col]; lane l
+    // takes entries l, l + 64, ... of the row, in that order.
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       const uint32_t row = row0 + r;
       if (row >= rows) break;
-      const uint32_t os = t.row_ptr[row], oe = t.row_ptr[row + 1];
-      for (uint32_t i = os + lane; i < oe; i += 64) {
-        const uint32_t pk = t.outliers[i];
+      for (uint32_t i = os[r] + lane; i < oe[r]; i += 64) {
+        const uint32_t pk = i < os[r] + 64 ? pk0[r] : t.outliers[i];
         const uint32_t col = pk & 0xffffu;
         if (col >= cols) continue;
         const float val = f16_to_f32(pk >> 16);
