@@ -41,7 +41,7 @@ METRIC = "decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s, 1×MI355X"
 # HBM bytes per launch of the headline kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
 # device-to-device copy of known size; see profiles/gemv_g64_config1.md.
-MEASURED_TRAFFIC_BYTES = {"config1": 12712110}
+MEASURED_TRAFFIC_BYTES = {"config1": 12709173}
 
 
 def log(msg: str) -> None:
