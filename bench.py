@@ -153,12 +153,13 @@ def bench_gemm(eng, m, M: int, steps: int, warmup: int, seed: int = 0):
 
 
 def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
-                ffn: int = 6144, seed: int = 40):
+                ffn: int = 6144, seed: int = 40, persistent: bool = False):
     """Config 4: tokens/s of the decode-step linear stack (matmul-only path).
 
     Per layer [q;k;v] (3 x hidden rows), o, [gate;up] (2 x ffn rows), down,
     then the Q8 LM head; every layer's weights are drawn separately.  One
-    token is captured as a HIP graph; ``tokens`` replays are timed.
+    token is captured as a HIP graph (or, ``persistent``, recorded as one
+    persistent launch); ``tokens`` replays are timed.
     """
     from vxg_amd import stack, synth
     gen = {"g64": synth.make_g64, "cb4": synth.make_cb4}[kind]
@@ -182,12 +183,12 @@ def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: i
     for _ in range(3):
         st.enqueue()
     eng.synchronize()
-    g = st.capture()
-    g.launch(3)
+    runner = st.persistent() if persistent else st.capture()
+    (runner.run if persistent else runner.launch)(3)
     t0 = time.perf_counter()
-    ev_ms = g.launch(tokens)
+    ev_ms = (runner.run if persistent else runner.launch)(tokens)
     wall = time.perf_counter() - t0
-    g.free()
+    runner.free()
     st.free()
     for L in lw:
         for t in (L.qkv, L.o, L.gate_up, L.down):
@@ -296,10 +297,12 @@ def main():
                     log(f"  config 3 {kind} M={M} K={K} N={N}: {rg['TFLOPs']:.1f} TFLOP/s")
     if "4" in run:
         head_m = synth.make_q8(151936, 2048, seed=5)
-        for kind in ("g64", "cb4"):
-            log(f"config 4: decode stack, 24 layers {kind} + Q8 LM head")
-            rs = bench_stack(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)))
-            secondary.append({"config": f"4: decode stack 24x{{[q;k;v],o,[gate;up],down}} {kind} + q8 head, M=1",
+        for kind, pers in (("g64", False), ("cb4", False), ("g64", True), ("cb4", True)):
+            how = "one persistent launch per token" if pers else "HIP graph of 97 launches per token"
+            log(f"config 4: decode stack, 24 layers {kind} + Q8 LM head, {how}")
+            rs = bench_stack(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)), persistent=pers)
+            secondary.append({"config": f"4: decode stack 24x{{[q;k;v],o,[gate;up],down}} {kind} + q8 head, M=1, "
+                                        f"{how}",
                               "tokens_per_s": round(rs["tokens_per_s"], 1),
                               "ms_per_token": round(rs["ms_per_token"], 4),
                               "bytes_per_token": rs["bytes_per_token"],

@@ -18,7 +18,8 @@ Only the matmuls run (the "matmul-only path"): attention, norms and the
 activation function are outside this module, so each projection reads a
 slice of the previous one's output instead.  The dependency chain between
 launches is the real one.  One token is 4 * layers + 1 launches; captured
-once into a HIP graph, it replays with no per-launch host work.
+once into a HIP graph, it replays with no per-launch host work;
+:meth:`DecodeStack.persistent` runs the same token as one persistent launch.
 """
 from __future__ import annotations
 
@@ -81,19 +82,28 @@ class DecodeStack:
         """Upload the token's bf16 activations (uint16 bits, [hidden])."""
         self.x.upload(x_bf16_bits)
 
+    def ops(self):
+        """The token's projections as ``(tensor, x_ptr, y_ptr, y_dtype)``, in order."""
+        bf16, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
+        out, x = [], self.x.ptr
+        for L in self.layers:
+            out += [(L.qkv, x, self.qkv_out.ptr, bf16), (L.o, self.qkv_out.ptr, self.o_out.ptr, bf16),
+                    (L.gate_up, self.o_out.ptr, self.gu_out.ptr, bf16),
+                    (L.down, self.gu_out.ptr, self.dn_out.ptr, bf16)]
+            x = self.dn_out.ptr
+        out.append((self.lm_head, x, self.logits.ptr, f32))
+        return out
+
+    def persistent(self) -> engine.Chain:
+        """The same token as one persistent launch (``HipEngine.chain``): each
+        projection's weights stream in while the one before it finishes."""
+        return self.eng.chain(self.ops())
+
     def enqueue(self, stream=None) -> None:
         """Queue one token's projections on ``stream`` (default: the engine's)."""
         stream = stream or self.eng.stream
-        mm = self.eng.matmul_dev
-        bf16, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
-        x = self.x.ptr
-        for L in self.layers:
-            mm(L.qkv, x, bf16, 1, self.qkv_out.ptr, bf16, stream)
-            mm(L.o, self.qkv_out.ptr, bf16, 1, self.o_out.ptr, bf16, stream)
-            mm(L.gate_up, self.o_out.ptr, bf16, 1, self.gu_out.ptr, bf16, stream)
-            mm(L.down, self.gu_out.ptr, bf16, 1, self.dn_out.ptr, bf16, stream)
-            x = self.dn_out.ptr
-        mm(self.lm_head, x, bf16, 1, self.logits.ptr, f32, stream)
+        for t, xp, yp, ydt in self.ops():
+            self.eng.matmul_dev(t, xp, engine.DTYPE_BF16, 1, yp, ydt, stream)
 
     def capture(self) -> engine.Graph:
         """Record one token into a HIP graph (replay with ``Graph.launch``)."""
