@@ -46,9 +46,17 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 struct Panel {
   uint16_t* hi;     // [N][kp] f16
-  uint16_t* lo;     // [N][kp] f16 (split kinds)
+  uint16_t* lo;     // [N][kp] f16 (hi/lo mode)
   float* inv;       // [N] 1 / s
+  float* dsc;       // [N][kp/32] block scales (Q8 block mode)
   uint32_t kp;      // K rounded up to BK
+};
+
+// How a panel represents the weights.
+enum WMode : int {
+  kWPlain = 0,    // f16 values (g64)
+  kWHiLo = 1,     // w*s = hi + lo*2^-11 (cb4; Q8 with f32 activations)
+  kWQBlock = 2,   // f16 int8 values + f32 scale per 32-column block (Q8, bf16 activations)
 };
 
 __host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -160,7 +168,7 @@ __device__ __forceinline__ void store32(const float (&w)[32], float s, uint16_t*
 // consecutive columns per 2048-column segment with 16-byte loads, as the
 // GEMV does, and writes them as 16-byte f16 pieces.
 template <uint32_t KIND>
-__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p) {
+__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, uint32_t qblock) {
   constexpr uint32_t kPair = 48;   // g64 pair-table stride (bytes) in the per-wave slot
   __shared__ __attribute__((aligned(64))) uint32_t s_slot[KIND == KIND_G64 ? 4 * 32 * kPair / 4 : 1];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
@@ -176,9 +184,13 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p) {
     float s = 1.0f;
     if constexpr (KIND == KIND_Q8) {
       const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
-      float dm = 0.0f;
-      for (uint32_t b = lane; b < kp / 32; b += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[b])));
-      s = row_scale(127.0f * wave_max(dm));
+      if (qblock) {   // block scales as f32; blocks past the weights' own are zero
+        for (uint32_t b = lane; b < KP / 32; b += 64) p.dsc[(size_t)n * (KP / 32) + b] = b < kp / 32 ? f16_to_f32_exact(dp[b]) : 0.0f;
+      } else {
+        float dm = 0.0f;
+        for (uint32_t b = lane; b < kp / 32; b += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[b])));
+        s = row_scale(127.0f * wave_max(dm));
+      }
     } else if constexpr (KIND == KIND_CB4) {
       const uint16_t* sp = t.p1 + (size_t)n * (kp / 128);
       const float* cent = s_cent + 16u * cent_table(t, n);
@@ -217,11 +229,15 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p) {
         const uint32_t kc = k0 < kp ? k0 : kp - 32;   // kp may be 32 short of KP
         const int8_t* qp = static_cast<const int8_t*>(t.p0) + (size_t)n * kp + kc;
         const uint4 a = *reinterpret_cast<const uint4*>(qp), b = *reinterpret_cast<const uint4*>(qp + 16);
-        const float d = f16_to_f32_exact(t.p1[(size_t)n * (kp / 32) + kc / 32]);
+        const float d = qblock ? 1.0f : f16_to_f32_exact(t.p1[(size_t)n * (kp / 32) + kc / 32]);
         const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
         for (int j = 0; j < 32; ++j)
           w[j] = k0 + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d : 0.0f;   // gguf.rs:223-229
+        if (qblock) {   // the int8 value itself, exact in f16
+          store32<false>(w, 1.0f, hi, lo, k0);
+          continue;
+        }
       } else {
         const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint32_t*>(t.p0) + (size_t)n * (kp / 8) + k0 / 8);
         const float sc = f16_to_f32_exact(t.p1[(size_t)n * (kp / 128) + k0 / 128]);
@@ -296,12 +312,15 @@ __device__ __forceinline__ void commit_tile(_Float16* sh, _Float16* sl, uint32_t
 // registers while tile k is multiplied, then written to the other stage.
 // blockIdx.y selects a K range; with gridDim.y > 1 the block writes fp32
 // partial sums (hi + lo combined, unscaled) to `partial` [z][M][N].
-template <int BM, int BN, bool SPLIT, bool SPLIT_A>
+template <int BM, int BN, int WMODE, bool SPLIT_A>
 __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t* __restrict__ ah,
                                                         const uint16_t* __restrict__ al, uint32_t M, uint32_t N,
                                                         void* __restrict__ y, uint32_t y_bf16,
                                                         float* __restrict__ partial, uint32_t kt_per_split,
                                                         uint32_t tiles_m) {
+  constexpr bool SPLIT = WMODE == kWHiLo;
+  constexpr bool QBLK = WMODE == kWQBlock;
+  static_assert(!(QBLK && SPLIT_A), "block-scaled weights take f16 activations");
   constexpr int FI = BM / 64, FJ = BN / 64;
   constexpr int PA = BM * 8 / THREADS, PB = BN * 8 / THREADS;   // 16-byte pieces per thread
   constexpr int SA = BM * LDK, SB = BN * LDK;                   // halves per stage
@@ -310,6 +329,9 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
   _Float16* sB = sA + 2 * SA;
   _Float16* sAl = sB + 2 * SB;
   _Float16* sBl = sAl + (SPLIT_A ? 2 * SA : 0);
+  // Q8 block mode: scales of the tile's two 32-column blocks, [stage][row][2]
+  float* sD = reinterpret_cast<float*>(sBl + (SPLIT ? 2 * SB : 0));
+  const uint32_t nblk = p.kp / 32;
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t wm = wave >> 1, wn = wave & 1;
@@ -331,12 +353,20 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
       }
 
   u32x4 ra[PA], ral[SPLIT_A ? PA : 1], rb[PB], rbl[SPLIT ? PB : 1];
+  float rd = 0.0f;   // Q8 block mode: this thread's block scale (row tid/2, block tid%2)
+  const uint32_t drow = std::min(n0 + (tid >> 1), N - 1);
 
   if (kt0 < kt1) {
     fetch_tile<PA, SPLIT_A>(ah, al, m0, M, kp, kt0 * BK, ra, ral);
     fetch_tile<PB, SPLIT>(p.hi, p.lo, n0, N, kp, kt0 * BK, rb, rbl);
+    if constexpr (QBLK) {
+      if (tid < 2 * BN) rd = p.dsc[(size_t)drow * nblk + kt0 * 2 + (tid & 1)];
+    }
     commit_tile<PA, SPLIT_A>(sA, sAl, 0, SA, ra, ral);
     commit_tile<PB, SPLIT>(sB, sBl, 0, SB, rb, rbl);
+    if constexpr (QBLK) {
+      if (tid < 2 * BN) sD[tid] = rd;
+    }
   }
   __syncthreads();
   for (uint32_t kt = kt0; kt < kt1; ++kt) {
@@ -344,6 +374,9 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
     if (kt + 1 < kt1) {
       fetch_tile<PA, SPLIT_A>(ah, al, m0, M, kp, (kt + 1) * BK, ra, ral);
       fetch_tile<PB, SPLIT>(p.hi, p.lo, n0, N, kp, (kt + 1) * BK, rb, rbl);
+      if constexpr (QBLK) {
+        if (tid < 2 * BN) rd = p.dsc[(size_t)drow * nblk + (kt + 1) * 2 + (tid & 1)];
+      }
     }
     const _Float16* a_st = sA + st * SA;
     const _Float16* b_st = sB + st * SB;
@@ -363,20 +396,44 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
         bf[j] = *reinterpret_cast<const half8*>(b_st + br);
         if constexpr (SPLIT) bfl[j] = *reinterpret_cast<const half8*>(sBl + st * SB + br);
       }
+      if constexpr (QBLK) {
+        // one 32-column block = two 16-deep MFMAs into a fresh fragment, then
+        // acc += d[n, block] * fragment (the lane's column n is fixed)
 #pragma unroll
-      for (int i = 0; i < FI; ++i)
+        for (int i = 0; i < FI; ++i)
 #pragma unroll
-        for (int j = 0; j < FJ; ++j) {
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-          if constexpr (SPLIT)
-            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], accl[i][j], 0, 0, 0);
-          if constexpr (SPLIT_A)   // lo * lo is below 2^-22 relative and dropped
-            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], accl[i][j], 0, 0, 0);
+          for (int j = 0; j < FJ; ++j)
+            accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], (ks & 1) ? accl[i][j] : float16v{},
+                                                                0, 0, 0);
+        if (ks & 1) {
+#pragma unroll
+          for (int j = 0; j < FJ; ++j) {
+            const float d = sD[st * 2 * BN + (wn * (BN / 2) + j * 32 + (lane & 31)) * 2 + (ks >> 1)];
+#pragma unroll
+            for (int i = 0; i < FI; ++i)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(d, accl[i][j][r], acc[i][j][r]);
+          }
         }
+      } else {
+#pragma unroll
+        for (int i = 0; i < FI; ++i)
+#pragma unroll
+          for (int j = 0; j < FJ; ++j) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            if constexpr (SPLIT)
+              accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bfl[j], accl[i][j], 0, 0, 0);
+            if constexpr (SPLIT_A)   // lo * lo is below 2^-22 relative and dropped
+              accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(afl[i], bf[j], accl[i][j], 0, 0, 0);
+          }
+      }
     }
     if (kt + 1 < kt1) {
       commit_tile<PA, SPLIT_A>(sA, sAl, st ^ 1u, SA, ra, ral);
       commit_tile<PB, SPLIT>(sB, sBl, st ^ 1u, SB, rb, rbl);
+      if constexpr (QBLK) {
+        if (tid < 2 * BN) sD[(st ^ 1u) * 2 * BN + tid] = rd;
+      }
     }
     __syncthreads();
   }
@@ -396,7 +453,7 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
         const uint32_t m = m0 + wm * (BM / 2) + i * 32 + (lane >> 5) * 4 + 8 * (r >> 2) + (r & 3);
         if (m >= M) continue;
         float v = acc[i][j][r];
-        if constexpr (SPLIT || SPLIT_A) v = __builtin_fmaf(accl[i][j][r], kLoInv, v);
+        if constexpr (SPLIT || SPLIT_A) v = __builtin_fmaf(accl[i][j][r], kLoInv, v);   // not in block mode
         if (to_partial) {
           partial[((size_t)blockIdx.y * M + m) * N + n] = v;
         } else {
@@ -410,12 +467,32 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
   }
 }
 
-// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n].
+// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n]; four outputs per
+// thread when N % 4 == 0.
 __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict__ partial, uint32_t splits,
                                                          const float* __restrict__ inv, uint32_t M, uint32_t N,
                                                          void* __restrict__ y, uint32_t y_bf16) {
-  const size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x;
   const size_t total = (size_t)M * N;
+  if (N % 4u == 0u) {
+    const size_t i = ((size_t)blockIdx.x * THREADS + threadIdx.x) * 4;
+    if (i >= total) return;
+    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t z = 0; z < splits; ++z) {
+      const float4 a = *reinterpret_cast<const float4*>(partial + (size_t)z * total + i);
+      v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+    }
+    const float4 iv = *reinterpret_cast<const float4*>(inv + i % N);
+    v.x *= iv.x; v.y *= iv.y; v.z *= iv.z; v.w *= iv.w;
+    if (y_bf16) {
+      const uint32_t lo = f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
+      const uint32_t hi = f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(y) + i) = make_uint2(lo, hi);
+    } else {
+      *reinterpret_cast<float4*>(static_cast<float*>(y) + i) = v;
+    }
+    return;
+  }
+  const size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x;
   if (i >= total) return;
   float v = 0.0f;
   for (uint32_t z = 0; z < splits; ++z) v += partial[(size_t)z * total + i];
@@ -429,67 +506,84 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
 // ---- planning ------------------------------------------------------------------
 
 struct Plan {
-  int bm, bn;
+  int bm, bn, wmode;
   uint32_t kp, splits, kt_per_split;
-  size_t panel_plane, panel_bytes, a_plane, a_bytes, partial_bytes;
+  size_t panel_plane, dsc_bytes, panel_bytes, a_plane, a_bytes, partial_bytes;
 };
 
 inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16) {
   Plan pl{};
-  const bool split_w = t.kind != KIND_G64;
+  pl.wmode = t.kind == KIND_G64 ? kWPlain : (t.kind == KIND_Q8 && x_bf16 ? kWQBlock : kWHiLo);
   pl.kp = (t.cols + BK - 1) / BK * BK;
   const uint32_t ktiles = pl.kp / BK;
   pl.bm = m >= 256 ? 128 : 64;
   pl.bn = pl.bm;
   const uint32_t tiles = ((m + pl.bm - 1) / pl.bm) * ((t.rows + pl.bn - 1) / pl.bn);
-  // Split K until the grid covers the 256 CUs, keeping >= 4 K tiles per split.
+  // Split K until the grid covers the 256 CUs (>= 4 K tiles per split), and
+  // on to two blocks per CU while the K ranges stay long (>= 16 K tiles):
+  // measured, the partial sums cost less than a half-empty second round.
   uint32_t splits = 1;
   while (tiles * splits < 256 && ktiles / (splits * 2) >= 4) splits *= 2;
+  while (tiles * splits < 512 && ktiles / (splits * 2) >= 16) splits *= 2;
   pl.kt_per_split = (ktiles + splits - 1) / splits;
   pl.splits = (ktiles + pl.kt_per_split - 1) / pl.kt_per_split;
   pl.panel_plane = al256((size_t)t.rows * pl.kp * 2);
-  pl.panel_bytes = pl.panel_plane * (split_w ? 2 : 1) + al256((size_t)t.rows * 4);
+  pl.dsc_bytes = pl.wmode == kWQBlock ? al256((size_t)t.rows * (pl.kp / 32) * 4) : 0;
+  pl.panel_bytes = pl.panel_plane * (pl.wmode == kWHiLo ? 2 : 1) + pl.dsc_bytes + al256((size_t)t.rows * 4);
   pl.a_plane = al256((size_t)m * pl.kp * 2);
   pl.a_bytes = pl.a_plane * (x_bf16 ? 1 : 2);
   pl.partial_bytes = pl.splits > 1 ? al256((size_t)pl.splits * m * t.rows * 4) : 0;
   return pl;
 }
 
-template <int BM, int BN, bool SPLIT, bool SPLIT_A>
+template <int BM, int BN, int WMODE, bool SPLIT_A>
 hipError_t launch_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, uint32_t m, uint32_t n, void* y,
                         bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
   constexpr size_t lds = (size_t)(2 * BM * LDK + 2 * BN * LDK + (SPLIT_A ? 2 * BM * LDK : 0) +
-                                  (SPLIT ? 2 * BN * LDK : 0)) * 2;
+                                  (WMODE == kWHiLo ? 2 * BN * LDK : 0)) * 2 +
+                         (WMODE == kWQBlock ? 2 * 2 * BN * 4 : 0);
   static_assert(lds <= 160 * 1024, "LDS budget");
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&dense_kernel<BM, BN, SPLIT, SPLIT_A>), hipFuncAttributeMaxDynamicSharedMemorySize,
-      (int)lds);
+      reinterpret_cast<const void*>(&dense_kernel<BM, BN, WMODE, SPLIT_A>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
   const uint32_t tiles_m = (m + BM - 1) / BM;
   const dim3 grid(tiles_m * ((n + BN - 1) / BN), pl.splits);
-  hipLaunchKernelGGL((dense_kernel<BM, BN, SPLIT, SPLIT_A>), grid, dim3(THREADS), lds, s, p, ah, al, m, n, y,
+  hipLaunchKernelGGL((dense_kernel<BM, BN, WMODE, SPLIT_A>), grid, dim3(THREADS), lds, s, p, ah, al, m, n, y,
                      (uint32_t)y_bf16, partial, pl.kt_per_split, tiles_m);
   return hipGetLastError();
 }
 
-template <int BM, bool SPLIT>
+template <int BM, int WMODE>
 hipError_t launch_dense_x(const Panel& p, const uint16_t* ah, const uint16_t* al, bool x_bf16, uint32_t m,
                           uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
-  if (x_bf16) return launch_dense<BM, BM, SPLIT, false>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
-  return launch_dense<BM, BM, SPLIT, true>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+  if (x_bf16) return launch_dense<BM, BM, WMODE, false>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+  if constexpr (WMODE == kWQBlock) {
+    return hipErrorInvalidValue;   // f32 activations use the hi/lo panel
+  } else {
+    return launch_dense<BM, BM, WMODE, true>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+  }
+}
+
+template <int WMODE>
+hipError_t launch_dense_m(const Panel& p, const uint16_t* ah, const uint16_t* al, bool x_bf16, uint32_t m,
+                          uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
+  if (pl.bm == 128) return launch_dense_x<128, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, s);
+  return launch_dense_x<64, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, s);
 }
 
 template <uint32_t KIND>
 hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
                size_t ws_bytes, hipStream_t s) {
-  constexpr bool SPLIT = KIND != KIND_G64;
   const Plan pl = plan(t, m, x_bf16);
   if (ws_bytes < pl.panel_bytes + pl.a_bytes + pl.partial_bytes) return hipErrorInvalidValue;
   char* base = static_cast<char*>(ws);
+  const bool hilo = pl.wmode == kWHiLo;
   Panel p;
   p.hi = reinterpret_cast<uint16_t*>(base);
-  p.lo = reinterpret_cast<uint16_t*>(base + (SPLIT ? pl.panel_plane : 0));
-  p.inv = reinterpret_cast<float*>(base + pl.panel_plane * (SPLIT ? 2 : 1));
+  p.lo = reinterpret_cast<uint16_t*>(base + (hilo ? pl.panel_plane : 0));
+  p.dsc = reinterpret_cast<float*>(base + pl.panel_plane * (hilo ? 2 : 1));
+  p.inv = reinterpret_cast<float*>(base + pl.panel_plane * (hilo ? 2 : 1) + pl.dsc_bytes);
   p.kp = pl.kp;
   uint16_t* ah = reinterpret_cast<uint16_t*>(base + pl.panel_bytes);
   uint16_t* al = reinterpret_cast<uint16_t*>(base + pl.panel_bytes + (x_bf16 ? 0 : pl.a_plane));
@@ -506,17 +600,25 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const uint32_t pgrid = std::min<uint32_t>((t.rows + 3) / 4, 2048);
-  hipLaunchKernelGGL((panel_kernel<KIND>), dim3(pgrid), dim3(THREADS), 0, s, t, p);
+  hipLaunchKernelGGL((panel_kernel<KIND>), dim3(pgrid), dim3(THREADS), 0, s, t, p,
+                     (uint32_t)(pl.wmode == kWQBlock ? 1u : 0u));
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (pl.bm == 128)
-    e = launch_dense_x<128, SPLIT>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
-  else
-    e = launch_dense_x<64, SPLIT>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+  if constexpr (KIND == KIND_G64) {
+    e = launch_dense_m<kWPlain>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+  } else if constexpr (KIND == KIND_Q8) {
+    if (pl.wmode == kWQBlock)
+      e = launch_dense_m<kWQBlock>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+    else
+      e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+  } else {
+    e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+  }
   if (e != hipSuccess || pl.splits == 1) return e;
   const size_t total = (size_t)m * t.rows;
-  hipLaunchKernelGGL(reduce_kernel, dim3((uint32_t)((total + THREADS - 1) / THREADS)), dim3(THREADS), 0, s, partial,
-                     pl.splits, p.inv, m, t.rows, y, (uint32_t)y_bf16);
+  const size_t threads = t.rows % 4u == 0u ? total / 4 : total;
+  hipLaunchKernelGGL(reduce_kernel, dim3((uint32_t)((threads + THREADS - 1) / THREADS)), dim3(THREADS), 0, s,
+                     partial, pl.splits, p.inv, m, t.rows, y, (uint32_t)y_bf16);
   return hipGetLastError();
 }
 
