@@ -189,6 +189,31 @@ VXT_API int vxt_hip_matmul_multi_dev(void* ctx, void* const* tensors, uint32_t n
 VXT_API int vxt_hip_dequant_rows_dev(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
                              float* out, void* stream, char* err, size_t err_cap);
 
+/* Embedding rows for batch_m token ids held in device memory (tokens[m]):
+ * out[m * out_stride + c] = decode_row(tokens[m])[c] for c < cols, bit-exact,
+ * multiplied by embed_scale when |embed_scale - 1| > 1e-7 (llm_cpu.rs:
+ * 224-229), and 0 for cols <= c < out_stride.  An id >= rows reads the last
+ * row, as the device runner's gather does (vxt_cb4_embed_exact_batch,
+ * vxt_cb4_fast_ops.metal:89-113, which reads the id the greedy step left in
+ * device memory); the CPU path rejects such ids (llm_cpu.rs:219-221), so
+ * callers that need the error check ids on the host.  Any kind. */
+VXT_API int vxt_hip_embed_dev(void* ctx, void* tensor, const uint32_t* tokens, uint32_t batch_m,
+                              float embed_scale, float* out, uint32_t out_stride, void* stream, char* err,
+                              size_t err_cap);
+
+/* Greedy token selection over n f32 logits (device memory): out[0] = the
+ * lowest index holding the largest non-NaN logit, or 0 when no logit is
+ * above -inf (n == 0, all -inf, all NaN); out[1] = 1 if any logit is NaN or
+ * +-inf, else 0.  -0 and +0 are equal.  Replaces the runner's greedy step
+ * (vxt_greedy_exact, vxt_llm_ops.metal:569-600, read back at
+ * metal_llm.mm:659-663; its test probe vxt_metal_llm_greedy_probe,
+ * metal_llm_tests.rs:17-26) and agrees with the CPU sampler's greedy branch
+ * (llm_ops.rs:318-327).  One launch, no allocation, no memset: capturable.
+ * Calls of one context share a small state block, so calls on different
+ * streams must not overlap in time. */
+VXT_API int vxt_hip_greedy_dev(void* ctx, const float* logits, uint32_t n, uint32_t* out, void* stream,
+                               char* err, size_t err_cap);
+
 /* ---- device memory, stream and graphs ---------------------------------- */
 /* What a host without another GPU runtime (the Rust engine, C callers) needs
  * to keep activations resident and to replay a decode loop without per-launch

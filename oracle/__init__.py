@@ -87,6 +87,8 @@ def lib():
         L.vxo_gemv_any.argtypes = [i32, vp, vp, vp, i32]
         L.vxo_gemv_any.restype = None
         L.vxo_hardware_threads.restype = C.c_int
+        L.vxo_greedy.argtypes = [vp, sz, C.POINTER(C.c_uint32)]
+        L.vxo_greedy.restype = C.c_uint32
         _lib = L
     return _lib
 
@@ -239,4 +241,30 @@ def q8_dequant(blocks) -> np.ndarray:
     assert b.size % 34 == 0
     out = np.empty(b.size // 34 * 32, dtype=np.float32)
     lib().vxo_q8_dequant(_ptr(b), b.size // 34, _ptr(out))
+    return out
+
+
+def greedy(logits) -> tuple[int, bool]:
+    """``(id, nonfinite)`` of the greedy pick over f32 logits (vxo_greedy)."""
+    a = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+    nf = C.c_uint32(0)
+    i = lib().vxo_greedy(_ptr(a) if a.size else None, a.size, C.byref(nf))
+    return int(i), bool(nf.value)
+
+
+def embed_rows(m, tokens, embed_scale: float = 1.0) -> np.ndarray:
+    """Token embedding rows [len(tokens), cols]: ``decode_row(token)``
+    (llm_cpu.rs:223), then every value times ``embed_scale`` when
+    ``|embed_scale - 1| > 1e-7`` in f32 (llm_cpu.rs:226-229; also llm.rs:
+    565-569).  Ids must be < rows (the CPU path rejects others, llm_cpu.rs:
+    219-221)."""
+    toks = [int(t) for t in np.asarray(tokens).reshape(-1)]
+    if any(t >= m.rows for t in toks):
+        raise ValueError("token id out of vocab")
+    out = np.zeros((len(toks), m.cols), dtype=np.float32)
+    for i, t in enumerate(toks):
+        out[i] = decode_rows(m, t, 1)[0]
+    s = np.float32(embed_scale)
+    if abs(s - np.float32(1.0)) > np.float32(1e-7):
+        out = out * s
     return out

@@ -511,6 +511,24 @@ VXO_API void vxo_gemv_any(int kind, const void* m, const float* x, float* y, int
     else vxo_q8_gemv((const vxo_q8*)m, x, y, threads);
 }
 
+/* Greedy selection.  The index follows the greedy branch of
+ * sample_logits_top_k_p (llm_ops.rs:307-327): an empty input gives 0; else a
+ * forward scan from (best_v = -inf, best_i = 0) that takes index i only when
+ * logits[i] > best_v, so the first of equal maxima wins, NaN never wins and
+ * nothing above -inf leaves 0.  *nonfinite is the flag vxt_greedy_exact adds
+ * (vxt_llm_ops.metal:569-600): 1 when any logit is NaN or +-inf. */
+VXO_API uint32_t vxo_greedy(const float* logits, size_t n, uint32_t* nonfinite) {
+    uint32_t best_i = 0, nf = 0;
+    float best_v = -INFINITY;
+    for (size_t i = 0; i < n; ++i) {
+        const float v = logits[i];
+        if (!isfinite(v)) nf = 1;
+        if (v > best_v) { best_v = v; best_i = (uint32_t)i; }
+    }
+    if (nonfinite) *nonfinite = nf;
+    return best_i;
+}
+
 VXO_API int vxo_hardware_threads(void) {
     long n = sysconf(_SC_NPROCESSORS_ONLN);
     return n > 0 ? (int)n : 1;

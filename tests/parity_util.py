@@ -10,7 +10,7 @@ import numpy as np
 
 import oracle
 from vxg_amd import engine, synth
-from vxg_amd.formats import bf16_bits_to_f32, f32_to_bf16_bits
+from vxg_amd.formats import CodebookMatrix, bf16_bits_to_f32, f32_to_bf16_bits, f32_to_f16_bits
 
 THREADS = min(os.cpu_count() or 1, 16)
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
@@ -83,3 +83,43 @@ def assert_bits_equal(a, b):
 
 def gemv_ref(m, X):
     return np.stack([oracle.gemv(m, X[i], threads=THREADS) for i in range(X.shape[0])])
+
+
+# metal_llm_tests.rs:95-117: 515 logits of -3 with the edits below; the
+# answers follow from llm_ops.rs:318-327 (strict > from -inf, first index).
+GREEDY_REFERENCE_CASES = [
+    # (edits, fill, expected id, expected nonfinite)
+    ({257: 9.0, 513: 9.0}, -3.0, 257, False),
+    ({514: 0.0}, -0.0, 0, False),                 # -0 == +0: index 0 stays
+    ({}, -np.inf, 0, True),                       # nothing above -inf
+    ({7: np.nan, 514: 4.0}, -3.0, 514, True),     # NaN never wins
+    ({300: np.inf, 2: np.inf}, -3.0, 2, True),    # equal +inf: lower index
+    ({}, np.nan, 0, True),
+]
+
+
+def greedy_reference_logits(case):
+    edits, fill, _, _ = case
+    a = np.full(515, fill, dtype=np.float32)
+    for i, v in edits.items():
+        a[i] = v
+    return a
+
+
+# metal_llm_tests.rs:31-58: the closed-form cb4 matrix of the reference's
+# embedding probe; packed_fn(cols) gives each row's packed outliers.
+def closed_form(rows, cols, packed_fn):
+    padded = (cols + 127) // 128 * 128
+    groups = padded // 128
+    cent = ((np.arange(16, dtype=np.float32) - np.float32(7.5)) * np.float32(0.1234567)).astype(np.float32)
+    scales = f32_to_f16_bits(np.float32(0.125) + (np.arange(rows * groups) % 11).astype(np.float32) * np.float32(0.25))
+    rot = np.array([((0x76543210 << s) | (0x76543210 >> (32 - s))) & 0xFFFFFFFF if s else 0x76543210
+                    for s in range(0, 32, 4)], dtype=np.uint64).astype(np.uint32)
+    words = rot[np.arange(rows * groups * 16) % 8]
+    packed = np.array([x for _ in range(rows) for x in packed_fn(cols)], np.uint32)
+    row_ptr = np.arange(0, packed.size + 1, packed.size // rows if rows else 1, dtype=np.uint32)
+    return CodebookMatrix(rows, cols, padded, cent, scales, words, row_ptr, packed)
+
+
+def f16b(v):
+    return int(f32_to_f16_bits(np.array([v], np.float32))[0])

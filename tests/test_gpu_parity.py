@@ -20,8 +20,8 @@ import oracle
 from vxg_amd import engine, synth
 from vxg_amd.formats import (CodebookMatrix, bf16_bits_to_f32, f32_to_bf16_bits,
                              f32_to_f16_bits)
-from parity_util import (GOLD, THREADS, assert_bf16_close, assert_bits_equal, floor_scale,
-                         gemv_ref, make, max_rel, q8_floor, run_dev)
+from parity_util import (GOLD, THREADS, assert_bf16_close, assert_bits_equal, closed_form, f16b,
+                         floor_scale, gemv_ref, make, max_rel, q8_floor, run_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -34,23 +34,6 @@ def eng():
 
 
 # ---------------------------------------------------------------- dequant
-
-def closed_form(rows, cols, packed_fn):
-    padded = (cols + 127) // 128 * 128
-    groups = padded // 128
-    cent = ((np.arange(16, dtype=np.float32) - np.float32(7.5)) * np.float32(0.1234567)).astype(np.float32)
-    scales = f32_to_f16_bits(np.float32(0.125) + (np.arange(rows * groups) % 11).astype(np.float32) * np.float32(0.25))
-    rot = np.array([((0x76543210 << s) | (0x76543210 >> (32 - s))) & 0xFFFFFFFF if s else 0x76543210
-                    for s in range(0, 32, 4)], dtype=np.uint64).astype(np.uint32)
-    words = rot[np.arange(rows * groups * 16) % 8]
-    packed = np.array([x for _ in range(rows) for x in packed_fn(cols)], np.uint32)
-    row_ptr = np.arange(0, packed.size + 1, packed.size // rows if rows else 1, dtype=np.uint32)
-    return CodebookMatrix(rows, cols, padded, cent, scales, words, row_ptr, packed)
-
-
-def f16b(v):
-    return int(f32_to_f16_bits(np.array([v], np.float32))[0])
-
 
 @pytest.mark.parametrize("cols", [1, 129, 257, 385])
 def test_dequant_closed_form_fixture(eng, cols):

@@ -31,6 +31,14 @@ gemm (llm_prefill.rs:156)   vs per-token GEMV, cosine > 0.999999 at rows=96,
                             cols=256, M=11 (vxt_roadmap_steps.rs:210-230); fp64
                             bound; 1- vs 4-worker bit identity; equals the dense
                             FMA chain of decoded rows
+embed_rows (llm_cpu.rs:223)  decode_rows at scale 1 and at 1 - 2^-24 (under the
+                            1e-7 threshold); an exact doubling at scale 2; the
+                            f64 product rounded once to f32 at sqrt(2048)
+greedy (llm_ops.rs:318,     the six tie / NaN / inf cases of metal_llm_tests.rs:
+vxt_llm_ops.metal:569)      95-117 with hand-derived answers; every array of
+                            length <= 4 over {-inf,-1,-0,+0,denormal,1,inf,NaN}
+                            and random arrays vs a numpy set formula (first index
+                            of numpy.nanmax, 0 when that is -inf or all NaN)
 ==========================  ====================================================
 
 The macOS ``cblas_sgemm`` branch of dense_tile_gemm (llm_prefill.rs:117-138)
@@ -43,6 +51,7 @@ import numpy as np
 import pytest
 
 import oracle
+from parity_util import GREEDY_REFERENCE_CASES, greedy_reference_logits
 from vxg_amd import synth
 from vxg_amd.formats import CodebookMatrix, Cb4G64Matrix, f32_to_f16_bits
 
@@ -395,3 +404,67 @@ def test_gemm_worker_invariance_and_dense_chain():
     Xi = np.random.default_rng(2).integers(-5, 6, size=(3, cols)).astype(np.float32)
     got = oracle.gemm(q, Xi, threads=2)
     assert np.array_equal(got, (Xi.astype(np.int64) @ qs.T.astype(np.int64)).astype(np.float32))
+
+
+# ---------------------------------------------------------------- greedy
+
+def greedy_by_sets(a):
+    """First index of numpy's nanmax; 0 when nothing is above -inf."""
+    a = np.asarray(a, dtype=np.float32)
+    ok = ~np.isnan(a)
+    nf = bool((~np.isfinite(a)).any())
+    if not ok.any():
+        return 0, nf
+    m = a[ok].max()
+    if m == -np.inf:
+        return 0, nf
+    return int(np.flatnonzero(a == m)[0]), nf
+
+
+@pytest.mark.parametrize("case", range(len(GREEDY_REFERENCE_CASES)))
+def test_greedy_reference_cases(case):
+    c = GREEDY_REFERENCE_CASES[case]
+    assert oracle.greedy(greedy_reference_logits(c)) == (c[2], c[3])
+
+
+def test_greedy_exhaustive_small_alphabet():
+    import itertools
+    alphabet = np.array([-np.inf, -1.0, -0.0, 0.0, 1e-45, 1.0, np.inf, np.nan], dtype=np.float32)
+    assert oracle.greedy([]) == (0, False)
+    for n in range(1, 5):
+        for combo in itertools.product(range(len(alphabet)), repeat=n):
+            a = alphabet[list(combo)]
+            assert oracle.greedy(a) == greedy_by_sets(a), a
+
+
+def test_greedy_random_vs_sets():
+    g = np.random.default_rng(11)
+    for trial in range(200):
+        n = int(g.integers(1, 3000))
+        a = g.standard_normal(n).astype(np.float32)
+        if trial % 3 == 0:      # many exact ties
+            a = np.round(a * 2).astype(np.float32)
+        if trial % 5 == 0:
+            a[g.integers(0, n, 3)] = np.nan
+        if trial % 7 == 0:
+            a[g.integers(0, n, 2)] = np.inf
+        assert oracle.greedy(a) == greedy_by_sets(a)
+
+
+# ---------------------------------------------------------------- embedding rows
+
+def test_embed_rows_scale_rule():
+    m = synth.make_cb4(40, 300, seed=3, outlier_frac=0.02)
+    toks = [0, 39, 7, 7]
+    base = oracle.decode_rows(m)[toks]
+    assert np.array_equal(oracle.embed_rows(m, toks).view(np.uint32), base.view(np.uint32))
+    below = np.float32(1.0) - np.float32(2.0 ** -24)           # |s - 1| < 1e-7: unscaled
+    assert np.array_equal(oracle.embed_rows(m, toks, below).view(np.uint32), base.view(np.uint32))
+    assert np.array_equal(oracle.embed_rows(m, toks, 2.0), base * 2)
+    s = np.float32(np.sqrt(2048.0))
+    want = (base.astype(np.float64) * np.float64(s)).astype(np.float32)   # one rounding (48-bit product)
+    assert np.array_equal(oracle.embed_rows(m, toks, s).view(np.uint32), want.view(np.uint32))
+    above = np.float32(1.0) + np.float32(2.0 ** -23)           # |s - 1| > 1e-7: scaled
+    assert not np.array_equal(oracle.embed_rows(m, toks, above), base)
+    with pytest.raises(ValueError):
+        oracle.embed_rows(m, [40])

@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -29,6 +30,10 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
                        size_t ws_bytes, hipStream_t s);
 hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
                           hipStream_t s);
+hipError_t launch_embed(const DevTensor& t, const uint32_t* tokens, uint32_t batch_m, float scale, bool scale_on,
+                        float* out, uint32_t stride, hipStream_t s);
+size_t greedy_state_bytes();
+hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
 struct ChainLaunch {
   const void* ops;
   uint32_t n_ops;
@@ -90,6 +95,7 @@ struct Ctx {
   size_t d_y_cap = 0;
   void* ws = nullptr;      // GEMM workspace: weight panel + split-K partial sums
   size_t ws_cap = 0;
+  void* greedy = nullptr;  // greedy-selection state words (zero between calls)
   std::mutex mu;
   std::set<Tensor*> tensors;
   std::set<void*> buffers;
@@ -307,7 +313,10 @@ void* vxt_hip_create(int32_t device, char* dev_name, size_t dev_name_cap, char* 
       VXT_HIP_CHECK(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking));
       VXT_HIP_CHECK(hipEventCreate(&c->ev0));
       VXT_HIP_CHECK(hipEventCreate(&c->ev1));
+      VXT_HIP_CHECK(hipMalloc(&c->greedy, vxt::greedy_state_bytes()));
+      VXT_HIP_CHECK(hipMemset(c->greedy, 0, vxt::greedy_state_bytes()));
     } catch (...) {
+      if (c->greedy) (void)hipFree(c->greedy);
       if (c->ev1) (void)hipEventDestroy(c->ev1);
       if (c->ev0) (void)hipEventDestroy(c->ev0);
       if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -340,6 +349,7 @@ void vxt_hip_destroy(void* ctx) {
   if (c->d_x) (void)hipFree(c->d_x);
   if (c->d_y) (void)hipFree(c->d_y);
   if (c->ws) (void)hipFree(c->ws);
+  if (c->greedy) (void)hipFree(c->greedy);
   (void)hipEventDestroy(c->ev0);
   (void)hipEventDestroy(c->ev1);
   (void)hipStreamDestroy(c->stream);
@@ -667,6 +677,39 @@ int vxt_hip_dequant_rows(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
     if (rc != VXT_OK) fail(rc, e2);
     VXT_HIP_CHECK(hipMemcpyAsync(out, c->d_y, ob, hipMemcpyDeviceToHost, c->stream));
     VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int vxt_hip_embed_dev(void* ctx, void* tensor, const uint32_t* tokens, uint32_t batch_m, float embed_scale,
+                      float* out, uint32_t out_stride, void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+    if (batch_m == 0) return;
+    if (!tokens || !out) fail(VXT_E_ARG, "null tokens or output");
+    if (out_stride < t->cols) fail(VXT_E_SHAPE, "out_stride < cols");
+    if (batch_m > 65535) fail(VXT_E_SHAPE, "batch_m > 65535");
+    if (!std::isfinite(embed_scale)) fail(VXT_E_ARG, "embed_scale is not finite");
+    // llm_cpu.rs:226: the scale applies when it differs from 1 by more than 1e-7.
+    const bool scale_on = std::fabs(embed_scale - 1.0f) > 1e-7f;
+    hipError_t e = vxt::launch_embed(t->dev(), tokens, batch_m, embed_scale, scale_on, out, out_stride,
+                                     static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("embed launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+int vxt_hip_greedy_dev(void* ctx, const float* logits, uint32_t n, uint32_t* out, void* stream, char* err,
+                       size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!out) fail(VXT_E_ARG, "null output");
+    if (!logits && n) fail(VXT_E_ARG, "null logits");
+    if ((reinterpret_cast<uintptr_t>(logits) & 3u) != 0) fail(VXT_E_ARG, "logits must be 4-byte aligned");
+    if ((reinterpret_cast<uintptr_t>(out) & 3u) != 0) fail(VXT_E_ARG, "out must be 4-byte aligned");
+    if (n > 0x7fffffffu) fail(VXT_E_SHAPE, "more than 2^31 - 1 logits");
+    hipError_t e = vxt::launch_greedy(logits, n, c->greedy, out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("greedy launch failed: ") + hipGetErrorString(e));
   });
 }
 

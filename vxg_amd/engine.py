@@ -53,7 +53,8 @@ ABI_SYMBOLS = (
     "vxt_hip_upload_cb4_g64",
     "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
-    "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev",
+    "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
+    "vxt_hip_embed_dev",
     "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
@@ -145,6 +146,10 @@ def load_library(path: str = LIB_PATH):
                                            u32, vp, cp, sz]
     L.vxt_hip_dequant_rows_dev.restype = C.c_int
     L.vxt_hip_dequant_rows_dev.argtypes = [vp, vp, u32, u32, vp, vp, cp, sz]
+    L.vxt_hip_greedy_dev.restype = C.c_int
+    L.vxt_hip_embed_dev.argtypes = [vp, vp, vp, u32, C.c_float, vp, u32, vp, cp, sz]
+    L.vxt_hip_embed_dev.restype = C.c_int
+    L.vxt_hip_greedy_dev.argtypes = [vp, vp, u32, vp, vp, cp, sz]
     L.vxt_hip_last_kernel_ms.restype = C.c_int
     L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
     L.vxt_hip_device_alloc.restype = vp
@@ -464,6 +469,22 @@ class HipEngine:
                                                    out.ctypes.data, buf, len(buf)), buf)
         return out
 
+    def greedy(self, logits) -> tuple[int, bool]:
+        """Greedy token over host f32 logits: ``(id, nonfinite)`` (see
+        :meth:`greedy_dev`).  Copies the logits to the device and back."""
+        logits = np.ascontiguousarray(logits, dtype=np.float32).reshape(-1)
+        src = self.to_device(logits) if logits.size else None
+        out = self.alloc(8)
+        try:
+            self.greedy_dev(src.ptr if src else 0, logits.size, out.ptr, self.stream)
+            self.synchronize()
+            r = out.download(np.uint32, (2,))
+        finally:
+            out.free()
+            if src:
+                src.free()
+        return int(r[0]), bool(r[1])
+
     def last_kernel_ms(self) -> float:
         ms = C.c_double()
         load_library().vxt_hip_last_kernel_ms(self.ctx, C.byref(ms))
@@ -531,6 +552,28 @@ class HipEngine:
         _check(load_library().vxt_hip_matmul_multi_dev(self.ctx, ta, len(ts), x_ptr, x_dtype,
                                                        batch_m, ya, y_dtype, stream or None, buf,
                                                        len(buf)), buf)
+
+    def greedy_dev(self, logits_ptr: int, n: int, out_ptr: int, stream: int = 0) -> None:
+        """``out[0]`` = the lowest index of the largest non-NaN logit (0 when
+        none is above -inf), ``out[1]`` = 1 if any logit is NaN or +-inf: the
+        runner's greedy step (``vxt_greedy_exact``, vxt_llm_ops.metal:569-600)
+        and the CPU sampler's greedy branch (llm_ops.rs:318-327).  One launch,
+        no allocation; capturable."""
+        buf = _errbuf()
+        _check(load_library().vxt_hip_greedy_dev(self.ctx, logits_ptr or None, n, out_ptr or None,
+                                                 stream or None, buf, len(buf)), buf)
+
+    def embed_dev(self, t: GpuPackedTensor, tokens_ptr: int, batch_m: int, out_ptr: int,
+                  out_stride: int | None = None, embed_scale: float = 1.0, stream: int = 0) -> None:
+        """f32 embedding rows of ``batch_m`` device-resident token ids
+        (``vxt_hip_embed_dev``): bit-exact ``decode_row``, scaled as
+        llm_cpu.rs:224-229, zero-padded to ``out_stride``; ids past the last
+        row read the last row."""
+        buf = _errbuf()
+        stride = t.cols if out_stride is None else out_stride
+        _check(load_library().vxt_hip_embed_dev(self.ctx, t.handle, tokens_ptr or None, batch_m,
+                                                embed_scale, out_ptr or None, stride, stream or None,
+                                                buf, len(buf)), buf)
 
     def dequant_rows_dev(self, t: GpuPackedTensor, row0: int, nrows: int, out_ptr: int,
                          stream: int = 0) -> None:
