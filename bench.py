@@ -152,18 +152,12 @@ def bench_gemm(eng, m, M: int, steps: int, warmup: int, seed: int = 0):
             "bytes_per_call": call_bytes(m, M, 2, 2)}
 
 
-def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
-                ffn: int = 6144, seed: int = 40, persistent: bool = False):
-    """Config 4: tokens/s of the decode-step linear stack (matmul-only path).
-
-    Per layer [q;k;v] (3 x hidden rows), o, [gate;up] (2 x ffn rows), down,
-    then the Q8 LM head; every layer's weights are drawn separately.  One
-    token is captured as a HIP graph (or, ``persistent``, recorded as one
-    persistent launch); ``tokens`` replays are timed.
-    """
+def _stack_layers(eng, kind: str, layers: int, hidden: int, ffn: int, seed: int):
+    """Per layer [q;k;v] (3 x hidden rows), o, [gate;up] (2 x ffn rows), down;
+    every layer's weights drawn separately.  Returns (layers, weight bytes)."""
     from vxg_amd import stack, synth
     gen = {"g64": synth.make_g64, "cb4": synth.make_cb4}[kind]
-    lw, nbytes = [], weight_bytes(head_m)
+    lw, nbytes = [], 0
     for li in range(layers):
         s = seed + 10 * li
         qkv = [gen(hidden, hidden, seed=s + i) for i in range(3)]
@@ -173,6 +167,26 @@ def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: i
         nbytes += sum(weight_bytes(m) for m in qkv + [o] + gu + [dn])
         lw.append(stack.LayerWeights(eng.upload_concat(qkv), eng.upload_packed(o),
                                      eng.upload_concat(gu), eng.upload_packed(dn)))
+    return lw, nbytes
+
+
+def _free_layers(lw):
+    for L in lw:
+        for t in (L.qkv, L.o, L.gate_up, L.down):
+            t.free()
+
+
+def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
+                ffn: int = 6144, seed: int = 40, persistent: bool = False):
+    """Config 4: tokens/s of the decode-step linear stack (matmul-only path).
+
+    The layers of ``_stack_layers`` then the Q8 LM head.  One token is
+    captured as a HIP graph (or, ``persistent``, recorded as one persistent
+    launch); ``tokens`` replays are timed.
+    """
+    from vxg_amd import stack, synth
+    lw, nbytes = _stack_layers(eng, kind, layers, hidden, ffn, seed)
+    nbytes += weight_bytes(head_m)
     head = eng.upload_packed(head_m)
     st = stack.DecodeStack(eng, lw, head)
     st.set_input(synth.make_x_bf16(1, hidden, seed=4)[0])
@@ -190,14 +204,51 @@ def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: i
     wall = time.perf_counter() - t0
     runner.free()
     st.free()
-    for L in lw:
-        for t in (L.qkv, L.o, L.gate_up, L.down):
-            t.free()
+    _free_layers(lw)
     head.free()
     ms_tok = ev_ms / tokens
     return {"tokens_per_s": tokens / (ev_ms * 1e-3), "wall_tokens_per_s": tokens / wall,
             "ms_per_token": ms_tok, "bytes_per_token": nbytes, "launches_per_token": st.launches,
             "GBps": nbytes / (ms_tok * 1e-3) / 1e9}
+
+
+def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
+               ffn: int = 6144, seed: int = 40):
+    """The whole decode step (``stack.DecodeStep``) on config 4's weights:
+    embedding gather (tied Q8 head), per layer RMSNorm, [q;k;v], o,
+    add + RMSNorm, fused [gate;up] + SwiGLU, down; final norm, LM head,
+    greedy.  Attention stands in as a slice, as in the matmul-only stack.
+    Captured once; each replay is one token, the id fed back on the device."""
+    import numpy as np
+    from vxg_amd import stack
+    lw, nbytes = _stack_layers(eng, kind, layers, hidden, ffn, seed)
+    nbytes += weight_bytes(head_m)
+    head = eng.upload_packed(head_m)
+    rng = np.random.default_rng(seed)
+    bufs = [eng.to_device((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+            for _ in range(2 * layers + 1)]
+    norms = [stack.LayerNorms(bufs[2 * i], bufs[2 * i + 1]) for i in range(layers)]
+    st = stack.DecodeStep(eng, lw, norms, bufs[-1], head, head)
+    st.set_token(1)
+    for _ in range(3):
+        st.enqueue()
+    eng.synchronize()
+    g = st.capture()
+    g.launch(3)
+    t0 = time.perf_counter()
+    ev_ms = g.launch(tokens)
+    wall = time.perf_counter() - t0
+    tok, bad = st.read_token()
+    g.free()
+    launches = st.launches
+    st.free()
+    for b in bufs:
+        b.free()
+    _free_layers(lw)
+    head.free()
+    ms_tok = ev_ms / tokens
+    return {"tokens_per_s": tokens / (ev_ms * 1e-3), "wall_tokens_per_s": tokens / wall,
+            "ms_per_token": ms_tok, "launches_per_token": launches, "last_token": tok, "nonfinite": bad}
 
 
 # --------------------------------------------------------------------------
@@ -311,6 +362,17 @@ def main():
                               "frac_hbm": round(rs["GBps"] / HBM_PEAK_GBS, 4)})
             log(f"  {rs['tokens_per_s']:.1f} tok/s ({rs['GBps']:.1f} GB/s, "
                 f"{rs['ms_per_token']*1e3:.1f} us/token)")
+        for kind in ("cb4",):
+            log(f"config 4 (whole step): 24 layers {kind} + norms, fused SwiGLU, Q8 head, greedy, embedding")
+            rw = bench_step(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)))
+            secondary.append({"config": f"4 (whole decode step): embed + 24x{{norm,[q;k;v],o,add+norm,"
+                                        f"[gate;up]+swiglu,down}} {kind} + norm + q8 head + greedy, M=1, "
+                                        f"HIP graph of {rw['launches_per_token']} launches per token",
+                              "tokens_per_s": round(rw["tokens_per_s"], 1),
+                              "ms_per_token": round(rw["ms_per_token"], 4),
+                              "launches_per_token": rw["launches_per_token"]})
+            log(f"  {rw['tokens_per_s']:.1f} tok/s ({rw['ms_per_token']*1e3:.1f} us/token, "
+                f"{rw['launches_per_token']} launches)")
         del head_m
 
     cpu = None

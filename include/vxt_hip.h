@@ -50,6 +50,10 @@ extern "C" {
 #define VXT_DTYPE_F32 0u
 #define VXT_DTYPE_BF16 1u
 
+/* FFN activations (llm_cpu.rs:457-464) */
+#define VXT_ACT_SILU 0u       /* silu(g) * u, llm_ops.rs:39-41                  */
+#define VXT_ACT_GELU_TANH 1u  /* gelu_tanh_f32(g) * u, llm_prefill.rs:66-71     */
+
 /* ---- tensor kinds (kind 2 = codebook, as VxtMetalOp.kind in
  *      native/metal_internal.h:14) ---------------------------------------- */
 #define VXT_KIND_CB4 2u     /* CodebookMatrix, bits = 4 (codebook.rs:9-24)   */
@@ -188,6 +192,32 @@ VXT_API int vxt_hip_matmul_multi_dev(void* ctx, void* const* tensors, uint32_t n
 /* Device-side bit-exact dequant of rows [row0, row0+nrows) into out (f32). */
 VXT_API int vxt_hip_dequant_rows_dev(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
                              float* out, void* stream, char* err, size_t err_cap);
+
+/* Gated FFN projection: tensor is the row-concatenated [gate; up] matrix
+ * (rows = 2 * n_ff, e.g. from vxt_hip_upload_cb4_concat); act[m * act_stride
+ * + i] = act(g_i) * u_i for i < n_ff with g = gate . x, u = up . x (fp32
+ * sums), and 0 for n_ff <= i < act_stride.  activation is VXT_ACT_SILU or
+ * VXT_ACT_GELU_TANH.  Replaces the runner's fused gate/up + SwiGLU GEMV
+ * (vxt_cb4_ffn_gu_nr2_m1, vxt_cb4_fast.metal:212-287) and, for batches, its
+ * GEMM + vxt_cb4_swiglu_batch (vxt_cb4_fast_ops.metal:236-262); the CPU
+ * step is forward_multi + the activation loop (llm_cpu.rs:448-464).
+ * batch_m 1..2 is one fused launch; larger batches stage g and u (f32) in
+ * the context workspace, with the workspace rules of vxt_hip_matmul_dev. */
+VXT_API int vxt_hip_ffn_glu_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype, uint32_t batch_m,
+                                void* act, uint32_t act_dtype, uint32_t act_stride, uint32_t activation,
+                                void* stream, char* err, size_t err_cap);
+
+/* Residual add + RMSNorm over batch_m rows of `stride` floats:
+ *   if delta: cur[i] += delta[i] (written back);
+ *   out[i] = cur[i] * scale * weight[i], scale = 1 / sqrt(sum cur^2 / dim + eps)
+ *   for i < dim, 0 for dim <= i < stride (out_dtype f32 or bf16).
+ * rms_norm of llm_ops.rs:48-57 after the residual add of llm_cpu.rs:443-446;
+ * the runner's vxt_cb4_add_rms_norm_batch / vxt_cb4_rms_norm_batch
+ * (vxt_cb4_fast_ops.metal:160-234).  out may alias cur (f32 only), not delta.
+ * Device pointers; no tensor involved. */
+VXT_API int vxt_hip_rms_norm_dev(void* ctx, float* cur, const float* delta, const float* weight, void* out,
+                                 uint32_t out_dtype, uint32_t dim, uint32_t stride, uint32_t batch_m, float eps,
+                                 void* stream, char* err, size_t err_cap);
 
 /* Embedding rows for batch_m token ids held in device memory (tokens[m]):
  * out[m * out_stride + c] = decode_row(tokens[m])[c] for c < cols, bit-exact,

@@ -87,6 +87,14 @@ def lib():
         L.vxo_gemv_any.argtypes = [i32, vp, vp, vp, i32]
         L.vxo_gemv_any.restype = None
         L.vxo_hardware_threads.restype = C.c_int
+        L.vxo_silu.argtypes = [C.c_float]
+        L.vxo_silu.restype = C.c_float
+        L.vxo_gelu_tanh.argtypes = [C.c_float]
+        L.vxo_gelu_tanh.restype = C.c_float
+        L.vxo_glu.argtypes = [vp, vp, sz, i32, vp]
+        L.vxo_glu.restype = None
+        L.vxo_rms_norm.argtypes = [vp, vp, sz, C.c_float, vp]
+        L.vxo_rms_norm.restype = None
         L.vxo_greedy.argtypes = [vp, sz, C.POINTER(C.c_uint32)]
         L.vxo_greedy.restype = C.c_uint32
         _lib = L
@@ -267,4 +275,35 @@ def embed_rows(m, tokens, embed_scale: float = 1.0) -> np.ndarray:
     s = np.float32(embed_scale)
     if abs(s - np.float32(1.0)) > np.float32(1e-7):
         out = out * s
+    return out
+
+
+def glu(g, u, gelu: bool = False) -> np.ndarray:
+    """``act(g) * u`` element-wise (vxo_glu; llm_cpu.rs:457-464)."""
+    g = np.ascontiguousarray(g, dtype=np.float32).reshape(-1)
+    u = np.ascontiguousarray(u, dtype=np.float32).reshape(-1)
+    assert g.size == u.size
+    out = np.empty_like(g)
+    if g.size:
+        lib().vxo_glu(_ptr(g), _ptr(u), g.size, int(gelu), _ptr(out))
+    return out
+
+
+def silu(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    return np.array([lib().vxo_silu(float(v)) for v in a], dtype=np.float32)
+
+
+def gelu_tanh(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    return np.array([lib().vxo_gelu_tanh(float(v)) for v in a], dtype=np.float32)
+
+
+def rms_norm(x, w, eps: float) -> np.ndarray:
+    """``rms_norm`` of llm_ops.rs:48-57 over one row (vxo_rms_norm)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    assert w.size >= x.size
+    out = np.empty_like(x)
+    lib().vxo_rms_norm(_ptr(x), _ptr(w), x.size, float(eps), _ptr(out))
     return out

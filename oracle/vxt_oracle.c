@@ -511,6 +511,32 @@ VXO_API void vxo_gemv_any(int kind, const void* m, const float* x, float* y, int
     else vxo_q8_gemv((const vxo_q8*)m, x, y, threads);
 }
 
+/* llm_ops.rs:39-41: silu(x) = x / (1 + exp(-x)) in f32 (Rust's f32::exp is
+ * the platform libm expf on Linux, which this calls). */
+VXO_API float vxo_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* llm_prefill.rs:66-71, each operation rounded in source order. */
+VXO_API float vxo_gelu_tanh(float g) {
+    const float z = 0.7978846f * (g + 0.044715f * g * g * g);
+    const float e2 = expf(-2.0f * fabsf(z));
+    const float th = copysignf((1.0f - e2) / (1.0f + e2), z);
+    return 0.5f * g * (1.0f + th);
+}
+
+/* llm_cpu.rs:457-464: out[i] = act(g[i]) * u[i]. */
+VXO_API void vxo_glu(const float* g, const float* u, size_t n, int gelu, float* out) {
+    for (size_t i = 0; i < n; ++i) out[i] = (gelu ? vxo_gelu_tanh(g[i]) : vxo_silu(g[i])) * u[i];
+}
+
+/* llm_ops.rs:48-57: sq = sequential f32 fma chain; scale = 1 / sqrt(sq / n +
+ * eps); out[i] = x[i] * scale * w[i] (two roundings, left to right). */
+VXO_API void vxo_rms_norm(const float* x, const float* w, size_t n, float eps, float* out) {
+    float sq = 0.0f;
+    for (size_t i = 0; i < n; ++i) sq = fmaf(x[i], x[i], sq);
+    const float scale = 1.0f / sqrtf(sq / (float)n + eps);
+    for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
+}
+
 /* Greedy selection.  The index follows the greedy branch of
  * sample_logits_top_k_p (llm_ops.rs:307-327): an empty input gives 0; else a
  * forward scan from (best_v = -inf, best_i = 0) that takes index i only when

@@ -174,6 +174,99 @@ def test_stack_shape_checks(eng):
         stack.DecodeStack(eng, [], a)
 
 
+# ---------------------------------------------------------------- whole decode step
+
+def small_step(eng, kind, n_layers, seed=0, activation=engine.ACT_SILU, hidden=256, ffn=384):
+    st, host, head = small_stack(eng, kind, n_layers, hidden=hidden, ffn=ffn, seed=seed)
+    rng = np.random.default_rng(seed + 5)
+    norm_w = [(1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32) for _ in range(2 * n_layers + 1)]
+    bufs = [eng.to_device(w) for w in norm_w]
+    norms = [stack.LayerNorms(bufs[2 * i], bufs[2 * i + 1]) for i in range(n_layers)]
+    step = stack.DecodeStep(eng, st.layers, norms, bufs[-1], st.lm_head, st.lm_head, eps=1e-6,
+                            activation=activation)
+    return step, st, host, head, norm_w, bufs
+
+
+def emulate_step(host, head, norm_w, token, gelu, eps=1e-6):
+    """The same step on the CPU from oracle pieces, bf16 where the GPU keeps bf16."""
+    from vxg_amd.formats import f32_to_bf16_bits
+    r16 = lambda v: bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(v, np.float32)))
+    cur = oracle.embed_rows(head, [token])[0]
+    delta = None
+    for i, (qkv, o, gu, dn) in enumerate(host):
+        if delta is not None:
+            cur = cur + delta
+        x = r16(oracle.rms_norm(cur, norm_w[2 * i], eps))
+        q = r16(np.concatenate([oracle.gemv(p, x, threads=THREADS) for p in qkv]))
+        a = oracle.gemv(o, q[: o.cols], threads=THREADS)
+        cur = cur + a
+        x = r16(oracle.rms_norm(cur, norm_w[2 * i + 1], eps))
+        act = r16(oracle.glu(oracle.gemv(gu[0], x, threads=THREADS), oracle.gemv(gu[1], x, threads=THREADS),
+                             gelu))
+        delta = oracle.gemv(dn, act, threads=THREADS)
+    cur = cur + delta
+    x = r16(oracle.rms_norm(cur, norm_w[-1], eps))
+    return oracle.gemv(head, x, threads=THREADS)
+
+
+@pytest.mark.parametrize("activation", [engine.ACT_SILU, engine.ACT_GELU_TANH])
+def test_decode_step_matches_cpu_emulation(eng, activation):
+    step, st, host, head, norm_w, bufs = small_step(eng, "cb4", 2, seed=3, activation=activation)
+    step.set_token(123)
+    step.enqueue()
+    eng.synchronize()
+    logits = step.logits.download(np.float32, head.rows)
+    tok, nonfinite = step.read_token()
+    assert (tok, nonfinite) == oracle.greedy(logits)
+    want = emulate_step(host, head, norm_w, 123, activation == engine.ACT_GELU_TANH)
+    # bf16 roundings at the projection inputs may land on different sides of
+    # a tie between the two computations; the drift stays small.
+    assert np.abs(logits - want).max() <= 2e-2 * np.abs(want).max()
+    cos = float(np.dot(logits, want) / np.linalg.norm(logits) / np.linalg.norm(want))
+    assert cos > 0.9999
+    assert step.launches == 16
+    step.free()
+    st.free()
+    for b in bufs:
+        b.free()
+
+
+def test_decode_step_graph_advances_tokens_like_eager(eng):
+    step, st, host, head, norm_w, bufs = small_step(eng, "g64", 3, seed=11)
+    step.set_token(7)
+    eager = []
+    for _ in range(4):
+        step.enqueue()
+        eng.synchronize()
+        eager.append((step.read_token(), step.logits.download(np.float32, head.rows)))
+    step.set_token(7)
+    g = step.capture()
+    try:
+        for i in range(4):
+            g.launch(1)
+            assert step.read_token() == eager[i][0], i
+            assert np.array_equal(step.logits.download(np.float32, head.rows), eager[i][1]), i
+    finally:
+        g.free()
+    step.free()
+    st.free()
+    for b in bufs:
+        b.free()
+
+
+def test_decode_step_shape_checks(eng):
+    st, host, head = small_stack(eng, "g64", 1)
+    w = eng.to_device(np.ones(256, np.float32))
+    with pytest.raises(ValueError):
+        stack.DecodeStep(eng, st.layers, [], w, st.lm_head, st.lm_head)
+    other = eng.upload_packed(synth.make_q8(10, 128, seed=1))
+    with pytest.raises(ValueError):
+        stack.DecodeStep(eng, st.layers, [stack.LayerNorms(w, w)], w, st.lm_head, other)
+    other.free()
+    w.free()
+    st.free()
+
+
 # ---------------------------------------------------------------- persistent chain
 
 @pytest.mark.parametrize("kind", ["cb4", "g64"])

@@ -34,6 +34,11 @@ gemm (llm_prefill.rs:156)   vs per-token GEMV, cosine > 0.999999 at rows=96,
 embed_rows (llm_cpu.rs:223)  decode_rows at scale 1 and at 1 - 2^-24 (under the
                             1e-7 threshold); an exact doubling at scale 2; the
                             f64 product rounded once to f32 at sqrt(2048)
+silu / gelu_tanh / glu     f64 formulas (tanh from numpy) within 4 ulp over
+(llm_ops.rs:39,             [-90, 90]; the limits silu(+-large), gelu(+-large);
+llm_prefill.rs:66)          signs; act(g) * u equals the product of the parts
+rms_norm (llm_ops.rs:48)    f64 computation within 1e-6; constant rows (closed
+                            form c / sqrt(c^2 + eps)); zero row; weight scaling
 greedy (llm_ops.rs:318,     the six tie / NaN / inf cases of metal_llm_tests.rs:
 vxt_llm_ops.metal:569)      95-117 with hand-derived answers; every array of
                             length <= 4 over {-inf,-1,-0,+0,denormal,1,inf,NaN}
@@ -468,3 +473,59 @@ def test_embed_rows_scale_rule():
     assert not np.array_equal(oracle.embed_rows(m, toks, above), base)
     with pytest.raises(ValueError):
         oracle.embed_rows(m, [40])
+
+
+# ---------------------------------------------------------------- activations, rms_norm
+
+def ulp_dist(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    a = np.where(a < 0, np.int64(-2**31) - a, a)
+    b = np.where(b < 0, np.int64(-2**31) - b, b)
+    return np.abs(a - b)
+
+
+def test_silu_and_gelu_vs_f64():
+    x = np.concatenate([np.linspace(-90, 90, 20001), np.linspace(-1e-3, 1e-3, 2001)]).astype(np.float32)
+    x = x[x != 0]
+    xd = x.astype(np.float64)
+    silu64 = (xd / (1.0 + np.exp(-xd))).astype(np.float32)
+    fin = x > -88.0                        # exp(-x) finite in f32
+    assert ulp_dist(oracle.silu(x[fin]), silu64[fin]).max() <= 4
+    assert np.all(oracle.silu(x[x < -88.8]) == 0)   # f32 exp overflows: x / inf = -0
+    # 1 + th cancels for large negative g (th rounds to -1 in f32): an absolute
+    # error of 0.5 |g| ulp(1) on top of a relative 1e-6.
+    g = oracle.gelu_tanh(x)
+    ref = 0.5 * xd * (1.0 + np.tanh(0.7978846 * (xd + 0.044715 * xd ** 3)))
+    assert np.all(np.abs(g - ref) <= 1e-6 * np.abs(ref) + 0.5 * np.abs(xd) * 2.0 ** -23)
+    assert oracle.silu([0.0])[0] == 0 and oracle.gelu_tanh([0.0])[0] == 0
+    assert oracle.silu([100.0])[0] == np.float32(100.0)
+    assert oracle.silu([-200.0])[0] == 0 and np.signbit(oracle.silu([-200.0])[0])
+    assert oracle.gelu_tanh([50.0])[0] == np.float32(50.0)
+    assert np.all(oracle.silu(x[x < 0]) <= 0) and np.all(oracle.silu(x[x > 0]) > 0)
+
+
+def test_glu_is_activation_times_up():
+    g = np.random.default_rng(0).standard_normal(5000).astype(np.float32) * 4
+    u = np.random.default_rng(1).standard_normal(5000).astype(np.float32)
+    assert np.array_equal(oracle.glu(g, u), oracle.silu(g) * u)
+    assert np.array_equal(oracle.glu(g, u, gelu=True), oracle.gelu_tanh(g) * u)
+
+
+def test_rms_norm_pins():
+    rng = np.random.default_rng(4)
+    for n in (1, 7, 2048, 6144):
+        x = rng.standard_normal(n).astype(np.float32) * 3
+        w = rng.standard_normal(n).astype(np.float32)
+        eps = 1e-6
+        xd = x.astype(np.float64)
+        ref = xd / np.sqrt((xd * xd).sum() / n + eps) * w.astype(np.float64)
+        got = oracle.rms_norm(x, w, eps)
+        assert np.all(np.abs(got - ref) <= 1e-6 * np.abs(ref) + 1e-30)
+    c = np.full(100, 0.5, np.float32)
+    got = oracle.rms_norm(c, np.ones(100, np.float32), 1e-5)
+    assert np.allclose(got, 0.5 / np.sqrt(0.25 + 1e-5), rtol=1e-7, atol=0)
+    assert np.array_equal(oracle.rms_norm(np.zeros(9, np.float32), np.ones(9, np.float32), 1e-6), np.zeros(9))
+    x = rng.standard_normal(64).astype(np.float32)
+    assert np.array_equal(oracle.rms_norm(x, np.full(64, 2.0, np.float32), 1e-6),
+                          oracle.rms_norm(x, np.ones(64, np.float32), 1e-6) * 2)

@@ -7,6 +7,12 @@ namespace vxt {
 hipError_t launch_gemv_q8(const DevTensor&, const void*, bool, uint32_t, void*, bool, hipStream_t);
 hipError_t launch_gemv_cb4(const DevTensor&, const void*, bool, uint32_t, void*, bool, hipStream_t);
 hipError_t launch_gemv_g64(const DevTensor&, const void*, bool, uint32_t, void*, bool, hipStream_t);
+hipError_t launch_glu_q8(const DevTensor&, const void*, bool, uint32_t, uint32_t, void*, bool, uint32_t, bool,
+                         hipStream_t);
+hipError_t launch_glu_cb4(const DevTensor&, const void*, bool, uint32_t, uint32_t, void*, bool, uint32_t, bool,
+                          hipStream_t);
+hipError_t launch_glu_g64(const DevTensor&, const void*, bool, uint32_t, uint32_t, void*, bool, uint32_t, bool,
+                          hipStream_t);
 
 // x_vec (x rows 16-byte aligned) is accepted for the ABI layer; the kernels
 // stage activations through LDS or read them element-wise.
@@ -17,6 +23,18 @@ hipError_t launch_gemv(const DevTensor& t, const void* x, bool x_bf16, bool x_ve
     case KIND_Q8: return launch_gemv_q8(t, x, x_bf16, m, y, y_bf16, s);
     case KIND_CB4: return launch_gemv_cb4(t, x, x_bf16, m, y, y_bf16, s);
     case KIND_G64: return launch_gemv_g64(t, x, x_bf16, m, y, y_bf16, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Gated gate/up GEMV (batch_m 1..8): t is [gate; up] with t.rows = 2 * n_ff.
+hipError_t launch_gemv_glu(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* act, bool act_bf16,
+                           uint32_t act_stride, bool gelu, hipStream_t s) {
+  const uint32_t n_ff = t.rows / 2;
+  switch (t.kind) {
+    case KIND_Q8: return launch_glu_q8(t, x, x_bf16, m, n_ff, act, act_bf16, act_stride, gelu, s);
+    case KIND_CB4: return launch_glu_cb4(t, x, x_bf16, m, n_ff, act, act_bf16, act_stride, gelu, s);
+    case KIND_G64: return launch_glu_g64(t, x, x_bf16, m, n_ff, act, act_bf16, act_stride, gelu, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -9,4 +9,9 @@ hipError_t launch_gemv_cb4(const DevTensor& t, const void* x, bool x_bf16, uint3
   return gv::launch_kind<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, s);
 }
 
+hipError_t launch_glu_cb4(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, uint32_t n_ff, void* y,
+                        bool y_bf16, uint32_t y_stride, bool gelu, hipStream_t s) {
+  return gv::launch_glu_kind<KIND_CB4>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, gelu, s);
+}
+
 }  // namespace vxt

@@ -27,6 +27,7 @@
 #pragma once
 #include <algorithm>
 
+#include "act.hpp"
 #include "common.hpp"
 
 namespace vxt {
@@ -185,21 +186,62 @@ __device__ __forceinline__ void dequant_chunk(const WChunk<KIND>& c, uint32_t cb
   }
 }
 
+// Output epilogues.  kEpiPlain: y[m][row] = sum.  kEpiSilu / kEpiGelu: the
+// matrix is [gate; up] (rows = 2 * n_ff) and the output is the gated
+// activation act[m][i] = f(gate_i) * up_i for i < n_ff, zero for
+// n_ff <= i < y_stride -- the fused gate/up kernel of the device runner
+// (vxt_cb4_ffn_gu_nr2_m1, vxt_cb4_fast.metal:212-287) with the CPU step's
+// activation (llm_cpu.rs:457-464).
+enum Epi : int { kEpiPlain = 0, kEpiSilu = 1, kEpiGelu = 2 };
+
+template <int EPI>
+__device__ __forceinline__ float gated(float g, float u) {
+  return gated_act(g, u, EPI == kEpiGelu);
+}
+
+// Output rows of one wave.  Plain: RPW consecutive rows from `first`.  Gated:
+// RPW / 2 outputs from `first`, i.e. gate rows first.. and up rows
+// n_ff + first..; rows past the end are clamped to a valid row (`valid`
+// false), so every load stays in bounds.
+template <int EPI, int RPW>
+__device__ __forceinline__ void wave_rows(uint32_t first, uint32_t rows, uint32_t n_ff, uint32_t (&rr)[RPW],
+                                          bool (&valid)[RPW]) {
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    if constexpr (EPI == kEpiPlain) {
+      valid[r] = first + r < rows;
+      rr[r] = valid[r] ? first + r : rows - 1;
+    } else {
+      constexpr int H = RPW / 2;
+      const uint32_t o = first + (r % H);
+      valid[r] = o < n_ff;
+      rr[r] = (r < H ? 0u : n_ff) + (valid[r] ? o : n_ff - 1);
+    }
+  }
+}
+
 // Kernel: MT tokens (MT in {1,2,4,8}; m >= M_rt are padding), RPW rows per
-// wave, up to S steps per batch.
-template <uint32_t KIND, int MT, int RPW, int S, bool XBF16>
+// wave, up to S steps per batch.  Gated epilogues take n_ff and the output
+// row stride; the plain epilogue ignores both.
+template <uint32_t KIND, int MT, int RPW, int S, bool XBF16, int EPI = kEpiPlain>
 __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const void* __restrict__ x,
                                                           void* __restrict__ y, uint32_t M_rt,
-                                                          uint32_t y_bf16, uint32_t x_vec) {
+                                                          uint32_t y_bf16, uint32_t x_vec, uint32_t n_ff = 0,
+                                                          uint32_t y_stride = 0) {
+  static_assert(EPI == kEpiPlain || RPW % 2 == 0, "gated rows come in gate/up pairs");
   __shared__ __attribute__((aligned(64))) float s_cent[48];
   __shared__ __attribute__((aligned(64))) uint4 s_slot[KIND == KIND_G64 ? kWaves * S * RPW * kSlotBytes / 16 : 1];
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = threadIdx.x >> 6;
-  const uint32_t row0 = (blockIdx.x * kWaves + wave) * RPW;
+  constexpr uint32_t kOut = EPI == kEpiPlain ? RPW : RPW / 2;   // outputs per wave
+  const uint32_t first = (blockIdx.x * kWaves + wave) * kOut;
   const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
   const uint32_t nsteps = (kp + kStep - 1) / kStep;
   constexpr bool kLateX = MT >= 4;
+  uint32_t rr[RPW];
+  bool rv[RPW];
+  wave_rows<EPI, RPW>(first, rows, n_ff, rr, rv);
 
   if constexpr (KIND == KIND_CB4) {   // before any global load is in flight
     if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
@@ -214,9 +256,8 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   if constexpr (KIND == KIND_CB4) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      const uint32_t row = row0 + r < rows ? row0 + r : rows - 1;
-      os[r] = t.row_ptr[row];
-      oe[r] = t.row_ptr[row + 1];
+      os[r] = t.row_ptr[rr[r]];
+      oe[r] = t.row_ptr[rr[r] + 1];
     }
   }
 
@@ -248,10 +289,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
         const uint32_t gmax = kp / 64 - 1;
         const uint32_t g = (s0 + s) * 32 + (lane >> 1);
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const uint32_t row = row0 + r < rows ? row0 + r : rows - 1;
-          load_chunk<KIND>(t, row, k0c, g < gmax ? g : gmax, lane & 1, wc[s][r]);
-        }
+        for (int r = 0; r < RPW; ++r) load_chunk<KIND>(t, rr[r], k0c, g < gmax ? g : gmax, lane & 1, wc[s][r]);
       }
     }
     if constexpr (KIND == KIND_CB4) {
@@ -290,7 +328,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
           *(__attribute__((address_space(3))) u32x4*)(size_t)(sl + (lane >> 1) * kPairStride + (lane & 1) * 16) =
               u32x4{wc[s][r].lut.x, wc[s][r].lut.y, wc[s][r].lut.z, wc[s][r].lut.w};
         uint32_t cbase = 0;
-        if constexpr (KIND == KIND_CB4) cbase = lds_addr(s_cent) + 64u * cent_table(t, row0 + r);
+        if constexpr (KIND == KIND_CB4) cbase = lds_addr(s_cent) + 64u * cent_table(t, rr[r]);
         float w[kChunk];
         dequant_chunk<KIND>(wc[s][r], cbase, sl, lane, w);
 #pragma unroll
@@ -331,8 +369,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
     // takes entries l, l + 64, ... of the row, in that order.
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
-      const uint32_t row = row0 + r;
-      if (row >= rows) break;
+      if (!rv[r]) {
+        if constexpr (EPI == kEpiPlain) break;   // later rows are past the end too
+        continue;
+      }
       for (uint32_t i = os[r] + lane; i < oe[r]; i += 64) {
         const uint32_t pk = i < os[r] + 64 ? pk0[r] : t.outliers[i];
         const uint32_t col = pk & 0xffffu;
@@ -352,18 +392,45 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
     }
   }
 
+  if constexpr (EPI == kEpiPlain) {
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const uint32_t row = row0 + r;
+    for (int r = 0; r < RPW; ++r) {
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const float v = wave_sum(acc[r][m]);
-      if (lane == 0 && row < rows && (uint32_t)m < M_rt) {
-        if (y_bf16)
-          static_cast<uint16_t*>(y)[(size_t)m * rows + row] = f32_to_bf16(v);
-        else
-          static_cast<float*>(y)[(size_t)m * rows + row] = v;
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_sum(acc[r][m]);
+        if (lane == 0 && rv[r] && (uint32_t)m < M_rt) {
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * rows + rr[r]] = f32_to_bf16(v);
+          else
+            static_cast<float*>(y)[(size_t)m * rows + rr[r]] = v;
+        }
       }
+    }
+  } else {
+#pragma unroll
+    for (int h = 0; h < (int)kOut; ++h) {
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float g = wave_sum(acc[h][m]);
+        const float u = wave_sum(acc[h + kOut][m]);
+        if (lane == 0 && rv[h] && (uint32_t)m < M_rt) {
+          const float v = gated<EPI>(g, u);
+          const size_t at = (size_t)m * y_stride + first + h;
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[at] = f32_to_bf16(v);
+          else
+            static_cast<float*>(y)[at] = v;
+        }
+      }
+    }
+    if (blockIdx.x == 0) {   // zero padding columns [n_ff, y_stride) of every token
+      for (uint32_t m = 0; m < M_rt; ++m)
+        for (uint32_t c = n_ff + threadIdx.x; c < y_stride; c += kWaves * 64) {
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * y_stride + c] = 0;
+          else
+            static_cast<float*>(y)[(size_t)m * y_stride + c] = 0.0f;
+        }
     }
   }
 }
@@ -722,6 +789,54 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   if (m <= 4) return launch_r<KIND, 4, 1>(t, x, x_bf16, m, y, y_bf16, s);
   if (m <= 8) return launch_r<KIND, 8, 1>(t, x, x_bf16, m, y, y_bf16, s);
   return hipErrorInvalidValue;
+}
+
+// Gated gate/up GEMV: one output (a gate row and its up row) per wave, the
+// generic kernel for every kind, M = 1 or 2 (the gate and up accumulators of
+// four or more tokens do not fit in registers without spilling; the caller
+// runs those as a plain GEMV and an element-wise activation pass).
+template <uint32_t KIND, int MT, int S, bool XBF16, int EPI>
+hipError_t launch_glu_t(const DevTensor& t, const void* x, uint32_t m, uint32_t n_ff, void* y, bool y_bf16,
+                        uint32_t y_stride, hipStream_t s) {
+  constexpr int RPW = 2;
+  const dim3 grid((n_ff + kWaves - 1) / kWaves);
+  const size_t esz = XBF16 ? 2 : 4;
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && t.cols % 8 == 0 &&
+                         ((size_t)t.cols * esz) % 16 == 0;
+  hipLaunchKernelGGL((gemv_kernel<KIND, MT, RPW, S, XBF16, EPI>), grid, dim3(kWaves * 64), 0, s, t, x, y, m,
+                     (uint32_t)(y_bf16 ? 1u : 0u), x_vec, n_ff, y_stride);
+  return hipGetLastError();
+}
+
+template <uint32_t KIND, int MT, bool XBF16, int EPI>
+hipError_t launch_glu_s(const DevTensor& t, const void* x, uint32_t m, uint32_t n_ff, void* y, bool y_bf16,
+                        uint32_t y_stride, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (nsteps == 1) return launch_glu_t<KIND, MT, 1, XBF16, EPI>(t, x, m, n_ff, y, y_bf16, y_stride, s);
+  if (nsteps == 3 && MT <= 2) return launch_glu_t<KIND, MT, 3, XBF16, EPI>(t, x, m, n_ff, y, y_bf16, y_stride, s);
+  return launch_glu_t<KIND, MT, 2, XBF16, EPI>(t, x, m, n_ff, y, y_bf16, y_stride, s);
+}
+
+template <uint32_t KIND, int MT, int EPI>
+hipError_t launch_glu_x(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, uint32_t n_ff, void* y,
+                        bool y_bf16, uint32_t y_stride, hipStream_t s) {
+  return x_bf16 ? launch_glu_s<KIND, MT, true, EPI>(t, x, m, n_ff, y, y_bf16, y_stride, s)
+                : launch_glu_s<KIND, MT, false, EPI>(t, x, m, n_ff, y, y_bf16, y_stride, s);
+}
+
+template <uint32_t KIND, int EPI>
+hipError_t launch_glu_m(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, uint32_t n_ff, void* y,
+                        bool y_bf16, uint32_t y_stride, hipStream_t s) {
+  if (m == 1) return launch_glu_x<KIND, 1, EPI>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s);
+  if (m == 2) return launch_glu_x<KIND, 2, EPI>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s);
+  return hipErrorInvalidValue;
+}
+
+template <uint32_t KIND>
+hipError_t launch_glu_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, uint32_t n_ff, void* y,
+                           bool y_bf16, uint32_t y_stride, bool gelu, hipStream_t s) {
+  return gelu ? launch_glu_m<KIND, kEpiGelu>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s)
+              : launch_glu_m<KIND, kEpiSilu>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s);
 }
 
 }  // namespace gv

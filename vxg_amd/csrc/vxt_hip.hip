@@ -30,6 +30,12 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
                        size_t ws_bytes, hipStream_t s);
 hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
                           hipStream_t s);
+hipError_t launch_gemv_glu(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* act, bool act_bf16,
+                           uint32_t act_stride, bool gelu, hipStream_t s);
+hipError_t launch_glu_act(const float* gu, uint32_t m, uint32_t n_ff, bool gelu, void* act, bool act_bf16,
+                          uint32_t act_stride, hipStream_t s);
+hipError_t launch_rms_norm(float* cur, const float* delta, const float* w, void* out, bool out_bf16, uint32_t dim,
+                           uint32_t stride, uint32_t m, float eps, hipStream_t s);
 hipError_t launch_embed(const DevTensor& t, const uint32_t* tokens, uint32_t batch_m, float scale, bool scale_on,
                         float* out, uint32_t stride, hipStream_t s);
 size_t greedy_state_bytes();
@@ -252,6 +258,22 @@ void check_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m
   if (m == 0) fail(VXT_E_SHAPE, "batch_m must be >= 1");
 }
 
+// The context workspace (GEMM weight panel and split-K partial sums, gated-FFN
+// staging) is shared by every call of this context (calls are ordered on one
+// stream, or the caller orders them).  It only grows outside a capture: a
+// captured graph keeps the pointer it recorded.
+void ensure_ws(Ctx* c, size_t need) {
+  if (need <= c->ws_cap) return;
+  if (c->capturing)
+    fail(VXT_E_ARG, "GEMM workspace too small inside a capture: run this shape once before capturing");
+  VXT_HIP_CHECK(hipDeviceSynchronize());   // earlier calls may still read the old workspace
+  if (c->ws) VXT_HIP_CHECK(hipFree(c->ws));
+  c->ws = nullptr;
+  c->ws_cap = 0;
+  VXT_HIP_CHECK(hipMalloc(&c->ws, need));
+  c->ws_cap = need;
+}
+
 void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, void* y,
                 uint32_t y_dtype, hipStream_t s) {
   const DevTensor d = t->dev();
@@ -263,20 +285,8 @@ void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, 
     const bool x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t->cols * esz) % 16 == 0;
     e = vxt::launch_gemv(d, x, xb, x_vec, m, y, yb, s);
   } else {
-    // The panel workspace is shared by every GEMM of this context (calls are
-    // ordered on one stream, or the caller orders them).  It only grows
-    // outside a capture: a captured graph keeps the pointer it recorded.
     const size_t need = vxt::gemm_workspace_bytes(d, m, xb);
-    if (need > c->ws_cap) {
-      if (c->capturing)
-        fail(VXT_E_ARG, "GEMM workspace too small inside a capture: run this shape once before capturing");
-      VXT_HIP_CHECK(hipDeviceSynchronize());   // earlier GEMMs may still read the old workspace
-      if (c->ws) VXT_HIP_CHECK(hipFree(c->ws));
-      c->ws = nullptr;
-      c->ws_cap = 0;
-      VXT_HIP_CHECK(hipMalloc(&c->ws, need));
-      c->ws_cap = need;
-    }
+    ensure_ws(c, need);
     e = vxt::launch_gemm(d, x, xb, m, y, yb, c->ws, c->ws_cap, s);
   }
   if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
@@ -677,6 +687,61 @@ int vxt_hip_dequant_rows(void* ctx, void* tensor, uint32_t row0, uint32_t nrows,
     if (rc != VXT_OK) fail(rc, e2);
     VXT_HIP_CHECK(hipMemcpyAsync(out, c->d_y, ob, hipMemcpyDeviceToHost, c->stream));
     VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int vxt_hip_ffn_glu_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype, uint32_t batch_m, void* act,
+                        uint32_t act_dtype, uint32_t act_stride, uint32_t activation, void* stream, char* err,
+                        size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    check_matmul(c, t, x, x_dtype, batch_m, act, act_dtype);
+    if (t->rows % 2 != 0) fail(VXT_E_SHAPE, "a [gate; up] tensor has an even row count");
+    if (activation > VXT_ACT_GELU_TANH) fail(VXT_E_ARG, "unknown activation");
+    const uint32_t n_ff = t->rows / 2;
+    if (act_stride < n_ff) fail(VXT_E_SHAPE, "act_stride < rows / 2");
+    const bool xb = x_dtype == VXT_DTYPE_BF16, ab = act_dtype == VXT_DTYPE_BF16;
+    const bool gelu = activation == VXT_ACT_GELU_TANH;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const DevTensor d = t->dev();
+    hipError_t e;
+    if (batch_m <= 2) {
+      e = vxt::launch_gemv_glu(d, x, xb, batch_m, act, ab, act_stride, gelu, s);
+    } else {
+      // Gate and up rows into f32 staging after the GEMM's own workspace,
+      // then the element-wise activation.
+      const size_t gemm_ws = batch_m > 8 ? (vxt::gemm_workspace_bytes(d, batch_m, xb) + 255) / 256 * 256 : 0;
+      const size_t stage = (size_t)batch_m * t->rows * sizeof(float);
+      ensure_ws(c, gemm_ws + stage);
+      float* gu = reinterpret_cast<float*>(static_cast<char*>(c->ws) + gemm_ws);
+      if (batch_m <= 8) {
+        e = vxt::launch_gemv(d, x, xb, false, batch_m, gu, false, s);
+      } else {
+        e = vxt::launch_gemm(d, x, xb, batch_m, gu, false, c->ws, gemm_ws, s);
+      }
+      if (e == hipSuccess) e = vxt::launch_glu_act(gu, batch_m, n_ff, gelu, act, ab, act_stride, s);
+    }
+    if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("gated FFN launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+int vxt_hip_rms_norm_dev(void* ctx, float* cur, const float* delta, const float* weight, void* out,
+                         uint32_t out_dtype, uint32_t dim, uint32_t stride, uint32_t batch_m, float eps,
+                         void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    (void)as_ctx(ctx);
+    if (batch_m == 0) return;
+    if (!cur || !weight || !out) fail(VXT_E_ARG, "null pointer");
+    if (!dtype_ok(out_dtype)) fail(VXT_E_ARG, "unknown dtype");
+    if (dim == 0 || stride < dim) fail(VXT_E_SHAPE, "need 0 < dim <= stride");
+    if (out_dtype == VXT_DTYPE_BF16 && (out == cur || out == delta))
+      fail(VXT_E_ARG, "a bf16 output cannot overwrite an f32 input");
+    if (delta && out == delta) fail(VXT_E_ARG, "out may alias cur, not delta");
+    hipError_t e = vxt::launch_rms_norm(cur, delta, weight, out, out_dtype == VXT_DTYPE_BF16, dim, stride, batch_m,
+                                        eps, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("rms_norm launch failed: ") + hipGetErrorString(e));
   });
 }
 

@@ -46,6 +46,7 @@ LIB_PATH = os.path.join(_HERE, "libvxt_hip.so")
 VXT_OK = 0
 VXT_E_ARG, VXT_E_SHAPE, VXT_E_FORMAT, VXT_E_DEVICE, VXT_E_UNSUPPORTED = -1, -2, -3, -4, -5
 DTYPE_F32, DTYPE_BF16 = 0, 1
+ACT_SILU, ACT_GELU_TANH = 0, 1
 KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
 
 ABI_SYMBOLS = (
@@ -54,7 +55,7 @@ ABI_SYMBOLS = (
     "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
-    "vxt_hip_embed_dev",
+    "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev",
     "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
@@ -149,6 +150,10 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_greedy_dev.restype = C.c_int
     L.vxt_hip_embed_dev.argtypes = [vp, vp, vp, u32, C.c_float, vp, u32, vp, cp, sz]
     L.vxt_hip_embed_dev.restype = C.c_int
+    L.vxt_hip_ffn_glu_dev.argtypes = [vp, vp, vp, u32, u32, vp, u32, u32, u32, vp, cp, sz]
+    L.vxt_hip_ffn_glu_dev.restype = C.c_int
+    L.vxt_hip_rms_norm_dev.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, C.c_float, vp, cp, sz]
+    L.vxt_hip_rms_norm_dev.restype = C.c_int
     L.vxt_hip_greedy_dev.argtypes = [vp, vp, u32, vp, vp, cp, sz]
     L.vxt_hip_last_kernel_ms.restype = C.c_int
     L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
@@ -562,6 +567,29 @@ class HipEngine:
         buf = _errbuf()
         _check(load_library().vxt_hip_greedy_dev(self.ctx, logits_ptr or None, n, out_ptr or None,
                                                  stream or None, buf, len(buf)), buf)
+
+    def ffn_glu_dev(self, t: GpuPackedTensor, x_ptr: int, x_dtype: int, batch_m: int, act_ptr: int,
+                    act_dtype: int, act_stride: int | None = None, activation: int = ACT_SILU,
+                    stream: int = 0) -> None:
+        """Gated FFN projection over a ``[gate; up]`` tensor
+        (``vxt_hip_ffn_glu_dev``): ``act = act(gate . x) * (up . x)``, the
+        fused gate/up kernel of the device runner (vxt_cb4_fast.metal:212-287)."""
+        buf = _errbuf()
+        stride = t.rows // 2 if act_stride is None else act_stride
+        _check(load_library().vxt_hip_ffn_glu_dev(self.ctx, t.handle, x_ptr or None, x_dtype, batch_m,
+                                                  act_ptr or None, act_dtype, stride, activation,
+                                                  stream or None, buf, len(buf)), buf)
+
+    def rms_norm_dev(self, cur_ptr: int, delta_ptr: int, weight_ptr: int, out_ptr: int, out_dtype: int,
+                     dim: int, stride: int | None = None, batch_m: int = 1, eps: float = 1e-6,
+                     stream: int = 0) -> None:
+        """``cur += delta`` (when ``delta_ptr``) then ``out = rms_norm(cur) * weight``
+        (``vxt_hip_rms_norm_dev``; llm_ops.rs:48-57 after llm_cpu.rs:443-446)."""
+        buf = _errbuf()
+        _check(load_library().vxt_hip_rms_norm_dev(self.ctx, cur_ptr or None, delta_ptr or None,
+                                                   weight_ptr or None, out_ptr or None, out_dtype, dim,
+                                                   dim if stride is None else stride, batch_m, eps,
+                                                   stream or None, buf, len(buf)), buf)
 
     def embed_dev(self, t: GpuPackedTensor, tokens_ptr: int, batch_m: int, out_ptr: int,
                   out_stride: int | None = None, embed_scale: float = 1.0, stream: int = 0) -> None:

@@ -112,3 +112,103 @@ class DecodeStack:
     def free(self) -> None:
         for b in (self.x, self.qkv_out, self.o_out, self.gu_out, self.dn_out, self.logits):
             b.free()
+
+
+@dataclass
+class LayerNorms:
+    """Device f32 RMSNorm weights of one layer ([hidden] each)."""
+
+    attn: engine.DeviceBuffer
+    post_attn: engine.DeviceBuffer
+
+
+class DecodeStep:
+    """One whole decode step for batch 1, token to token on the device.
+
+    The reference CPU step (``forward_step``, llm_cpu.rs:251-482) and the
+    device runner (metal_cb4_fast_run.mm:81-92, 355-387) do, per layer::
+
+        normed = rms_norm(cur [+= delta], attn_norm)     vxt_hip_rms_norm_dev
+        qkv    = W_qkv . normed                           vxt_hip_matmul_dev
+        o      = W_o . attention(qkv)                     (attention stands in
+                                                           as the first hidden
+                                                           outputs of qkv)
+        normed = rms_norm(cur += o, post_attn_norm)       vxt_hip_rms_norm_dev
+        act    = act(W_gate . normed) * (W_up . normed)   vxt_hip_ffn_glu_dev
+        delta  = W_down . act                             vxt_hip_matmul_dev
+
+    then ``normed = rms_norm(cur += delta, output_norm)``, ``logits =
+    W_head . normed``, the greedy id (``vxt_hip_greedy_dev``) and the next
+    token's embedding row (``vxt_hip_embed_dev``), which starts the next
+    step.  The residual stream ``cur`` and the deltas are f32; the inputs of
+    the projections are bf16.  ``embed`` may be the LM head itself (tied
+    embeddings, llm_cpu.rs:480).  One step is 6 * layers + 4 launches.
+    """
+
+    def __init__(self, eng: engine.HipEngine, layers: Sequence[LayerWeights], norms: Sequence[LayerNorms],
+                 output_norm: engine.DeviceBuffer, lm_head: engine.GpuPackedTensor,
+                 embed: engine.GpuPackedTensor, eps: float = 1e-6, activation: int = engine.ACT_SILU,
+                 embed_scale: float = 1.0):
+        if not layers or len(norms) != len(layers):
+            raise ValueError("one LayerNorms per layer, at least one layer")
+        self.eng, self.layers, self.norms = eng, list(layers), list(norms)
+        self.output_norm, self.lm_head, self.embed = output_norm, lm_head, embed
+        self.eps, self.activation, self.embed_scale = eps, activation, embed_scale
+        H = self.hidden = lm_head.cols
+        if embed.cols != H:
+            raise ValueError("embedding width != hidden size")
+        for i, L in enumerate(self.layers):
+            if L.qkv.cols != H or L.o.rows != H or L.gate_up.cols != H or L.down.rows != H:
+                raise ValueError(f"layer {i}: projection shapes do not chain")
+            if L.o.cols > L.qkv.rows or L.gate_up.rows % 2 or L.down.cols != L.gate_up.rows // 2:
+                raise ValueError(f"layer {i}: o / gate-up / down sizes do not match")
+        big_qkv = max(L.qkv.rows for L in self.layers)
+        big_ff = max(L.gate_up.rows // 2 for L in self.layers)
+        self.cur = eng.alloc(H * 4)
+        self.delta = eng.alloc(H * 4)
+        self.normed = eng.alloc(H * 2)
+        self.qkv_out = eng.alloc(big_qkv * 2)
+        self.act = eng.alloc(big_ff * 2)
+        self.logits = eng.alloc(lm_head.rows * 4)
+        self.token = eng.alloc(8)          # [id, nonfinite] from the greedy step
+
+    @property
+    def launches(self) -> int:
+        return 6 * len(self.layers) + 4
+
+    def set_token(self, token: int) -> None:
+        import numpy as np
+        self.token.upload(np.array([token, 0], np.uint32))
+
+    def read_token(self) -> tuple[int, bool]:
+        import numpy as np
+        r = self.token.download(np.uint32, (2,))
+        return int(r[0]), bool(r[1])
+
+    def enqueue(self, stream=None) -> None:
+        e, s = self.eng, stream or self.eng.stream
+        bf16, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
+        H = self.hidden
+        e.embed_dev(self.embed, self.token.ptr, 1, self.cur.ptr, H, self.embed_scale, s)
+        for i, (L, N) in enumerate(zip(self.layers, self.norms)):
+            e.rms_norm_dev(self.cur.ptr, self.delta.ptr if i else 0, N.attn.ptr, self.normed.ptr, bf16, H, H, 1,
+                           self.eps, s)
+            e.matmul_dev(L.qkv, self.normed.ptr, bf16, 1, self.qkv_out.ptr, bf16, s)
+            e.matmul_dev(L.o, self.qkv_out.ptr, bf16, 1, self.delta.ptr, f32, s)
+            e.rms_norm_dev(self.cur.ptr, self.delta.ptr, N.post_attn.ptr, self.normed.ptr, bf16, H, H, 1,
+                           self.eps, s)
+            e.ffn_glu_dev(L.gate_up, self.normed.ptr, bf16, 1, self.act.ptr, bf16, L.gate_up.rows // 2,
+                          self.activation, s)
+            e.matmul_dev(L.down, self.act.ptr, bf16, 1, self.delta.ptr, f32, s)
+        e.rms_norm_dev(self.cur.ptr, self.delta.ptr, self.output_norm.ptr, self.normed.ptr, bf16, H, H, 1,
+                       self.eps, s)
+        e.matmul_dev(self.lm_head, self.normed.ptr, bf16, 1, self.logits.ptr, f32, s)
+        e.greedy_dev(self.logits.ptr, self.lm_head.rows, self.token.ptr, s)
+
+    def capture(self) -> engine.Graph:
+        """Record one step into a HIP graph; each replay advances one token."""
+        return self.eng.capture(lambda s: self.enqueue(s))
+
+    def free(self) -> None:
+        for b in (self.cur, self.delta, self.normed, self.qkv_out, self.act, self.logits, self.token):
+            b.free()
