@@ -213,12 +213,13 @@ def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: i
 
 
 def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
-               ffn: int = 6144, seed: int = 40):
+               ffn: int = 6144, seed: int = 40, fuse_norm: bool = True):
     """The whole decode step (``stack.DecodeStep``) on config 4's weights:
     embedding gather (tied Q8 head), per layer RMSNorm, [q;k;v], o,
     add + RMSNorm, fused [gate;up] + SwiGLU, down; final norm, LM head,
     greedy.  Attention stands in as a slice, as in the matmul-only stack.
-    Captured once; each replay is one token, the id fed back on the device."""
+    Captured once; each replay is one token, the id fed back on the device.
+    ``fuse_norm``: each RMSNorm built inside the projection that reads it."""
     import numpy as np
     from vxg_amd import stack
     lw, nbytes = _stack_layers(eng, kind, layers, hidden, ffn, seed)
@@ -228,7 +229,7 @@ def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: in
     bufs = [eng.to_device((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
             for _ in range(2 * layers + 1)]
     norms = [stack.LayerNorms(bufs[2 * i], bufs[2 * i + 1]) for i in range(layers)]
-    st = stack.DecodeStep(eng, lw, norms, bufs[-1], head, head)
+    st = stack.DecodeStep(eng, lw, norms, bufs[-1], head, head, fuse_norm=fuse_norm)
     st.set_token(1)
     for _ in range(3):
         st.enqueue()
@@ -362,12 +363,13 @@ def main():
                               "frac_hbm": round(rs["GBps"] / HBM_PEAK_GBS, 4)})
             log(f"  {rs['tokens_per_s']:.1f} tok/s ({rs['GBps']:.1f} GB/s, "
                 f"{rs['ms_per_token']*1e3:.1f} us/token)")
-        for kind in ("cb4",):
-            log(f"config 4 (whole step): 24 layers {kind} + norms, fused SwiGLU, Q8 head, greedy, embedding")
-            rw = bench_step(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)))
+        for kind, fuse in (("cb4", False), ("cb4", True)):
+            how = "norms inside the projections" if fuse else "separate norm launches"
+            log(f"config 4 (whole step): 24 layers {kind} + norms, fused SwiGLU, Q8 head, greedy, embedding; {how}")
+            rw = bench_step(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)), fuse_norm=fuse)
             secondary.append({"config": f"4 (whole decode step): embed + 24x{{norm,[q;k;v],o,add+norm,"
                                         f"[gate;up]+swiglu,down}} {kind} + norm + q8 head + greedy, M=1, "
-                                        f"HIP graph of {rw['launches_per_token']} launches per token",
+                                        f"{how}, HIP graph of {rw['launches_per_token']} launches per token",
                               "tokens_per_s": round(rw["tokens_per_s"], 1),
                               "ms_per_token": round(rw["ms_per_token"], 4),
                               "launches_per_token": rw["launches_per_token"]})

@@ -54,6 +54,11 @@ extern "C" {
 #define VXT_ACT_SILU 0u       /* silu(g) * u, llm_ops.rs:39-41                  */
 #define VXT_ACT_GELU_TANH 1u  /* gelu_tanh_f32(g) * u, llm_prefill.rs:66-71     */
 
+/* vxt_hip_norm_matmul_dev modes */
+#define VXT_NORM_PLAIN 0u          /* y = W x                                   */
+#define VXT_NORM_GLU_SILU 1u       /* y = silu(gate . x) * (up . x)             */
+#define VXT_NORM_GLU_GELU_TANH 2u  /* y = gelu_tanh(gate . x) * (up . x)        */
+
 /* ---- tensor kinds (kind 2 = codebook, as VxtMetalOp.kind in
  *      native/metal_internal.h:14) ---------------------------------------- */
 #define VXT_KIND_CB4 2u     /* CodebookMatrix, bits = 4 (codebook.rs:9-24)   */
@@ -218,6 +223,21 @@ VXT_API int vxt_hip_ffn_glu_dev(void* ctx, void* tensor, const void* x, uint32_t
 VXT_API int vxt_hip_rms_norm_dev(void* ctx, float* cur, const float* delta, const float* weight, void* out,
                                  uint32_t out_dtype, uint32_t dim, uint32_t stride, uint32_t batch_m, float eps,
                                  void* stream, char* err, size_t err_cap);
+
+/* Batch-1 projection of a normalised residual stream, one launch:
+ *   v = delta ? cur + delta : cur;  x = bf16(rms_norm(v) * norm_w)  (as
+ *   vxt_hip_rms_norm_dev with a bf16 output, bit for bit);
+ *   y = W x (VXT_NORM_PLAIN), or the gated activation of [gate; up] as in
+ *   vxt_hip_ffn_glu_dev (VXT_NORM_GLU_*; y_stride >= rows / 2, zero padded);
+ *   with delta, cur_out (a buffer other than cur and delta) receives v.
+ * The pair it replaces is the runner's add-RMSNorm kernel and the GEMV that
+ * reads its output (metal_cb4_fast_run.mm:81-92, 355-387); here every
+ * workgroup builds x itself from cur, delta and norm_w, so the pair costs
+ * one launch.  cols <= 4096 (VXT_E_UNSUPPORTED otherwise: use the two calls). */
+VXT_API int vxt_hip_norm_matmul_dev(void* ctx, void* tensor, const float* cur, const float* delta,
+                                    const float* norm_w, float eps, float* cur_out, uint32_t mode, void* y,
+                                    uint32_t y_dtype, uint32_t y_stride, void* stream, char* err,
+                                    size_t err_cap);
 
 /* Embedding rows for batch_m token ids held in device memory (tokens[m]):
  * out[m * out_stride + c] = decode_row(tokens[m])[c] for c < cols, bit-exact,

@@ -262,3 +262,109 @@ def test_rms_norm_errors(eng):
             assert e.value.code == code
     finally:
         buf.free()
+
+
+# ---------------------------------------------------------------- norm prologue
+
+def norm_pair_reference(eng, t, cur, delta, w, eps, mode, y_dtype, y_stride):
+    """The two-launch form on the GPU: vxt_hip_rms_norm_dev (bf16 out) then the
+    projection reading it."""
+    H = cur.size
+    cd, wd = eng.to_device(cur), eng.to_device(w)
+    dd = eng.to_device(delta) if delta is not None else None
+    xd = eng.alloc(H * 2)
+    esz = 2 if y_dtype == engine.DTYPE_BF16 else 4
+    outs = t.rows if mode == engine.NORM_PLAIN else y_stride
+    yd = eng.alloc(outs * esz)
+    try:
+        eng.rms_norm_dev(cd.ptr, dd.ptr if dd else 0, wd.ptr, xd.ptr, engine.DTYPE_BF16, H, H, 1, eps, eng.stream)
+        if mode == engine.NORM_PLAIN:
+            eng.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 1, yd.ptr, y_dtype, eng.stream)
+        else:
+            act = engine.ACT_GELU_TANH if mode == engine.NORM_GLU_GELU_TANH else engine.ACT_SILU
+            eng.ffn_glu_dev(t, xd.ptr, engine.DTYPE_BF16, 1, yd.ptr, y_dtype, y_stride, act, eng.stream)
+        eng.synchronize()
+        return cd.download(np.float32, (H,)), yd.download(np.uint16 if esz == 2 else np.uint32, (outs,))
+    finally:
+        for b in (cd, wd, dd, xd, yd):
+            if b is not None:
+                b.free()
+
+
+def run_norm_matmul(eng, t, cur, delta, w, eps, mode, y_dtype, y_stride):
+    H = cur.size
+    cd, wd = eng.to_device(cur), eng.to_device(w)
+    dd = eng.to_device(delta) if delta is not None else None
+    od = eng.to_device(np.full(H, np.nan, np.float32))
+    esz = 2 if y_dtype == engine.DTYPE_BF16 else 4
+    outs = t.rows if mode == engine.NORM_PLAIN else y_stride
+    yd = eng.to_device(np.full(outs * esz, 0x7F, np.uint8))
+    try:
+        eng.norm_matmul_dev(t, cd.ptr, dd.ptr if dd else 0, wd.ptr, eps, od.ptr if dd else 0, mode, yd.ptr,
+                            y_dtype, y_stride, eng.stream)
+        eng.synchronize()
+        return od.download(np.float32, (H,)), yd.download(np.uint16 if esz == 2 else np.uint32, (outs,))
+    finally:
+        for b in (cd, wd, dd, od, yd):
+            if b is not None:
+                b.free()
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("mode", [engine.NORM_PLAIN, engine.NORM_GLU_SILU, engine.NORM_GLU_GELU_TANH])
+@pytest.mark.parametrize("cols", [64, 300, 2048, 4096])
+def test_norm_matmul_bit_identical_to_the_pair(eng, kind, mode, cols):
+    rows = 3000 if mode == engine.NORM_PLAIN else 2 * 1500
+    print(f"norm_matmul kind={kind} mode={mode} cols={cols}", flush=True)
+    t = eng.upload_packed(make(kind, rows, cols, seed=cols + mode))
+    rng = np.random.default_rng(cols)
+    cur = rng.standard_normal(cols).astype(np.float32) * 3
+    delta = rng.standard_normal(cols).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    stride = rows // 2 + 7 if mode != engine.NORM_PLAIN else None
+    for d in (None, delta):
+        for ydt in (engine.DTYPE_F32, engine.DTYPE_BF16):
+            ref_cur, ref_y = norm_pair_reference(eng, t, cur, d, w, 1e-6, mode, ydt, stride)
+            got_cur, got_y = run_norm_matmul(eng, t, cur, d, w, 1e-6, mode, ydt, stride)
+            assert np.array_equal(got_y, ref_y), (d is None, ydt)
+            if d is not None:
+                assert np.array_equal(got_cur.view(np.uint32), (cur + d).view(np.uint32))
+                assert np.array_equal(got_cur, ref_cur)
+            else:
+                assert np.all(np.isnan(got_cur))          # nothing stored without delta
+    t.free()
+
+
+def test_norm_matmul_lm_head_rows(eng):
+    """The four-rows-per-wave launch (rows >= 65536), Q8 like the LM head."""
+    t = eng.upload_packed(make("q8", 70001, 256, seed=1))
+    rng = np.random.default_rng(0)
+    cur, delta = rng.standard_normal(256).astype(np.float32), rng.standard_normal(256).astype(np.float32)
+    w = np.ones(256, np.float32)
+    ref = norm_pair_reference(eng, t, cur, delta, w, 1e-5, engine.NORM_PLAIN, engine.DTYPE_F32, None)[1]
+    got = run_norm_matmul(eng, t, cur, delta, w, 1e-5, engine.NORM_PLAIN, engine.DTYPE_F32, None)[1]
+    assert np.array_equal(got, ref)
+    t.free()
+
+
+def test_norm_matmul_errors(eng):
+    wide = eng.upload_packed(make("q8", 8, 4128, seed=0))
+    odd = eng.upload_packed(make("q8", 7, 64, seed=0))
+    ok = eng.upload_packed(make("q8", 8, 64, seed=0))
+    buf = eng.alloc(1 << 16)
+    p = buf.ptr
+    try:
+        cases = [(wide, dict(delta_ptr=0, cur_out_ptr=0, mode=0), engine.VXT_E_UNSUPPORTED),
+                 (odd, dict(delta_ptr=0, cur_out_ptr=0, mode=1), engine.VXT_E_SHAPE),
+                 (ok, dict(delta_ptr=p + 4096, cur_out_ptr=0, mode=0), engine.VXT_E_ARG),
+                 (ok, dict(delta_ptr=p + 4096, cur_out_ptr=p, mode=0), engine.VXT_E_ARG),
+                 (ok, dict(delta_ptr=p + 4096, cur_out_ptr=p + 4096, mode=0), engine.VXT_E_ARG),
+                 (ok, dict(delta_ptr=0, cur_out_ptr=0, mode=9), engine.VXT_E_ARG)]
+        for t, kw, code in cases:
+            with pytest.raises(engine.BackendError) as e:
+                eng.norm_matmul_dev(t, p, weight_ptr=p + 8192, eps=1e-6, y_ptr=p + 16384,
+                                    y_dtype=engine.DTYPE_F32, stream=eng.stream, **kw)
+            assert e.value.code == code
+    finally:
+        for x in (buf, wide, odd, ok):
+            x.free()

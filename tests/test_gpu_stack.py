@@ -176,14 +176,14 @@ def test_stack_shape_checks(eng):
 
 # ---------------------------------------------------------------- whole decode step
 
-def small_step(eng, kind, n_layers, seed=0, activation=engine.ACT_SILU, hidden=256, ffn=384):
+def small_step(eng, kind, n_layers, seed=0, activation=engine.ACT_SILU, hidden=256, ffn=384, fuse_norm=False):
     st, host, head = small_stack(eng, kind, n_layers, hidden=hidden, ffn=ffn, seed=seed)
     rng = np.random.default_rng(seed + 5)
     norm_w = [(1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32) for _ in range(2 * n_layers + 1)]
     bufs = [eng.to_device(w) for w in norm_w]
     norms = [stack.LayerNorms(bufs[2 * i], bufs[2 * i + 1]) for i in range(n_layers)]
     step = stack.DecodeStep(eng, st.layers, norms, bufs[-1], st.lm_head, st.lm_head, eps=1e-6,
-                            activation=activation)
+                            activation=activation, fuse_norm=fuse_norm)
     return step, st, host, head, norm_w, bufs
 
 
@@ -252,6 +252,40 @@ def test_decode_step_graph_advances_tokens_like_eager(eng):
     st.free()
     for b in bufs:
         b.free()
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64"])
+def test_decode_step_fused_norms_bit_identical(eng, kind):
+    """Norms built inside the projections: same tokens, logits and residual
+    stream as the separate RMSNorm launches, eager and captured."""
+    runs = []
+    for fuse in (False, True):
+        step, st, host, head, norm_w, bufs = small_step(eng, kind, 3, seed=21,
+                                                        activation=engine.ACT_GELU_TANH, fuse_norm=fuse)
+        assert step.launches == (16 if fuse else 22)
+        step.set_token(99)
+        seq = []
+        for _ in range(3):
+            step.enqueue()
+            eng.synchronize()
+            seq.append((step.read_token(), step.logits.download(np.float32, head.rows),
+                        step.residual.download(np.float32, (step.hidden,))))
+        step.set_token(99)
+        g = step.capture()
+        for i in range(3):
+            g.launch(1)
+            assert step.read_token() == seq[i][0]
+            assert np.array_equal(step.logits.download(np.float32, head.rows), seq[i][1])
+        g.free()
+        runs.append(seq)
+        step.free()
+        st.free()
+        for b in bufs:
+            b.free()
+    for (ta, la, ca), (tb, lb, cb) in zip(*runs):
+        assert ta == tb
+        assert np.array_equal(la, lb)
+        assert np.array_equal(ca, cb)
 
 
 def test_decode_step_shape_checks(eng):

@@ -92,6 +92,16 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
   return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
 }
 
+// Inputs of a GEMV whose activations are an RMSNorm of the residual stream
+// (batch 1): x = bf16(rms_norm(cur [+ delta]) * w).
+struct NormIn {
+  const float* cur;
+  const float* delta;    // null: x = norm(cur), nothing stored
+  const float* w;
+  float* cur_out;        // with delta: receives cur + delta (must not alias cur or delta)
+  float eps;
+};
+
 // ---- wave64 reductions ----------------------------------------------------
 
 template <int CTRL>

@@ -14,4 +14,9 @@ hipError_t launch_glu_g64(const DevTensor& t, const void* x, bool x_bf16, uint32
   return gv::launch_glu_kind<KIND_G64>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, gelu, s);
 }
 
+hipError_t launch_norm_g64(const DevTensor& t, const NormIn& nin, int epi, void* y, bool y_bf16,
+                         uint32_t y_stride, hipStream_t s) {
+  return gv::launch_norm_kind<KIND_G64>(t, nin, epi, y, y_bf16, y_stride, s);
+}
+
 }  // namespace vxt

@@ -220,15 +220,83 @@ __device__ __forceinline__ void wave_rows(uint32_t first, uint32_t rows, uint32_
   }
 }
 
+// Norm prologue (batch 1): x is not read from memory but built by every
+// workgroup as bf16(rms_norm(cur [+ delta]) * w), with the reduction of the
+// stand-alone RMSNorm kernel (ffn.hip) step for step -- element i = tid +
+// 256 j summed by FMA in ascending j, the DPP wave sum, the four wave sums
+// added in order -- so x is bit-identical to that kernel's bf16 output.
+// Workgroup 0 also stores cur + delta to cur_out (the residual stream).
+// Inputs: NormIn (common.hpp).
+constexpr uint32_t kNormPer = 16;   // most elements per thread: cols <= 4096
+
+// The norm arithmetic on the values the caller loaded (element i = tid +
+// 256 j), then x in LDS: bf16 for i < cols, zero up to xlen.  Ends with a
+// barrier, so the caller reads s_xn right after.
+template <uint32_t NP>
+__device__ __forceinline__ void norm_prologue(const NormIn& nin, uint32_t cols, uint32_t xlen, const float (&c)[NP],
+                                              const float (&d)[NP], const float (&w)[NP], uint16_t* s_xn) {
+#pragma clang fp contract(off)
+  __shared__ float s_part[kWaves];
+  const uint32_t tid = threadIdx.x;
+  const bool add = nin.delta != nullptr;
+  float v[NP];
+  float sq = 0.0f;
+#pragma unroll
+  for (uint32_t j = 0; j < NP; ++j) {
+    v[j] = add ? c[j] + d[j] : c[j];
+    if (tid + 256u * j < cols) sq = __builtin_fmaf(v[j], v[j], sq);
+  }
+  sq = wave_sum(sq);
+  if ((tid & 63u) == 0) s_part[tid >> 6] = sq;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k < kWaves; ++k) total += s_part[k];
+  const float scale = 1.0f / sqrtf(total / (float)cols + nin.eps);
+  const bool store = add && blockIdx.x == 0;
+#pragma unroll
+  for (uint32_t j = 0; j < NP; ++j) {
+    const uint32_t i = tid + 256u * j;
+    if (i < cols) {
+      s_xn[i] = f32_to_bf16(v[j] * scale * w[j]);
+      if (store) nin.cur_out[i] = v[j];
+    } else if (i < xlen) {
+      s_xn[i] = 0;
+    }
+  }
+  for (uint32_t i = tid + 256u * NP; i < xlen; i += 256u) s_xn[i] = 0;
+  __syncthreads();
+}
+
+// 32 bf16 activations at k0 from the LDS copy (64 bytes, 16-byte aligned).
+__device__ __forceinline__ void read_x_lds(const uint16_t* s_xn, uint32_t k0, float (&xv)[kChunk]) {
+  typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+  const uint32_t base = lds_addr(s_xn) + k0 * 2u;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 q = *(lds_u32x4*)(size_t)(base + 16u * i);
+    const uint32_t wv[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      xv[8 * i + 2 * j] = __uint_as_float(wv[j] << 16);
+      xv[8 * i + 2 * j + 1] = __uint_as_float(wv[j] & 0xffff0000u);
+    }
+  }
+}
+
 // Kernel: MT tokens (MT in {1,2,4,8}; m >= M_rt are padding), RPW rows per
 // wave, up to S steps per batch.  Gated epilogues take n_ff and the output
-// row stride; the plain epilogue ignores both.
-template <uint32_t KIND, int MT, int RPW, int S, bool XBF16, int EPI = kEpiPlain>
+// row stride; the plain epilogue ignores both.  NORM: the norm prologue above
+// (MT = 1, bf16 x staged in dynamic LDS of nsteps * kStep elements).
+template <uint32_t KIND, int MT, int RPW, int S, bool XBF16, int EPI = kEpiPlain, bool NORM = false,
+          uint32_t NP = kNormPer>
 __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const void* __restrict__ x,
                                                           void* __restrict__ y, uint32_t M_rt,
                                                           uint32_t y_bf16, uint32_t x_vec, uint32_t n_ff = 0,
-                                                          uint32_t y_stride = 0) {
+                                                          uint32_t y_stride = 0, NormIn nin = {}) {
   static_assert(EPI == kEpiPlain || RPW % 2 == 0, "gated rows come in gate/up pairs");
+  static_assert(!NORM || (MT == 1 && XBF16), "the norm prologue serves one token with bf16 x");
+  extern __shared__ __attribute__((aligned(16))) uint16_t s_xn[];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
   __shared__ __attribute__((aligned(64))) uint4 s_slot[KIND == KIND_G64 ? kWaves * S * RPW * kSlotBytes / 16 : 1];
 
@@ -261,6 +329,26 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
     }
   }
 
+  // Norm inputs are requested before any weight, so waiting for them leaves
+  // the weight loads in flight.
+  float n_c[NORM ? NP : 1], n_d[NORM ? NP : 1], n_w[NORM ? NP : 1];
+  if constexpr (NORM) {
+#pragma unroll
+    for (uint32_t j = 0; j < NP; ++j) {
+      const uint32_t i = threadIdx.x + 256u * j;
+      const uint32_t ic = i < cols ? i : cols - 1;
+      n_c[j] = nin.cur[ic];
+      n_w[j] = nin.w[ic];
+    }
+    if (nin.delta) {
+#pragma unroll
+      for (uint32_t j = 0; j < NP; ++j) {
+        const uint32_t i = threadIdx.x + 256u * j;
+        n_d[j] = nin.delta[i < cols ? i : cols - 1];
+      }
+    }
+  }
+
   float acc[RPW][MT];
 #pragma unroll
   for (int r = 0; r < RPW; ++r)
@@ -274,7 +362,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
     WChunk<KIND> wc[S][RPW];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-      if (!kLateX && (uint32_t)s < ns && x_vec) {
+      if (!NORM && !kLateX && (uint32_t)s < ns && x_vec) {
         const uint32_t k0 = (s0 + s) * kStep + lane * kChunk;
 #pragma unroll
         for (int m = 0; m < MT; ++m)
@@ -302,6 +390,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
         }
       }
     }
+    if constexpr (NORM) {
+      if (s0 == 0) norm_prologue<NP>(nin, cols, nsteps * kStep, n_c, n_d, n_w, s_xn);
+    }
     // ---- consume
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -312,7 +403,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
       // token is loaded and unpacked where it is used, so the registers hold
       // one token's 32 values at a time.
       float xv[kLateX ? 1 : MT][kChunk];
-      if constexpr (!kLateX) {
+      if constexpr (NORM) {
+        read_x_lds(s_xn, k0, xv[0]);
+      } else if constexpr (!kLateX) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
           if (x_vec)
@@ -382,7 +475,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
         for (int m = 0; m < MT; ++m) {
           const uint32_t mm = (uint32_t)m < M_rt ? m : 0;
           float xc;
-          if constexpr (XBF16)
+          if constexpr (NORM)
+            xc = bf16_to_f32(s_xn[col]);
+          else if constexpr (XBF16)
             xc = bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)mm * cols + col]);
           else
             xc = static_cast<const float*>(x)[(size_t)mm * cols + col];
@@ -837,6 +932,49 @@ hipError_t launch_glu_kind(const DevTensor& t, const void* x, bool x_bf16, uint3
                            bool y_bf16, uint32_t y_stride, bool gelu, hipStream_t s) {
   return gelu ? launch_glu_m<KIND, kEpiGelu>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s)
               : launch_glu_m<KIND, kEpiSilu>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s);
+}
+
+// Norm-prologue GEMV, batch 1 (plain or gated epilogue): the same row and
+// step choices as the plain M = 1 launches and the gated launches.
+template <uint32_t KIND, int RPW, int S, int EPI, uint32_t NP>
+hipError_t launch_norm_np(const DevTensor& t, const NormIn& nin, uint32_t outs, void* y, bool y_bf16,
+                          uint32_t y_stride, hipStream_t s) {
+  constexpr uint32_t per_block = kWaves * (EPI == kEpiPlain ? RPW : RPW / 2);
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  const size_t lds = (size_t)nsteps * kStep * 2;
+  hipLaunchKernelGGL((gemv_kernel<KIND, 1, RPW, S, true, EPI, true, NP>), dim3((outs + per_block - 1) / per_block),
+                     dim3(kWaves * 64), lds, s, t, nullptr, y, 1u, (uint32_t)(y_bf16 ? 1u : 0u), 1u,
+                     EPI == kEpiPlain ? 0u : outs, y_stride, nin);
+  return hipGetLastError();
+}
+
+// Norm inputs held per thread: 8 up to 2048 columns, else 16.
+template <uint32_t KIND, int RPW, int S, int EPI>
+hipError_t launch_norm_t(const DevTensor& t, const NormIn& nin, uint32_t outs, void* y, bool y_bf16,
+                         uint32_t y_stride, hipStream_t s) {
+  if (t.cols <= 2048) return launch_norm_np<KIND, RPW, S, EPI, 8>(t, nin, outs, y, y_bf16, y_stride, s);
+  return launch_norm_np<KIND, RPW, S, EPI, 16>(t, nin, outs, y, y_bf16, y_stride, s);
+}
+
+template <uint32_t KIND, int RPW, int EPI>
+hipError_t launch_norm_s(const DevTensor& t, const NormIn& nin, uint32_t outs, void* y, bool y_bf16,
+                         uint32_t y_stride, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (nsteps == 1) return launch_norm_t<KIND, RPW, 1, EPI>(t, nin, outs, y, y_bf16, y_stride, s);
+  return launch_norm_t<KIND, RPW, 2, EPI>(t, nin, outs, y, y_bf16, y_stride, s);
+}
+
+// epi: kEpiPlain (y = W x, outs = rows) or a gated epilogue (outs = rows / 2).
+// Requires cols <= 256 * kNormPer.
+template <uint32_t KIND>
+hipError_t launch_norm_kind(const DevTensor& t, const NormIn& nin, int epi, void* y, bool y_bf16,
+                            uint32_t y_stride, hipStream_t s) {
+  if (t.cols > 256u * kNormPer) return hipErrorInvalidValue;
+  if (epi == kEpiSilu) return launch_norm_s<KIND, 2, kEpiSilu>(t, nin, t.rows / 2, y, y_bf16, y_stride, s);
+  if (epi == kEpiGelu) return launch_norm_s<KIND, 2, kEpiGelu>(t, nin, t.rows / 2, y, y_bf16, y_stride, s);
+  if (t.rows >= 65536) return launch_norm_s<KIND, 4, kEpiPlain>(t, nin, t.rows, y, y_bf16, t.rows, s);
+  if (t.rows >= 4096) return launch_norm_s<KIND, 2, kEpiPlain>(t, nin, t.rows, y, y_bf16, t.rows, s);
+  return launch_norm_s<KIND, 1, kEpiPlain>(t, nin, t.rows, y, y_bf16, t.rows, s);
 }
 
 }  // namespace gv

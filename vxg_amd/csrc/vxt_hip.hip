@@ -30,6 +30,8 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
                        size_t ws_bytes, hipStream_t s);
 hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
                           hipStream_t s);
+hipError_t launch_gemv_norm(const DevTensor& t, const NormIn& nin, int epi, void* y, bool y_bf16, uint32_t y_stride,
+                            hipStream_t s);
 hipError_t launch_gemv_glu(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* act, bool act_bf16,
                            uint32_t act_stride, bool gelu, hipStream_t s);
 hipError_t launch_glu_act(const float* gu, uint32_t m, uint32_t n_ff, bool gelu, void* act, bool act_bf16,
@@ -724,6 +726,30 @@ int vxt_hip_ffn_glu_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype
     }
     if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
     if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("gated FFN launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+int vxt_hip_norm_matmul_dev(void* ctx, void* tensor, const float* cur, const float* delta, const float* norm_w,
+                            float eps, float* cur_out, uint32_t mode, void* y, uint32_t y_dtype, uint32_t y_stride,
+                            void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
+    if (!cur || !norm_w || !y) fail(VXT_E_ARG, "null pointer");
+    if (!dtype_ok(y_dtype)) fail(VXT_E_ARG, "unknown dtype");
+    if (mode > VXT_NORM_GLU_GELU_TANH) fail(VXT_E_ARG, "unknown mode");
+    if (delta && (!cur_out || cur_out == cur || cur_out == delta))
+      fail(VXT_E_ARG, "with delta, cur_out must be a separate buffer");
+    if (t->cols > 4096) fail(VXT_E_UNSUPPORTED, "the norm prologue takes cols <= 4096");
+    const bool gated = mode != VXT_NORM_PLAIN;
+    if (gated && t->rows % 2 != 0) fail(VXT_E_SHAPE, "a [gate; up] tensor has an even row count");
+    if (gated && y_stride < t->rows / 2) fail(VXT_E_SHAPE, "y_stride < rows / 2");
+    vxt::NormIn nin{cur, delta, norm_w, delta ? cur_out : nullptr, eps};
+    const int epi = mode == VXT_NORM_PLAIN ? 0 : mode == VXT_NORM_GLU_SILU ? 1 : 2;
+    hipError_t e = vxt::launch_gemv_norm(t->dev(), nin, epi, y, y_dtype == VXT_DTYPE_BF16, gated ? y_stride : t->rows,
+                                         static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("norm matmul launch failed: ") + hipGetErrorString(e));
   });
 }
 

@@ -47,6 +47,7 @@ VXT_OK = 0
 VXT_E_ARG, VXT_E_SHAPE, VXT_E_FORMAT, VXT_E_DEVICE, VXT_E_UNSUPPORTED = -1, -2, -3, -4, -5
 DTYPE_F32, DTYPE_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
+NORM_PLAIN, NORM_GLU_SILU, NORM_GLU_GELU_TANH = 0, 1, 2
 KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
 
 ABI_SYMBOLS = (
@@ -55,7 +56,7 @@ ABI_SYMBOLS = (
     "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
-    "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev",
+    "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
     "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
@@ -154,6 +155,8 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_ffn_glu_dev.restype = C.c_int
     L.vxt_hip_rms_norm_dev.argtypes = [vp, vp, vp, vp, vp, u32, u32, u32, u32, C.c_float, vp, cp, sz]
     L.vxt_hip_rms_norm_dev.restype = C.c_int
+    L.vxt_hip_norm_matmul_dev.argtypes = [vp, vp, vp, vp, vp, C.c_float, vp, u32, vp, u32, u32, vp, cp, sz]
+    L.vxt_hip_norm_matmul_dev.restype = C.c_int
     L.vxt_hip_greedy_dev.argtypes = [vp, vp, u32, vp, vp, cp, sz]
     L.vxt_hip_last_kernel_ms.restype = C.c_int
     L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
@@ -579,6 +582,19 @@ class HipEngine:
         _check(load_library().vxt_hip_ffn_glu_dev(self.ctx, t.handle, x_ptr or None, x_dtype, batch_m,
                                                   act_ptr or None, act_dtype, stride, activation,
                                                   stream or None, buf, len(buf)), buf)
+
+    def norm_matmul_dev(self, t: GpuPackedTensor, cur_ptr: int, delta_ptr: int, weight_ptr: int, eps: float,
+                        cur_out_ptr: int, mode: int, y_ptr: int, y_dtype: int, y_stride: int | None = None,
+                        stream: int = 0) -> None:
+        """Batch-1 projection of ``bf16(rms_norm(cur [+ delta]) * w)`` in one
+        launch (``vxt_hip_norm_matmul_dev``); with ``delta_ptr`` the sum goes
+        to ``cur_out_ptr``."""
+        buf = _errbuf()
+        stride = (t.rows // 2 if mode != NORM_PLAIN else t.rows) if y_stride is None else y_stride
+        _check(load_library().vxt_hip_norm_matmul_dev(self.ctx, t.handle, cur_ptr or None, delta_ptr or None,
+                                                      weight_ptr or None, eps, cur_out_ptr or None, mode,
+                                                      y_ptr or None, y_dtype, stride, stream or None, buf,
+                                                      len(buf)), buf)
 
     def rms_norm_dev(self, cur_ptr: int, delta_ptr: int, weight_ptr: int, out_ptr: int, out_dtype: int,
                      dim: int, stride: int | None = None, batch_m: int = 1, eps: float = 1e-6,

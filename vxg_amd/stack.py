@@ -143,18 +143,29 @@ class DecodeStep:
     step.  The residual stream ``cur`` and the deltas are f32; the inputs of
     the projections are bf16.  ``embed`` may be the LM head itself (tied
     embeddings, llm_cpu.rs:480).  One step is 6 * layers + 4 launches.
+
+    ``fuse_norm`` (hidden <= 4096): the two RMSNorms of a layer are built
+    inside the projections that read them (``vxt_hip_norm_matmul_dev`` for
+    [q;k;v] and [gate;up]), the residual stream alternating between two
+    buffers (it ends a step in ``cur2``, see ``residual``); bit-identical,
+    4 * layers + 4 launches.  The final norm stays a
+    launch of its own: every workgroup of the prologue rebuilds the norm, and
+    the LM head has thousands of them.
     """
 
     def __init__(self, eng: engine.HipEngine, layers: Sequence[LayerWeights], norms: Sequence[LayerNorms],
                  output_norm: engine.DeviceBuffer, lm_head: engine.GpuPackedTensor,
                  embed: engine.GpuPackedTensor, eps: float = 1e-6, activation: int = engine.ACT_SILU,
-                 embed_scale: float = 1.0):
+                 embed_scale: float = 1.0, fuse_norm: bool = False):
         if not layers or len(norms) != len(layers):
             raise ValueError("one LayerNorms per layer, at least one layer")
         self.eng, self.layers, self.norms = eng, list(layers), list(norms)
         self.output_norm, self.lm_head, self.embed = output_norm, lm_head, embed
         self.eps, self.activation, self.embed_scale = eps, activation, embed_scale
+        self.fuse_norm = fuse_norm
         H = self.hidden = lm_head.cols
+        if fuse_norm and H > 4096:
+            raise ValueError("the fused norm takes hidden <= 4096")
         if embed.cols != H:
             raise ValueError("embedding width != hidden size")
         for i, L in enumerate(self.layers):
@@ -165,6 +176,7 @@ class DecodeStep:
         big_qkv = max(L.qkv.rows for L in self.layers)
         big_ff = max(L.gate_up.rows // 2 for L in self.layers)
         self.cur = eng.alloc(H * 4)
+        self.cur2 = eng.alloc(H * 4)       # second residual buffer (fused norms)
         self.delta = eng.alloc(H * 4)
         self.normed = eng.alloc(H * 2)
         self.qkv_out = eng.alloc(big_qkv * 2)
@@ -174,7 +186,7 @@ class DecodeStep:
 
     @property
     def launches(self) -> int:
-        return 6 * len(self.layers) + 4
+        return (4 * len(self.layers) + 4) if self.fuse_norm else (6 * len(self.layers) + 4)
 
     def set_token(self, token: int) -> None:
         import numpy as np
@@ -185,7 +197,14 @@ class DecodeStep:
         r = self.token.download(np.uint32, (2,))
         return int(r[0]), bool(r[1])
 
+    @property
+    def residual(self) -> engine.DeviceBuffer:
+        """The buffer holding the residual stream at the end of a step."""
+        return self.cur2 if self.fuse_norm else self.cur
+
     def enqueue(self, stream=None) -> None:
+        if self.fuse_norm:
+            return self._enqueue_fused(stream)
         e, s = self.eng, stream or self.eng.stream
         bf16, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
         H = self.hidden
@@ -205,10 +224,37 @@ class DecodeStep:
         e.matmul_dev(self.lm_head, self.normed.ptr, bf16, 1, self.logits.ptr, f32, s)
         e.greedy_dev(self.logits.ptr, self.lm_head.rows, self.token.ptr, s)
 
+    def _enqueue_fused(self, stream=None) -> None:
+        e, s = self.eng, stream or self.eng.stream
+        bf16, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
+        H = self.hidden
+        bufs, c = (self.cur, self.cur2), 0
+        glu = engine.NORM_GLU_GELU_TANH if self.activation == engine.ACT_GELU_TANH else engine.NORM_GLU_SILU
+        e.embed_dev(self.embed, self.token.ptr, 1, bufs[0].ptr, H, self.embed_scale, s)
+
+        def normed(t, w, mode, y, ydt, ystride, add):
+            nonlocal c
+            e.norm_matmul_dev(t, bufs[c].ptr, self.delta.ptr if add else 0, w.ptr, self.eps,
+                              bufs[1 - c].ptr if add else 0, mode, y, ydt, ystride, s)
+            if add:
+                c = 1 - c
+
+        for i, (L, N) in enumerate(zip(self.layers, self.norms)):
+            normed(L.qkv, N.attn, engine.NORM_PLAIN, self.qkv_out.ptr, bf16, None, i > 0)
+            e.matmul_dev(L.o, self.qkv_out.ptr, bf16, 1, self.delta.ptr, f32, s)
+            normed(L.gate_up, N.post_attn, glu, self.act.ptr, bf16, L.gate_up.rows // 2, True)
+            e.matmul_dev(L.down, self.act.ptr, bf16, 1, self.delta.ptr, f32, s)
+        # 2 * layers - 1 swaps: the stream is in bufs[1] (cur2), where the
+        # final add-norm leaves it.
+        e.rms_norm_dev(bufs[c].ptr, self.delta.ptr, self.output_norm.ptr, self.normed.ptr, bf16, H, H, 1,
+                       self.eps, s)
+        e.matmul_dev(self.lm_head, self.normed.ptr, bf16, 1, self.logits.ptr, f32, s)
+        e.greedy_dev(self.logits.ptr, self.lm_head.rows, self.token.ptr, s)
+
     def capture(self) -> engine.Graph:
         """Record one step into a HIP graph; each replay advances one token."""
         return self.eng.capture(lambda s: self.enqueue(s))
 
     def free(self) -> None:
-        for b in (self.cur, self.delta, self.normed, self.qkv_out, self.act, self.logits, self.token):
+        for b in (self.cur, self.cur2, self.delta, self.normed, self.qkv_out, self.act, self.logits, self.token):
             b.free()
