@@ -239,6 +239,62 @@ VXT_API int vxt_hip_norm_matmul_dev(void* ctx, void* tensor, const float* cur, c
                                     uint32_t y_dtype, uint32_t y_stride, void* stream, char* err,
                                     size_t err_cap);
 
+/* ---- Weight containers ----------------------------------------------------
+ * Readers over bytes the caller holds (e.g. a mapped file); they keep no
+ * pointer after returning.  Offsets below are byte offsets into those bytes. */
+
+/* One tensor section of a .vxt (VXT1) archive (format.rs:178-294 layout).
+ * The plane fields are filled for kind 2 (KIND_CODEBOOK) only. */
+typedef struct VxtArchiveEntry {
+    uint64_t name_off, name_len;    /* UTF-8 name                            */
+    uint32_t kind, sub;             /* kind 2 = codebook, sub = bits         */
+    uint64_t rows, cols, padded_cols;
+    uint64_t section_off, section_len;
+    uint64_t centroids_off;         /* 16 f32                                */
+    uint64_t scales_off, n_scales;  /* u16 [rows * padded_cols / 128]        */
+    uint64_t words_off, n_words;    /* u32 [rows * padded_cols / 128 * 4 * bits] */
+    uint64_t row_ptr_off, n_row_ptr;/* u32 [rows + 1]                        */
+    uint64_t outliers_off, n_outliers; /* u32 col | f16 << 16                */
+} VxtArchiveEntry;
+
+/* Parse and verify a .vxt archive (read_vxt_model, format.rs:301-451): the
+ * archive and per-section FNV-1a64 tags, the codebook header and plane
+ * rules (bits 3 or 4, padded_cols = ceil(cols/256)*256, plane lengths) and
+ * the outlier CSR rules (format.rs:565-574).  Call with entries = NULL to
+ * get *count, then with an array of `cap` >= *count.  *meta_count receives
+ * the metadata entry count (values are stepped over).  Sections of kind 7
+ * (entropy-coded TurboWht) stop the walk with VXT_E_UNSUPPORTED. */
+VXT_API int vxt_hip_vxt_parse(const uint8_t* bytes, size_t len, VxtArchiveEntry* entries, uint32_t cap,
+                              uint32_t* count, uint32_t* meta_count, char* err, size_t err_cap);
+
+/* Upload a parsed 4-bit codebook entry of the same bytes to the device (the
+ * path upload_packed takes for PackedTensor::Codebook, metal.rs:162-177). */
+VXT_API void* vxt_hip_upload_vxt_entry(void* ctx, const uint8_t* bytes, size_t len, const VxtArchiveEntry* e,
+                                       char* err, size_t err_cap);
+
+/* One tensor of a GGUF v2/v3 file (GgufTensorMeta, gguf.rs:52-73). */
+typedef struct VxtGgufTensor {
+    uint64_t name_off, name_len;
+    uint32_t ggml_type, n_dims;     /* ggml type id (8 = Q8_0)               */
+    uint64_t ne[8];                 /* ne[0] = contiguous cols               */
+    uint64_t data_off, data_len;    /* absolute; data_len 0 if unsupported   */
+    uint32_t supported, reserved;   /* type with a known byte size (gguf.rs:32-41) */
+} VxtGgufTensor;
+
+/* Parse a GGUF file's header, metadata (general.alignment honoured, the rest
+ * stepped over by type) and tensor table (GgufView::parse, gguf.rs:83-158);
+ * every supported tensor's bytes are checked to lie inside the file
+ * (tensor_bytes, gguf.rs:160-172).  Two-call pattern as vxt_hip_vxt_parse. */
+VXT_API int vxt_hip_gguf_parse(const uint8_t* bytes, size_t len, VxtGgufTensor* tensors, uint32_t cap,
+                               uint32_t* count, uint32_t* version, uint64_t* alignment, char* err,
+                               size_t err_cap);
+
+/* Upload a Q8_0 GGUF matrix (rows = ne[1] * ne[2] ..., cols = ne[0]) from
+ * its bytes as they lie in the file, with no f32 expansion on the host
+ * (llm.rs:164 expands; this keeps the blocks). */
+VXT_API void* vxt_hip_upload_gguf_q8_0(void* ctx, const uint8_t* bytes, size_t len, const VxtGgufTensor* t,
+                                       char* err, size_t err_cap);
+
 /* Embedding rows for batch_m token ids held in device memory (tokens[m]):
  * out[m * out_stride + c] = decode_row(tokens[m])[c] for c < cols, bit-exact,
  * multiplied by embed_scale when |embed_scale - 1| > 1e-7 (llm_cpu.rs:

@@ -57,6 +57,7 @@ ABI_SYMBOLS = (
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
     "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
+    "vxt_hip_vxt_parse", "vxt_hip_upload_vxt_entry", "vxt_hip_gguf_parse", "vxt_hip_upload_gguf_q8_0",
     "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
@@ -96,6 +97,21 @@ class Cb4G64View(C.Structure):
 class ChainOpView(C.Structure):
     _fields_ = [("tensor", C.c_void_p), ("x", C.c_void_p), ("y", C.c_void_p), ("y_dtype", C.c_uint32),
                 ("reserved", C.c_uint32)]
+
+
+class VxtArchiveEntry(C.Structure):
+    _fields_ = [("name_off", C.c_uint64), ("name_len", C.c_uint64), ("kind", C.c_uint32), ("sub", C.c_uint32),
+                ("rows", C.c_uint64), ("cols", C.c_uint64), ("padded_cols", C.c_uint64),
+                ("section_off", C.c_uint64), ("section_len", C.c_uint64), ("centroids_off", C.c_uint64),
+                ("scales_off", C.c_uint64), ("n_scales", C.c_uint64), ("words_off", C.c_uint64),
+                ("n_words", C.c_uint64), ("row_ptr_off", C.c_uint64), ("n_row_ptr", C.c_uint64),
+                ("outliers_off", C.c_uint64), ("n_outliers", C.c_uint64)]
+
+
+class VxtGgufTensor(C.Structure):
+    _fields_ = [("name_off", C.c_uint64), ("name_len", C.c_uint64), ("ggml_type", C.c_uint32),
+                ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 8), ("data_off", C.c_uint64),
+                ("data_len", C.c_uint64), ("supported", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 class HipJob(C.Structure):
@@ -157,6 +173,16 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_rms_norm_dev.restype = C.c_int
     L.vxt_hip_norm_matmul_dev.argtypes = [vp, vp, vp, vp, vp, C.c_float, vp, u32, vp, u32, u32, vp, cp, sz]
     L.vxt_hip_norm_matmul_dev.restype = C.c_int
+    L.vxt_hip_vxt_parse.argtypes = [vp, sz, C.POINTER(VxtArchiveEntry), u32, C.POINTER(u32), C.POINTER(u32),
+                                    cp, sz]
+    L.vxt_hip_vxt_parse.restype = C.c_int
+    L.vxt_hip_upload_vxt_entry.argtypes = [vp, vp, sz, C.POINTER(VxtArchiveEntry), cp, sz]
+    L.vxt_hip_upload_vxt_entry.restype = vp
+    L.vxt_hip_gguf_parse.argtypes = [vp, sz, C.POINTER(VxtGgufTensor), u32, C.POINTER(u32), C.POINTER(u32),
+                                     C.POINTER(C.c_uint64), cp, sz]
+    L.vxt_hip_gguf_parse.restype = C.c_int
+    L.vxt_hip_upload_gguf_q8_0.argtypes = [vp, vp, sz, C.POINTER(VxtGgufTensor), cp, sz]
+    L.vxt_hip_upload_gguf_q8_0.restype = vp
     L.vxt_hip_greedy_dev.argtypes = [vp, vp, u32, vp, vp, cp, sz]
     L.vxt_hip_last_kernel_ms.restype = C.c_int
     L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
