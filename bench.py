@@ -252,6 +252,35 @@ def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: in
             "ms_per_token": ms_tok, "launches_per_token": launches, "last_token": tok, "nonfinite": bad}
 
 
+def bench_attn(eng, seq: int, n_head: int, n_kv: int, hd: int, calls: int = 200, seed: int = 6):
+    """Decode attention over a Q8_0 KV cache of ``seq`` positions: one
+    ``vxt_hip_attn_q8_dev`` call per step, timed as a captured graph of
+    ``calls`` calls.  Bytes: the cache's K and V values and scales."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    cache = eng.kv_q8_cache(seq, n_kv, hd)
+    per = n_kv * hd
+    # fill the cache: values and scales straight into the planes
+    cache.k_qs.upload(rng.integers(-127, 128, size=seq * per, dtype=np.int8))
+    cache.v_qs.upload(rng.integers(-127, 128, size=seq * per, dtype=np.int8))
+    d = np.float16(rng.uniform(0.002, 0.02, size=seq * per // 32)).view(np.uint16)
+    cache.k_d.upload(d)
+    cache.v_d.upload(d)
+    q = eng.to_device(rng.standard_normal(n_head * hd).astype(np.float32))
+    out = eng.alloc(n_head * hd * 4)
+    cache.attend(q.ptr, n_head, seq, out.ptr, 0, eng.stream)      # sizes the workspace
+    eng.synchronize()
+    g = eng.capture(lambda s: [cache.attend(q.ptr, n_head, seq, out.ptr, 0, s) for _ in range(calls)])
+    g.launch(1)
+    ms = g.launch(1) / calls
+    g.free()
+    q.free()
+    out.free()
+    cache.free()
+    nbytes = 2 * seq * per * (1 + 2 / 32)
+    return {"us": ms * 1e3, "bytes": nbytes, "GBps": nbytes / (ms * 1e-3) / 1e9}
+
+
 # --------------------------------------------------------------------------
 # CPU baseline (reference CPU path, C restatement in oracle/)
 # --------------------------------------------------------------------------
@@ -290,7 +319,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="0,2,3,4", help="secondary configurations to run")
+    ap.add_argument("--configs", default="0,2,3,4,a",
+                    help="secondary configurations to run (a: KV-Q8 decode attention)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()
 
@@ -376,6 +406,15 @@ def main():
             log(f"  {rw['tokens_per_s']:.1f} tok/s ({rw['ms_per_token']*1e3:.1f} us/token, "
                 f"{rw['launches_per_token']} launches)")
         del head_m
+
+    if "a" in run:
+        for seq, nh, nkv in ((4096, 16, 16), (32768, 16, 16), (32768, 16, 4), (131072, 16, 4)):
+            ra = bench_attn(eng, seq, nh, nkv, 128)
+            secondary.append({"config": f"attention over a Q8_0 KV cache: {nh} heads / {nkv} kv heads x 128, "
+                                        f"{seq} positions, one decode step",
+                              "kernel_us": round(ra["us"], 2), "bytes": int(ra["bytes"]),
+                              "GBps": round(ra["GBps"], 1), "frac_hbm": round(ra["GBps"] / HBM_PEAK_GBS, 4)})
+            log(f"  attention seq={seq} heads={nh}/{nkv}: {ra['us']:.2f} us, {ra['GBps']:.1f} GB/s")
 
     cpu = None
     if not args.no_cpu:

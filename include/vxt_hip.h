@@ -239,6 +239,39 @@ VXT_API int vxt_hip_norm_matmul_dev(void* ctx, void* tensor, const float* cur, c
                                     uint32_t y_dtype, uint32_t y_stride, void* stream, char* err,
                                     size_t err_cap);
 
+/* ---- Q8_0 KV cache (decode attention) --------------------------------------
+ * The cache of one layer, device memory the caller allocates: position t's
+ * values at k_qs[t * n_kv * head_dim ...] (int8, 16-byte aligned plane) and
+ * their scales at k_d[t * n_kv * head_dim / 32 ...] (f16 bits), likewise for
+ * V.  Every value and scale has the bits of KvQ8Block::quantize
+ * (llm_prefill.rs:27-42); the block's two fields are kept as two planes. */
+typedef struct VxtKvQ8Cache {
+    void* k_qs;        /* int8 [max_seq][n_kv * head_dim]                     */
+    void* k_d;         /* f16  [max_seq][n_kv * head_dim / 32]                */
+    void* v_qs;
+    void* v_d;
+    uint32_t max_seq, n_kv, head_dim, reserved;   /* head_dim 32/64/128/256 */
+} VxtKvQ8Cache;
+
+/* Quantise one position's K and V ([n_kv * head_dim] f32 each, already
+ * normed and rotated) into row pos: the cache writes of step_full_gqa_q8
+ * (llm_prefill.rs:300-313). */
+VXT_API int vxt_hip_kv_q8_append_dev(void* ctx, const VxtKvQ8Cache* cache, const float* k, const float* v,
+                                     uint32_t pos, void* stream, char* err, size_t err_cap);
+
+/* Attention of one decode step over positions [0, seq_len): q [n_head *
+ * head_dim] (normed, rotated), head h reads kv head h / (n_head / n_kv);
+ * scores q.K / sqrt(head_dim), softmax, sum of weights times V; gate (NULL
+ * or [n_head * head_dim]) multiplies by 1 / (1 + exp(-g)); out [n_head *
+ * head_dim] f32.  The scoring, softmax and accumulation of step_full_gqa_q8
+ * (llm_prefill.rs:315-367) with KvQ8Block::dot_f32 / axpy_f32, computed over
+ * chunks of positions in parallel (fp32; the order of the sums differs).
+ * Uses the context workspace (rules of vxt_hip_matmul_dev).  n_head / n_kv
+ * <= 8. */
+VXT_API int vxt_hip_attn_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const float* q, uint32_t n_head,
+                                uint32_t seq_len, const float* gate, float* out, void* stream, char* err,
+                                size_t err_cap);
+
 /* ---- Weight containers ----------------------------------------------------
  * Readers over bytes the caller holds (e.g. a mapped file); they keep no
  * pointer after returning.  Offsets below are byte offsets into those bytes. */

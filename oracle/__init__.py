@@ -95,6 +95,8 @@ def lib():
         L.vxo_glu.restype = None
         L.vxo_rms_norm.argtypes = [vp, vp, sz, C.c_float, vp]
         L.vxo_rms_norm.restype = None
+        L.vxo_attn_q8.argtypes = [vp, vp, vp, sz, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]
+        L.vxo_attn_q8.restype = None
         L.vxo_greedy.argtypes = [vp, sz, C.POINTER(C.c_uint32)]
         L.vxo_greedy.restype = C.c_uint32
         _lib = L
@@ -306,4 +308,27 @@ def rms_norm(x, w, eps: float) -> np.ndarray:
     assert w.size >= x.size
     out = np.empty_like(x)
     lib().vxo_rms_norm(_ptr(x), _ptr(w), x.size, float(eps), _ptr(out))
+    return out
+
+
+def kv_q8_blocks(x, n_kv: int, hd: int) -> np.ndarray:
+    """One position's K or V rows as KvQ8Block bytes [n_kv * hd / 32][34]
+    (the quantize loop of llm_prefill.rs:306-312)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(n_kv * hd // 32, 32)
+    out = np.empty((x.shape[0], 34), dtype=np.uint8)
+    for i in range(x.shape[0]):
+        lib().vxo_q8_quantize(_ptr(x[i]), _ptr(out[i]))
+    return out
+
+
+def attn_q8(q, k_blocks, v_blocks, seq_len: int, n_head: int, n_kv: int, hd: int, gate=None) -> np.ndarray:
+    """Attention of one decode step over a Q8 cache (vxo_attn_q8)."""
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+    kb = np.ascontiguousarray(k_blocks, dtype=np.uint8).reshape(-1)
+    vb = np.ascontiguousarray(v_blocks, dtype=np.uint8).reshape(-1)
+    assert q.size == n_head * hd and kb.size >= seq_len * n_kv * hd // 32 * 34 and vb.size == kb.size
+    g = None if gate is None else np.ascontiguousarray(gate, dtype=np.float32).reshape(-1)
+    out = np.empty(n_head * hd, dtype=np.float32)
+    lib().vxo_attn_q8(_ptr(q), _ptr(kb), _ptr(vb), seq_len, n_head, n_kv, hd,
+                      None if g is None else _ptr(g), _ptr(out))
     return out

@@ -537,6 +537,54 @@ VXO_API void vxo_rms_norm(const float* x, const float* w, size_t n, float eps, f
     for (size_t i = 0; i < n; ++i) out[i] = x[i] * scale * w[i];
 }
 
+/* llm_prefill.rs:317-367: the attention of one decode step over a Q8 KV
+ * cache, after q and k are normed and rotated and the step's K/V blocks are
+ * in the cache.  q: [n_head * hd]; k_blocks / v_blocks: 34-byte KvQ8Block
+ * rows laid out [t][kv_head][hd / 32] for t < seq_len; gate: NULL or
+ * [n_head * hd]; out: [n_head * hd].  Scores are block dots summed in block
+ * order, scaled by 1 / sqrt(hd); softmax subtracts the running max; the
+ * output accumulates axpy_f32 of every position in order; a gate multiplies
+ * by 1 / (1 + exp(-g)). */
+VXO_API void vxo_attn_q8(const float* q, const uint8_t* k_blocks, const uint8_t* v_blocks, size_t seq_len,
+                         uint32_t n_head, uint32_t n_kv, uint32_t hd, const float* gate, float* out) {
+    const size_t bph = hd / 32, stride = (size_t)n_kv * bph;
+    const uint32_t gqa = n_head / n_kv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* scores = (float*)malloc((seq_len ? seq_len : 1) * sizeof(float));
+    for (uint32_t h = 0; h < n_head; ++h) {
+        const uint32_t kv_h = h / gqa;
+        const float* qh = q + (size_t)h * hd;
+        float max_s = -INFINITY;
+        for (size_t t = 0; t < seq_len; ++t) {
+            const uint8_t* kb = k_blocks + (t * stride + (size_t)kv_h * bph) * 34;
+            float dot = 0.0f;
+            for (size_t b = 0; b < bph; ++b) dot += vxo_q8_dot_f32(kb + b * 34, qh + b * 32);
+            const float sc = dot * scale;
+            scores[t] = sc;
+            if (sc > max_s) max_s = sc;
+        }
+        float sum_exp = 0.0f;
+        for (size_t t = 0; t < seq_len; ++t) {
+            const float e = expf(scores[t] - max_s);
+            scores[t] = e;
+            sum_exp += e;
+        }
+        const float inv_sum = 1.0f / sum_exp;
+        float* oh = out + (size_t)h * hd;
+        for (uint32_t i = 0; i < hd; ++i) oh[i] = 0.0f;
+        for (size_t t = 0; t < seq_len; ++t) {
+            const float w = scores[t] * inv_sum;
+            const uint8_t* vb = v_blocks + (t * stride + (size_t)kv_h * bph) * 34;
+            for (size_t b = 0; b < bph; ++b) vxo_q8_axpy_f32(vb + b * 34, w, oh + b * 32);
+        }
+        if (gate) {
+            const float* gh = gate + (size_t)h * hd;
+            for (uint32_t i = 0; i < hd; ++i) oh[i] *= 1.0f / (1.0f + expf(-gh[i]));
+        }
+    }
+    free(scores);
+}
+
 /* Greedy selection.  The index follows the greedy branch of
  * sample_logits_top_k_p (llm_ops.rs:307-327): an empty input gives 0; else a
  * forward scan from (best_v = -inf, best_i = 0) that takes index i only when

@@ -39,6 +39,10 @@ silu / gelu_tanh / glu     f64 formulas (tanh from numpy) within 4 ulp over
 llm_prefill.rs:66)          signs; act(g) * u equals the product of the parts
 rms_norm (llm_ops.rs:48)    f64 computation within 1e-6; constant rows (closed
                             form c / sqrt(c^2 + eps)); zero row; weight scaling
+attn_q8 (llm_prefill.rs:   one position: exactly the dequantised V block; f64
+317-367)                    softmax attention over the dequantised cache within
+                            1e-5 max|V|; GQA head-to-KV mapping; q = 0 gives the
+                            mean of V; the gate is the sigmoid factor
 greedy (llm_ops.rs:318,     the six tie / NaN / inf cases of metal_llm_tests.rs:
 vxt_llm_ops.metal:569)      95-117 with hand-derived answers; every array of
                             length <= 4 over {-inf,-1,-0,+0,denormal,1,inf,NaN}
@@ -529,3 +533,62 @@ def test_rms_norm_pins():
     x = rng.standard_normal(64).astype(np.float32)
     assert np.array_equal(oracle.rms_norm(x, np.full(64, 2.0, np.float32), 1e-6),
                           oracle.rms_norm(x, np.ones(64, np.float32), 1e-6) * 2)
+
+
+# ---------------------------------------------------------------- attention over a Q8 cache
+
+def q8_cache(seq, n_kv, hd, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    K = (rng.standard_normal((seq, n_kv * hd)) * scale).astype(np.float32)
+    V = rng.standard_normal((seq, n_kv * hd)).astype(np.float32)
+    kb = np.concatenate([oracle.kv_q8_blocks(K[t], n_kv, hd) for t in range(seq)])
+    vb = np.concatenate([oracle.kv_q8_blocks(V[t], n_kv, hd) for t in range(seq)])
+    return kb, vb
+
+
+def attn_f64(q, kb, vb, seq, n_head, n_kv, hd):
+    Kd = oracle.q8_dequant(kb).reshape(seq, n_kv, hd).astype(np.float64)
+    Vd = oracle.q8_dequant(vb).reshape(seq, n_kv, hd).astype(np.float64)
+    out = np.zeros((n_head, hd))
+    for h in range(n_head):
+        kv = h // (n_head // n_kv)
+        s = Kd[:, kv, :] @ q.reshape(n_head, hd)[h].astype(np.float64) / np.sqrt(hd)
+        p = np.exp(s - s.max())
+        out[h] = (p / p.sum()) @ Vd[:, kv, :]
+    return out.reshape(-1), np.abs(Vd).max()
+
+
+def test_attn_q8_single_position_is_the_v_block():
+    kb, vb = q8_cache(1, 2, 64, seed=1)
+    q = np.random.default_rng(2).standard_normal(4 * 64).astype(np.float32)
+    out = oracle.attn_q8(q, kb, vb, 1, 4, 2, 64).reshape(4, 64)
+    vd = oracle.q8_dequant(vb).reshape(2, 64)
+    for h in range(4):
+        assert np.array_equal(out[h].view(np.uint32), vd[h // 2].view(np.uint32))
+
+
+@pytest.mark.parametrize("seq,n_head,n_kv,hd", [(7, 4, 4, 32), (100, 8, 2, 128), (513, 4, 1, 64)])
+def test_attn_q8_vs_f64(seq, n_head, n_kv, hd):
+    kb, vb = q8_cache(seq, n_kv, hd, seed=seq, scale=0.3)
+    q = np.random.default_rng(seq).standard_normal(n_head * hd).astype(np.float32)
+    got = oracle.attn_q8(q, kb, vb, seq, n_head, n_kv, hd)
+    ref, vmax = attn_f64(q, kb, vb, seq, n_head, n_kv, hd)
+    assert np.abs(got - ref).max() <= 1e-5 * vmax
+
+
+def test_attn_q8_gqa_mapping_uniform_scores_and_gate():
+    seq, n_kv, hd = 9, 2, 32
+    kb, vb = q8_cache(seq, n_kv, hd, seed=5)
+    vb = vb.reshape(seq, n_kv, 1, 34).copy()
+    vb[:, 1, :, 2:] = 0                                    # kv head 1: all-zero values
+    vb = vb.reshape(-1, 34)
+    q = np.random.default_rng(3).standard_normal(4 * hd).astype(np.float32)
+    out = oracle.attn_q8(q, kb, vb, seq, 4, n_kv, hd).reshape(4, hd)
+    assert np.all(out[2:] == 0) and np.any(out[:2] != 0)   # heads 2, 3 read kv head 1
+    zero = oracle.attn_q8(np.zeros(4 * hd, np.float32), kb, vb, seq, 4, n_kv, hd).reshape(4, hd)
+    vmean = oracle.q8_dequant(vb).reshape(seq, n_kv, hd).astype(np.float64).mean(axis=0)
+    assert np.abs(zero[0] - vmean[0]).max() <= 1e-6 * np.abs(vmean[0]).max()
+    g = np.random.default_rng(4).standard_normal(4 * hd).astype(np.float32)
+    gated = oracle.attn_q8(q, kb, vb, seq, 4, n_kv, hd, gate=g).reshape(4, hd)
+    sig = 1 / (1 + np.exp(-g.astype(np.float64)))
+    assert np.allclose(gated, out * sig.reshape(4, hd), rtol=1e-6, atol=1e-30)

@@ -1,0 +1,355 @@
+// attn.hip -- Q8_0 KV cache for decode: append one position, attend over
+// the cache.
+//
+// Reference: KvQ8Block (llm_prefill.rs:17-63) and the attention of
+// step_full_gqa_q8 (llm_prefill.rs:300-367).
+//
+// Device layout (the caller's VxtKvQ8Cache; row t holds position t):
+//   k_qs, v_qs  int8 [max_seq][n_kv * hd]        (16-byte aligned rows)
+//   k_d,  v_d   f16  [max_seq][n_kv * hd / 32]   (one scale per 32 values)
+// -- the KvQ8Block's two fields as separate planes, so a position's values
+// load as aligned 16-byte pieces.  The bits of every value and scale are
+// those KvQ8Block::quantize produces.
+//
+// Append: one lane per value, a 32-lane group per block: amax of |x| (NaN
+// ignored, as f32::max does), d = f16(amax / 127) rounded to nearest even,
+// q = round_ties_even(x / f32(d)) clamped to +-127 (NaN -> 0).
+//
+// Attention (split sequence): workgroup (kv head, chunk of positions) serves
+// the query heads that share the kv head.  Each position is read once: a
+// position's K and V rows are split across hd / 16 lanes (16 values each),
+// all requested up front; the dot with every head's q (staged in LDS) is
+// reduced over those lanes and scaled by 1 / sqrt(hd); the chunk's scores
+// stay in LDS; the chunk's max m, the sum l of exp(s - m) and sum exp(s - m) V
+// go to a partials buffer.  A second kernel merges the chunks per head
+// (exp(m_c - m) rescaling), divides by the total and applies the optional
+// sigmoid gate.  The sums run in a
+// different order from the CPU loop (fp32, parity by tolerance).
+#include "common.hpp"
+
+#include <algorithm>
+
+namespace vxt {
+
+struct KvQ8Dev {
+  int8_t* k_qs;
+  uint16_t* k_d;
+  int8_t* v_qs;
+  uint16_t* v_d;
+  uint32_t max_seq, n_kv, hd;
+};
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr uint32_t kMaxGroup = 8;   // query heads per kv head
+
+// f32 -> f16 bits, round to nearest even, subnormals kept (fp16.rs:33-77).
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float val) {
+  const uint32_t b = __float_as_uint(val);
+  const uint32_t sign = (b >> 16) & 0x8000u;
+  const int32_t exp = (int32_t)((b >> 23) & 0xffu);
+  const uint32_t mant = b & 0x007fffffu;
+  if (exp == 255) return mant ? (sign | 0x7e00u | (mant >> 13)) : (sign | 0x7c00u);
+  const int32_t unb = exp - 127;
+  if (unb > 15) return sign | 0x7c00u;
+  if (unb < -25) return sign;
+  if (unb < -14) {
+    const uint32_t shift = (uint32_t)(-14 - unb);
+    const uint32_t full = mant | 0x00800000u;
+    const uint32_t rs = 13u + shift;
+    const uint32_t half = 1u << (rs - 1), rem = full & ((1u << rs) - 1u);
+    uint32_t m16 = full >> rs;
+    if (rem > half || (rem == half && (m16 & 1u))) m16 += 1;
+    return sign | m16;
+  }
+  const uint32_t e16 = (uint32_t)(unb + 15) << 10;
+  const uint32_t rem = mant & 0x1fffu;
+  uint32_t m16 = mant >> 13;
+  if (rem > 0x1000u || (rem == 0x1000u && (m16 & 1u))) {
+    m16 += 1;
+    if (m16 == 0x0400u) return sign | (e16 + 0x0400u);
+  }
+  return sign | e16 | m16;
+}
+
+__global__ __launch_bounds__(kThreads) void kv_append_kernel(KvQ8Dev c, const float* __restrict__ k,
+                                                            const float* __restrict__ v, uint32_t pos) {
+#pragma clang fp contract(off)
+  const uint32_t per = c.n_kv * c.hd;
+  const uint32_t e = blockIdx.x * kThreads + threadIdx.x;   // per % 32 == 0: a 32-group never straddles K/V
+  const bool live = e < 2u * per;
+  const bool is_v = e >= per;
+  const uint32_t i = is_v ? e - per : e;
+  const float x = live ? (is_v ? v[i] : k[i]) : 0.0f;
+  const float a = fabsf(x);
+  float amax = a == a ? a : 0.0f;
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  const uint32_t dh = f32_to_f16_bits(amax / 127.0f);
+  const float df = f16_to_f32_exact(dh);
+  const float inv = df > 0.0f ? 1.0f / df : 0.0f;
+  const float r = rintf(x * inv);
+  const int q = r != r ? 0 : (int)fminf(fmaxf(r, -127.0f), 127.0f);
+  if (!live) return;
+  int8_t* qs = is_v ? c.v_qs : c.k_qs;
+  uint16_t* ds = is_v ? c.v_d : c.k_d;
+  qs[(size_t)pos * per + i] = (int8_t)q;
+  if ((i & 31u) == 0) ds[(size_t)pos * (per / 32) + i / 32] = (uint16_t)dh;
+}
+
+// 16 int8 -> f32
+__device__ __forceinline__ void unpack16(const u32x4 w, float (&f)[16]) {
+  const uint32_t a[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((a[j >> 2] >> ((j & 3) * 8)) & 0xffu);
+}
+
+// LPT lanes per position (hd = 16 * LPT).  A chunk is 4 passes of the
+// 4 * TPW positions the workgroup covers at once, so every lane requests its
+// 4 K pieces and 4 V pieces (16 bytes each, plus scales) before any wait:
+// one trip to memory per workgroup.
+template <int LPT>
+__global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const float* __restrict__ q, uint32_t group,
+                                                             uint32_t seq_len, uint32_t n_chunks,
+                                                             float* __restrict__ part) {
+  constexpr uint32_t HD = LPT * 16, TPW = 64 / LPT, PASSES = 4, CH = PASSES * 4 * TPW;
+  extern __shared__ __attribute__((aligned(16))) float smem[];
+  float* s_q = smem;                       // [group][HD]
+  float* s_p = smem + group * HD;          // [group][CH] scores, then exp(s - m)
+  float* s_red = s_p + group * CH;         // [4 waves][4 heads][HD] reduction space
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t slot = lane / LPT, sub = lane % LPT;
+  const uint32_t kvh = blockIdx.x, ck = blockIdx.y;
+  const uint32_t t0 = ck * CH, n = min(seq_len - t0, CH);
+  const uint32_t row_q = c.n_kv * HD, row_d = c.n_kv * (HD / 32);
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  // q first (small, cached), then every K and V piece of the chunk.
+  float qv[kMaxGroup * HD / kThreads + 1];
+  const uint32_t nq = group * HD;
+#pragma unroll
+  for (uint32_t r = 0; r < kMaxGroup * HD / kThreads + 1; ++r) {
+    const uint32_t i = tid + r * kThreads;
+    qv[r] = i < nq ? q[(size_t)kvh * nq + i] : 0.0f;
+  }
+  // Raw scale bits: converting them here would wait for the load (and, the
+  // memory counter draining in order, for every load issued before it).
+  u32x4 kw[PASSES], vw[PASSES];
+  uint32_t kdb[PASSES], vdb[PASSES];
+  uint32_t tl[PASSES];
+#pragma unroll
+  for (uint32_t p = 0; p < PASSES; ++p) {
+    tl[p] = (p * 4u + wave) * TPW + slot;
+    const uint32_t tc = t0 + (tl[p] < n ? tl[p] : n - 1);
+    const size_t qo = (size_t)tc * row_q + kvh * HD + sub * 16u;
+    const size_t dof = (size_t)tc * row_d + kvh * (HD / 32) + sub / 2u;
+    kw[p] = *reinterpret_cast<const u32x4*>(c.k_qs + qo);
+    vw[p] = *reinterpret_cast<const u32x4*>(c.v_qs + qo);
+    kdb[p] = c.k_d[dof];
+    vdb[p] = c.v_d[dof];
+  }
+#pragma unroll
+  for (uint32_t r = 0; r < kMaxGroup * HD / kThreads + 1; ++r) {
+    const uint32_t i = tid + r * kThreads;
+    if (i < nq) s_q[i] = qv[r];
+  }
+  __syncthreads();
+
+  // ---- scores
+#pragma unroll
+  for (uint32_t p = 0; p < PASSES; ++p) {
+    float kf[16];
+    unpack16(kw[p], kf);
+    for (uint32_t g = 0; g < group; ++g) {
+      const float* qg = s_q + g * HD + sub * 16u;
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = __builtin_fmaf(qg[j], kf[j], acc);
+      acc *= f16_to_f32_exact(kdb[p]);
+#pragma unroll
+      for (int off = 1; off < LPT; off <<= 1) acc += __shfl_xor(acc, off, 64);
+      if (sub == 0 && tl[p] < n) s_p[g * CH + tl[p]] = acc * scale;
+    }
+  }
+  __syncthreads();
+
+  // ---- chunk softmax pieces: one wave per head
+  for (uint32_t g = wave; g < group; g += 4u) {
+    float m = -__builtin_inff();
+    for (uint32_t t = lane; t < n; t += 64u) m = fmaxf(m, s_p[g * CH + t]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    float l = 0.0f;
+    for (uint32_t t = lane; t < n; t += 64u) {
+      const float e = expf(s_p[g * CH + t] - m);
+      s_p[g * CH + t] = e;
+      l += e;
+    }
+    l = wave_sum(l);
+    if (lane == 0) {
+      float* pp = part + ((size_t)(kvh * group + g) * n_chunks + ck) * (HD + 2);
+      pp[0] = m;
+      pp[1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- sum exp(s - m) V from the registers, four heads at a time
+  float vf[PASSES][16];
+#pragma unroll
+  for (uint32_t p = 0; p < PASSES; ++p) {
+    unpack16(vw[p], vf[p]);
+    const float vd = f16_to_f32_exact(vdb[p]);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) vf[p][j] *= vd;
+  }
+  for (uint32_t g0 = 0; g0 < group; g0 += 4u) {
+    const uint32_t gn = min(4u, group - g0);
+    float acc[4][16];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[a][j] = 0.0f;
+#pragma unroll
+    for (uint32_t p = 0; p < PASSES; ++p) {
+      const bool ok = tl[p] < n;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float w = (ok && (uint32_t)a < gn) ? s_p[(g0 + a) * CH + tl[p]] : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[a][j] = __builtin_fmaf(w, vf[p][j], acc[a][j]);
+      }
+    }
+    // reduce over the slots of the wave (lanes with the same sub), then over
+    // waves; only the heads present
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      if ((uint32_t)a >= gn) break;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+#pragma unroll
+        for (int off = LPT; off < 64; off <<= 1) acc[a][j] += __shfl_xor(acc[a][j], off, 64);
+      if (slot == 0) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s_red[(wave * 4u + a) * HD + sub * 16u + j] = acc[a][j];
+      }
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < gn * HD; i += kThreads) {
+      const uint32_t a = i / HD, d = i % HD;
+      const float sum = (s_red[(0 * 4u + a) * HD + d] + s_red[(1 * 4u + a) * HD + d]) +
+                        (s_red[(2 * 4u + a) * HD + d] + s_red[(3 * 4u + a) * HD + d]);
+      part[((size_t)(kvh * group + g0 + a) * n_chunks + ck) * (HD + 2) + 2 + d] = sum;
+    }
+    __syncthreads();
+  }
+}
+
+// Merge: workgroup (head, 64 dimensions).  The chunks' maximum first, then
+// each wave sums a quarter of the chunks (four at a time in flight), then
+// the waves' sums are added in order.
+__global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
+                                                             uint32_t n_chunks, const float* __restrict__ gate,
+                                                             float* __restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ float s_m[4], s_acc[4][64], s_l[4];
+  const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t d = blockIdx.y * 64u + lane;
+  const size_t stride = hd + 2;
+  const float* ph = part + (size_t)h * n_chunks * stride;
+  float m = -__builtin_inff();
+  for (uint32_t c = tid; c < n_chunks; c += kThreads) m = fmaxf(m, ph[c * stride]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  if (lane == 0) s_m[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  const uint32_t dc = d < hd ? d : hd - 1;
+  float acc = 0.0f, l = 0.0f;
+  uint32_t c = wave;
+  for (; c + 12u < n_chunks; c += 16u) {
+    float mc[4], lc[4], ac[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float* pc = ph + (size_t)(c + 4u * u) * stride;
+      mc[u] = pc[0];
+      lc[u] = pc[1];
+      ac[u] = pc[2 + dc];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float e = expf(mc[u] - m);
+      l += lc[u] * e;
+      acc += ac[u] * e;
+    }
+  }
+  for (; c < n_chunks; c += 4u) {
+    const float* pc = ph + (size_t)c * stride;
+    const float e = expf(pc[0] - m);
+    l += pc[1] * e;
+    acc += pc[2 + dc] * e;
+  }
+  s_acc[wave][lane] = acc;
+  if (lane == 0) s_l[wave] = l;
+  __syncthreads();
+  if (wave != 0 || d >= hd) return;
+  const float tot = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
+  float o = ((s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane])) / tot;
+  if (gate) o *= 1.0f / (1.0f + expf(-gate[(size_t)h * hd + d]));
+  out[(size_t)h * hd + d] = o;
+}
+
+template <int LPT>
+hipError_t launch_chunks(const KvQ8Dev& c, const float* q, uint32_t group, uint32_t seq_len, uint32_t n_chunks,
+                         float* part, hipStream_t s) {
+  constexpr uint32_t HD = LPT * 16, CH = 16u * (64u / LPT);
+  const size_t lds = ((size_t)group * HD + (size_t)group * CH + 16u * HD) * 4u;
+  hipLaunchKernelGGL(attn_chunk_kernel<LPT>, dim3(c.n_kv, n_chunks), dim3(kThreads), lds, s, c, q, group, seq_len,
+                     n_chunks, part);
+  return hipGetLastError();
+}
+
+// Positions per chunk: 4 passes of 4 waves x 64 / (hd / 16) positions.
+uint32_t chunk_of(uint32_t hd) { return 16u * (64u / (hd / 16u)); }
+
+}  // namespace
+
+hipError_t launch_kv_append(const KvQ8Dev& c, const float* k, const float* v, uint32_t pos, hipStream_t s) {
+  const uint32_t n = 2u * c.n_kv * c.hd;
+  hipLaunchKernelGGL(kv_append_kernel, dim3((n + kThreads - 1) / kThreads), dim3(kThreads), 0, s, c, k, v, pos);
+  return hipGetLastError();
+}
+
+size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd) {
+  (void)n_kv;
+  const uint32_t chunk = chunk_of(hd);
+  const uint32_t n_chunks = (seq_len + chunk - 1) / chunk;
+  return (size_t)n_head * n_chunks * (hd + 2) * sizeof(float);
+}
+
+// Requires hd in {32, 64, 128, 256}, n_head % n_kv == 0, n_head / n_kv <= 8,
+// 1 <= seq_len <= max_seq; ws holds attn_workspace_bytes.
+hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq_len, const float* gate,
+                       float* out, void* ws, hipStream_t s) {
+  const uint32_t group = n_head / c.n_kv;
+  if (group == 0 || group > kMaxGroup) return hipErrorInvalidValue;
+  const uint32_t chunk = chunk_of(c.hd);
+  const uint32_t n_chunks = (seq_len + chunk - 1) / chunk;
+  if (n_chunks > 65535u) return hipErrorInvalidValue;
+  float* part = static_cast<float*>(ws);
+  hipError_t e;
+  switch (c.hd) {
+    case 32: e = launch_chunks<2>(c, q, group, seq_len, n_chunks, part, s); break;
+    case 64: e = launch_chunks<4>(c, q, group, seq_len, n_chunks, part, s); break;
+    case 128: e = launch_chunks<8>(c, q, group, seq_len, n_chunks, part, s); break;
+    case 256: e = launch_chunks<16>(c, q, group, seq_len, n_chunks, part, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64), dim3(kThreads), 0, s, part, c.hd, n_chunks,
+                     gate, out);
+  return hipGetLastError();
+}
+
+}  // namespace vxt

@@ -40,6 +40,17 @@ hipError_t launch_rms_norm(float* cur, const float* delta, const float* w, void*
                            uint32_t stride, uint32_t m, float eps, hipStream_t s);
 hipError_t launch_embed(const DevTensor& t, const uint32_t* tokens, uint32_t batch_m, float scale, bool scale_on,
                         float* out, uint32_t stride, hipStream_t s);
+struct KvQ8Dev {
+  int8_t* k_qs;
+  uint16_t* k_d;
+  int8_t* v_qs;
+  uint16_t* v_d;
+  uint32_t max_seq, n_kv, hd;
+};
+hipError_t launch_kv_append(const KvQ8Dev& c, const float* k, const float* v, uint32_t pos, hipStream_t s);
+size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd);
+hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq_len, const float* gate,
+                       float* out, void* ws, hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
 struct ChainLaunch {
@@ -750,6 +761,48 @@ int vxt_hip_norm_matmul_dev(void* ctx, void* tensor, const float* cur, const flo
     hipError_t e = vxt::launch_gemv_norm(t->dev(), nin, epi, y, y_dtype == VXT_DTYPE_BF16, gated ? y_stride : t->rows,
                                          static_cast<hipStream_t>(stream));
     if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("norm matmul launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+namespace {
+vxt::KvQ8Dev kv_cache_dev(const VxtKvQ8Cache* kc) {
+  if (!kc) fail(VXT_E_ARG, "null cache");
+  if (!kc->k_qs || !kc->k_d || !kc->v_qs || !kc->v_d) fail(VXT_E_ARG, "null cache plane");
+  if (kc->head_dim != 32 && kc->head_dim != 64 && kc->head_dim != 128 && kc->head_dim != 256)
+    fail(VXT_E_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
+  if (kc->n_kv == 0 || kc->max_seq == 0) fail(VXT_E_SHAPE, "empty cache");
+  if (((uintptr_t)kc->k_qs | (uintptr_t)kc->v_qs) % 16 || ((uintptr_t)kc->k_d | (uintptr_t)kc->v_d) % 2)
+    fail(VXT_E_ARG, "value planes must be 16-byte aligned, scale planes 2-byte aligned");
+  return vxt::KvQ8Dev{static_cast<int8_t*>(kc->k_qs), static_cast<uint16_t*>(kc->k_d),
+                      static_cast<int8_t*>(kc->v_qs), static_cast<uint16_t*>(kc->v_d), kc->max_seq, kc->n_kv,
+                      kc->head_dim};
+}
+}  // namespace
+
+int vxt_hip_kv_q8_append_dev(void* ctx, const VxtKvQ8Cache* cache, const float* k, const float* v, uint32_t pos,
+                             void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    (void)as_ctx(ctx);
+    const vxt::KvQ8Dev c = kv_cache_dev(cache);
+    if (!k || !v) fail(VXT_E_ARG, "null k or v");
+    if (pos >= c.max_seq) fail(VXT_E_SHAPE, "pos >= max_seq");
+    hipError_t e = vxt::launch_kv_append(c, k, v, pos, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("kv append launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+int vxt_hip_attn_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const float* q, uint32_t n_head, uint32_t seq_len,
+                        const float* gate, float* out, void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    const vxt::KvQ8Dev kc = kv_cache_dev(cache);
+    if (!q || !out) fail(VXT_E_ARG, "null q or out");
+    if (seq_len == 0 || seq_len > kc.max_seq) fail(VXT_E_SHAPE, "need 1 <= seq_len <= max_seq");
+    if (n_head == 0 || n_head % kc.n_kv != 0) fail(VXT_E_SHAPE, "n_head must be a multiple of n_kv");
+    if (n_head / kc.n_kv > 8) fail(VXT_E_UNSUPPORTED, "at most 8 query heads per kv head");
+    ensure_ws(c, vxt::attn_workspace_bytes(n_head, seq_len, kc.n_kv, kc.hd));
+    hipError_t e = vxt::launch_attn(kc, q, n_head, seq_len, gate, out, c->ws, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention launch failed: ") + hipGetErrorString(e));
   });
 }
 

@@ -58,6 +58,7 @@ ABI_SYMBOLS = (
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
     "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
     "vxt_hip_vxt_parse", "vxt_hip_upload_vxt_entry", "vxt_hip_gguf_parse", "vxt_hip_upload_gguf_q8_0",
+    "vxt_hip_kv_q8_append_dev", "vxt_hip_attn_q8_dev",
     "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
@@ -112,6 +113,11 @@ class VxtGgufTensor(C.Structure):
     _fields_ = [("name_off", C.c_uint64), ("name_len", C.c_uint64), ("ggml_type", C.c_uint32),
                 ("n_dims", C.c_uint32), ("ne", C.c_uint64 * 8), ("data_off", C.c_uint64),
                 ("data_len", C.c_uint64), ("supported", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+class KvQ8CacheView(C.Structure):
+    _fields_ = [("k_qs", C.c_void_p), ("k_d", C.c_void_p), ("v_qs", C.c_void_p), ("v_d", C.c_void_p),
+                ("max_seq", C.c_uint32), ("n_kv", C.c_uint32), ("head_dim", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 class HipJob(C.Structure):
@@ -173,6 +179,10 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_rms_norm_dev.restype = C.c_int
     L.vxt_hip_norm_matmul_dev.argtypes = [vp, vp, vp, vp, vp, C.c_float, vp, u32, vp, u32, u32, vp, cp, sz]
     L.vxt_hip_norm_matmul_dev.restype = C.c_int
+    L.vxt_hip_kv_q8_append_dev.argtypes = [vp, C.POINTER(KvQ8CacheView), vp, vp, u32, vp, cp, sz]
+    L.vxt_hip_kv_q8_append_dev.restype = C.c_int
+    L.vxt_hip_attn_q8_dev.argtypes = [vp, C.POINTER(KvQ8CacheView), vp, u32, u32, vp, vp, vp, cp, sz]
+    L.vxt_hip_attn_q8_dev.restype = C.c_int
     L.vxt_hip_vxt_parse.argtypes = [vp, sz, C.POINTER(VxtArchiveEntry), u32, C.POINTER(u32), C.POINTER(u32),
                                     cp, sz]
     L.vxt_hip_vxt_parse.restype = C.c_int
@@ -320,6 +330,47 @@ class DeviceBuffer:
         if self.ptr and self._engine.ctx:
             load_library().vxt_hip_device_free(self._engine.ctx, self.ptr)
         self.ptr = None
+
+
+class KvQ8Cache:
+    """One layer's Q8_0 KV cache in device memory (``VxtKvQ8Cache``)."""
+
+    def __init__(self, engine: "HipEngine", max_seq: int, n_kv: int, head_dim: int):
+        self._engine = engine
+        self.max_seq, self.n_kv, self.head_dim = int(max_seq), int(n_kv), int(head_dim)
+        per = self.n_kv * self.head_dim
+        self.k_qs, self.v_qs = engine.alloc(max_seq * per), engine.alloc(max_seq * per)
+        self.k_d, self.v_d = engine.alloc(max_seq * per // 16), engine.alloc(max_seq * per // 16)
+        self.view = KvQ8CacheView(self.k_qs.ptr, self.k_d.ptr, self.v_qs.ptr, self.v_d.ptr, self.max_seq,
+                                  self.n_kv, self.head_dim, 0)
+
+    def append(self, k_ptr: int, v_ptr: int, pos: int, stream: int = 0) -> None:
+        buf = _errbuf()
+        _check(load_library().vxt_hip_kv_q8_append_dev(self._engine.ctx, C.byref(self.view), k_ptr or None,
+                                                       v_ptr or None, pos, stream or None, buf, len(buf)), buf)
+
+    def attend(self, q_ptr: int, n_head: int, seq_len: int, out_ptr: int, gate_ptr: int = 0,
+               stream: int = 0) -> None:
+        buf = _errbuf()
+        _check(load_library().vxt_hip_attn_q8_dev(self._engine.ctx, C.byref(self.view), q_ptr or None, n_head,
+                                                  seq_len, gate_ptr or None, out_ptr or None, stream or None, buf,
+                                                  len(buf)), buf)
+
+    def blocks(self, which: str, seq_len: int):
+        """Positions [0, seq_len) as KvQ8Block bytes [seq][n_kv * hd / 32][34] (host copy)."""
+        import numpy as np
+        qs_buf, d_buf = (self.k_qs, self.k_d) if which == "k" else (self.v_qs, self.v_d)
+        per = self.n_kv * self.head_dim
+        qs = qs_buf.download(np.int8, (seq_len, per // 32, 32))
+        d = d_buf.download(np.uint16, (seq_len, per // 32, 1))
+        out = np.empty((seq_len, per // 32, 34), np.uint8)
+        out[..., :2] = d.view(np.uint8)
+        out[..., 2:] = qs.view(np.uint8)
+        return out
+
+    def free(self) -> None:
+        for b in (self.k_qs, self.v_qs, self.k_d, self.v_d):
+            b.free()
 
 
 class Graph:
@@ -552,6 +603,9 @@ class HipEngine:
         if not h:
             _raise(VXT_E_DEVICE, buf)
         return Graph(self, h)
+
+    def kv_q8_cache(self, max_seq: int, n_kv: int, head_dim: int) -> KvQ8Cache:
+        return KvQ8Cache(self, max_seq, n_kv, head_dim)
 
     def chain(self, ops: Sequence) -> Chain:
         """A persistent decode-step chain of ``(tensor, x_ptr, y_ptr, y_dtype)``
