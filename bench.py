@@ -213,7 +213,7 @@ def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: i
 
 
 def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
-               ffn: int = 6144, seed: int = 40, fuse_norm: bool = True):
+               ffn: int = 6144, seed: int = 40, fuse_norm: bool = True, eager: bool = False):
     """The whole decode step (``stack.DecodeStep``) on config 4's weights:
     embedding gather (tied Q8 head), per layer RMSNorm, [q;k;v], o,
     add + RMSNorm, fused [gate;up] + SwiGLU, down; final norm, LM head,
@@ -234,13 +234,21 @@ def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: in
     for _ in range(3):
         st.enqueue()
     eng.synchronize()
-    g = st.capture()
-    g.launch(3)
-    t0 = time.perf_counter()
-    ev_ms = g.launch(tokens)
-    wall = time.perf_counter() - t0
+    if eager:   # plain launches (for profilers that do not follow graph replays)
+        t0 = time.perf_counter()
+        for _ in range(tokens):
+            st.enqueue()
+        eng.synchronize()
+        wall = time.perf_counter() - t0
+        ev_ms = wall * 1e3
+    else:
+        g = st.capture()
+        g.launch(3)
+        t0 = time.perf_counter()
+        ev_ms = g.launch(tokens)
+        wall = time.perf_counter() - t0
+        g.free()
     tok, bad = st.read_token()
-    g.free()
     launches = st.launches
     st.free()
     for b in bufs:
@@ -252,7 +260,8 @@ def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: in
             "ms_per_token": ms_tok, "launches_per_token": launches, "last_token": tok, "nonfinite": bad}
 
 
-def bench_attn(eng, seq: int, n_head: int, n_kv: int, hd: int, calls: int = 200, seed: int = 6):
+def bench_attn(eng, seq: int, n_head: int, n_kv: int, hd: int, calls: int = 200, seed: int = 6,
+               eager: bool = False):
     """Decode attention over a Q8_0 KV cache of ``seq`` positions: one
     ``vxt_hip_attn_q8_dev`` call per step, timed as a captured graph of
     ``calls`` calls.  Bytes: the cache's K and V values and scales."""
@@ -270,10 +279,17 @@ def bench_attn(eng, seq: int, n_head: int, n_kv: int, hd: int, calls: int = 200,
     out = eng.alloc(n_head * hd * 4)
     cache.attend(q.ptr, n_head, seq, out.ptr, 0, eng.stream)      # sizes the workspace
     eng.synchronize()
-    g = eng.capture(lambda s: [cache.attend(q.ptr, n_head, seq, out.ptr, 0, s) for _ in range(calls)])
-    g.launch(1)
-    ms = g.launch(1) / calls
-    g.free()
+    if eager:   # plain launches (for profilers that do not follow graph replays)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            cache.attend(q.ptr, n_head, seq, out.ptr, 0, eng.stream)
+        eng.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / calls
+    else:
+        g = eng.capture(lambda s: [cache.attend(q.ptr, n_head, seq, out.ptr, 0, s) for _ in range(calls)])
+        g.launch(1)
+        ms = g.launch(1) / calls
+        g.free()
     q.free()
     out.free()
     cache.free()
@@ -319,9 +335,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="0,2,3,4,a",
-                    help="secondary configurations to run (a: KV-Q8 decode attention)")
+    ap.add_argument("--configs", default="0,2,3,4,s,a",
+                    help="secondary configurations to run (s: whole decode step on config 4's weights, "
+                         "a: KV-Q8 decode attention)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="time configs s and a with plain launches instead of graph replays (for profilers)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -393,10 +412,15 @@ def main():
                               "frac_hbm": round(rs["GBps"] / HBM_PEAK_GBS, 4)})
             log(f"  {rs['tokens_per_s']:.1f} tok/s ({rs['GBps']:.1f} GB/s, "
                 f"{rs['ms_per_token']*1e3:.1f} us/token)")
+        del head_m
+
+    if "s" in run:
+        head_m = synth.make_q8(151936, 2048, seed=5)
         for kind, fuse in (("cb4", False), ("cb4", True)):
             how = "norms inside the projections" if fuse else "separate norm launches"
             log(f"config 4 (whole step): 24 layers {kind} + norms, fused SwiGLU, Q8 head, greedy, embedding; {how}")
-            rw = bench_step(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)), fuse_norm=fuse)
+            rw = bench_step(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)), fuse_norm=fuse,
+                            eager=args.eager)
             secondary.append({"config": f"4 (whole decode step): embed + 24x{{norm,[q;k;v],o,add+norm,"
                                         f"[gate;up]+swiglu,down}} {kind} + norm + q8 head + greedy, M=1, "
                                         f"{how}, HIP graph of {rw['launches_per_token']} launches per token",
@@ -406,10 +430,9 @@ def main():
             log(f"  {rw['tokens_per_s']:.1f} tok/s ({rw['ms_per_token']*1e3:.1f} us/token, "
                 f"{rw['launches_per_token']} launches)")
         del head_m
-
     if "a" in run:
         for seq, nh, nkv in ((4096, 16, 16), (32768, 16, 16), (32768, 16, 4), (131072, 16, 4)):
-            ra = bench_attn(eng, seq, nh, nkv, 128)
+            ra = bench_attn(eng, seq, nh, nkv, 128, eager=args.eager)
             secondary.append({"config": f"attention over a Q8_0 KV cache: {nh} heads / {nkv} kv heads x 128, "
                                         f"{seq} positions, one decode step",
                               "kernel_us": round(ra["us"], 2), "bytes": int(ra["bytes"]),

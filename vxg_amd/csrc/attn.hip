@@ -247,7 +247,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
 }
 
 // Merge: workgroup (head, 64 dimensions).  The chunks' maximum first, then
-// each wave sums a quarter of the chunks (four at a time in flight), then
+// each wave sums a quarter of the chunks (sixteen at a time in flight), then
 // the waves' sums are added in order.
 __global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
                                                              uint32_t n_chunks, const float* __restrict__ gate,
@@ -268,17 +268,18 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __res
   const uint32_t dc = d < hd ? d : hd - 1;
   float acc = 0.0f, l = 0.0f;
   uint32_t c = wave;
-  for (; c + 12u < n_chunks; c += 16u) {
-    float mc[4], lc[4], ac[4];
+  constexpr int U = 16;   // chunks in flight per lane
+  for (; c + 4u * (U - 1) < n_chunks; c += 4u * U) {
+    float mc[U], lc[U], ac[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const float* pc = ph + (size_t)(c + 4u * u) * stride;
       mc[u] = pc[0];
       lc[u] = pc[1];
       ac[u] = pc[2 + dc];
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < U; ++u) {
       const float e = expf(mc[u] - m);
       l += lc[u] * e;
       acc += ac[u] * e;
