@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvxt_hip.so")
-SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip",
+SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip",
            "dequant.hip", "chain.hip", "greedy.hip", "ffn.hip", "attn.hip", "archive.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -36,6 +36,9 @@ struct DevTensor {
   float cent[48];            // CB4 only: 3 centroid tables of 16
 };
 
+// Prefill GEMM path (batch_m > 8): chosen per call, or pinned by the caller.
+enum GemmMode : int { kGemmAuto = 0, kGemmPanel = 1, kGemmFused = 2 };
+
 // Centroid table serving `row` (rows of up to 3 concatenated sub-matrices).
 __device__ __forceinline__ uint32_t cent_table(const DevTensor& t, uint32_t row) {
   return (uint32_t)(row >= t.split0) + (uint32_t)(row >= t.split1);

@@ -33,6 +33,9 @@
 
 namespace vxt {
 
+hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
+                              bool y_bf16, hipStream_t s);
+
 namespace gp {
 
 constexpr int BK = 64;
@@ -164,11 +167,15 @@ __device__ __forceinline__ void store32(const float (&w)[32], float s, uint16_t*
   }
 }
 
-// One wave per weight row (grid-stride over rows); a lane decodes 32
-// consecutive columns per 2048-column segment with 16-byte loads, as the
-// GEMV does, and writes them as 16-byte f16 pieces.
+// One wave per (weight row, 2048-column segment): a lane decodes 32
+// consecutive columns with 16-byte loads, as the GEMV does, and writes them
+// as 16-byte f16 pieces.  Rows that need a power-of-two scale (hi/lo modes)
+// derive it in every segment's wave from the row's scales and residuals,
+// requested together with the segment's own weights, so no wave walks a row
+// serially.  cb4 residuals are applied by the wave owning the column's
+// segment, after its dense stores, in CSR order.
 template <uint32_t KIND>
-__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, uint32_t qblock) {
+__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, uint32_t qblock, uint32_t nseg) {
   constexpr uint32_t kPair = 48;   // g64 pair-table stride (bytes) in the per-wave slot
   __shared__ __attribute__((aligned(64))) uint32_t s_slot[KIND == KIND_G64 ? 4 * 32 * kPair / 4 : 1];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
@@ -178,101 +185,100 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
     if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
     __syncthreads();
   }
-  for (uint32_t n = blockIdx.x * 4 + wave; n < N; n += gridDim.x * 4) {
-    uint16_t* hi = p.hi + (size_t)n * KP;
-    uint16_t* lo = p.lo + (size_t)n * KP;
-    float s = 1.0f;
-    if constexpr (KIND == KIND_Q8) {
-      const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
-      if (qblock) {   // block scales as f32; blocks past the weights' own are zero
-        for (uint32_t b = lane; b < KP / 32; b += 64) p.dsc[(size_t)n * (KP / 32) + b] = b < kp / 32 ? f16_to_f32_exact(dp[b]) : 0.0f;
-      } else {
-        float dm = 0.0f;
-        for (uint32_t b = lane; b < kp / 32; b += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[b])));
-        s = row_scale(127.0f * wave_max(dm));
-      }
-    } else if constexpr (KIND == KIND_CB4) {
-      const uint16_t* sp = t.p1 + (size_t)n * (kp / 128);
-      const float* cent = s_cent + 16u * cent_table(t, n);
-      float sm = 0.0f, rs = 0.0f, cm = 0.0f;
-      for (uint32_t g = lane; g < kp / 128; g += 64) sm = fmaxf(sm, fabsf(f16_to_f32_exact(sp[g])));
-      for (uint32_t o = t.row_ptr[n] + lane; o < t.row_ptr[n + 1]; o += 64)
-        rs += fabsf(f16_to_f32_exact(t.outliers[o] >> 16));
+  const uint32_t unit = blockIdx.x * 4 + wave;
+  if (unit >= N * nseg) return;
+  const uint32_t n = unit / nseg, seg = (unit % nseg) * (64 * 32);
+  const uint32_t k0 = seg + lane * 32;
+  const bool live = k0 < KP;   // KP % 64 == 0: a lane pair is wholly inside or outside
+  uint16_t* hi = p.hi + (size_t)n * KP;
+  uint16_t* lo = p.lo + (size_t)n * KP;
+  float s = 1.0f;
+  float w[32];
+  if constexpr (KIND == KIND_G64) {
+    const uint32_t kc = live ? k0 : 0;
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2) + kc / 2);
+    const uint4 lt = *reinterpret_cast<const uint4*>(t.p1 + ((size_t)n * (kp / 64) + kc / 64) * 16 + (lane & 1) * 8);
+    const uint32_t slot = wave * 32 * kPair + (lane >> 1) * kPair;   // bytes
+    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_slot) + slot + (lane & 1) * 16) = lt;
+    const uint16_t* tab = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(s_slot) + slot);
+    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+    uint32_t h[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) cm = fmaxf(cm, fabsf(cent[i]));
-      s = row_scale(wave_max(sm) * cm + wave_add(rs));
+    for (int j = 0; j < 16; ++j) {
+      const uint32_t c0 = 2 * j, c1 = c0 + 1;
+      const uint32_t e0 = k0 + c0 < K ? tab[(wd[c0 >> 3] >> ((c0 & 7) * 4)) & 0xfu] : 0u;
+      const uint32_t e1 = k0 + c1 < K ? tab[(wd[c1 >> 3] >> ((c1 & 7) * 4)) & 0xfu] : 0u;
+      h[j] = e0 | (e1 << 16);
     }
-    for (uint32_t seg = 0; seg < KP; seg += 64 * 32) {
-      const uint32_t k0 = seg + lane * 32;
-      if (k0 >= KP) break;   // KP % 64 == 0: a lane pair is wholly inside or outside
-      float w[32];
-      if constexpr (KIND == KIND_G64) {
-        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2) + k0 / 2);
-        const uint4 lt = *reinterpret_cast<const uint4*>(t.p1 + ((size_t)n * (kp / 64) + k0 / 64) * 16 + (lane & 1) * 8);
-        const uint32_t slot = wave * 32 * kPair + (lane >> 1) * kPair;   // bytes
-        *reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_slot) + slot + (lane & 1) * 16) = lt;
-        const uint16_t* tab = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(s_slot) + slot);
-        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-        uint32_t h[16];
+    if (live) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const uint32_t c0 = 2 * j, c1 = c0 + 1;
-          const uint32_t e0 = k0 + c0 < K ? tab[(wd[c0 >> 3] >> ((c0 & 7) * 4)) & 0xfu] : 0u;
-          const uint32_t e1 = k0 + c1 < K ? tab[(wd[c1 >> 3] >> ((c1 & 7) * 4)) & 0xfu] : 0u;
-          h[j] = e0 | (e1 << 16);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          *reinterpret_cast<uint4*>(hi + k0 + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
-        continue;
-      } else if constexpr (KIND == KIND_Q8) {
-        const uint32_t kc = k0 < kp ? k0 : kp - 32;   // kp may be 32 short of KP
-        const int8_t* qp = static_cast<const int8_t*>(t.p0) + (size_t)n * kp + kc;
-        const uint4 a = *reinterpret_cast<const uint4*>(qp), b = *reinterpret_cast<const uint4*>(qp + 16);
-        const float d = qblock ? 1.0f : f16_to_f32_exact(t.p1[(size_t)n * (kp / 32) + kc / 32]);
-        const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int j = 0; j < 32; ++j)
-          w[j] = k0 + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d : 0.0f;   // gguf.rs:223-229
-        if (qblock) {   // the int8 value itself, exact in f16
-          store32<false>(w, 1.0f, hi, lo, k0);
-          continue;
-        }
-      } else {
-        const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint32_t*>(t.p0) + (size_t)n * (kp / 8) + k0 / 8);
-        const float sc = f16_to_f32_exact(t.p1[(size_t)n * (kp / 128) + k0 / 128]);
-        const float* cent = s_cent + 16u * cent_table(t, n);
-        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int j = 0; j < 32; ++j) w[j] = k0 + j < K ? sc * cent[(wd[j >> 3] >> ((j & 7) * 4)) & 0xfu] : 0.0f;
-      }
-      store32<true>(w, s, hi, lo, k0);
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<uint4*>(hi + k0 + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
     }
-    if constexpr (KIND == KIND_CB4) {
-      // CSR residuals (codebook.rs:316-333): the lane holding a column's first
-      // entry rebuilds that column from sc * cent[q] and adds the column's
-      // residuals in CSR order, then overwrites the two halves written above.
-      const uint32_t os = t.row_ptr[n], oe = t.row_ptr[n + 1];
-      if (oe > os) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // the dense stores above land first
-        const float* cent = s_cent + 16u * cent_table(t, n);
-        for (uint32_t i = os + lane; i < oe; i += 64) {
-          const uint32_t c = t.outliers[i] & 0xffffu;
-          bool first = c < K;
-          for (uint32_t j = os; j < i && first; ++j) first = (t.outliers[j] & 0xffffu) != c;
-          if (!first) continue;
-          const uint32_t wd = static_cast<const uint32_t*>(t.p0)[(size_t)n * (kp / 8) + c / 8];
-          float v = f16_to_f32_exact(t.p1[(size_t)n * (kp / 128) + c / 128]) * cent[(wd >> ((c % 8) * 4)) & 0xfu];
-          for (uint32_t j = i; j < oe; ++j) {
-            const uint32_t pk = t.outliers[j];
-            if ((pk & 0xffffu) == c) v += f16_to_f32_exact(pk >> 16);
-          }
-          split_write(v, s, hi, lo, c);
+  } else if constexpr (KIND == KIND_Q8) {
+    const uint32_t kc = live ? (k0 < kp ? k0 : kp - 32) : 0;   // kp may be 32 short of KP
+    const int8_t* qp = static_cast<const int8_t*>(t.p0) + (size_t)n * kp + kc;
+    const uint4 a = *reinterpret_cast<const uint4*>(qp), b = *reinterpret_cast<const uint4*>(qp + 16);
+    const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
+    const float d = qblock ? 1.0f : f16_to_f32_exact(dp[kc / 32]);
+    if (qblock) {   // block scales as f32; blocks past the weights' own are zero
+      const uint32_t b0 = seg / 32 + lane;
+      if (b0 < KP / 32)
+        p.dsc[(size_t)n * (KP / 32) + b0] = b0 < kp / 32 ? f16_to_f32_exact(dp[b0]) : 0.0f;
+    } else {
+      float dm = 0.0f;
+      for (uint32_t g = lane; g < kp / 32; g += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[g])));
+      s = row_scale(127.0f * wave_max(dm));
+    }
+    const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int j = 0; j < 32; ++j)
+      w[j] = k0 + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d : 0.0f;   // gguf.rs:223-229
+    if (live) {
+      if (qblock)   // the int8 value itself, exact in f16
+        store32<false>(w, 1.0f, hi, lo, k0);
+      else
+        store32<true>(w, s, hi, lo, k0);
+    }
+  } else {
+    const uint32_t kc = live ? k0 : 0;
+    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint32_t*>(t.p0) + (size_t)n * (kp / 8) + kc / 8);
+    const uint16_t* sp = t.p1 + (size_t)n * (kp / 128);
+    const float sc = f16_to_f32_exact(sp[kc / 128]);
+    const uint32_t os = t.row_ptr[n], oe = t.row_ptr[n + 1];
+    const float* cent = s_cent + 16u * cent_table(t, n);
+    float sm = 0.0f, rs = 0.0f, cm = 0.0f;
+    for (uint32_t g = lane; g < kp / 128; g += 64) sm = fmaxf(sm, fabsf(f16_to_f32_exact(sp[g])));
+    for (uint32_t o = os + lane; o < oe; o += 64) rs += fabsf(f16_to_f32_exact(t.outliers[o] >> 16));
+#pragma unroll
+    for (int i = 0; i < 16; ++i) cm = fmaxf(cm, fabsf(cent[i]));
+    s = row_scale(wave_max(sm) * cm + wave_add(rs));
+    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int j = 0; j < 32; ++j) w[j] = k0 + j < K ? sc * cent[(wd[j >> 3] >> ((j & 7) * 4)) & 0xfu] : 0.0f;
+    if (live) store32<true>(w, s, hi, lo, k0);
+    // CSR residuals of this segment's columns (codebook.rs:316-333): the lane
+    // holding a column's first entry rebuilds the column from sc * cent[q] and
+    // adds its residuals in CSR order, over the halves stored above.
+    if (oe > os) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // the dense stores above land first
+      const uint32_t c_end = seg + 64 * 32;
+      for (uint32_t i = os + lane; i < oe; i += 64) {
+        const uint32_t c = t.outliers[i] & 0xffffu;
+        bool first = c < K && c >= seg && c < c_end;
+        for (uint32_t j = os; j < i && first; ++j) first = (t.outliers[j] & 0xffffu) != c;
+        if (!first) continue;
+        const uint32_t cw = static_cast<const uint32_t*>(t.p0)[(size_t)n * (kp / 8) + c / 8];
+        float v = f16_to_f32_exact(sp[c / 128]) * cent[(cw >> ((c % 8) * 4)) & 0xfu];
+        for (uint32_t j = i; j < oe; ++j) {
+          const uint32_t pk = t.outliers[j];
+          if ((pk & 0xffffu) == c) v += f16_to_f32_exact(pk >> 16);
         }
+        split_write(v, s, hi, lo, c);
       }
     }
-    if (lane == 0) p.inv[n] = 1.0f / s;
   }
+  if (lane == 0 && seg == 0) p.inv[n] = 1.0f / s;
 }
 
 // ---- phase 2: dense GEMM -----------------------------------------------------
@@ -482,8 +488,8 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
   }
 }
 
-// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n]; four outputs per
-// thread when N % 4 == 0.
+// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n] (no scaling when
+// inv is null); four outputs per thread when N % 4 == 0.
 __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict__ partial, uint32_t splits,
                                                          const float* __restrict__ inv, uint32_t M, uint32_t N,
                                                          void* __restrict__ y, uint32_t y_bf16) {
@@ -496,8 +502,10 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
       const float4 a = *reinterpret_cast<const float4*>(partial + (size_t)z * total + i);
       v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
     }
-    const float4 iv = *reinterpret_cast<const float4*>(inv + i % N);
-    v.x *= iv.x; v.y *= iv.y; v.z *= iv.z; v.w *= iv.w;
+    if (inv) {
+      const float4 iv = *reinterpret_cast<const float4*>(inv + i % N);
+      v.x *= iv.x; v.y *= iv.y; v.z *= iv.z; v.w *= iv.w;
+    }
     if (y_bf16) {
       const uint32_t lo = f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
       const uint32_t hi = f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
@@ -511,7 +519,7 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
   if (i >= total) return;
   float v = 0.0f;
   for (uint32_t z = 0; z < splits; ++z) v += partial[(size_t)z * total + i];
-  v *= inv[i % N];
+  if (inv) v *= inv[i % N];
   if (y_bf16)
     static_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
   else
@@ -614,9 +622,10 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
     hipLaunchKernelGGL((xconv_kernel<false>), dim3(xgrid), dim3(THREADS), 0, s, x, m, t.cols, pl.kp, ah, al, x_vec);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const uint32_t pgrid = std::min<uint32_t>((t.rows + 3) / 4, 2048);
+  const uint32_t nseg = (p.kp + 64 * 32 - 1) / (64 * 32);
+  const uint32_t pgrid = (uint32_t)(((size_t)t.rows * nseg + 3) / 4);
   hipLaunchKernelGGL((panel_kernel<KIND>), dim3(pgrid), dim3(THREADS), 0, s, t, p,
-                     (uint32_t)(pl.wmode == kWQBlock ? 1u : 0u));
+                     (uint32_t)(pl.wmode == kWQBlock ? 1u : 0u), nseg);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   if constexpr (KIND == KIND_G64) {
@@ -630,23 +639,48 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
     e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
   }
   if (e != hipSuccess || pl.splits == 1) return e;
-  const size_t total = (size_t)m * t.rows;
-  const size_t threads = t.rows % 4u == 0u ? total / 4 : total;
-  hipLaunchKernelGGL(reduce_kernel, dim3((uint32_t)((threads + THREADS - 1) / THREADS)), dim3(THREADS), 0, s,
-                     partial, pl.splits, p.inv, m, t.rows, y, (uint32_t)y_bf16);
-  return hipGetLastError();
+  return launch_gemm_reduce(partial, pl.splits, p.inv, m, t.rows, y, y_bf16, s);
 }
 
 }  // namespace gp
 
-size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16) {
+hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
+                              bool y_bf16, hipStream_t s) {
+  const size_t total = (size_t)m * n;
+  const size_t threads = n % 4u == 0u ? total / 4 : total;
+  hipLaunchKernelGGL(gp::reduce_kernel, dim3((uint32_t)((threads + gp::THREADS - 1) / gp::THREADS)),
+                     dim3(gp::THREADS), 0, s, partial, splits, inv, m, n, y, (uint32_t)y_bf16);
+  return hipGetLastError();
+}
+
+bool gemm_fused_supported(const DevTensor& t, bool x_bf16);
+size_t gemm_fused_workspace_bytes(const DevTensor& t, uint32_t m);
+hipError_t launch_gemm_fused(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
+                             size_t ws_bytes, hipStream_t s);
+
+// Path choice: the fused kernel where it applies (g64 and Q8 weights, bf16
+// activations) and batch_m is at most kFusedMaxM, unless the caller pins a
+// path.  Measured on MI355X (6144 x 2048 and 2048 x 6144): the fused kernel
+// is 1.5-3x faster up to M = 128 and level at M = 512, where the dense
+// kernel's 128 x 128 tiles reuse each decoded weight 4x more.
+constexpr uint32_t kFusedMaxM = 256;
+
+static bool fused_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
+  if (mode == kGemmPanel || !gemm_fused_supported(t, x_bf16)) return false;
+  return mode == kGemmFused || m <= kFusedMaxM;
+}
+
+size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
+  if (fused_path(t, m, x_bf16, mode)) return gemm_fused_workspace_bytes(t, m);
   const gp::Plan pl = gp::plan(t, m, x_bf16);
   return pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
 }
 
 hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
-                       size_t ws_bytes, hipStream_t s) {
+                       size_t ws_bytes, hipStream_t s, int mode) {
   if (m == 0 || (size_t)m * t.rows > (size_t)1 << 40) return hipErrorInvalidValue;
+  if (fused_path(t, m, x_bf16, mode))
+    return launch_gemm_fused(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
   switch (t.kind) {
     case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
     case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);

@@ -25,9 +25,9 @@
 namespace vxt {
 hipError_t launch_gemv(const DevTensor& t, const void* x, bool x_bf16, bool x_vec, uint32_t m,
                        void* y, bool y_bf16, hipStream_t s);
-size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16);
+size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode);
 hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
-                       size_t ws_bytes, hipStream_t s);
+                       size_t ws_bytes, hipStream_t s, int mode);
 hipError_t launch_dequant(const DevTensor& t, uint32_t row0, uint32_t nrows, float* out,
                           hipStream_t s);
 hipError_t launch_gemv_norm(const DevTensor& t, const NormIn& nin, int epi, void* y, bool y_bf16, uint32_t y_stride,
@@ -115,6 +115,7 @@ struct Ctx {
   void* ws = nullptr;      // GEMM workspace: weight panel + split-K partial sums
   size_t ws_cap = 0;
   void* greedy = nullptr;  // greedy-selection state words (zero between calls)
+  int gemm_mode = vxt::kGemmAuto;
   std::mutex mu;
   std::set<Tensor*> tensors;
   std::set<void*> buffers;
@@ -298,9 +299,9 @@ void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, 
     const bool x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t->cols * esz) % 16 == 0;
     e = vxt::launch_gemv(d, x, xb, x_vec, m, y, yb, s);
   } else {
-    const size_t need = vxt::gemm_workspace_bytes(d, m, xb);
+    const size_t need = vxt::gemm_workspace_bytes(d, m, xb, c->gemm_mode);
     ensure_ws(c, need);
-    e = vxt::launch_gemm(d, x, xb, m, y, yb, c->ws, c->ws_cap, s);
+    e = vxt::launch_gemm(d, x, xb, m, y, yb, c->ws, c->ws_cap, s, c->gemm_mode);
   }
   if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
   if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e));
@@ -724,14 +725,15 @@ int vxt_hip_ffn_glu_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype
     } else {
       // Gate and up rows into f32 staging after the GEMM's own workspace,
       // then the element-wise activation.
-      const size_t gemm_ws = batch_m > 8 ? (vxt::gemm_workspace_bytes(d, batch_m, xb) + 255) / 256 * 256 : 0;
+      const size_t gemm_ws =
+          batch_m > 8 ? (vxt::gemm_workspace_bytes(d, batch_m, xb, c->gemm_mode) + 255) / 256 * 256 : 0;
       const size_t stage = (size_t)batch_m * t->rows * sizeof(float);
       ensure_ws(c, gemm_ws + stage);
       float* gu = reinterpret_cast<float*>(static_cast<char*>(c->ws) + gemm_ws);
       if (batch_m <= 8) {
         e = vxt::launch_gemv(d, x, xb, false, batch_m, gu, false, s);
       } else {
-        e = vxt::launch_gemm(d, x, xb, batch_m, gu, false, c->ws, gemm_ws, s);
+        e = vxt::launch_gemm(d, x, xb, batch_m, gu, false, c->ws, gemm_ws, s, c->gemm_mode);
       }
       if (e == hipSuccess) e = vxt::launch_glu_act(gu, batch_m, n_ff, gelu, act, ab, act_stride, s);
     }
@@ -975,6 +977,14 @@ void vxt_hip_graph_free(void* graph) {
 int vxt_hip_last_kernel_ms(void* ctx, double* ms) {
   if (!ctx || !ms) return VXT_E_ARG;
   *ms = static_cast<Ctx*>(ctx)->last_ms;
+  return VXT_OK;
+}
+
+int vxt_hip_set_gemm_path(void* ctx, uint32_t path) {
+  if (!ctx || path > VXT_GEMM_FUSED) return VXT_E_ARG;
+  Ctx* c = static_cast<Ctx*>(ctx);
+  std::lock_guard<std::mutex> lk(c->mu);
+  c->gemm_mode = (int)path;
   return VXT_OK;
 }
 

@@ -48,6 +48,7 @@ VXT_E_ARG, VXT_E_SHAPE, VXT_E_FORMAT, VXT_E_DEVICE, VXT_E_UNSUPPORTED = -1, -2, 
 DTYPE_F32, DTYPE_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 NORM_PLAIN, NORM_GLU_SILU, NORM_GLU_GELU_TANH = 0, 1, 2
+GEMM_AUTO, GEMM_PANEL, GEMM_FUSED = 0, 1, 2
 KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
 
 ABI_SYMBOLS = (
@@ -59,7 +60,7 @@ ABI_SYMBOLS = (
     "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
     "vxt_hip_vxt_parse", "vxt_hip_upload_vxt_entry", "vxt_hip_gguf_parse", "vxt_hip_upload_gguf_q8_0",
     "vxt_hip_kv_q8_append_dev", "vxt_hip_attn_q8_dev",
-    "vxt_hip_last_kernel_ms", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
+    "vxt_hip_last_kernel_ms", "vxt_hip_set_gemm_path", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
     "vxt_hip_chain_enqueue", "vxt_hip_chain_status", "vxt_hip_chain_set_spin_limit", "vxt_hip_chain_free",
@@ -196,6 +197,8 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_greedy_dev.argtypes = [vp, vp, u32, vp, vp, cp, sz]
     L.vxt_hip_last_kernel_ms.restype = C.c_int
     L.vxt_hip_last_kernel_ms.argtypes = [vp, C.POINTER(C.c_double)]
+    L.vxt_hip_set_gemm_path.restype = C.c_int
+    L.vxt_hip_set_gemm_path.argtypes = [vp, u32]
     L.vxt_hip_device_alloc.restype = vp
     L.vxt_hip_device_alloc.argtypes = [vp, sz, cp, sz]
     L.vxt_hip_device_free.restype = None
@@ -569,6 +572,12 @@ class HipEngine:
             if src:
                 src.free()
         return int(r[0]), bool(r[1])
+
+    def set_gemm_path(self, path: int) -> None:
+        """Pin the prefill GEMM path (``GEMM_AUTO``, ``GEMM_PANEL``, ``GEMM_FUSED``)."""
+        rc = load_library().vxt_hip_set_gemm_path(self.ctx, path)
+        if rc != VXT_OK:
+            raise BackendError(rc, f"unknown GEMM path {path}")
 
     def last_kernel_ms(self) -> float:
         ms = C.c_double()
