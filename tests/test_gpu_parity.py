@@ -371,6 +371,40 @@ def test_gemm_extreme_weight_magnitudes(eng):
         gemm_check(run_dev(eng, t, xb, engine.DTYPE_BF16, 24, engine.DTYPE_BF16), yref, W, X, True)
 
 
+@pytest.mark.parametrize("M", [16, 300])
+def test_gemm_cb4_unsorted_and_duplicate_outliers(eng, M):
+    """CSR rows in any order, with repeated columns (decode_row adds them in
+    CSR order, codebook.rs:316-333): the panel decode takes its general path
+    for such rows and the sorted fast path for the others."""
+    m = synth.make_cb4(130, 2500, seed=9, outlier_frac=0.03)
+    g = np.random.default_rng(9)
+    rp, pk = m.outlier_row_ptr, m.outliers_packed
+    rows = []
+    for r in range(m.rows):
+        e = pk[rp[r]:rp[r + 1]].copy()
+        if r % 3 == 0 and e.size:        # shuffled, plus a second residual on two columns
+            g.shuffle(e)
+            extra = (e[:2] & np.uint32(0xFFFF)) | (np.uint32(f16b(0.0625)) << np.uint32(16))
+            e = np.concatenate([e, extra])
+        rows.append(e)
+    m.outliers_packed = np.concatenate(rows).astype(np.uint32)
+    m.outlier_row_ptr = np.r_[0, np.cumsum([len(e) for e in rows])].astype(np.uint32)
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(M, m.cols, seed=M)
+    X = bf16_bits_to_f32(xb).reshape(M, m.cols)
+    W = oracle.decode_rows(m)
+    sel = np.r_[0:4, M - 4:M]
+    yref = oracle.gemm(m, X[sel], threads=THREADS)
+    for path in (engine.GEMM_AUTO, engine.GEMM_PANEL):
+        eng.set_gemm_path(path)
+        try:
+            y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        finally:
+            eng.set_gemm_path(engine.GEMM_AUTO)
+        gemm_check(y[sel], yref, W, X[sel], False)
+    t.free()
+
+
 @pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
 @pytest.mark.parametrize("M,N,K", [(16, 64, 4096), (40, 300, 3000), (9, 2048, 6144)])
 def test_gemm_split_k(eng, kind, M, N, K):

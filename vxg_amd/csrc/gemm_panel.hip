@@ -259,20 +259,34 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
     if (live) store32<true>(w, s, hi, lo, k0);
     // CSR residuals of this segment's columns (codebook.rs:316-333): the lane
     // holding a column's first entry rebuilds the column from sc * cent[q] and
-    // adds its residuals in CSR order, over the halves stored above.
+    // adds its residuals in CSR order, over the halves stored above.  A row
+    // whose columns strictly increase (what the reference's encoders emit,
+    // codebook.rs:228-250 and cb4_opt.rs) has one entry per column, proved by
+    // one parallel comparison with the previous entry; only other rows scan
+    // the row for earlier and later entries of the same column.
     if (oe > os) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");   // the dense stores above land first
       const uint32_t c_end = seg + 64 * 32;
+      bool inc = true;
+      for (uint32_t i = os + 1 + lane; i < oe; i += 64)
+        inc = inc && (t.outliers[i] & 0xffffu) > (t.outliers[i - 1] & 0xffffu);
+      const bool unique = __all(inc);
       for (uint32_t i = os + lane; i < oe; i += 64) {
-        const uint32_t c = t.outliers[i] & 0xffffu;
+        const uint32_t pk0 = t.outliers[i];
+        const uint32_t c = pk0 & 0xffffu;
         bool first = c < K && c >= seg && c < c_end;
-        for (uint32_t j = os; j < i && first; ++j) first = (t.outliers[j] & 0xffffu) != c;
+        if (!unique)
+          for (uint32_t j = os; j < i && first; ++j) first = (t.outliers[j] & 0xffffu) != c;
         if (!first) continue;
         const uint32_t cw = static_cast<const uint32_t*>(t.p0)[(size_t)n * (kp / 8) + c / 8];
         float v = f16_to_f32_exact(sp[c / 128]) * cent[(cw >> ((c % 8) * 4)) & 0xfu];
-        for (uint32_t j = i; j < oe; ++j) {
-          const uint32_t pk = t.outliers[j];
-          if ((pk & 0xffffu) == c) v += f16_to_f32_exact(pk >> 16);
+        if (unique) {
+          v += f16_to_f32_exact(pk0 >> 16);
+        } else {
+          for (uint32_t j = i; j < oe; ++j) {
+            const uint32_t pk = t.outliers[j];
+            if ((pk & 0xffffu) == c) v += f16_to_f32_exact(pk >> 16);
+          }
         }
         split_write(v, s, hi, lo, c);
       }
