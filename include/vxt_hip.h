@@ -391,16 +391,21 @@ VXT_API void vxt_hip_graph_free(void* graph);
 VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
 
 /* Prefill GEMM path (batch_m > 8) of this context's later calls.  AUTO (the
- * default) decodes g64 and Q8_0 weights inside the MFMA loop when the
- * activations are bf16 and batch_m <= 256, and takes the two-phase path
- * (decoded f16 panel, then a dense MFMA GEMM) otherwise; PANEL pins the
- * two-phase path; FUSED takes the fused kernel at every batch_m it applies to.
- * A tuning and test control with no counterpart in the reference, whose
- * gemm_cpu (llm_prefill.rs:156-255) has a single path.  Returns VXT_E_ARG for
- * an unknown path. */
+ * default): g64 and Q8_0 weights with bf16 activations and batch_m <= 256
+ * are decoded inside the MFMA loop (fused); other calls at batch_m <= 256
+ * take the two-phase path (decoded f16 panel, then this library's dense MFMA
+ * kernel); batch_m > 256 with batch_m * rows >= 512 * 6144 takes the
+ * two-phase path with the dense phase on hipBLASLt (smaller products keep the
+ * own dense kernel).  PANEL pins the two-phase path with the own dense kernel;
+ * FUSED takes the fused kernel at every batch_m it applies to; LIBRARY pins
+ * the hipBLASLt dense phase (falling back to the own kernel for a shape the
+ * library has no algorithm for).  A tuning and test control with no
+ * counterpart in the reference, whose gemm_cpu (llm_prefill.rs:156-255) has a
+ * single path.  Returns VXT_E_ARG for an unknown path. */
 #define VXT_GEMM_AUTO 0u
 #define VXT_GEMM_PANEL 1u
 #define VXT_GEMM_FUSED 2u
+#define VXT_GEMM_LIBRARY 3u
 VXT_API int vxt_hip_set_gemm_path(void* ctx, uint32_t path);
 
 /* ---- decode-step chain: one persistent launch per token ------------------ */

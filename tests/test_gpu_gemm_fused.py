@@ -173,4 +173,4 @@ def test_fused_unaligned_activations(eng):
 
 def test_gemm_path_rejects_unknown(eng):
     with pytest.raises(engine.BackendError):
-        eng.set_gemm_path(3)
+        eng.set_gemm_path(4)

@@ -420,6 +420,66 @@ def test_gemm_split_k(eng, kind, M, N, K):
     assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
 
 
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("M,N,K,xdt", [(300, 130, 700, "bf16"), (257, 2048, 2048, "f32"), (1024, 96, 4096, "bf16")])
+def test_gemm_library_dense_phase(eng, kind, M, N, K, xdt):
+    """Two-phase GEMM with the dense phase on hipBLASLt (automatic above
+    batch 256): hi/lo terms for cb4 and Q8, split f32 activations, the 1/s
+    epilogue and bf16 rounding, against the oracle and the own dense kernel."""
+    m = make(kind, N, K, seed=M + N + K)
+    t = eng.upload_packed(m)
+    if xdt == "bf16":
+        xh = synth.make_x_bf16(M, K, seed=M)
+        X = bf16_bits_to_f32(xh).reshape(M, K)
+        xd = engine.DTYPE_BF16
+    else:
+        X = synth.make_x_f32(M, K, seed=M)
+        xh, xd = X, engine.DTYPE_F32
+    sel = np.r_[0:3, M // 2, M - 3:M]
+    W = oracle.decode_rows(m)
+    yref = oracle.gemm(m, X[sel], threads=THREADS)
+    out = {}
+    for path in (engine.GEMM_LIBRARY, engine.GEMM_PANEL):
+        eng.set_gemm_path(path)
+        try:
+            out[path, 0] = run_dev(eng, t, xh, xd, M, engine.DTYPE_F32)
+            out[path, 1] = run_dev(eng, t, xh, xd, M, engine.DTYPE_BF16)
+        finally:
+            eng.set_gemm_path(engine.GEMM_AUTO)
+        gemm_check(out[path, 0][sel], yref, W, X[sel], False)
+        gemm_check(out[path, 1][sel], yref, W, X[sel], True)
+    assert np.array_equal(out[engine.GEMM_LIBRARY, 1], f32_to_bf16_bits(out[engine.GEMM_LIBRARY, 0]))
+    t.free()
+
+
+def test_gemm_library_in_captured_graph():
+    """The library dense phase records into a graph; every replay (with eager
+    work and synchronisation between replays) matches the eager result."""
+    e = engine.HipEngine()
+    try:
+        for kind in ("g64", "cb4"):
+            m = make(kind, 640, 1024, seed=12)
+            t = e.upload_packed(m)
+            xd = e.to_device(synth.make_x_bf16(512, 1024, seed=13))
+            yd = e.alloc(512 * 640 * 2)
+            e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 512, yd.ptr, engine.DTYPE_BF16, e.stream)
+            e.synchronize()
+            ref = yd.download(np.uint16, (512, 640))
+            g = e.capture(lambda s: e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 512, yd.ptr, engine.DTYPE_BF16, s))
+            for rep in range(3):
+                yd.upload(np.full((512, 640), 0x7FC0, np.uint16))
+                g.launch(1)
+                assert np.array_equal(yd.download(np.uint16, (512, 640)), ref), (kind, rep)
+                e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 512, yd.ptr, engine.DTYPE_BF16, e.stream)
+                e.synchronize()
+            g.free()
+            t.free()
+            xd.free()
+            yd.free()
+    finally:
+        e.close()
+
+
 def test_gemm_in_captured_graph():
     """A GEMM records into a graph once its workspace is sized by an eager call."""
     e = engine.HipEngine()

@@ -14,7 +14,10 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvxt_hip.so")
 SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip",
-           "dequant.hip", "chain.hip", "greedy.hip", "ffn.hip", "attn.hip", "archive.cpp"]
+           "gemm_blas.cpp", "dequant.hip", "chain.hip", "greedy.hip", "ffn.hip", "attn.hip", "archive.cpp"]
+
+# hipBLASLt runs the dense phase of large-batch prefill GEMMs (gemm_blas.cpp).
+LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -52,7 +55,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(lambda so: _compile(so[0], so[1], verbose), zip(srcs, objs)))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, *LIBS, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

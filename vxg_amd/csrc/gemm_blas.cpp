@@ -1,0 +1,113 @@
+// gemm_blas.cpp -- the dense phase of the two-phase prefill GEMM on
+// hipBLASLt, for large batches.
+//
+// Once the weights are decoded into an f16 panel (gemm_panel.hip), what is
+// left is a plain f16 x f16 -> f32 GEMM, D[M][N] = alpha * A[M][K] * B[N][K]^T
+// + beta * D, both operands K-contiguous.  Column-major, that is
+// D^T (N x M) = op_T(B as K x N) * (A as K x M): hipBLASLt's "TN" case.
+// Handles are per device; the descriptors and the heuristic's first
+// algorithm are cached per shape.  No workspace is offered to the library, so
+// the algorithms it picks never clear one (a clearing node recorded into a
+// captured graph is not replayed reliably on this platform).
+#include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+
+namespace vxt {
+
+namespace {
+
+struct Entry {
+  hipblasLtMatmulDesc_t op = nullptr;
+  hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
+  hipblasLtMatmulAlgo_t algo{};
+};
+
+using Key = std::tuple<int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;   // device, M, N, K, lda, ldb
+
+std::mutex g_mu;
+std::map<int, hipblasLtHandle_t> g_handles;
+std::map<Key, Entry> g_entries;
+constexpr size_t kMaxEntries = 512;
+
+hipError_t status(hipblasStatus_t st) {
+  if (st == HIPBLAS_STATUS_SUCCESS) return hipSuccess;
+  return st == HIPBLAS_STATUS_NOT_SUPPORTED ? hipErrorNotSupported : hipErrorUnknown;
+}
+
+// The cached entry for this shape on the current device (created on first
+// use, outside any capture: the caller's eager call sizes the workspace
+// before a capture is allowed).
+hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb, hipblasLtHandle_t* h,
+                     const Entry** out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto hi = g_handles.find(dev);
+  if (hi == g_handles.end()) {
+    hipblasLtHandle_t nh = nullptr;
+    hipError_t e = status(hipblasLtCreate(&nh));
+    if (e != hipSuccess) return e;
+    hi = g_handles.emplace(dev, nh).first;
+  }
+  *h = hi->second;
+  const Key key{dev, M, N, K, lda, ldb};
+  auto it = g_entries.find(key);
+  if (it != g_entries.end()) {
+    *out = &it->second;
+    return hipSuccess;
+  }
+  if (g_entries.size() >= kMaxEntries) return hipErrorNotSupported;
+  Entry en;
+  hipError_t e = status(hipblasLtMatmulDescCreate(&en.op, HIPBLAS_COMPUTE_32F, HIP_R_32F));
+  const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+  if (e == hipSuccess)
+    e = status(hipblasLtMatmulDescSetAttribute(en.op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof(ta)));
+  if (e == hipSuccess)
+    e = status(hipblasLtMatmulDescSetAttribute(en.op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof(tb)));
+  if (e == hipSuccess) e = status(hipblasLtMatrixLayoutCreate(&en.la, HIP_R_16F, K, N, ldb));   // weights
+  if (e == hipSuccess) e = status(hipblasLtMatrixLayoutCreate(&en.lb, HIP_R_16F, K, M, lda));   // activations
+  if (e == hipSuccess) e = status(hipblasLtMatrixLayoutCreate(&en.ld, HIP_R_32F, N, M, N));
+  hipblasLtMatmulPreference_t pref = nullptr;
+  if (e == hipSuccess) e = status(hipblasLtMatmulPreferenceCreate(&pref));
+  const uint64_t no_ws = 0;
+  if (e == hipSuccess)
+    e = status(hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_ws,
+                                                     sizeof(no_ws)));
+  hipblasLtMatmulHeuristicResult_t res{};
+  int nres = 0;
+  if (e == hipSuccess) e = status(hipblasLtMatmulAlgoGetHeuristic(*h, en.op, en.la, en.lb, en.ld, en.ld, pref, 1,
+                                                                  &res, &nres));
+  if (pref) hipblasLtMatmulPreferenceDestroy(pref);
+  if (e == hipSuccess && nres < 1) e = hipErrorNotSupported;
+  if (e != hipSuccess) {
+    if (en.ld) hipblasLtMatrixLayoutDestroy(en.ld);
+    if (en.lb) hipblasLtMatrixLayoutDestroy(en.lb);
+    if (en.la) hipblasLtMatrixLayoutDestroy(en.la);
+    if (en.op) hipblasLtMatmulDescDestroy(en.op);
+    return e;
+  }
+  en.algo = res.algo;
+  *out = &g_entries.emplace(key, en).first->second;
+  return hipSuccess;
+}
+
+}  // namespace
+
+// D[M][N] (f32, row-major) = alpha * A[M][K] * B[N][K]^T + beta * D; A and B
+// f16 row-major with row strides lda, ldb (elements).
+hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
+                            uint32_t K, float alpha, float beta, float* D, hipStream_t s) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  hipblasLtHandle_t h = nullptr;
+  const Entry* en = nullptr;
+  e = entry_for(dev, M, N, K, lda, ldb, &h, &en);
+  if (e != hipSuccess) return e;
+  return status(hipblasLtMatmul(h, en->op, &alpha, B, en->la, A, en->lb, &beta, D, en->ld, D, en->ld, &en->algo,
+                                nullptr, 0, s));
+}
+
+}  // namespace vxt

@@ -35,6 +35,8 @@ namespace vxt {
 
 hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
                               bool y_bf16, hipStream_t s);
+hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
+                            uint32_t K, float alpha, float beta, float* D, hipStream_t s);
 
 namespace gp {
 
@@ -544,13 +546,17 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
 
 struct Plan {
   int bm, bn, wmode;
+  bool lib;   // dense phase on the vendor library (gemm_blas.cpp)
   uint32_t kp, splits, kt_per_split;
   size_t panel_plane, dsc_bytes, panel_bytes, a_plane, a_bytes, partial_bytes;
 };
 
-inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16) {
+inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   Plan pl{};
-  pl.wmode = t.kind == KIND_G64 ? kWPlain : (t.kind == KIND_Q8 && x_bf16 ? kWQBlock : kWHiLo);
+  pl.lib = lib;
+  // The library multiplies plain f16 operands: Q8 then takes the hi/lo panel
+  // (exact for q * d) instead of int8 values with block scales.
+  pl.wmode = t.kind == KIND_G64 ? kWPlain : (t.kind == KIND_Q8 && x_bf16 && !lib ? kWQBlock : kWHiLo);
   pl.kp = (t.cols + BK - 1) / BK * BK;
   const uint32_t ktiles = pl.kp / BK;
   pl.bm = m >= 256 ? 128 : 64;
@@ -570,6 +576,9 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16) {
   pl.a_plane = al256((size_t)m * pl.kp * 2);
   pl.a_bytes = pl.a_plane * (x_bf16 ? 1 : 2);
   pl.partial_bytes = pl.splits > 1 ? al256((size_t)pl.splits * m * t.rows * 4) : 0;
+  // Library: fp32 D [M][N] (also room for the own kernel's partial sums, its
+  // fallback when the library offers no algorithm for a shape).
+  if (lib) pl.partial_bytes = std::max(pl.partial_bytes, al256((size_t)m * t.rows * 4));
   return pl;
 }
 
@@ -609,10 +618,30 @@ hipError_t launch_dense_m(const Panel& p, const uint16_t* ah, const uint16_t* al
   return launch_dense_x<64, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, s);
 }
 
+// The dense phase on the vendor library: D = sum of f16 GEMMs over the
+// hi/lo planes present (lo terms scaled by 2^-11; lo x lo dropped, as in
+// dense_kernel), then Y = D / s through reduce_kernel with one split.
+// hipErrorNotSupported when the library has no algorithm for the shape.
+hipError_t library_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, bool split_a, int wmode, uint32_t m,
+                         uint32_t n, void* y, bool y_bf16, float* d, hipStream_t s) {
+  struct Term { const uint16_t* a; const uint16_t* b; float alpha; };
+  Term terms[3];
+  int nt = 0;
+  terms[nt++] = {ah, p.hi, 1.0f};
+  if (wmode == kWHiLo) terms[nt++] = {ah, p.lo, kLoInv};
+  if (split_a) terms[nt++] = {al, p.hi, kLoInv};
+  for (int i = 0; i < nt; ++i) {
+    const hipError_t e = blas_gemm_f16_tn(terms[i].a, p.kp, terms[i].b, p.kp, m, n, p.kp, terms[i].alpha,
+                                          i == 0 ? 0.0f : 1.0f, d, s);
+    if (e != hipSuccess) return e;
+  }
+  return launch_gemm_reduce(d, 1, p.inv, m, n, y, y_bf16, s);
+}
+
 template <uint32_t KIND>
 hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
-               size_t ws_bytes, hipStream_t s) {
-  const Plan pl = plan(t, m, x_bf16);
+               size_t ws_bytes, hipStream_t s, bool lib) {
+  const Plan pl = plan(t, m, x_bf16, lib);
   if (ws_bytes < pl.panel_bytes + pl.a_bytes + pl.partial_bytes) return hipErrorInvalidValue;
   char* base = static_cast<char*>(ws);
   const bool hilo = pl.wmode == kWHiLo;
@@ -642,6 +671,11 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
                      (uint32_t)(pl.wmode == kWQBlock ? 1u : 0u), nseg);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (pl.lib) {
+    e = library_dense(p, ah, al, !x_bf16, pl.wmode, m, t.rows, y, y_bf16, partial, s);
+    if (e != hipErrorNotSupported) return e;
+    (void)hipGetLastError();   // no algorithm for this shape: the own dense kernel on the same panel
+  }
   if constexpr (KIND == KIND_G64) {
     e = launch_dense_m<kWPlain>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
   } else if constexpr (KIND == KIND_Q8) {
@@ -680,13 +714,25 @@ hipError_t launch_gemm_fused(const DevTensor& t, const uint16_t* x, uint32_t m, 
 constexpr uint32_t kFusedMaxM = 256;
 
 static bool fused_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
-  if (mode == kGemmPanel || !gemm_fused_supported(t, x_bf16)) return false;
+  if (mode == kGemmPanel || mode == kGemmLibrary || !gemm_fused_supported(t, x_bf16)) return false;
   return mode == kGemmFused || m <= kFusedMaxM;
+}
+
+// Two-phase with the vendor dense GEMM: pinned, or automatically above the
+// fused kernel's batch limit when the product has at least 512 x 6144
+// outputs.  Measured (graph-timed, whole call, config 3): 1.2-1.3x faster
+// than dense_kernel at M = 512 x N = 6144 and M = 2048; slower for the
+// hi/lo kinds at M = 512 x N = 2048, a grid too small for the library
+// without a split-K workspace (none is offered, see gemm_blas.cpp).
+constexpr size_t kLibMinOutputs = (size_t)512 * 6144;
+
+static bool library_path(uint32_t m, uint32_t n, int mode) {
+  return mode == kGemmLibrary || (mode == kGemmAuto && m > kFusedMaxM && (size_t)m * n >= kLibMinOutputs);
 }
 
 size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
   if (fused_path(t, m, x_bf16, mode)) return gemm_fused_workspace_bytes(t, m);
-  const gp::Plan pl = gp::plan(t, m, x_bf16);
+  const gp::Plan pl = gp::plan(t, m, x_bf16, library_path(m, t.rows, mode));
   return pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
 }
 
@@ -695,10 +741,11 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   if (m == 0 || (size_t)m * t.rows > (size_t)1 << 40) return hipErrorInvalidValue;
   if (fused_path(t, m, x_bf16, mode))
     return launch_gemm_fused(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
+  const bool lib = library_path(m, t.rows, mode);
   switch (t.kind) {
-    case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
-    case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
-    case KIND_CB4: return gp::run<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s);
+    case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
+    case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
+    case KIND_CB4: return gp::run<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
     default: return hipErrorInvalidValue;
   }
 }

@@ -981,7 +981,7 @@ int vxt_hip_last_kernel_ms(void* ctx, double* ms) {
 }
 
 int vxt_hip_set_gemm_path(void* ctx, uint32_t path) {
-  if (!ctx || path > VXT_GEMM_FUSED) return VXT_E_ARG;
+  if (!ctx || path > VXT_GEMM_LIBRARY) return VXT_E_ARG;
   Ctx* c = static_cast<Ctx*>(ctx);
   std::lock_guard<std::mutex> lk(c->mu);
   c->gemm_mode = (int)path;

@@ -48,7 +48,7 @@ VXT_E_ARG, VXT_E_SHAPE, VXT_E_FORMAT, VXT_E_DEVICE, VXT_E_UNSUPPORTED = -1, -2, 
 DTYPE_F32, DTYPE_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 NORM_PLAIN, NORM_GLU_SILU, NORM_GLU_GELU_TANH = 0, 1, 2
-GEMM_AUTO, GEMM_PANEL, GEMM_FUSED = 0, 1, 2
+GEMM_AUTO, GEMM_PANEL, GEMM_FUSED, GEMM_LIBRARY = 0, 1, 2, 3
 KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
 
 ABI_SYMBOLS = (
@@ -574,7 +574,7 @@ class HipEngine:
         return int(r[0]), bool(r[1])
 
     def set_gemm_path(self, path: int) -> None:
-        """Pin the prefill GEMM path (``GEMM_AUTO``, ``GEMM_PANEL``, ``GEMM_FUSED``)."""
+        """Pin the prefill GEMM path (``GEMM_AUTO``, ``GEMM_PANEL``, ``GEMM_FUSED``, ``GEMM_LIBRARY``)."""
         rc = load_library().vxt_hip_set_gemm_path(self.ctx, path)
         if rc != VXT_OK:
             raise BackendError(rc, f"unknown GEMM path {path}")
