@@ -86,15 +86,25 @@ __device__ __forceinline__ void split_write(float w, float s, uint16_t* hi, uint
 
 // ---- phase 1: activations and panel -----------------------------------------
 
-// X [M][K] (bf16 or f32) -> A [M][kp] f16, zero for k >= K; f32 X also gets
-// the lo plane (x - hi) * 2^11.  One thread per 8 columns.
+// Activation conversion, run by the first `blocks` workgroups of the panel
+// launch: X [M][K] (bf16 or f32) -> A [M][kp] f16, zero for k >= K; f32 X
+// also gets the lo plane (x - hi) * 2^11.  One thread per 8 columns.
+struct XConv {
+  const void* x;
+  uint16_t* ah;
+  uint16_t* al;
+  uint32_t m, cols, x_bf16, x_vec, blocks;
+};
+
 template <bool XBF16>
-__global__ __launch_bounds__(THREADS) void xconv_kernel(const void* __restrict__ x, uint32_t M, uint32_t K, uint32_t kp,
-                                                        uint16_t* __restrict__ ah, uint16_t* __restrict__ al,
-                                                        uint32_t x_vec) {
+__device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
+  const void* __restrict__ x = c.x;
+  uint16_t* __restrict__ ah = c.ah;
+  uint16_t* __restrict__ al = c.al;
+  const uint32_t K = c.cols, x_vec = c.x_vec;
   const uint32_t ppr = kp / 8;
-  const size_t pieces = (size_t)M * ppr;
-  for (size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x; i < pieces; i += (size_t)gridDim.x * THREADS) {
+  const size_t pieces = (size_t)c.m * ppr;
+  for (size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x; i < pieces; i += (size_t)c.blocks * THREADS) {
     const uint32_t m = (uint32_t)(i / ppr), k = (uint32_t)(i % ppr) * 8;
     float v[8];
     if (x_vec && k + 8 <= K) {
@@ -177,17 +187,24 @@ __device__ __forceinline__ void store32(const float (&w)[32], float s, uint16_t*
 // serially.  cb4 residuals are applied by the wave owning the column's
 // segment, after its dense stores, in CSR order.
 template <uint32_t KIND>
-__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, uint32_t qblock, uint32_t nseg) {
+__global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, uint32_t qblock, uint32_t nseg, XConv xc) {
   constexpr uint32_t kPair = 48;   // g64 pair-table stride (bytes) in the per-wave slot
   __shared__ __attribute__((aligned(64))) uint32_t s_slot[KIND == KIND_G64 ? 4 * 32 * kPair / 4 : 1];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
+  if (blockIdx.x < xc.blocks) {   // uniform per workgroup: the activation conversion's share
+    if (xc.x_bf16)
+      xconv_blocks<true>(xc, p.kp);
+    else
+      xconv_blocks<false>(xc, p.kp);
+    return;
+  }
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t N = t.rows, K = t.cols, kp = t.kp, KP = p.kp;
   if constexpr (KIND == KIND_CB4) {
     if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
     __syncthreads();
   }
-  const uint32_t unit = blockIdx.x * 4 + wave;
+  const uint32_t unit = (blockIdx.x - xc.blocks) * 4 + wave;
   if (unit >= N * nseg) return;
   const uint32_t n = unit / nseg, seg = (unit % nseg) * (64 * 32);
   const uint32_t k0 = seg + lane * 32;
@@ -657,19 +674,16 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
 
   const size_t esz = x_bf16 ? 2 : 4;
   const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t.cols * esz) % 16 == 0;
+  // One launch: the activation conversion's workgroups first, then one
+  // wave per (weight row, 2048-column segment) of the panel decode.
   const size_t pieces = (size_t)m * (pl.kp / 8);
-  const uint32_t xgrid = (uint32_t)std::min<size_t>((pieces + THREADS - 1) / THREADS, 2048);
-  if (x_bf16)
-    hipLaunchKernelGGL((xconv_kernel<true>), dim3(xgrid), dim3(THREADS), 0, s, x, m, t.cols, pl.kp, ah, al, x_vec);
-  else
-    hipLaunchKernelGGL((xconv_kernel<false>), dim3(xgrid), dim3(THREADS), 0, s, x, m, t.cols, pl.kp, ah, al, x_vec);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  XConv xc{x, ah, al, m, t.cols, (uint32_t)x_bf16, x_vec,
+           (uint32_t)std::min<size_t>((pieces + THREADS - 1) / THREADS, 1024)};
   const uint32_t nseg = (p.kp + 64 * 32 - 1) / (64 * 32);
   const uint32_t pgrid = (uint32_t)(((size_t)t.rows * nseg + 3) / 4);
-  hipLaunchKernelGGL((panel_kernel<KIND>), dim3(pgrid), dim3(THREADS), 0, s, t, p,
-                     (uint32_t)(pl.wmode == kWQBlock ? 1u : 0u), nseg);
-  e = hipGetLastError();
+  hipLaunchKernelGGL((panel_kernel<KIND>), dim3(xc.blocks + pgrid), dim3(THREADS), 0, s, t, p,
+                     (uint32_t)(pl.wmode == kWQBlock ? 1u : 0u), nseg, xc);
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (pl.lib) {
     e = library_dense(p, ah, al, !x_bf16, pl.wmode, m, t.rows, y, y_bf16, partial, s);
