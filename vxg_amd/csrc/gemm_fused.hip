@@ -373,7 +373,7 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
 }
 
 struct Plan {
-  int fi, kw;
+  int fi;
   uint32_t tiles_m, tiles_n, cps, splits;
   size_t partial_bytes;
 };
@@ -381,7 +381,6 @@ struct Plan {
 inline Plan plan(const DevTensor& t, uint32_t m) {
   Plan p{};
   p.fi = m <= 32 ? 1 : (m <= 64 ? 2 : 4);
-  p.kw = t.kind == KIND_Q8 && p.fi == 4 ? 1 : 2;
   p.tiles_m = (m + 32 * p.fi - 1) / (32 * p.fi);
   p.tiles_n = (t.rows + BN - 1) / BN;
   const uint32_t kt = (t.kp + BK - 1) / BK;

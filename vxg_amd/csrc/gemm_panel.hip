@@ -21,6 +21,12 @@
 //      hi + lo like the weights, with one more MFMA (lo * lo dropped).
 //      Small M*N grids split K across workgroups; reduce_kernel then adds the
 //      partial sums in a fixed order (results do not depend on timing).
+//      For large products the dense phase runs on hipBLASLt instead
+//      (library_dense below, gemm_blas.cpp), with reduce_kernel as the
+//      1/s + bf16 epilogue.
+//
+// g64 and Q8_0 weights with bf16 activations at small batches take the fused
+// kernel of gemm_fused.hip instead of either phase (launch_gemm chooses).
 //
 // The panel costs one pass over the packed weights plus one f16 (or 2 x f16)
 // write; the fused alternative re-decodes every weight tile once per M tile
