@@ -84,8 +84,7 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvQ8Dev c, const fl
   const float x = live ? (is_v ? v[i] : k[i]) : 0.0f;
   const float a = fabsf(x);
   float amax = a == a ? a : 0.0f;
-#pragma unroll
-  for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+  amax = lane_reduce<32, true>(amax);
   const uint32_t dh = f32_to_f16_bits(amax / 127.0f);
   const float df = f16_to_f32_exact(dh);
   const float inv = df > 0.0f ? 1.0f / df : 0.0f;
@@ -167,8 +166,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc = __builtin_fmaf(qg[j], kf[j], acc);
       acc *= f16_to_f32_exact(kdb[p]);
-#pragma unroll
-      for (int off = 1; off < LPT; off <<= 1) acc += __shfl_xor(acc, off, 64);
+      acc = lane_reduce<LPT>(acc);
       if (sub == 0 && tl[p] < n) s_p[g * CH + tl[p]] = acc * scale;
     }
   }
@@ -178,8 +176,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   for (uint32_t g = wave; g < group; g += 4u) {
     float m = -__builtin_inff();
     for (uint32_t t = lane; t < n; t += 64u) m = fmaxf(m, s_p[g * CH + t]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    m = lane_reduce<64, true>(m);
     float l = 0.0f;
     for (uint32_t t = lane; t < n; t += 64u) {
       const float e = expf(s_p[g * CH + t] - m);
@@ -228,8 +225,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
       if ((uint32_t)a >= gn) break;
 #pragma unroll
       for (int j = 0; j < 16; ++j)
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1) acc[a][j] += __shfl_xor(acc[a][j], off, 64);
+        acc[a][j] = stride_sum<LPT>(acc[a][j]);
       if (slot == 0) {
 #pragma unroll
         for (int j = 0; j < 16; ++j) s_red[(wave * 4u + a) * HD + sub * 16u + j] = acc[a][j];
@@ -260,8 +256,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __res
   const float* ph = part + (size_t)h * n_chunks * stride;
   float m = -__builtin_inff();
   for (uint32_t c = tid; c < n_chunks; c += kThreads) m = fmaxf(m, ph[c * stride]);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+  m = lane_reduce<64, true>(m);
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
   m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));

@@ -112,6 +112,49 @@ __device__ __forceinline__ float dpp_mov(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
 
+// Lane-group reductions with no LDS traffic (every lane active): DPP
+// quad_perm xor 1 / xor 2, row_half_mirror and row_mirror pair the lanes of
+// aligned groups of 2..16; v_permlane16_swap / v_permlane32_swap called with
+// v as both operands return v and its xor-16 (xor-32) partner, one in each
+// result, so combining the pair gives the group of 32 (64).
+__device__ __forceinline__ float xor16_pair(float v, bool mx) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return mx ? fmaxf(a, b) : a + b;
+}
+__device__ __forceinline__ float xor32_pair(float v, bool mx) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+  return mx ? fmaxf(a, b) : a + b;
+}
+
+// Sum (MAX: maximum) over aligned groups of N consecutive lanes, N a power of
+// two <= 64, returned in every lane of the group.
+template <int N, bool MAX = false>
+__device__ __forceinline__ float lane_reduce(float v) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if constexpr (N >= 2) v = op(v, dpp_mov<0xB1>(v));    // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) v = op(v, dpp_mov<0x4E>(v));    // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) v = op(v, dpp_mov<0x141>(v));   // row_half_mirror
+  if constexpr (N >= 16) v = op(v, dpp_mov<0x140>(v));  // row_mirror
+  if constexpr (N >= 32) v = xor16_pair(v, MAX);
+  if constexpr (N >= 64) v = xor32_pair(v, MAX);
+  return v;
+}
+
+// Sum over the lanes that share lane % S (S a power of two <= 16), returned
+// in every lane: row_ror by S, 2S, .. 8 inside each 16-lane row, then across
+// rows and halves.
+template <int S>
+__device__ __forceinline__ float stride_sum(float v) {
+  if constexpr (S <= 1) v += dpp_mov<0x121>(v);   // row_ror:1
+  if constexpr (S <= 2) v += dpp_mov<0x122>(v);   // row_ror:2
+  if constexpr (S <= 4) v += dpp_mov<0x124>(v);   // row_ror:4
+  if constexpr (S <= 8) v += dpp_mov<0x128>(v);   // row_ror:8
+  v = xor16_pair(v, false);
+  return xor32_pair(v, false);
+}
+
 // Sum over the 64 lanes, returned in every lane (uniform).  DPP butterflies
 // inside each 16-lane row (quad_perm xor 1, xor 2, half-mirror, mirror), then
 // the four row sums are read out with v_readlane.  No LDS round trips.
