@@ -242,33 +242,39 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   }
 }
 
-// Merge: workgroup (head, 64 dimensions).  The chunks' maximum first, then
-// each wave sums a quarter of the chunks (sixteen at a time in flight), then
-// the waves' sums are added in order.
-__global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
-                                                             uint32_t n_chunks, const float* __restrict__ gate,
-                                                             float* __restrict__ out) {
+// Merge: workgroup (head, 64 dimensions) of kMergeWaves waves.  The chunks'
+// maximum first, then wave w sums chunks w, w + kMergeWaves, ... (sixteen
+// at a time in flight), then the waves' sums are added in wave order.
+constexpr uint32_t kMergeWaves = 16;
+
+__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
+                                                                     uint32_t n_chunks,
+                                                                     const float* __restrict__ gate,
+                                                                     float* __restrict__ out) {
 #pragma clang fp contract(off)
-  __shared__ float s_m[4], s_acc[4][64], s_l[4];
+  constexpr uint32_t W = kMergeWaves;
+  __shared__ float s_m[W], s_acc[W][64], s_l[W];
   const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t d = blockIdx.y * 64u + lane;
   const size_t stride = hd + 2;
   const float* ph = part + (size_t)h * n_chunks * stride;
   float m = -__builtin_inff();
-  for (uint32_t c = tid; c < n_chunks; c += kThreads) m = fmaxf(m, ph[c * stride]);
+  for (uint32_t c = tid; c < n_chunks; c += W * 64u) m = fmaxf(m, ph[c * stride]);
   m = lane_reduce<64, true>(m);
   if (lane == 0) s_m[wave] = m;
   __syncthreads();
-  m = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  m = s_m[0];
+#pragma unroll
+  for (uint32_t w = 1; w < W; ++w) m = fmaxf(m, s_m[w]);
   const uint32_t dc = d < hd ? d : hd - 1;
   float acc = 0.0f, l = 0.0f;
   uint32_t c = wave;
   constexpr int U = 16;   // chunks in flight per lane
-  for (; c + 4u * (U - 1) < n_chunks; c += 4u * U) {
+  for (; c + W * (U - 1) < n_chunks; c += W * U) {
     float mc[U], lc[U], ac[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float* pc = ph + (size_t)(c + 4u * u) * stride;
+      const float* pc = ph + (size_t)(c + W * u) * stride;
       mc[u] = pc[0];
       lc[u] = pc[1];
       ac[u] = pc[2 + dc];
@@ -280,7 +286,7 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __res
       acc += ac[u] * e;
     }
   }
-  for (; c < n_chunks; c += 4u) {
+  for (; c < n_chunks; c += W) {
     const float* pc = ph + (size_t)c * stride;
     const float e = expf(pc[0] - m);
     l += pc[1] * e;
@@ -290,8 +296,13 @@ __global__ __launch_bounds__(kThreads) void attn_merge_kernel(const float* __res
   if (lane == 0) s_l[wave] = l;
   __syncthreads();
   if (wave != 0 || d >= hd) return;
-  const float tot = (s_l[0] + s_l[1]) + (s_l[2] + s_l[3]);
-  float o = ((s_acc[0][lane] + s_acc[1][lane]) + (s_acc[2][lane] + s_acc[3][lane])) / tot;
+  float tot = s_l[0], o = s_acc[0][lane];
+#pragma unroll
+  for (uint32_t w = 1; w < W; ++w) {
+    tot += s_l[w];
+    o += s_acc[w][lane];
+  }
+  o = o / tot;
   if (gate) o *= 1.0f / (1.0f + expf(-gate[(size_t)h * hd + d]));
   out[(size_t)h * hd + d] = o;
 }
@@ -343,8 +354,8 @@ hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64), dim3(kThreads), 0, s, part, c.hd, n_chunks,
-                     gate, out);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64), dim3(kMergeWaves * 64), 0, s, part, c.hd,
+                     n_chunks, gate, out);
   return hipGetLastError();
 }
 

@@ -154,17 +154,8 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
   }
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-
-__device__ __forceinline__ float wave_add(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return lane_reduce<64, true>(v); }
+__device__ __forceinline__ float wave_add(float v) { return lane_reduce<64>(v); }
 
 // 32 consecutive f32 weights -> hi (and lo) f16 pieces at column k0 of the row.
 template <bool SPLIT>
