@@ -272,6 +272,53 @@ VXT_API int vxt_hip_attn_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const floa
                                 uint32_t seq_len, const float* gate, float* out, void* stream, char* err,
                                 size_t err_cap);
 
+/* The scalar arguments of step_full_gqa_q8 (llm_prefill.rs:259-278) plus the
+ * optional biases the Metal runner's prep adds (vxt_cb4_gqa_prep_batch,
+ * vxt_cb4_fast_gqa.metal:455-541); the cache supplies n_kv and head_dim.
+ * Pointers are device memory or NULL. */
+typedef struct VxtGqaParams {
+    const float* q_norm;   /* NULL or [head_dim]: RMSNorm weight of every q head   */
+    const float* k_norm;   /* NULL or [head_dim]                                   */
+    const float* q_bias;   /* NULL or [q_rows], added to q_raw before anything else */
+    const float* k_bias;   /* NULL or [n_kv * head_dim]                            */
+    const float* v_bias;   /* NULL or [n_kv * head_dim]                            */
+    uint32_t n_head;
+    uint32_t gated_q;      /* 1: q_raw holds [q | gate] per head, q_rows = 2 * n_head * head_dim;
+                              0: q_rows = n_head * head_dim                         */
+    uint32_t rope_dim;     /* rotated values per head (clamped to head_dim); 0: none */
+    uint32_t rope_neox;    /* 1: pairs (i, i + r / 2); 0: pairs (2i, 2i + 1)        */
+    float rope_freq_base;
+    float eps;             /* of the q / k RMSNorm                                  */
+} VxtGqaParams;
+
+/* The q / k preparation of step_full_gqa_q8 (llm_prefill.rs:284-313) for
+ * batch_m tokens: token m reads q_raw + m * q_stride, k_cur + m * kv_stride,
+ * v_cur + m * kv_stride (strides ignored for batch_m 1), and is at cache row
+ * pos + m and rope position rope_pos + m.  Per query head: the q half (and,
+ * gated, the gate half -> gate_out), rms_norm with q_norm (llm_ops.rs:48-57),
+ * apply_rope (llm_ops.rs:81-99) -> q_out [batch_m][n_head * head_dim].  Per kv
+ * head: K normed with k_norm and rotated, then K and V quantised into the
+ * token's cache row (KvQ8Block::quantize bits).  k_cur is read, not
+ * rewritten (the reference rotates it in place).  fp32; the norm's sum of
+ * squares runs in another order than the reference loop, the rotation's
+ * frequencies are the reference's powf values. */
+VXT_API int vxt_hip_attn_prep_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaParams* params,
+                                     const float* q_raw, uint32_t q_stride, const float* k_cur, const float* v_cur,
+                                     uint32_t kv_stride, uint32_t batch_m, uint32_t pos, uint32_t rope_pos,
+                                     float* q_out, float* gate_out, void* stream, char* err, size_t err_cap);
+
+/* step_full_gqa_q8 (llm_prefill.rs:259-367) whole, for batch_m tokens at
+ * positions pos .. pos + batch_m - 1: the prep above, then token m's
+ * attention over cache rows [0, pos + m] with its gate -> out + m * n_head *
+ * head_dim.  batch_m 1 is the decode step (llm_cpu.rs:395-412); a batch is the
+ * per-token loop of the tiled prefill (llm_prefill.rs:505-517), causal.
+ * Uses the context workspace (rules of vxt_hip_matmul_dev).  n_head / n_kv
+ * <= 8. */
+VXT_API int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaParams* params,
+                                     const float* q_raw, uint32_t q_stride, const float* k_cur, const float* v_cur,
+                                     uint32_t kv_stride, uint32_t batch_m, uint32_t pos, uint32_t rope_pos,
+                                     float* out, void* stream, char* err, size_t err_cap);
+
 /* ---- Weight containers ----------------------------------------------------
  * Readers over bytes the caller holds (e.g. a mapped file); they keep no
  * pointer after returning.  Offsets below are byte offsets into those bytes. */

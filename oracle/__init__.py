@@ -97,6 +97,14 @@ def lib():
         L.vxo_rms_norm.restype = None
         L.vxo_attn_q8.argtypes = [vp, vp, vp, sz, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]
         L.vxo_attn_q8.restype = None
+        L.vxo_apply_rope.argtypes = [vp, sz, sz, sz, C.c_float, i32]
+        L.vxo_apply_rope.restype = None
+        gqa = [vp, vp, vp, vp, vp, i32, C.c_uint32, C.c_uint32, C.c_uint32, sz, sz, sz, C.c_float, i32, C.c_float,
+               vp, vp]
+        L.vxo_gqa_prep_q8.argtypes = gqa + [vp, vp]
+        L.vxo_gqa_prep_q8.restype = None
+        L.vxo_gqa_step_q8.argtypes = gqa + [vp]
+        L.vxo_gqa_step_q8.restype = None
         L.vxo_greedy.argtypes = [vp, sz, C.POINTER(C.c_uint32)]
         L.vxo_greedy.restype = C.c_uint32
         _lib = L
@@ -319,6 +327,61 @@ def kv_q8_blocks(x, n_kv: int, hd: int) -> np.ndarray:
     for i in range(x.shape[0]):
         lib().vxo_q8_quantize(_ptr(x[i]), _ptr(out[i]))
     return out
+
+
+def apply_rope(vec, pos: int, rope_dim: int, freq_base: float, neox: bool) -> np.ndarray:
+    """``apply_rope`` of llm_ops.rs:81-99 on a copy of one head's vector."""
+    v = np.array(vec, dtype=np.float32).reshape(-1)
+    lib().vxo_apply_rope(_ptr(v), v.size, int(pos), int(rope_dim), float(freq_base), int(bool(neox)))
+    return v
+
+
+class GqaStep:
+    """Scalar arguments of step_full_gqa_q8 (llm_prefill.rs:259-278)."""
+
+    def __init__(self, n_head, n_kv, hd, gated=False, q_norm=None, k_norm=None, rope_dim=0,
+                 freq_base=10000.0, neox=False, eps=1e-6):
+        self.n_head, self.n_kv, self.hd = n_head, n_kv, hd
+        self.gated, self.rope_dim, self.freq_base, self.neox, self.eps = gated, rope_dim, freq_base, neox, eps
+        self.q_norm = None if q_norm is None else np.ascontiguousarray(q_norm, dtype=np.float32)
+        self.k_norm = None if k_norm is None else np.ascontiguousarray(k_norm, dtype=np.float32)
+
+    @property
+    def q_rows(self):
+        return self.n_head * self.hd * (2 if self.gated else 1)
+
+    def _args(self, q_raw, k_cur, v_cur, pos, rope_pos, kb, vb):
+        p = self
+        return (_ptr(q_raw), _ptr(k_cur), _ptr(v_cur), None if p.q_norm is None else _ptr(p.q_norm),
+                None if p.k_norm is None else _ptr(p.k_norm), int(p.gated), p.n_head, p.n_kv, p.hd, int(pos),
+                int(rope_pos), int(p.rope_dim), float(p.freq_base), int(p.neox), float(p.eps), _ptr(kb), _ptr(vb))
+
+    def _inputs(self, q_raw, k_cur, v_cur, kb, vb, pos):
+        q_raw = np.ascontiguousarray(q_raw, dtype=np.float32).reshape(-1)
+        k_cur = np.array(k_cur, dtype=np.float32).reshape(-1)
+        v_cur = np.ascontiguousarray(v_cur, dtype=np.float32).reshape(-1)
+        kvd = self.n_kv * self.hd
+        assert q_raw.size == self.q_rows and k_cur.size == kvd and v_cur.size == kvd
+        assert kb.dtype == np.uint8 and vb.dtype == np.uint8 and kb.flags.c_contiguous and vb.flags.c_contiguous
+        assert kb.size >= (pos + 1) * kvd // 32 * 34 and vb.size == kb.size
+        return q_raw, k_cur, v_cur
+
+    def prep(self, q_raw, k_cur, v_cur, kb, vb, pos: int, rope_pos: int):
+        """vxo_gqa_prep_q8: returns (q heads, gates or None, normed and rotated
+        k); writes row ``pos`` of the block arrays ``kb`` / ``vb`` in place."""
+        q_raw, k_cur, v_cur = self._inputs(q_raw, k_cur, v_cur, kb, vb, pos)
+        qh = np.empty(self.n_head * self.hd, dtype=np.float32)
+        qg = np.empty(self.n_head * self.hd, dtype=np.float32) if self.gated else None
+        lib().vxo_gqa_prep_q8(*self._args(q_raw, k_cur, v_cur, pos, rope_pos, kb, vb), _ptr(qh),
+                              None if qg is None else _ptr(qg))
+        return qh, qg, k_cur
+
+    def step(self, q_raw, k_cur, v_cur, kb, vb, pos: int, rope_pos: int) -> np.ndarray:
+        """vxo_gqa_step_q8: one whole step; writes row ``pos`` of kb / vb."""
+        q_raw, k_cur, v_cur = self._inputs(q_raw, k_cur, v_cur, kb, vb, pos)
+        out = np.empty(self.n_head * self.hd, dtype=np.float32)
+        lib().vxo_gqa_step_q8(*self._args(q_raw, k_cur, v_cur, pos, rope_pos, kb, vb), _ptr(out))
+        return out
 
 
 def attn_q8(q, k_blocks, v_blocks, seq_len: int, n_head: int, n_kv: int, hd: int, gate=None) -> np.ndarray:

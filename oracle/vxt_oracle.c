@@ -585,6 +585,83 @@ VXO_API void vxo_attn_q8(const float* q, const uint8_t* k_blocks, const uint8_t*
     free(scores);
 }
 
+/* llm_ops.rs:81-99 apply_rope: rotate pairs of vec[0 .. min(rope_dim, len))
+ * by theta_i = pos * freq_base^(-2i / rdim), i < rdim / 2 (f32 powf, the
+ * product pos * freq in f32, sinf / cosf); neox pairs (i, i + rdim / 2),
+ * otherwise (2i, 2i + 1).  x0' = x0 c - x1 s, x1' = x0 s + x1 c, each
+ * product rounded on its own. */
+VXO_API void vxo_apply_rope(float* vec, size_t len, size_t pos, size_t rope_dim, float freq_base, int neox) {
+    const size_t rdim = rope_dim < len ? rope_dim : len;
+    const size_t half = rdim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const float freq = powf(freq_base, -(2.0f * (float)i) / (float)rdim);
+        const float theta = (float)pos * freq;
+        const float sin_t = sinf(theta), cos_t = cosf(theta);
+        const size_t i0 = neox ? i : 2 * i, i1 = neox ? i + half : 2 * i + 1;
+        const float x0 = vec[i0], x1 = vec[i1];
+        vec[i0] = x0 * cos_t - x1 * sin_t;
+        vec[i1] = x0 * sin_t + x1 * cos_t;
+    }
+}
+
+/* llm_prefill.rs:284-313: the part of step_full_gqa_q8 before the scores.
+ * Per query head h: q_raw's head slice (gated: [q | gate], 2 hd values;
+ * else hd), q_norm'd (rms_norm, llm_ops.rs:48-57) when q_norm is given,
+ * rotated at rope_pos -> q_heads[h * hd ..], the gate half -> q_gates.  Per kv
+ * head: k_cur's slice k_norm'd and rotated in place, then K and V quantised
+ * (KvQ8Block::quantize) into row pos of the [t][kv head][hd / 32] block
+ * arrays. */
+VXO_API void vxo_gqa_prep_q8(const float* q_raw, float* k_cur, const float* v_cur, const float* q_norm,
+                             const float* k_norm, int gated, uint32_t n_head, uint32_t n_kv, uint32_t hd, size_t pos,
+                             size_t rope_pos, size_t rope_dim, float freq_base, int neox, float eps,
+                             uint8_t* k_blocks, uint8_t* v_blocks, float* q_heads, float* q_gates) {
+    float* tmp = (float*)malloc(hd * sizeof(float));
+    for (uint32_t h = 0; h < n_head; ++h) {
+        float* q_dst = q_heads + (size_t)h * hd;
+        const float* src = q_raw + (size_t)h * (gated ? 2u : 1u) * hd;
+        memcpy(q_dst, src, hd * sizeof(float));
+        if (gated) memcpy(q_gates + (size_t)h * hd, src + hd, hd * sizeof(float));
+        if (q_norm) {
+            memcpy(tmp, q_dst, hd * sizeof(float));
+            vxo_rms_norm(tmp, q_norm, hd, eps, q_dst);
+        }
+        vxo_apply_rope(q_dst, hd, rope_pos, rope_dim, freq_base, neox);
+    }
+    for (uint32_t kh = 0; kh < n_kv; ++kh) {
+        float* ks = k_cur + (size_t)kh * hd;
+        if (k_norm) {
+            memcpy(tmp, ks, hd * sizeof(float));
+            vxo_rms_norm(tmp, k_norm, hd, eps, ks);
+        }
+        vxo_apply_rope(ks, hd, rope_pos, rope_dim, freq_base, neox);
+    }
+    const size_t bph = hd / 32, stride = (size_t)n_kv * bph;
+    for (uint32_t kh = 0; kh < n_kv; ++kh) {
+        for (size_t b = 0; b < bph; ++b) {
+            const size_t off = (size_t)kh * hd + b * 32, blk = pos * stride + (size_t)kh * bph + b;
+            vxo_q8_quantize(k_cur + off, k_blocks + blk * 34);
+            vxo_q8_quantize(v_cur + off, v_blocks + blk * 34);
+        }
+    }
+    free(tmp);
+}
+
+/* llm_prefill.rs:259-367 step_full_gqa_q8, whole: the prep above, then the
+ * attention of the query heads over positions [0, pos] (vxo_attn_q8) with the
+ * gate of a gated q.  out: [n_head * hd]. */
+VXO_API void vxo_gqa_step_q8(const float* q_raw, float* k_cur, const float* v_cur, const float* q_norm,
+                             const float* k_norm, int gated, uint32_t n_head, uint32_t n_kv, uint32_t hd, size_t pos,
+                             size_t rope_pos, size_t rope_dim, float freq_base, int neox, float eps,
+                             uint8_t* k_blocks, uint8_t* v_blocks, float* out) {
+    float* qh = (float*)malloc((size_t)n_head * hd * sizeof(float));
+    float* qg = gated ? (float*)malloc((size_t)n_head * hd * sizeof(float)) : NULL;
+    vxo_gqa_prep_q8(q_raw, k_cur, v_cur, q_norm, k_norm, gated, n_head, n_kv, hd, pos, rope_pos, rope_dim, freq_base,
+                    neox, eps, k_blocks, v_blocks, qh, qg);
+    vxo_attn_q8(qh, k_blocks, v_blocks, pos + 1, n_head, n_kv, hd, qg, out);
+    free(qg);
+    free(qh);
+}
+
 /* Greedy selection.  The index follows the greedy branch of
  * sample_logits_top_k_p (llm_ops.rs:307-327): an empty input gives 0; else a
  * forward scan from (best_v = -inf, best_i = 0) that takes index i only when

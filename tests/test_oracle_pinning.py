@@ -592,3 +592,125 @@ def test_attn_q8_gqa_mapping_uniform_scores_and_gate():
     gated = oracle.attn_q8(q, kb, vb, seq, 4, n_kv, hd, gate=g).reshape(4, hd)
     sig = 1 / (1 + np.exp(-g.astype(np.float64)))
     assert np.allclose(gated, out * sig.reshape(4, hd), rtol=1e-6, atol=1e-30)
+
+
+# ---------------------------------------------------------------- RoPE and the whole GQA step
+
+def rope_f64(x, pos, rope_dim, base, neox):
+    """The rotation of llm_ops.rs:81-99 as complex multiplication in f64; the
+    angle is formed the reference's way (f32 exponent, f32 power rounded from
+    f64, f32 product with the position) so the test sees the same angles."""
+    x = np.asarray(x, np.float32).astype(np.float64).copy()
+    rdim = min(rope_dim, x.size)
+    half = rdim // 2
+    for i in range(half):
+        e = np.float32(-(np.float32(2.0) * np.float32(i))) / np.float32(rdim)
+        freq = np.float32(np.float64(np.float32(base)) ** np.float64(e))
+        theta = np.float64(np.float32(np.float32(pos) * freq))
+        i0, i1 = (i, i + half) if neox else (2 * i, 2 * i + 1)
+        z = complex(x[i0], x[i1]) * complex(np.cos(theta), np.sin(theta))
+        x[i0], x[i1] = z.real, z.imag
+    return x
+
+
+@pytest.mark.parametrize("neox", [False, True])
+@pytest.mark.parametrize("n,rope_dim", [(32, 32), (64, 32), (128, 128), (128, 64), (64, 7), (32, 0), (32, 1),
+                                        (16, 40)])
+@pytest.mark.parametrize("pos", [0, 1, 37, 4095, 40000])
+def test_apply_rope_vs_complex_rotation(neox, n, rope_dim, pos):
+    rng = np.random.default_rng(n * 7 + rope_dim + pos)
+    x = (rng.standard_normal(n) * 2).astype(np.float32)
+    for base in (10000.0, 1e6):
+        got = oracle.apply_rope(x, pos, rope_dim, base, neox)
+        ref = rope_f64(x, pos, rope_dim, base, neox)
+        # two f32 products per output plus 1-ulp sin / cos, on |x| <= max|x|
+        assert np.abs(got - ref).max() <= 2.0 ** -21 * np.abs(x).max()
+        rdim = min(rope_dim, n)
+        touched = np.zeros(n, bool)
+        half = rdim // 2
+        for i in range(half):
+            touched[[i, i + half] if neox else [2 * i, 2 * i + 1]] = True
+        assert np.array_equal(got[~touched].view(np.uint32), x[~touched].view(np.uint32))
+        if pos == 0:
+            assert np.array_equal(got, x)
+        # a rotation keeps each pair's length
+        i0 = np.arange(half) if neox else 2 * np.arange(half)
+        i1 = i0 + half if neox else i0 + 1
+        r_in = np.hypot(x[i0].astype(np.float64), x[i1].astype(np.float64))
+        r_out = np.hypot(got[i0].astype(np.float64), got[i1].astype(np.float64))
+        assert np.all(np.abs(r_out - r_in) <= 1e-6 * np.abs(x).max())
+
+
+def gqa_inputs(p, seed, scale=1.0):
+    rng = np.random.default_rng(seed)
+    q_raw = (rng.standard_normal(p.q_rows) * scale).astype(np.float32)
+    k = (rng.standard_normal(p.n_kv * p.hd) * scale).astype(np.float32)
+    v = rng.standard_normal(p.n_kv * p.hd).astype(np.float32)
+    return q_raw, k, v
+
+
+def prep_f64(p, q_raw, k, rope_pos):
+    """Independent split / norm / rotation in f64 (llm_prefill.rs:284-309)."""
+    hd = p.hd
+    qs = np.asarray(q_raw, np.float64).reshape(p.n_head, (2 if p.gated else 1) * hd)
+    q, gate = qs[:, :hd], (qs[:, hd:] if p.gated else None)
+
+    def norm(x, w):
+        if w is None:
+            return x
+        return x / np.sqrt((x * x).sum(axis=1, keepdims=True) / hd + p.eps) * w.astype(np.float64)
+
+    qn, kn = norm(q, p.q_norm), norm(np.asarray(k, np.float64).reshape(p.n_kv, hd), p.k_norm)
+    qr = np.stack([rope_f64(r.astype(np.float32), rope_pos, p.rope_dim, p.freq_base, p.neox) for r in qn])
+    kr = np.stack([rope_f64(r.astype(np.float32), rope_pos, p.rope_dim, p.freq_base, p.neox) for r in kn])
+    return qr.reshape(-1), gate, kr.reshape(-1)
+
+
+@pytest.mark.parametrize("gated,norms,neox,rope_dim,hd", [
+    (False, False, False, 0, 32), (True, True, True, 64, 64), (True, False, False, 32, 128),
+    (False, True, True, 128, 128), (True, True, False, 16, 256)])
+def test_gqa_prep_vs_f64_parts(gated, norms, neox, rope_dim, hd):
+    rng = np.random.default_rng(hd + rope_dim)
+    n_head, n_kv, pos, rope_pos = 8, 2, 5, 1234
+    p = oracle.GqaStep(n_head, n_kv, hd, gated=gated, rope_dim=rope_dim, freq_base=1e6, neox=neox, eps=1e-6,
+                       q_norm=rng.standard_normal(hd) if norms else None,
+                       k_norm=rng.standard_normal(hd) if norms else None)
+    q_raw, k, v = gqa_inputs(p, seed=hd, scale=3.0)
+    blk = n_kv * hd // 32
+    kb = np.zeros(((pos + 1) * blk, 34), np.uint8)
+    vb = np.zeros_like(kb)
+    qh, qg, k_rot = p.prep(q_raw, k, v, kb, vb, pos, rope_pos)
+    q_ref, g_ref, k_ref = prep_f64(p, q_raw, k, rope_pos)
+    qmax = np.abs(q_ref).max()
+    assert np.abs(qh - q_ref).max() <= 2e-6 * qmax
+    assert np.abs(k_rot - k_ref).max() <= 2e-6 * np.abs(k_ref).max()
+    if gated:
+        assert np.array_equal(qg, g_ref.reshape(-1).astype(np.float32))
+    else:
+        assert qg is None
+    # row pos holds K (normed, rotated) and V, each KvQ8Block::quantize'd; rows below untouched
+    assert np.array_equal(kb[pos * blk:], oracle.kv_q8_blocks(k_rot, n_kv, hd))
+    assert np.array_equal(vb[pos * blk:], oracle.kv_q8_blocks(v, n_kv, hd))
+    assert not kb[:pos * blk].any() and not vb[:pos * blk].any()
+
+
+def test_gqa_step_is_prep_then_attention_over_positions_up_to_pos():
+    n_head, n_kv, hd, S = 8, 2, 64, 40
+    rng = np.random.default_rng(11)
+    p = oracle.GqaStep(n_head, n_kv, hd, gated=True, rope_dim=64, freq_base=10000.0, neox=True, eps=1e-6,
+                       q_norm=rng.standard_normal(hd), k_norm=rng.standard_normal(hd))
+    blk = n_kv * hd // 32
+    kb = np.zeros((S * blk, 34), np.uint8)
+    vb = np.zeros_like(kb)
+    for pos in range(S):
+        q_raw, k, v = gqa_inputs(p, seed=100 + pos)
+        kb2, vb2 = kb.copy(), vb.copy()
+        out = p.step(q_raw, k, v, kb, vb, pos, pos + 3)
+        qh, qg, _ = p.prep(q_raw, k, v, kb2, vb2, pos, pos + 3)
+        assert np.array_equal(kb, kb2) and np.array_equal(vb, vb2)
+        assert np.array_equal(out, oracle.attn_q8(qh, kb, vb, pos + 1, n_head, n_kv, hd, gate=qg))
+        if pos in (0, S - 1):
+            # brute force over the dequantised cache, the gate as the sigmoid factor
+            ref, vmax = attn_f64(qh, kb[:(pos + 1) * blk], vb[:(pos + 1) * blk], pos + 1, n_head, n_kv, hd)
+            sig = 1 / (1 + np.exp(-qg.astype(np.float64)))
+            assert np.abs(out - ref * sig).max() <= 1e-5 * vmax

@@ -1,8 +1,10 @@
-// attn.hip -- Q8_0 KV cache for decode: append one position, attend over
-// the cache.
+// attn.hip -- Q8_0 KV cache for decode and prefill: prepare a step's q and
+// k, append positions, attend over the cache.
 //
-// Reference: KvQ8Block (llm_prefill.rs:17-63) and the attention of
-// step_full_gqa_q8 (llm_prefill.rs:300-367).
+// Reference: KvQ8Block (llm_prefill.rs:17-63), step_full_gqa_q8
+// (llm_prefill.rs:259-367) and apply_rope (llm_ops.rs:81-99); the Metal
+// runner's batched prep (vxt_cb4_gqa_prep_batch, vxt_cb4_fast_gqa.metal:
+// 455-541).
 //
 // Device layout (the caller's VxtKvQ8Cache; row t holds position t):
 //   k_qs, v_qs  int8 [max_seq][n_kv * hd]        (16-byte aligned rows)
@@ -15,29 +17,27 @@
 // ignored, as f32::max does), d = f16(amax / 127) rounded to nearest even,
 // q = round_ties_even(x / f32(d)) clamped to +-127 (NaN -> 0).
 //
-// Attention (split sequence): workgroup (kv head, chunk of positions) serves
-// the query heads that share the kv head.  Each position is read once: a
-// position's K and V rows are split across hd / 16 lanes (16 values each),
-// all requested up front; the dot with every head's q (staged in LDS) is
-// reduced over those lanes and scaled by 1 / sqrt(hd); the chunk's scores
-// stay in LDS; the chunk's max m, the sum l of exp(s - m) and sum exp(s - m) V
-// go to a partials buffer.  A second kernel merges the chunks per head
-// (exp(m_c - m) rescaling), divides by the total and applies the optional
-// sigmoid gate.  The sums run in a
-// different order from the CPU loop (fp32, parity by tolerance).
+// Prep: one wave per (head, token) splits a gated q, applies the per-head
+// RMSNorm and RoPE to q and k and quantises K and V into the token's row.
+//
+// Attention (split sequence): workgroup (kv head, chunk of positions, token)
+// serves the query heads that share the kv head.  Each position is read once
+// per token: a position's K and V rows are split across hd / 16 lanes (16
+// values each), all requested up front; the dot with every head's q (staged
+// in LDS) is reduced over those lanes and scaled by 1 / sqrt(hd); the chunk's
+// scores stay in LDS; the chunk's max m, the sum l of exp(s - m) and
+// sum exp(s - m) V go to a partials buffer.  A second kernel merges the
+// chunks per head (exp(m_c - m) rescaling), divides by the total and applies
+// the optional sigmoid gate.  Token z of a batch attends to positions
+// [0, seq0 + z) (causal prefill).  The sums run in a different order from the
+// CPU loop (fp32, parity by tolerance).
 #include "common.hpp"
 
 #include <algorithm>
+#include <cmath>
+#include <cstring>
 
 namespace vxt {
-
-struct KvQ8Dev {
-  int8_t* k_qs;
-  uint16_t* k_d;
-  int8_t* v_qs;
-  uint16_t* v_d;
-  uint32_t max_seq, n_kv, hd;
-};
 
 namespace {
 
@@ -73,28 +73,159 @@ __device__ __forceinline__ uint32_t f32_to_f16_bits(float val) {
   return sign | e16 | m16;
 }
 
+// KvQ8Block::quantize of one value per lane, each aligned 32-lane group
+// holding one block (every lane of the wave must call it): amax of |x| with
+// NaN ignored, dh = f16 bits of amax / 127, q = round_ties_even(x / f32(dh))
+// clamped to +-127, NaN -> 0.
+__device__ __forceinline__ int q8_lane(float x, uint32_t& dh) {
+#pragma clang fp contract(off)
+  const float a = fabsf(x);
+  float amax = a == a ? a : 0.0f;
+  amax = lane_reduce<32, true>(amax);
+  dh = f32_to_f16_bits(amax / 127.0f);
+  const float df = f16_to_f32_exact(dh);
+  const float inv = df > 0.0f ? 1.0f / df : 0.0f;
+  const float r = rintf(x * inv);
+  return r != r ? 0 : (int)fminf(fmaxf(r, -127.0f), 127.0f);
+}
+
 __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvQ8Dev c, const float* __restrict__ k,
                                                             const float* __restrict__ v, uint32_t pos) {
-#pragma clang fp contract(off)
   const uint32_t per = c.n_kv * c.hd;
   const uint32_t e = blockIdx.x * kThreads + threadIdx.x;   // per % 32 == 0: a 32-group never straddles K/V
   const bool live = e < 2u * per;
   const bool is_v = e >= per;
   const uint32_t i = is_v ? e - per : e;
   const float x = live ? (is_v ? v[i] : k[i]) : 0.0f;
-  const float a = fabsf(x);
-  float amax = a == a ? a : 0.0f;
-  amax = lane_reduce<32, true>(amax);
-  const uint32_t dh = f32_to_f16_bits(amax / 127.0f);
-  const float df = f16_to_f32_exact(dh);
-  const float inv = df > 0.0f ? 1.0f / df : 0.0f;
-  const float r = rintf(x * inv);
-  const int q = r != r ? 0 : (int)fminf(fmaxf(r, -127.0f), 127.0f);
+  uint32_t dh;
+  const int q = q8_lane(x, dh);
   if (!live) return;
   int8_t* qs = is_v ? c.v_qs : c.k_qs;
   uint16_t* ds = is_v ? c.v_d : c.k_d;
   qs[(size_t)pos * per + i] = (int8_t)q;
   if ((i & 31u) == 0) ds[(size_t)pos * (per / 32) + i / 32] = (uint16_t)dh;
+}
+
+// ---- the step's q / k preparation (llm_prefill.rs:284-313) ----------------
+// One wave per (head, token): blockIdx.x < n_head is query head x, the rest
+// are kv heads; blockIdx.y is the token.  A lane holds the values d = lane +
+// 64 j of its head.  Query head: q_raw slice (+ bias), the gate half copied
+// out, RMSNorm with q_norm (sum of squares over the wave, then x * scale * w
+// as two roundings), RoPE, q_out.  Kv head: V (+ bias) quantised into the
+// cache; K (+ bias), RMSNorm with k_norm, RoPE, quantised.  RoPE angles are
+// (float)(rope_pos + token) * freq[i] with freq[i] = powf(base, -2i / rdim)
+// evaluated on the host (the same call as the reference's), sine and cosine
+// of the f32 angle evaluated in double and rounded once; both rotation
+// products round separately.
+struct RopeFreq {
+  float f[128];
+};
+
+template <int HD>
+__global__ __launch_bounds__(64) void gqa_prep_kernel(KvQ8Dev c, GqaPrep a, RopeFreq rf) {
+#pragma clang fp contract(off)
+  constexpr int J = HD >= 64 ? HD / 64 : 1;
+  __shared__ float s_x[HD];
+  const uint32_t lane = threadIdx.x, idx = blockIdx.x, m = blockIdx.y;
+  const bool is_q = idx < a.n_head;
+  const uint32_t kvh = is_q ? 0u : idx - a.n_head;
+  const uint32_t per = c.n_kv * HD;
+  const size_t row = (size_t)a.pos + m;
+  const uint32_t qoff = idx * (a.gated ? 2u : 1u) * HD;
+  const float* src = is_q ? a.q_raw + (size_t)m * a.q_stride + qoff : a.k_cur + (size_t)m * a.kv_stride + kvh * HD;
+  const float* bias = is_q ? (a.q_bias ? a.q_bias + qoff : nullptr) : (a.k_bias ? a.k_bias + kvh * HD : nullptr);
+  const float* nw = is_q ? a.q_norm : a.k_norm;
+
+  float x[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t d = lane + 64u * j;
+    x[j] = 0.0f;
+    if (d < HD) {
+      x[j] = src[d];
+      if (bias) x[j] = x[j] + bias[d];
+    }
+  }
+  if (is_q && a.gated) {
+    float* g = a.gate_out + (size_t)m * a.n_head * HD + (size_t)idx * HD;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      if (d < HD) g[d] = bias ? src[HD + d] + bias[HD + d] : src[HD + d];
+    }
+  }
+  if (!is_q) {
+    const float* vs = a.v_cur + (size_t)m * a.kv_stride + kvh * HD;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      float vv = 0.0f;
+      if (d < HD) {
+        vv = vs[d];
+        if (a.v_bias) vv = vv + a.v_bias[kvh * HD + d];
+      }
+      uint32_t dh;
+      const int q = q8_lane(vv, dh);
+      if (d < HD) {
+        c.v_qs[row * per + kvh * HD + d] = (int8_t)q;
+        if ((d & 31u) == 0) c.v_d[row * (per / 32) + (kvh * HD + d) / 32] = (uint16_t)dh;
+      }
+    }
+  }
+  if (nw) {
+    float sq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) sq = __builtin_fmaf(x[j], x[j], sq);
+    sq = lane_reduce<64>(sq);
+    const float scale = 1.0f / sqrtf(sq / (float)HD + a.eps);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      if (d < HD) x[j] = x[j] * scale * nw[d];
+    }
+  }
+  if (a.half) {
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      if (d < HD) s_x[d] = x[j];
+    }
+    __syncthreads();
+    const float p = (float)(a.rope_pos + m);
+    for (uint32_t i = lane; i < a.half; i += 64u) {
+      const float theta = p * rf.f[i];
+      const float sn = (float)sin((double)theta), cs = (float)cos((double)theta);
+      const uint32_t i0 = a.neox ? i : 2u * i, i1 = a.neox ? i + a.half : 2u * i + 1u;
+      const float x0 = s_x[i0], x1 = s_x[i1];
+      s_x[i0] = x0 * cs - x1 * sn;
+      s_x[i1] = x0 * sn + x1 * cs;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      if (d < HD) x[j] = s_x[d];
+    }
+  }
+  if (is_q) {
+    float* qo = a.q_out + (size_t)m * a.n_head * HD + (size_t)idx * HD;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      if (d < HD) qo[d] = x[j];
+    }
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
+    const uint32_t d = lane + 64u * j;
+    uint32_t dh;
+    const int q = q8_lane(x[j], dh);
+    if (d < HD) {
+      c.k_qs[row * per + kvh * HD + d] = (int8_t)q;
+      if ((d & 31u) == 0) c.k_d[row * (per / 32) + (kvh * HD + d) / 32] = (uint16_t)dh;
+    }
+  }
 }
 
 // 16 int8 -> f32
@@ -110,7 +241,7 @@ __device__ __forceinline__ void unpack16(const u32x4 w, float (&f)[16]) {
 // one trip to memory per workgroup.
 template <int LPT>
 __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const float* __restrict__ q, uint32_t group,
-                                                             uint32_t seq_len, uint32_t n_chunks,
+                                                             uint32_t seq0, uint32_t n_chunks,
                                                              float* __restrict__ part) {
   constexpr uint32_t HD = LPT * 16, TPW = 64 / LPT, PASSES = 4, CH = PASSES * 4 * TPW;
   extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -120,7 +251,12 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t slot = lane / LPT, sub = lane % LPT;
   const uint32_t kvh = blockIdx.x, ck = blockIdx.y;
-  const uint32_t t0 = ck * CH, n = min(seq_len - t0, CH);
+  const uint32_t seq_len = seq0 + blockIdx.z;             // token z sees positions [0, seq0 + z)
+  const uint32_t t0 = ck * CH;
+  if (t0 >= seq_len) return;                              // a chunk past this token's positions
+  const uint32_t n = min(seq_len - t0, CH);
+  q += (size_t)blockIdx.z * c.n_kv * group * HD;
+  part += (size_t)blockIdx.z * c.n_kv * group * n_chunks * (HD + 2);
   const uint32_t row_q = c.n_kv * HD, row_d = c.n_kv * (HD / 32);
   const float scale = 1.0f / sqrtf((float)HD);
 
@@ -248,16 +384,20 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
 constexpr uint32_t kMergeWaves = 16;
 
 __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
-                                                                     uint32_t n_chunks,
-                                                                     const float* __restrict__ gate,
+                                                                     uint32_t chunk_stride, uint32_t chunk,
+                                                                     uint32_t seq0, const float* __restrict__ gate,
                                                                      float* __restrict__ out) {
 #pragma clang fp contract(off)
   constexpr uint32_t W = kMergeWaves;
   __shared__ float s_m[W], s_acc[W][64], s_l[W];
   const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t d = blockIdx.y * 64u + lane;
+  const uint32_t z = blockIdx.z, n_head = gridDim.x;
+  const uint32_t n_chunks = (seq0 + z + chunk - 1u) / chunk;   // token z's chunks
   const size_t stride = hd + 2;
-  const float* ph = part + (size_t)h * n_chunks * stride;
+  const float* ph = part + ((size_t)z * n_head + h) * chunk_stride * stride;
+  if (gate) gate += (size_t)z * n_head * hd;
+  out += (size_t)z * n_head * hd;
   float m = -__builtin_inff();
   for (uint32_t c = tid; c < n_chunks; c += W * 64u) m = fmaxf(m, ph[c * stride]);
   m = lane_reduce<64, true>(m);
@@ -308,17 +448,22 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
 }
 
 template <int LPT>
-hipError_t launch_chunks(const KvQ8Dev& c, const float* q, uint32_t group, uint32_t seq_len, uint32_t n_chunks,
-                         float* part, hipStream_t s) {
+hipError_t launch_chunks(const KvQ8Dev& c, const float* q, uint32_t group, uint32_t seq0, uint32_t n_chunks,
+                         uint32_t batch, float* part, hipStream_t s) {
   constexpr uint32_t HD = LPT * 16, CH = 16u * (64u / LPT);
   const size_t lds = ((size_t)group * HD + (size_t)group * CH + 16u * HD) * 4u;
-  hipLaunchKernelGGL(attn_chunk_kernel<LPT>, dim3(c.n_kv, n_chunks), dim3(kThreads), lds, s, c, q, group, seq_len,
-                     n_chunks, part);
+  hipLaunchKernelGGL(attn_chunk_kernel<LPT>, dim3(c.n_kv, n_chunks, batch), dim3(kThreads), lds, s, c, q, group,
+                     seq0, n_chunks, part);
   return hipGetLastError();
 }
 
 // Positions per chunk: 4 passes of 4 waves x 64 / (hd / 16) positions.
 uint32_t chunk_of(uint32_t hd) { return 16u * (64u / (hd / 16u)); }
+
+template <int HD>
+void launch_prep(const KvQ8Dev& c, const GqaPrep& a, const RopeFreq& rf, uint32_t batch, hipStream_t s) {
+  hipLaunchKernelGGL(gqa_prep_kernel<HD>, dim3(a.n_head + c.n_kv, batch), dim3(64), 0, s, c, a, rf);
+}
 
 }  // namespace
 
@@ -328,34 +473,61 @@ hipError_t launch_kv_append(const KvQ8Dev& c, const float* k, const float* v, ui
   return hipGetLastError();
 }
 
-size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd) {
-  (void)n_kv;
-  const uint32_t chunk = chunk_of(hd);
-  const uint32_t n_chunks = (seq_len + chunk - 1) / chunk;
-  return (size_t)n_head * n_chunks * (hd + 2) * sizeof(float);
+// The rotation frequencies are a function of (freq_base, rdim) only; the last
+// table is kept per host thread.
+hipError_t launch_gqa_prep(const KvQ8Dev& c, GqaPrep a, uint32_t rope_dim, float freq_base, uint32_t batch,
+                           hipStream_t s) {
+  thread_local RopeFreq tab{};
+  thread_local uint32_t tab_rdim = 0;
+  thread_local float tab_base = 0.0f;
+  const uint32_t rdim = std::min(rope_dim, c.hd);
+  a.half = rdim / 2u;
+  if (a.half && (tab_rdim != rdim || std::memcmp(&tab_base, &freq_base, sizeof(float)) != 0)) {
+    for (uint32_t i = 0; i < a.half; ++i) tab.f[i] = powf(freq_base, -(2.0f * (float)i) / (float)rdim);
+    tab_rdim = rdim;
+    tab_base = freq_base;
+  }
+  switch (c.hd) {
+    case 32: launch_prep<32>(c, a, tab, batch, s); break;
+    case 64: launch_prep<64>(c, a, tab, batch, s); break;
+    case 128: launch_prep<128>(c, a, tab, batch, s); break;
+    case 256: launch_prep<256>(c, a, tab, batch, s); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
-// Requires hd in {32, 64, 128, 256}, n_head % n_kv == 0, n_head / n_kv <= 8,
-// 1 <= seq_len <= max_seq; ws holds attn_workspace_bytes.
-hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq_len, const float* gate,
-                       float* out, void* ws, hipStream_t s) {
+// Partials of a batch: batch x n_head x chunks of the longest token x (hd + 2).
+size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd, uint32_t batch) {
+  (void)n_kv;
+  const uint32_t chunk = chunk_of(hd);
+  const size_t n_chunks = ((size_t)seq_len + batch - 1 + chunk - 1) / chunk;
+  return (size_t)batch * n_head * n_chunks * (hd + 2) * sizeof(float);
+}
+
+// batch tokens; token z has q at q + z * n_head * hd and attends to positions
+// [0, seq0 + z).  Requires hd in {32, 64, 128, 256}, n_head % n_kv == 0,
+// n_head / n_kv <= 8, 1 <= seq0, seq0 + batch - 1 <= max_seq; ws holds
+// attn_workspace_bytes(n_head, seq0, n_kv, hd, batch).
+hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq0, uint32_t batch,
+                       const float* gate, float* out, void* ws, hipStream_t s) {
   const uint32_t group = n_head / c.n_kv;
-  if (group == 0 || group > kMaxGroup) return hipErrorInvalidValue;
+  if (group == 0 || group > kMaxGroup || batch == 0 || batch > 65535u) return hipErrorInvalidValue;
   const uint32_t chunk = chunk_of(c.hd);
-  const uint32_t n_chunks = (seq_len + chunk - 1) / chunk;
+  const uint32_t n_chunks = (uint32_t)(((size_t)seq0 + batch - 1 + chunk - 1) / chunk);
   if (n_chunks > 65535u) return hipErrorInvalidValue;
   float* part = static_cast<float*>(ws);
   hipError_t e;
   switch (c.hd) {
-    case 32: e = launch_chunks<2>(c, q, group, seq_len, n_chunks, part, s); break;
-    case 64: e = launch_chunks<4>(c, q, group, seq_len, n_chunks, part, s); break;
-    case 128: e = launch_chunks<8>(c, q, group, seq_len, n_chunks, part, s); break;
-    case 256: e = launch_chunks<16>(c, q, group, seq_len, n_chunks, part, s); break;
+    case 32: e = launch_chunks<2>(c, q, group, seq0, n_chunks, batch, part, s); break;
+    case 64: e = launch_chunks<4>(c, q, group, seq0, n_chunks, batch, part, s); break;
+    case 128: e = launch_chunks<8>(c, q, group, seq0, n_chunks, batch, part, s); break;
+    case 256: e = launch_chunks<16>(c, q, group, seq0, n_chunks, batch, part, s); break;
     default: return hipErrorInvalidValue;
   }
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64), dim3(kMergeWaves * 64), 0, s, part, c.hd,
-                     n_chunks, gate, out);
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64, batch), dim3(kMergeWaves * 64), 0, s, part,
+                     c.hd, n_chunks, chunk, seq0, gate, out);
   return hipGetLastError();
 }
 

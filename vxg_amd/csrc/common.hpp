@@ -105,6 +105,34 @@ struct NormIn {
   float eps;
 };
 
+// One layer's Q8_0 KV cache (the planes of VxtKvQ8Cache): row t holds
+// position t, n_kv * hd int8 values and n_kv * hd / 32 f16 scales per plane.
+struct KvQ8Dev {
+  int8_t* k_qs;
+  uint16_t* k_d;
+  int8_t* v_qs;
+  uint16_t* v_d;
+  uint32_t max_seq, n_kv, hd;
+};
+
+// The q / k preparation of an attention step for a batch of tokens: token m
+// reads q_raw + m * q_stride, k_cur / v_cur + m * kv_stride, writes cache row
+// pos + m and q_out / gate_out + m * n_head * hd, and rotates at rope_pos + m.
+struct GqaPrep {
+  const float* q_raw;
+  const float* k_cur;
+  const float* v_cur;
+  const float* q_norm;   // null: no norm
+  const float* k_norm;
+  const float* q_bias;   // null: no bias
+  const float* k_bias;
+  const float* v_bias;
+  float* q_out;
+  float* gate_out;       // gated only
+  uint32_t q_stride, kv_stride, n_head, gated, half, neox, pos, rope_pos;
+  float eps;
+};
+
 // ---- wave64 reductions ----------------------------------------------------
 
 template <int CTRL>

@@ -40,17 +40,12 @@ hipError_t launch_rms_norm(float* cur, const float* delta, const float* w, void*
                            uint32_t stride, uint32_t m, float eps, hipStream_t s);
 hipError_t launch_embed(const DevTensor& t, const uint32_t* tokens, uint32_t batch_m, float scale, bool scale_on,
                         float* out, uint32_t stride, hipStream_t s);
-struct KvQ8Dev {
-  int8_t* k_qs;
-  uint16_t* k_d;
-  int8_t* v_qs;
-  uint16_t* v_d;
-  uint32_t max_seq, n_kv, hd;
-};
 hipError_t launch_kv_append(const KvQ8Dev& c, const float* k, const float* v, uint32_t pos, hipStream_t s);
-size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd);
-hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq_len, const float* gate,
-                       float* out, void* ws, hipStream_t s);
+hipError_t launch_gqa_prep(const KvQ8Dev& c, GqaPrep a, uint32_t rope_dim, float freq_base, uint32_t batch,
+                           hipStream_t s);
+size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd, uint32_t batch);
+hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq0, uint32_t batch,
+                       const float* gate, float* out, void* ws, hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
 struct ChainLaunch {
@@ -802,9 +797,103 @@ int vxt_hip_attn_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const float* q, ui
     if (seq_len == 0 || seq_len > kc.max_seq) fail(VXT_E_SHAPE, "need 1 <= seq_len <= max_seq");
     if (n_head == 0 || n_head % kc.n_kv != 0) fail(VXT_E_SHAPE, "n_head must be a multiple of n_kv");
     if (n_head / kc.n_kv > 8) fail(VXT_E_UNSUPPORTED, "at most 8 query heads per kv head");
-    ensure_ws(c, vxt::attn_workspace_bytes(n_head, seq_len, kc.n_kv, kc.hd));
-    hipError_t e = vxt::launch_attn(kc, q, n_head, seq_len, gate, out, c->ws, static_cast<hipStream_t>(stream));
+    ensure_ws(c, vxt::attn_workspace_bytes(n_head, seq_len, kc.n_kv, kc.hd, 1));
+    hipError_t e = vxt::launch_attn(kc, q, n_head, seq_len, 1, gate, out, c->ws, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+namespace {
+// Checks shared by the prep and the whole step; fills the device arguments
+// (q_out / gate_out left to the caller).
+vxt::GqaPrep gqa_prep_args(const vxt::KvQ8Dev& kc, const VxtGqaParams* p, const float* q_raw, uint32_t q_stride,
+                           const float* k_cur, const float* v_cur, uint32_t kv_stride, uint32_t batch_m, uint32_t pos,
+                           uint32_t rope_pos) {
+  if (!p) fail(VXT_E_ARG, "null params");
+  if (!q_raw || !k_cur || !v_cur) fail(VXT_E_ARG, "null q_raw, k_cur or v_cur");
+  if (p->n_head == 0) fail(VXT_E_SHAPE, "n_head must be >= 1");
+  if (p->gated_q > 1 || p->rope_neox > 1) fail(VXT_E_ARG, "gated_q and rope_neox are 0 or 1");
+  if (batch_m == 0 || batch_m > 65535u) fail(VXT_E_SHAPE, "need 1 <= batch_m <= 65535");
+  if (pos >= kc.max_seq || batch_m > kc.max_seq - pos) fail(VXT_E_SHAPE, "pos + batch_m > max_seq");
+  if (rope_pos > UINT32_MAX - (batch_m - 1)) fail(VXT_E_SHAPE, "rope_pos + batch_m - 1 overflows");
+  const uint64_t q_rows = (uint64_t)p->n_head * kc.hd * (p->gated_q ? 2u : 1u);
+  if (batch_m > 1 && q_stride < q_rows) fail(VXT_E_SHAPE, "q_stride < q_rows");
+  if (batch_m > 1 && kv_stride < kc.n_kv * kc.hd) fail(VXT_E_SHAPE, "kv_stride < n_kv * head_dim");
+  if (!(p->eps >= 0.0f) || !std::isfinite(p->rope_freq_base)) fail(VXT_E_ARG, "eps or rope_freq_base out of range");
+  vxt::GqaPrep a{};
+  a.q_raw = q_raw;
+  a.k_cur = k_cur;
+  a.v_cur = v_cur;
+  a.q_norm = p->q_norm;
+  a.k_norm = p->k_norm;
+  a.q_bias = p->q_bias;
+  a.k_bias = p->k_bias;
+  a.v_bias = p->v_bias;
+  a.q_stride = q_stride;
+  a.kv_stride = kv_stride;
+  a.n_head = p->n_head;
+  a.gated = p->gated_q;
+  a.neox = p->rope_neox;
+  a.pos = pos;
+  a.rope_pos = rope_pos;
+  a.eps = p->eps;
+  return a;
+}
+}  // namespace
+
+int vxt_hip_attn_prep_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaParams* params, const float* q_raw,
+                             uint32_t q_stride, const float* k_cur, const float* v_cur, uint32_t kv_stride,
+                             uint32_t batch_m, uint32_t pos, uint32_t rope_pos, float* q_out, float* gate_out,
+                             void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    (void)as_ctx(ctx);
+    const vxt::KvQ8Dev kc = kv_cache_dev(cache);
+    vxt::GqaPrep a = gqa_prep_args(kc, params, q_raw, q_stride, k_cur, v_cur, kv_stride, batch_m, pos, rope_pos);
+    if (!q_out) fail(VXT_E_ARG, "null q_out");
+    if (params->gated_q && !gate_out) fail(VXT_E_ARG, "a gated q needs gate_out");
+    a.q_out = q_out;
+    a.gate_out = params->gated_q ? gate_out : nullptr;
+    hipError_t e = vxt::launch_gqa_prep(kc, a, params->rope_dim, params->rope_freq_base, batch_m,
+                                        static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention prep launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaParams* params, const float* q_raw,
+                             uint32_t q_stride, const float* k_cur, const float* v_cur, uint32_t kv_stride,
+                             uint32_t batch_m, uint32_t pos, uint32_t rope_pos, float* out, void* stream, char* err,
+                             size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    const vxt::KvQ8Dev kc = kv_cache_dev(cache);
+    vxt::GqaPrep a = gqa_prep_args(kc, params, q_raw, q_stride, k_cur, v_cur, kv_stride, batch_m, pos, rope_pos);
+    if (!out) fail(VXT_E_ARG, "null out");
+    const uint32_t n_head = params->n_head;
+    if (n_head % kc.n_kv != 0) fail(VXT_E_SHAPE, "n_head must be a multiple of n_kv");
+    if (n_head / kc.n_kv > 8) fail(VXT_E_UNSUPPORTED, "at most 8 query heads per kv head");
+    // Workspace: q (and gate) of every token, then the partial sums of one
+    // group of tokens at a time, groups sized to keep that part near 16 MiB.
+    const size_t q_bytes = (size_t)batch_m * n_head * kc.hd * sizeof(float);
+    const size_t qg_bytes = (q_bytes * (params->gated_q ? 2u : 1u) + 255u) & ~(size_t)255u;
+    const size_t per_tok = vxt::attn_workspace_bytes(n_head, pos + batch_m, kc.n_kv, kc.hd, 1);
+    const uint32_t group_m =
+        (uint32_t)std::max<size_t>(1, std::min<size_t>(batch_m, ((size_t)16 << 20) / std::max<size_t>(per_tok, 1)));
+    ensure_ws(c, qg_bytes + vxt::attn_workspace_bytes(n_head, pos + batch_m - group_m + 1, kc.n_kv, kc.hd, group_m));
+    float* q_ws = static_cast<float*>(c->ws);
+    float* g_ws = params->gated_q ? q_ws + (size_t)batch_m * n_head * kc.hd : nullptr;
+    void* part = static_cast<char*>(c->ws) + qg_bytes;
+    a.q_out = q_ws;
+    a.gate_out = g_ws;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = vxt::launch_gqa_prep(kc, a, params->rope_dim, params->rope_freq_base, batch_m, s);
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention prep launch failed: ") + hipGetErrorString(e));
+    const size_t row = (size_t)n_head * kc.hd;
+    for (uint32_t t = 0; t < batch_m; t += group_m) {
+      const uint32_t nb = std::min(group_m, batch_m - t);
+      e = vxt::launch_attn(kc, q_ws + t * row, n_head, pos + t + 1, nb, g_ws ? g_ws + t * row : nullptr,
+                           out + t * row, part, s);
+      if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention launch failed: ") + hipGetErrorString(e));
+    }
   });
 }
 

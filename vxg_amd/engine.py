@@ -59,7 +59,7 @@ ABI_SYMBOLS = (
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
     "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
     "vxt_hip_vxt_parse", "vxt_hip_upload_vxt_entry", "vxt_hip_gguf_parse", "vxt_hip_upload_gguf_q8_0",
-    "vxt_hip_kv_q8_append_dev", "vxt_hip_attn_q8_dev",
+    "vxt_hip_kv_q8_append_dev", "vxt_hip_attn_q8_dev", "vxt_hip_attn_prep_q8_dev", "vxt_hip_attn_step_q8_dev",
     "vxt_hip_last_kernel_ms", "vxt_hip_set_gemm_path", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
@@ -119,6 +119,14 @@ class VxtGgufTensor(C.Structure):
 class KvQ8CacheView(C.Structure):
     _fields_ = [("k_qs", C.c_void_p), ("k_d", C.c_void_p), ("v_qs", C.c_void_p), ("v_d", C.c_void_p),
                 ("max_seq", C.c_uint32), ("n_kv", C.c_uint32), ("head_dim", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+class GqaParams(C.Structure):
+    """``VxtGqaParams``: the scalar arguments of step_full_gqa_q8
+    (llm_prefill.rs:259-278) and the optional device pointers (0 = none)."""
+    _fields_ = [("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("q_bias", C.c_void_p), ("k_bias", C.c_void_p),
+                ("v_bias", C.c_void_p), ("n_head", C.c_uint32), ("gated_q", C.c_uint32), ("rope_dim", C.c_uint32),
+                ("rope_neox", C.c_uint32), ("rope_freq_base", C.c_float), ("eps", C.c_float)]
 
 
 class HipJob(C.Structure):
@@ -184,6 +192,11 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_kv_q8_append_dev.restype = C.c_int
     L.vxt_hip_attn_q8_dev.argtypes = [vp, C.POINTER(KvQ8CacheView), vp, u32, u32, vp, vp, vp, cp, sz]
     L.vxt_hip_attn_q8_dev.restype = C.c_int
+    gqa = [vp, C.POINTER(KvQ8CacheView), C.POINTER(GqaParams), vp, u32, vp, vp, u32, u32, u32, u32]
+    L.vxt_hip_attn_prep_q8_dev.argtypes = gqa + [vp, vp, vp, cp, sz]
+    L.vxt_hip_attn_prep_q8_dev.restype = C.c_int
+    L.vxt_hip_attn_step_q8_dev.argtypes = gqa + [vp, vp, cp, sz]
+    L.vxt_hip_attn_step_q8_dev.restype = C.c_int
     L.vxt_hip_vxt_parse.argtypes = [vp, sz, C.POINTER(VxtArchiveEntry), u32, C.POINTER(u32), C.POINTER(u32),
                                     cp, sz]
     L.vxt_hip_vxt_parse.restype = C.c_int
@@ -358,6 +371,25 @@ class KvQ8Cache:
         _check(load_library().vxt_hip_attn_q8_dev(self._engine.ctx, C.byref(self.view), q_ptr or None, n_head,
                                                   seq_len, gate_ptr or None, out_ptr or None, stream or None, buf,
                                                   len(buf)), buf)
+
+    def prep(self, params: GqaParams, q_raw: int, k_cur: int, v_cur: int, pos: int, rope_pos: int, q_out: int,
+             gate_out: int = 0, batch_m: int = 1, q_stride: int = 0, kv_stride: int = 0, stream: int = 0) -> None:
+        """vxt_hip_attn_prep_q8_dev: q / k preparation and the cache writes of
+        ``batch_m`` tokens at rows pos .. pos + batch_m - 1."""
+        buf = _errbuf()
+        _check(load_library().vxt_hip_attn_prep_q8_dev(
+            self._engine.ctx, C.byref(self.view), C.byref(params), q_raw or None, q_stride, k_cur or None,
+            v_cur or None, kv_stride, batch_m, pos, rope_pos, q_out or None, gate_out or None, stream or None, buf,
+            len(buf)), buf)
+
+    def step(self, params: GqaParams, q_raw: int, k_cur: int, v_cur: int, pos: int, rope_pos: int, out: int,
+             batch_m: int = 1, q_stride: int = 0, kv_stride: int = 0, stream: int = 0) -> None:
+        """vxt_hip_attn_step_q8_dev: the whole attention step of ``batch_m``
+        tokens (causal), out [batch_m][n_head * head_dim]."""
+        buf = _errbuf()
+        _check(load_library().vxt_hip_attn_step_q8_dev(
+            self._engine.ctx, C.byref(self.view), C.byref(params), q_raw or None, q_stride, k_cur or None,
+            v_cur or None, kv_stride, batch_m, pos, rope_pos, out or None, stream or None, buf, len(buf)), buf)
 
     def blocks(self, which: str, seq_len: int):
         """Positions [0, seq_len) as KvQ8Block bytes [seq][n_kv * hd / 32][34] (host copy)."""
