@@ -48,6 +48,49 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def bench_attn_step(eng, seq: int, n_head: int, n_kv: int, hd: int, batch: int = 1, calls: int = 100,
+                    seed: int = 7):
+    """The whole attention step (``vxt_hip_attn_step_q8_dev``: gated q, q / k
+    RMSNorm, RoPE over half of each head, K / V into the cache, attention) of
+    ``batch`` tokens at positions seq - batch .. seq - 1 over a filled cache,
+    timed as a captured graph of ``calls`` calls."""
+    import numpy as np
+    from vxg_amd import engine as E
+    rng = np.random.default_rng(seed)
+    cache = eng.kv_q8_cache(seq, n_kv, hd)
+    per = n_kv * hd
+    cache.k_qs.upload(rng.integers(-127, 128, size=seq * per, dtype=np.int8))
+    cache.v_qs.upload(rng.integers(-127, 128, size=seq * per, dtype=np.int8))
+    d = np.float16(rng.uniform(0.002, 0.02, size=seq * per // 32)).view(np.uint16)
+    cache.k_d.upload(d)
+    cache.v_d.upload(d)
+    q_rows = 2 * n_head * hd
+    bufs = [eng.to_device(a) for a in (rng.standard_normal(batch * q_rows).astype(np.float32),
+                                       rng.standard_normal(batch * per).astype(np.float32),
+                                       rng.standard_normal(batch * per).astype(np.float32),
+                                       (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32),
+                                       (1 + 0.1 * rng.standard_normal(hd)).astype(np.float32))]
+    qd, kd, vd, qn, kn = bufs
+    out = eng.alloc(batch * n_head * hd * 4)
+    p = E.GqaParams(qn.ptr, kn.ptr, 0, 0, 0, n_head, 1, hd // 2, 1, 1e6, 1e-6)
+    pos = seq - batch
+
+    def one(s):
+        cache.step(p, qd.ptr, kd.ptr, vd.ptr, pos, pos, out.ptr, batch_m=batch, q_stride=q_rows, kv_stride=per,
+                   stream=s)
+
+    one(eng.stream)                     # sizes the workspace
+    eng.synchronize()
+    g = eng.capture(lambda s: [one(s) for _ in range(calls)])
+    g.launch(1)
+    ms = g.launch(1) / calls
+    g.free()
+    for b in bufs + [out]:
+        b.free()
+    cache.free()
+    return {"us": ms * 1e3, "us_per_token": ms * 1e3 / batch}
+
+
 # --------------------------------------------------------------------------
 # algorithmic bytes per call
 # --------------------------------------------------------------------------
@@ -438,6 +481,15 @@ def main():
                               "kernel_us": round(ra["us"], 2), "bytes": int(ra["bytes"]),
                               "GBps": round(ra["GBps"], 1), "frac_hbm": round(ra["GBps"] / HBM_PEAK_GBS, 4)})
             log(f"  attention seq={seq} heads={nh}/{nkv}: {ra['us']:.2f} us, {ra['GBps']:.1f} GB/s")
+        for seq, nh, nkv, batch, calls in ((4096, 16, 16, 1, 200), (32768, 16, 4, 1, 200), (2048, 16, 4, 2048, 5),
+                                           (8192, 16, 4, 512, 5)):
+            rs = bench_attn_step(eng, seq, nh, nkv, 128, batch=batch, calls=calls)
+            secondary.append({"config": f"attention step (gated q, q/k RMSNorm, RoPE, K/V append, attention): "
+                                        f"{nh} heads / {nkv} kv heads x 128, {batch} token(s) ending at position "
+                                        f"{seq}",
+                              "us_per_call": round(rs["us"], 2), "us_per_token": round(rs["us_per_token"], 3)})
+            log(f"  attention step seq={seq} heads={nh}/{nkv} batch={batch}: {rs['us']:.2f} us per call, "
+                f"{rs['us_per_token']:.3f} us per token")
 
     cpu = None
     if not args.no_cpu:
