@@ -49,7 +49,7 @@ def log(msg: str) -> None:
 
 
 def bench_attn_step(eng, seq: int, n_head: int, n_kv: int, hd: int, batch: int = 1, calls: int = 100,
-                    seed: int = 7):
+                    seed: int = 7, eager: bool = False):
     """The whole attention step (``vxt_hip_attn_step_q8_dev``: gated q, q / k
     RMSNorm, RoPE over half of each head, K / V into the cache, attention) of
     ``batch`` tokens at positions seq - batch .. seq - 1 over a filled cache,
@@ -81,10 +81,17 @@ def bench_attn_step(eng, seq: int, n_head: int, n_kv: int, hd: int, batch: int =
 
     one(eng.stream)                     # sizes the workspace
     eng.synchronize()
-    g = eng.capture(lambda s: [one(s) for _ in range(calls)])
-    g.launch(1)
-    ms = g.launch(1) / calls
-    g.free()
+    if eager:   # plain launches (for profilers that do not follow graph replays)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            one(eng.stream)
+        eng.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / calls
+    else:
+        g = eng.capture(lambda s: [one(s) for _ in range(calls)])
+        g.launch(1)
+        ms = g.launch(1) / calls
+        g.free()
     for b in bufs + [out]:
         b.free()
     cache.free()
@@ -483,7 +490,7 @@ def main():
             log(f"  attention seq={seq} heads={nh}/{nkv}: {ra['us']:.2f} us, {ra['GBps']:.1f} GB/s")
         for seq, nh, nkv, batch, calls in ((4096, 16, 16, 1, 200), (32768, 16, 4, 1, 200), (2048, 16, 4, 2048, 5),
                                            (8192, 16, 4, 512, 5)):
-            rs = bench_attn_step(eng, seq, nh, nkv, 128, batch=batch, calls=calls)
+            rs = bench_attn_step(eng, seq, nh, nkv, 128, batch=batch, calls=calls, eager=args.eager)
             secondary.append({"config": f"attention step (gated q, q/k RMSNorm, RoPE, K/V append, attention): "
                                         f"{nh} heads / {nkv} kv heads x 128, {batch} token(s) ending at position "
                                         f"{seq}",

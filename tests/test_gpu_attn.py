@@ -59,6 +59,48 @@ def test_append_bit_exact(eng, n_kv, hd):
     cache.free()
 
 
+def f16_boundary_amaxes():
+    """Block maxima whose scale amax / 127 lands on, next to and between f16
+    rounding boundaries: ties between neighbouring f16 values (normal and
+    subnormal, both parities), one f32 ulp either side, the largest finite
+    f16 and the overflow threshold, and the underflow threshold 2^-25."""
+    h = np.concatenate([np.arange(1, 64), np.arange(1000, 1040), np.arange(0x0400 - 8, 0x0400 + 8),
+                        np.arange(0x3bf0, 0x3c10), np.arange(0x5000, 0x5010), np.arange(0x7bf0, 0x7bff)])
+    lo = oracle.f16_to_f32(h.astype(np.uint16)).astype(np.float64)
+    hi = oracle.f16_to_f32((h + 1).astype(np.uint16)).astype(np.float64)
+    mids = np.float32((lo + hi) / 2)
+    scales = np.concatenate([mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0)),
+                             np.float32(lo), np.float32([65504.0, 65519.99, 65520.0, 2.0 ** -25,
+                                                          np.nextafter(np.float32(2.0 ** -25), np.float32(1))])])
+    # amax near 127 * scale, plus its f32 neighbours (the division decides)
+    a = np.float32(scales.astype(np.float64) * 127)
+    return np.unique(np.concatenate([a, np.nextafter(a, np.float32(np.inf)), np.nextafter(a, np.float32(0))]))
+
+
+def test_append_scale_rounding_boundaries(eng):
+    """Every block's f16 scale and values bit-equal to KvQ8Block::quantize for
+    block maxima around f16 rounding boundaries (the scale conversion is the
+    hardware's round-to-nearest-even)."""
+    amax = f16_boundary_amaxes()
+    n_kv, hd = 4, 64
+    per_row = n_kv * hd // 32
+    seq = (amax.size + per_row - 1) // per_row
+    rng = np.random.default_rng(12)
+    X = (rng.uniform(-1, 1, (seq * per_row, 32)) * 0.999).astype(np.float32)
+    a = np.resize(amax, seq * per_row)
+    X *= a[:, None]
+    X[np.arange(X.shape[0]), rng.integers(0, 32, X.shape[0])] = a * np.where(rng.random(X.shape[0]) < 0.5, 1, -1)
+    K = X.reshape(seq, n_kv * hd)
+    V = K[::-1].copy()
+    cache = eng.kv_q8_cache(seq, n_kv, hd)
+    append_all(eng, cache, K, V)
+    for which, M in (("k", K), ("v", V)):
+        got = cache.blocks(which, seq)
+        want = np.stack([oracle.kv_q8_blocks(M[t], n_kv, hd) for t in range(seq)])
+        assert np.array_equal(got, want), which
+    cache.free()
+
+
 @pytest.mark.parametrize("seq,n_head,n_kv,hd", [(1, 4, 4, 128), (7, 8, 2, 64), (100, 16, 16, 128),
                                                 (1000, 16, 4, 128), (5000, 8, 1, 32), (300, 4, 4, 256),
                                                 (4097, 16, 16, 128)])

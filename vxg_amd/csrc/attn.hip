@@ -44,33 +44,13 @@ namespace {
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kMaxGroup = 8;   // query heads per kv head
 
-// f32 -> f16 bits, round to nearest even, subnormals kept (fp16.rs:33-77).
+// f32 -> f16 bits, round to nearest even with f16 subnormals kept and
+// overflow to infinity: what fp16.rs:33-77 computes with integer steps, here
+// v_cvt_f16_f32 (default round-to-nearest-even mode, f16 denormals on).
+// Inputs are never NaN (the callers pass a maximum of magnitudes that skips
+// NaN).
 __device__ __forceinline__ uint32_t f32_to_f16_bits(float val) {
-  const uint32_t b = __float_as_uint(val);
-  const uint32_t sign = (b >> 16) & 0x8000u;
-  const int32_t exp = (int32_t)((b >> 23) & 0xffu);
-  const uint32_t mant = b & 0x007fffffu;
-  if (exp == 255) return mant ? (sign | 0x7e00u | (mant >> 13)) : (sign | 0x7c00u);
-  const int32_t unb = exp - 127;
-  if (unb > 15) return sign | 0x7c00u;
-  if (unb < -25) return sign;
-  if (unb < -14) {
-    const uint32_t shift = (uint32_t)(-14 - unb);
-    const uint32_t full = mant | 0x00800000u;
-    const uint32_t rs = 13u + shift;
-    const uint32_t half = 1u << (rs - 1), rem = full & ((1u << rs) - 1u);
-    uint32_t m16 = full >> rs;
-    if (rem > half || (rem == half && (m16 & 1u))) m16 += 1;
-    return sign | m16;
-  }
-  const uint32_t e16 = (uint32_t)(unb + 15) << 10;
-  const uint32_t rem = mant & 0x1fffu;
-  uint32_t m16 = mant >> 13;
-  if (rem > 0x1000u || (rem == 0x1000u && (m16 & 1u))) {
-    m16 += 1;
-    if (m16 == 0x0400u) return sign | (e16 + 0x0400u);
-  }
-  return sign | e16 | m16;
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)val);
 }
 
 // KvQ8Block::quantize of one value per lane, each aligned 32-lane group
@@ -194,7 +174,9 @@ __global__ __launch_bounds__(64) void gqa_prep_kernel(KvQ8Dev c, GqaPrep a, Rope
     const float p = (float)(a.rope_pos + m);
     for (uint32_t i = lane; i < a.half; i += 64u) {
       const float theta = p * rf.f[i];
-      const float sn = (float)sin((double)theta), cs = (float)cos((double)theta);
+      double sd, cd;
+      sincos((double)theta, &sd, &cd);
+      const float sn = (float)sd, cs = (float)cd;
       const uint32_t i0 = a.neox ? i : 2u * i, i1 = a.neox ? i + a.half : 2u * i + 1u;
       const float x0 = s_x[i0], x1 = s_x[i1];
       s_x[i0] = x0 * cs - x1 * sn;
@@ -235,19 +217,57 @@ __device__ __forceinline__ void unpack16(const u32x4 w, float (&f)[16]) {
   for (int j = 0; j < 16; ++j) f[j] = (float)(int8_t)((a[j >> 2] >> ((j & 3) * 8)) & 0xffu);
 }
 
+// The prep of a decode step inside the chunk kernel (PREP): every
+// workgroup builds its heads' q from q_raw (bias, RMSNorm, RoPE) in LDS,
+// and the workgroup whose chunk holds the current position (the last one)
+// also prepares that position's K and V, writes them to the cache row and
+// uses them in place of the row it loaded before writing it.  Values are
+// those of gqa_prep_kernel (same operations, same order).
+//
+// Normalise heads [0, nh) of buf (HD floats each) with the weight values
+// w[j] = weight[lane + 64 j] (loaded beforehand): one wave per head, wave
+// (g + first) % 4 taking head g.
+template <int HD, int J>
+__device__ __forceinline__ void norm_heads(float* buf, uint32_t nh, uint32_t first, const float (&w)[J], float eps,
+                                           uint32_t wave, uint32_t lane) {
+#pragma clang fp contract(off)
+  for (uint32_t g = (wave + 4u - first % 4u) % 4u; g < nh; g += 4u) {
+    float x[J];
+    float sq = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      x[j] = d < HD ? buf[g * HD + d] : 0.0f;
+      sq = __builtin_fmaf(x[j], x[j], sq);
+    }
+    sq = lane_reduce<64>(sq);
+    const float scale = 1.0f / sqrtf(sq / (float)HD + eps);
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+      const uint32_t d = lane + 64u * j;
+      if (d < HD) buf[g * HD + d] = x[j] * scale * w[j];
+    }
+  }
+}
+
 // LPT lanes per position (hd = 16 * LPT).  A chunk is 4 passes of the
 // 4 * TPW positions the workgroup covers at once, so every lane requests its
 // 4 K pieces and 4 V pieces (16 bytes each, plus scales) before any wait:
 // one trip to memory per workgroup.
-template <int LPT>
+template <int LPT, bool PREP>
 __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const float* __restrict__ q, uint32_t group,
                                                              uint32_t seq0, uint32_t n_chunks,
-                                                             float* __restrict__ part) {
+                                                             float* __restrict__ part, GqaPrep pp, RopeFreq rf) {
   constexpr uint32_t HD = LPT * 16, TPW = 64 / LPT, PASSES = 4, CH = PASSES * 4 * TPW;
   extern __shared__ __attribute__((aligned(16))) float smem[];
   float* s_q = smem;                       // [group][HD]
   float* s_p = smem + group * HD;          // [group][CH] scores, then exp(s - m)
   float* s_red = s_p + group * CH;         // [4 waves][4 heads][HD] reduction space
+  // PREP only: [HD / 2][2] sin, cos; [HD] current k; [2][HD] int8 K, V; [2][HD / 32] scale bits
+  float* s_cs = s_red + 16u * HD;
+  float* s_k = s_cs + HD;
+  int8_t* s_q8 = reinterpret_cast<int8_t*>(s_k + HD);
+  uint16_t* s_d8 = reinterpret_cast<uint16_t*>(s_q8 + 2u * HD);
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t slot = lane / LPT, sub = lane % LPT;
   const uint32_t kvh = blockIdx.x, ck = blockIdx.y;
@@ -255,18 +275,53 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   const uint32_t t0 = ck * CH;
   if (t0 >= seq_len) return;                              // a chunk past this token's positions
   const uint32_t n = min(seq_len - t0, CH);
-  q += (size_t)blockIdx.z * c.n_kv * group * HD;
+  if constexpr (!PREP) q += (size_t)blockIdx.z * c.n_kv * group * HD;
   part += (size_t)blockIdx.z * c.n_kv * group * n_chunks * (HD + 2);
   const uint32_t row_q = c.n_kv * HD, row_d = c.n_kv * (HD / 32);
   const float scale = 1.0f / sqrtf((float)HD);
 
-  // q first (small, cached), then every K and V piece of the chunk.
-  float qv[kMaxGroup * HD / kThreads + 1];
+  // q first (small, cached), then every K and V piece of the chunk.  Every
+  // early load is unconditional (clamped index) and combined only where it is
+  // used: the memory counter drains in order, so a load that has to be waited
+  // for inside a branch, or one issued after the cache rows, makes the wave
+  // wait for everything issued before it.
+  constexpr uint32_t R = kMaxGroup * HD / kThreads + 1;
   const uint32_t nq = group * HD;
+  float qv[R], qb[R];
 #pragma unroll
-  for (uint32_t r = 0; r < kMaxGroup * HD / kThreads + 1; ++r) {
-    const uint32_t i = tid + r * kThreads;
-    qv[r] = i < nq ? q[(size_t)kvh * nq + i] : 0.0f;
+  for (uint32_t r = 0; r < R; ++r) {
+    const uint32_t i = min(tid + r * kThreads, nq - 1u);
+    if constexpr (PREP) {
+      const uint32_t off = (kvh * group + i / HD) * (pp.gated ? 2u : 1u) * HD + i % HD;
+      qv[r] = pp.q_raw[off];
+      qb[r] = (pp.q_bias ? pp.q_bias : pp.q_raw)[off];
+    } else {
+      qv[r] = q[(size_t)kvh * nq + i];
+    }
+  }
+  // PREP: the current position's k and v (and biases), and this lane's
+  // rotation frequency, loaded by every workgroup before the cache rows.
+  constexpr int JP = PREP ? (HD >= 64 ? HD / 64 : 1) : 1;
+  float kc[JP], vc[JP], kbs[JP], vbs[JP], wq[JP], wk[JP];
+  float fr = 0.0f;
+  if constexpr (PREP) {
+    const size_t base = (size_t)kvh * HD;
+    const float* kb = pp.k_bias ? pp.k_bias : pp.k_cur;
+    const float* vb = pp.v_bias ? pp.v_bias : pp.v_cur;
+    const float* qn = pp.q_norm ? pp.q_norm : pp.k_cur;
+    const float* kn = pp.k_norm ? pp.k_norm : pp.k_cur;
+#pragma unroll
+    for (int j = 0; j < JP; ++j) {
+      const uint32_t d = min(lane + 64u * j, HD - 1u);
+      kc[j] = pp.k_cur[base + d];
+      vc[j] = pp.v_cur[base + d];
+      kbs[j] = kb[base + d];
+      vbs[j] = vb[base + d];
+      wq[j] = qn[d];
+      wk[j] = kn[d];
+    }
+    fr = rf.f[(tid - 64u) & 127u];
+    asm volatile("" ::: "memory");   // keep the loads above ahead of the cache rows
   }
   // Raw scale bits: converting them here would wait for the load (and, the
   // memory counter draining in order, for every load issued before it).
@@ -285,23 +340,111 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
     vdb[p] = c.v_d[dof];
   }
 #pragma unroll
-  for (uint32_t r = 0; r < kMaxGroup * HD / kThreads + 1; ++r) {
+  for (uint32_t r = 0; r < R; ++r) {
     const uint32_t i = tid + r * kThreads;
-    if (i < nq) s_q[i] = qv[r];
+    if (i < nq) s_q[i] = PREP && pp.q_bias ? qv[r] + qb[r] : qv[r];
   }
-  __syncthreads();
+  if constexpr (PREP) {
+#pragma clang fp contract(off)
+    constexpr int J = HD >= 64 ? HD / 64 : 1;
+    const uint32_t pos = seq_len - 1u;
+    const bool cur = pos - t0 < CH;                       // this chunk holds the current position
+    if (cur && wave == 0) {                               // the current position's k, raw
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d < HD) s_k[d] = pp.k_bias ? kc[j] + kbs[j] : kc[j];
+      }
+    }
+    lds_barrier();
+    // sine and cosine of pair i by thread 64 + i (waves 1 and 2), beside the
+    // norms and the V quantisation
+    if (tid >= 64u && tid - 64u < pp.half) {
+      const float th = (float)pp.rope_pos * fr;
+      double sd, cd;
+      sincos((double)th, &sd, &cd);
+      s_cs[2u * (tid - 64u)] = (float)sd;
+      s_cs[2u * (tid - 64u) + 1u] = (float)cd;
+    }
+    if (pp.q_norm) norm_heads<HD>(s_q, group, 0, wq, pp.eps, wave, lane);
+    if (cur && pp.k_norm) norm_heads<HD>(s_k, 1, group, wk, pp.eps, wave, lane);
+    if (cur) {
+      // V quantised as it is, alongside the norms: wave 3 - j takes values
+      // lane + 64 j
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        if (wave != 3u - (uint32_t)j) continue;
+        const uint32_t d = lane + 64u * j;
+        const float vv = d < HD ? (pp.v_bias ? vc[j] + vbs[j] : vc[j]) : 0.0f;
+        uint32_t dh;
+        const int qq = q8_lane(vv, dh);
+        if (d < HD) {
+          s_q8[HD + d] = (int8_t)qq;
+          if ((d & 31u) == 0) s_d8[HD / 32 + d / 32] = (uint16_t)dh;
+        }
+      }
+    }
+    lds_barrier();
+    if (pp.half) {
+      const uint32_t nh = group + (cur ? 1u : 0u);
+      for (uint32_t idx = tid; idx < nh * pp.half; idx += kThreads) {
+        const uint32_t g = idx / pp.half, i = idx - g * pp.half;
+        float* v = g < group ? s_q + g * HD : s_k;
+        const uint32_t i0 = pp.neox ? i : 2u * i, i1 = pp.neox ? i + pp.half : 2u * i + 1u;
+        const float sn = s_cs[2u * i], cs = s_cs[2u * i + 1u];
+        const float x0 = v[i0], x1 = v[i1];
+        v[i0] = x0 * cs - x1 * sn;
+        v[i1] = x0 * sn + x1 * cs;
+      }
+      lds_barrier();
+    }
+    if (cur) {
+      // K quantised: wave j takes values lane + 64 j
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        if (wave != (uint32_t)j) continue;
+        const uint32_t d = lane + 64u * j;
+        uint32_t dh;
+        const int qq = q8_lane(d < HD ? s_k[d] : 0.0f, dh);
+        if (d < HD) {
+          s_q8[d] = (int8_t)qq;
+          if ((d & 31u) == 0) s_d8[d / 32] = (uint16_t)dh;
+        }
+      }
+      lds_barrier();
+    }
+  } else {
+    __syncthreads();
+  }
+  // PREP: the current row's K / V pieces of this lane, taken in place of the
+  // loaded ones (stale: the row is written at the end) by the lanes whose
+  // (clamped) position is the current one, at each use.
+  u32x4 fk{}, fv{};
+  uint32_t fkd = 0, fvd = 0;
+  bool here[PASSES];
+#pragma unroll
+  for (uint32_t p = 0; p < PASSES; ++p) here[p] = false;
+  if constexpr (PREP) {
+    fk = *reinterpret_cast<const u32x4*>(s_q8 + sub * 16u);
+    fv = *reinterpret_cast<const u32x4*>(s_q8 + HD + sub * 16u);
+    fkd = s_d8[sub / 2u];
+    fvd = s_d8[HD / 32 + sub / 2u];
+    const uint32_t pos = seq_len - 1u;
+#pragma unroll
+    for (uint32_t p = 0; p < PASSES; ++p) here[p] = t0 + (tl[p] < n ? tl[p] : n - 1) == pos;
+  }
 
   // ---- scores
 #pragma unroll
   for (uint32_t p = 0; p < PASSES; ++p) {
     float kf[16];
-    unpack16(kw[p], kf);
+    unpack16(here[p] ? fk : kw[p], kf);
     for (uint32_t g = 0; g < group; ++g) {
       const float* qg = s_q + g * HD + sub * 16u;
       float acc = 0.0f;
 #pragma unroll
       for (int j = 0; j < 16; ++j) acc = __builtin_fmaf(qg[j], kf[j], acc);
-      acc *= f16_to_f32_exact(kdb[p]);
+      acc *= f16_to_f32_exact(here[p] ? fkd : kdb[p]);
       acc = lane_reduce<LPT>(acc);
       if (sub == 0 && tl[p] < n) s_p[g * CH + tl[p]] = acc * scale;
     }
@@ -332,8 +475,8 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   float vf[PASSES][16];
 #pragma unroll
   for (uint32_t p = 0; p < PASSES; ++p) {
-    unpack16(vw[p], vf[p]);
-    const float vd = f16_to_f32_exact(vdb[p]);
+    unpack16(here[p] ? fv : vw[p], vf[p]);
+    const float vd = f16_to_f32_exact(here[p] ? fvd : vdb[p]);
 #pragma unroll
     for (int j = 0; j < 16; ++j) vf[p][j] *= vd;
   }
@@ -376,6 +519,24 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
     }
     __syncthreads();
   }
+  if constexpr (PREP) {
+    // the current position's K and V rows, from LDS, once nothing waits on them
+    const uint32_t pos = seq_len - 1u;
+    if (pos - t0 < CH && wave == 0) {
+      const size_t vo = (size_t)pos * row_q + (size_t)kvh * HD, so = (size_t)pos * row_d + kvh * (HD / 32);
+      for (uint32_t w = lane; w < HD / 2u; w += 64u) {      // 4 bytes a lane: K words, then V words
+        const bool is_v = w >= HD / 4u;
+        const uint32_t o = (is_v ? w - HD / 4u : w) * 4u;
+        *reinterpret_cast<uint32_t*>((is_v ? c.v_qs : c.k_qs) + vo + o) =
+            *reinterpret_cast<const uint32_t*>(s_q8 + (is_v ? HD : 0u) + o);
+      }
+      if (lane < HD / 16u) {
+        const bool is_v = lane >= HD / 32u;
+        const uint32_t b = is_v ? lane - HD / 32u : lane;
+        (is_v ? c.v_d : c.k_d)[so + b] = s_d8[(is_v ? HD / 32u : 0u) + b];
+      }
+    }
+  }
 }
 
 // Merge: workgroup (head, 64 dimensions) of kMergeWaves waves.  The chunks'
@@ -386,6 +547,8 @@ constexpr uint32_t kMergeWaves = 16;
 __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
                                                                      uint32_t chunk_stride, uint32_t chunk,
                                                                      uint32_t seq0, const float* __restrict__ gate,
+                                                                     uint32_t gate_stride,
+                                                                     const float* __restrict__ gate_bias,
                                                                      float* __restrict__ out) {
 #pragma clang fp contract(off)
   constexpr uint32_t W = kMergeWaves;
@@ -396,7 +559,7 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
   const uint32_t n_chunks = (seq0 + z + chunk - 1u) / chunk;   // token z's chunks
   const size_t stride = hd + 2;
   const float* ph = part + ((size_t)z * n_head + h) * chunk_stride * stride;
-  if (gate) gate += (size_t)z * n_head * hd;
+  if (gate) gate += (size_t)z * n_head * gate_stride;
   out += (size_t)z * n_head * hd;
   float m = -__builtin_inff();
   for (uint32_t c = tid; c < n_chunks; c += W * 64u) m = fmaxf(m, ph[c * stride]);
@@ -443,18 +606,52 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
     o += s_acc[w][lane];
   }
   o = o / tot;
-  if (gate) o *= 1.0f / (1.0f + expf(-gate[(size_t)h * hd + d]));
+  if (gate) {
+    float g = gate[(size_t)h * gate_stride + d];
+    if (gate_bias) g = g + gate_bias[(size_t)h * gate_stride + d];
+    o *= 1.0f / (1.0f + expf(-g));
+  }
   out[(size_t)h * hd + d] = o;
 }
 
-template <int LPT>
+template <int LPT, bool PREP>
 hipError_t launch_chunks(const KvQ8Dev& c, const float* q, uint32_t group, uint32_t seq0, uint32_t n_chunks,
-                         uint32_t batch, float* part, hipStream_t s) {
+                         uint32_t batch, float* part, const GqaPrep& pp, const RopeFreq& rf, hipStream_t s) {
   constexpr uint32_t HD = LPT * 16, CH = 16u * (64u / LPT);
-  const size_t lds = ((size_t)group * HD + (size_t)group * CH + 16u * HD) * 4u;
-  hipLaunchKernelGGL(attn_chunk_kernel<LPT>, dim3(c.n_kv, n_chunks, batch), dim3(kThreads), lds, s, c, q, group,
-                     seq0, n_chunks, part);
+  size_t lds = ((size_t)group * HD + (size_t)group * CH + 16u * HD) * 4u;
+  if (PREP) lds += 2u * HD * 4u + 2u * HD + 2u * (HD / 32u) * 2u;
+  hipLaunchKernelGGL((attn_chunk_kernel<LPT, PREP>), dim3(c.n_kv, n_chunks, batch), dim3(kThreads), lds, s, c, q,
+                     group, seq0, n_chunks, part, pp, rf);
   return hipGetLastError();
+}
+
+template <bool PREP>
+hipError_t launch_chunks_hd(const KvQ8Dev& c, const float* q, uint32_t group, uint32_t seq0, uint32_t n_chunks,
+                            uint32_t batch, float* part, const GqaPrep& pp, const RopeFreq& rf, hipStream_t s) {
+  switch (c.hd) {
+    case 32: return launch_chunks<2, PREP>(c, q, group, seq0, n_chunks, batch, part, pp, rf, s);
+    case 64: return launch_chunks<4, PREP>(c, q, group, seq0, n_chunks, batch, part, pp, rf, s);
+    case 128: return launch_chunks<8, PREP>(c, q, group, seq0, n_chunks, batch, part, pp, rf, s);
+    case 256: return launch_chunks<16, PREP>(c, q, group, seq0, n_chunks, batch, part, pp, rf, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// The rotation frequencies powf(base, -2i / rdim), i < rdim / 2, with rdim =
+// min(rope_dim, hd): a function of (freq_base, rdim) only, so the last table
+// is kept per host thread.
+const RopeFreq& rope_table(uint32_t rope_dim, float freq_base, uint32_t hd, uint32_t* half) {
+  thread_local RopeFreq tab{};
+  thread_local uint32_t tab_rdim = 0;
+  thread_local float tab_base = 0.0f;
+  const uint32_t rdim = std::min(rope_dim, hd);
+  *half = rdim / 2u;
+  if (*half && (tab_rdim != rdim || std::memcmp(&tab_base, &freq_base, sizeof(float)) != 0)) {
+    for (uint32_t i = 0; i < *half; ++i) tab.f[i] = powf(freq_base, -(2.0f * (float)i) / (float)rdim);
+    tab_rdim = rdim;
+    tab_base = freq_base;
+  }
+  return tab;
 }
 
 // Positions per chunk: 4 passes of 4 waves x 64 / (hd / 16) positions.
@@ -473,20 +670,9 @@ hipError_t launch_kv_append(const KvQ8Dev& c, const float* k, const float* v, ui
   return hipGetLastError();
 }
 
-// The rotation frequencies are a function of (freq_base, rdim) only; the last
-// table is kept per host thread.
 hipError_t launch_gqa_prep(const KvQ8Dev& c, GqaPrep a, uint32_t rope_dim, float freq_base, uint32_t batch,
                            hipStream_t s) {
-  thread_local RopeFreq tab{};
-  thread_local uint32_t tab_rdim = 0;
-  thread_local float tab_base = 0.0f;
-  const uint32_t rdim = std::min(rope_dim, c.hd);
-  a.half = rdim / 2u;
-  if (a.half && (tab_rdim != rdim || std::memcmp(&tab_base, &freq_base, sizeof(float)) != 0)) {
-    for (uint32_t i = 0; i < a.half; ++i) tab.f[i] = powf(freq_base, -(2.0f * (float)i) / (float)rdim);
-    tab_rdim = rdim;
-    tab_base = freq_base;
-  }
+  const RopeFreq& tab = rope_table(rope_dim, freq_base, c.hd, &a.half);
   switch (c.hd) {
     case 32: launch_prep<32>(c, a, tab, batch, s); break;
     case 64: launch_prep<64>(c, a, tab, batch, s); break;
@@ -517,17 +703,32 @@ hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32
   const uint32_t n_chunks = (uint32_t)(((size_t)seq0 + batch - 1 + chunk - 1) / chunk);
   if (n_chunks > 65535u) return hipErrorInvalidValue;
   float* part = static_cast<float*>(ws);
-  hipError_t e;
-  switch (c.hd) {
-    case 32: e = launch_chunks<2>(c, q, group, seq0, n_chunks, batch, part, s); break;
-    case 64: e = launch_chunks<4>(c, q, group, seq0, n_chunks, batch, part, s); break;
-    case 128: e = launch_chunks<8>(c, q, group, seq0, n_chunks, batch, part, s); break;
-    case 256: e = launch_chunks<16>(c, q, group, seq0, n_chunks, batch, part, s); break;
-    default: return hipErrorInvalidValue;
-  }
+  hipError_t e = launch_chunks_hd<false>(c, q, group, seq0, n_chunks, batch, part, GqaPrep{}, RopeFreq{}, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64, batch), dim3(kMergeWaves * 64), 0, s, part,
-                     c.hd, n_chunks, chunk, seq0, gate, out);
+                     c.hd, n_chunks, chunk, seq0, gate, c.hd, nullptr, out);
+  return hipGetLastError();
+}
+
+// One decode step (a single token at row pp.pos, rope position pp.rope_pos)
+// in two launches: the chunk kernel with the prep folded in, then the merge
+// (the gate read from q_raw's gate halves).  ws holds
+// attn_workspace_bytes(n_head, pp.pos + 1, n_kv, hd, 1).
+hipError_t launch_attn_step(const KvQ8Dev& c, GqaPrep pp, uint32_t rope_dim, float freq_base, float* out, void* ws,
+                            hipStream_t s) {
+  const uint32_t group = pp.n_head / c.n_kv;
+  if (group == 0 || group > kMaxGroup) return hipErrorInvalidValue;
+  const RopeFreq& tab = rope_table(rope_dim, freq_base, c.hd, &pp.half);
+  const uint32_t chunk = chunk_of(c.hd), seq0 = pp.pos + 1u;
+  const uint32_t n_chunks = (seq0 + chunk - 1) / chunk;
+  if (n_chunks > 65535u) return hipErrorInvalidValue;
+  float* part = static_cast<float*>(ws);
+  hipError_t e = launch_chunks_hd<true>(c, nullptr, group, seq0, n_chunks, 1, part, pp, tab, s);
+  if (e != hipSuccess) return e;
+  const float* gate = pp.gated ? pp.q_raw + c.hd : nullptr;
+  const float* gate_bias = pp.gated && pp.q_bias ? pp.q_bias + c.hd : nullptr;
+  hipLaunchKernelGGL(attn_merge_kernel, dim3(pp.n_head, (c.hd + 63) / 64, 1), dim3(kMergeWaves * 64), 0, s, part,
+                     c.hd, n_chunks, chunk, seq0, gate, 2u * c.hd, gate_bias, out);
   return hipGetLastError();
 }
 

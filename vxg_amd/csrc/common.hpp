@@ -133,6 +133,13 @@ struct GqaPrep {
   float eps;
 };
 
+// Workgroup barrier that orders LDS traffic only.  __syncthreads() also
+// waits for every global load the wave has in flight (its release fence
+// drains the vector memory counter); this one waits for the wave's LDS and
+// scalar operations, then meets the other waves, so loads issued before it
+// stay in flight.  Global memory written before it is not made visible by it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---- wave64 reductions ----------------------------------------------------
 
 template <int CTRL>

@@ -46,6 +46,8 @@ hipError_t launch_gqa_prep(const KvQ8Dev& c, GqaPrep a, uint32_t rope_dim, float
 size_t attn_workspace_bytes(uint32_t n_head, uint32_t seq_len, uint32_t n_kv, uint32_t hd, uint32_t batch);
 hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32_t seq0, uint32_t batch,
                        const float* gate, float* out, void* ws, hipStream_t s);
+hipError_t launch_attn_step(const KvQ8Dev& c, GqaPrep pp, uint32_t rope_dim, float freq_base, float* out, void* ws,
+                            hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
 struct ChainLaunch {
@@ -871,6 +873,14 @@ int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaP
     const uint32_t n_head = params->n_head;
     if (n_head % kc.n_kv != 0) fail(VXT_E_SHAPE, "n_head must be a multiple of n_kv");
     if (n_head / kc.n_kv > 8) fail(VXT_E_UNSUPPORTED, "at most 8 query heads per kv head");
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (batch_m == 1) {
+      // decode: the prep runs inside the attention's chunk kernel
+      ensure_ws(c, vxt::attn_workspace_bytes(n_head, pos + 1, kc.n_kv, kc.hd, 1));
+      hipError_t e = vxt::launch_attn_step(kc, a, params->rope_dim, params->rope_freq_base, out, c->ws, s);
+      if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention step launch failed: ") + hipGetErrorString(e));
+      return;
+    }
     // Workspace: q (and gate) of every token, then the partial sums of one
     // group of tokens at a time, groups sized to keep that part near 16 MiB.
     const size_t q_bytes = (size_t)batch_m * n_head * kc.hd * sizeof(float);
@@ -884,7 +894,6 @@ int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaP
     void* part = static_cast<char*>(c->ws) + qg_bytes;
     a.q_out = q_ws;
     a.gate_out = g_ws;
-    hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e = vxt::launch_gqa_prep(kc, a, params->rope_dim, params->rope_freq_base, batch_m, s);
     if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention prep launch failed: ") + hipGetErrorString(e));
     const size_t row = (size_t)n_head * kc.hd;
