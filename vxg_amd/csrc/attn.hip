@@ -539,19 +539,17 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   }
 }
 
-// Merge: workgroup (head, 64 dimensions) of kMergeWaves waves.  The chunks'
-// maximum first, then wave w sums chunks w, w + kMergeWaves, ... (sixteen
-// at a time in flight), then the waves' sums are added in wave order.
-constexpr uint32_t kMergeWaves = 16;
-
-__global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
-                                                                     uint32_t chunk_stride, uint32_t chunk,
-                                                                     uint32_t seq0, const float* __restrict__ gate,
-                                                                     uint32_t gate_stride,
-                                                                     const float* __restrict__ gate_bias,
-                                                                     float* __restrict__ out) {
+// Merge: workgroup (head, 64 dimensions, token) of W waves.  The chunks'
+// maximum first, then wave w sums chunks w, w + W, ... (sixteen at a time in
+// flight), then the waves' sums are added in wave order.  W = 16 for a long
+// decode sequence; a prefill token has few chunks, and fewer waves serve it.
+template <uint32_t W>
+__global__ __launch_bounds__(W * 64) void attn_merge_kernel(const float* __restrict__ part, uint32_t hd,
+                                                            uint32_t chunk_stride, uint32_t chunk, uint32_t seq0,
+                                                            const float* __restrict__ gate, uint32_t gate_stride,
+                                                            const float* __restrict__ gate_bias,
+                                                            float* __restrict__ out) {
 #pragma clang fp contract(off)
-  constexpr uint32_t W = kMergeWaves;
   __shared__ float s_m[W], s_acc[W][64], s_l[W];
   const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t d = blockIdx.y * 64u + lane;
@@ -571,13 +569,13 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
   for (uint32_t w = 1; w < W; ++w) m = fmaxf(m, s_m[w]);
   const uint32_t dc = d < hd ? d : hd - 1;
   float acc = 0.0f, l = 0.0f;
-  uint32_t c = wave;
   constexpr int U = 16;   // chunks in flight per lane
-  for (; c + W * (U - 1) < n_chunks; c += W * U) {
+  uint32_t c0 = wave;
+  for (; c0 + W * (U - 1) < n_chunks; c0 += W * U) {
     float mc[U], lc[U], ac[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float* pc = ph + (size_t)(c + W * u) * stride;
+      const float* pc = ph + (size_t)(c0 + W * u) * stride;
       mc[u] = pc[0];
       lc[u] = pc[1];
       ac[u] = pc[2 + dc];
@@ -589,11 +587,24 @@ __global__ __launch_bounds__(kMergeWaves * 64) void attn_merge_kernel(const floa
       acc += ac[u] * e;
     }
   }
-  for (; c < n_chunks; c += W) {
-    const float* pc = ph + (size_t)c * stride;
-    const float e = expf(pc[0] - m);
-    l += pc[1] * e;
-    acc += pc[2 + dc] * e;
+  if (c0 < n_chunks) {
+    // the last, partial batch: loads from clamped indices, all in flight
+    // together, only the valid ones used
+    float mc[U], lc[U], ac[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float* pc = ph + (size_t)min(c0 + W * u, n_chunks - 1u) * stride;
+      mc[u] = pc[0];
+      lc[u] = pc[1];
+      ac[u] = pc[2 + dc];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + W * u >= n_chunks) break;   // uniform across the wave
+      const float e = expf(mc[u] - m);
+      l += lc[u] * e;
+      acc += ac[u] * e;
+    }
   }
   s_acc[wave][lane] = acc;
   if (lane == 0) s_l[wave] = l;
@@ -654,6 +665,25 @@ const RopeFreq& rope_table(uint32_t rope_dim, float freq_base, uint32_t hd, uint
   return tab;
 }
 
+// The merge: 16 waves per workgroup when there are few workgroups (a decode
+// step: the chunks of one token spread over the waves), fewer when a batch
+// already gives every CU workgroups (prefill: a token has few chunks).
+hipError_t launch_merge(const float* part, uint32_t hd, uint32_t n_head, uint32_t batch, uint32_t n_chunks,
+                        uint32_t chunk, uint32_t seq0, const float* gate, uint32_t gate_stride,
+                        const float* gate_bias, float* out, hipStream_t s) {
+  const dim3 grid(n_head, (hd + 63) / 64, batch);
+  if ((size_t)grid.x * grid.y * grid.z < 512u)
+    hipLaunchKernelGGL(attn_merge_kernel<16>, grid, dim3(16 * 64), 0, s, part, hd, n_chunks, chunk, seq0, gate,
+                       gate_stride, gate_bias, out);
+  else if (n_chunks >= 8)
+    hipLaunchKernelGGL(attn_merge_kernel<4>, grid, dim3(4 * 64), 0, s, part, hd, n_chunks, chunk, seq0, gate,
+                       gate_stride, gate_bias, out);
+  else
+    hipLaunchKernelGGL(attn_merge_kernel<1>, grid, dim3(64), 0, s, part, hd, n_chunks, chunk, seq0, gate,
+                       gate_stride, gate_bias, out);
+  return hipGetLastError();
+}
+
 // Positions per chunk: 4 passes of 4 waves x 64 / (hd / 16) positions.
 uint32_t chunk_of(uint32_t hd) { return 16u * (64u / (hd / 16u)); }
 
@@ -705,9 +735,7 @@ hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32
   float* part = static_cast<float*>(ws);
   hipError_t e = launch_chunks_hd<false>(c, q, group, seq0, n_chunks, batch, part, GqaPrep{}, RopeFreq{}, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(n_head, (c.hd + 63) / 64, batch), dim3(kMergeWaves * 64), 0, s, part,
-                     c.hd, n_chunks, chunk, seq0, gate, c.hd, nullptr, out);
-  return hipGetLastError();
+  return launch_merge(part, c.hd, n_head, batch, n_chunks, chunk, seq0, gate, c.hd, nullptr, out, s);
 }
 
 // One decode step (a single token at row pp.pos, rope position pp.rope_pos)
@@ -727,9 +755,7 @@ hipError_t launch_attn_step(const KvQ8Dev& c, GqaPrep pp, uint32_t rope_dim, flo
   if (e != hipSuccess) return e;
   const float* gate = pp.gated ? pp.q_raw + c.hd : nullptr;
   const float* gate_bias = pp.gated && pp.q_bias ? pp.q_bias + c.hd : nullptr;
-  hipLaunchKernelGGL(attn_merge_kernel, dim3(pp.n_head, (c.hd + 63) / 64, 1), dim3(kMergeWaves * 64), 0, s, part,
-                     c.hd, n_chunks, chunk, seq0, gate, 2u * c.hd, gate_bias, out);
-  return hipGetLastError();
+  return launch_merge(part, c.hd, pp.n_head, 1, n_chunks, chunk, seq0, gate, 2u * c.hd, gate_bias, out, s);
 }
 
 }  // namespace vxt
