@@ -203,12 +203,17 @@ def test_decode_steps_match_oracle(eng, n_head, n_kv, hd, gated, norms, neox, ro
         case.free()
 
 
-@pytest.mark.parametrize("pos0,m,n_head,n_kv,hd", [(0, 37, 8, 2, 64), (5, 64, 16, 4, 128), (3000, 150, 16, 2, 128)])
+@pytest.mark.parametrize("pos0,m,n_head,n_kv,hd", [
+    (0, 37, 8, 2, 64), (5, 64, 16, 4, 128), (3000, 150, 16, 2, 128),   # MFMA prefill
+    (0, 100, 6, 2, 64), (17, 40, 8, 1, 32), (0, 300, 16, 16, 128), (33, 16, 4, 4, 128),
+    (2, 7, 8, 2, 64), (10, 20, 4, 1, 256), (3000, 15, 16, 2, 128)])    # per-token kernels
 def test_batched_step_is_causal(eng, pos0, m, n_head, n_kv, hd):
     """A batch of tokens in one call (the prefill loop of llm_prefill.rs:
-    505-517): token t attends to rows [0, pos0 + t] only.  The last case
-    splits the batch into several launch groups (partial sums bounded per
-    launch)."""
+    505-517): token t attends to rows [0, pos0 + t] only.  Batches of 16 or
+    more tokens with head_dim <= 128 take the MFMA prefill kernel (query
+    blocks of 128 / group tokens: groups 1, 2, 3, 4, 8 here); smaller ones and
+    head_dim 256 the per-token kernels, the last case split into several
+    launch groups (partial sums bounded per launch)."""
     print(f"batched step pos0={pos0} m={m} heads={n_head}/{n_kv} hd={hd}", flush=True)
     case = Case(eng, n_head, n_kv, hd, gated=True, norms=True, neox=True, rope_dim=hd // 2, biases=True,
                 seed=pos0 + m)
@@ -222,7 +227,7 @@ def test_batched_step_is_causal(eng, pos0, m, n_head, n_kv, hd):
         qi, _, _ = case.host_inputs(q, k, v)
         kb_dev, vb_dev = cache.blocks("k", pos0 + m), cache.blocks("v", pos0 + m)
         rows = case.kvd // 32
-        sample = sorted(set([0, 1, m // 2, m - 2, m - 1]))
+        sample = sorted(set([0, 1, m // 2, m - 2, m - 1] + list(range(min(m, 130) - 3, min(m, 130)))))
         for t in sample:
             L = pos0 + t + 1
             qh, qg = oracle_q(case, qi[t], pos0 + t)

@@ -44,6 +44,10 @@ namespace {
 constexpr uint32_t kThreads = 256;
 constexpr uint32_t kMaxGroup = 8;   // query heads per kv head
 
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t kSegTiles = 16;   // prefill: 32-position tiles per position segment
+
 // f32 -> f16 bits, round to nearest even with f16 subnormals kept and
 // overflow to infinity: what fp16.rs:33-77 computes with integer steps, here
 // v_cvt_f16_f32 (default round-to-nearest-even mode, f16 denormals on).
@@ -625,6 +629,208 @@ __global__ __launch_bounds__(W * 64) void attn_merge_kernel(const float* __restr
   out[(size_t)h * hd + d] = o;
 }
 
+// ---- prefill: causal attention of a batch of prepared queries on fp32 MFMA
+// Workgroup (kv head, block of tq tokens): 4 waves, 32 query rows each; row
+// r is token tb + r / group, query head kvh * group + r % group.  Positions
+// are walked in tiles of 32 from 0 to the block's last token; K and V of a
+// tile are dequantised into LDS as f32 (int8 x f16 scale is exact in f32),
+// the next tile's bytes already in flight.  Per wave and tile:
+//   S^T (32 positions x 32 rows) = K Q^T: 64 v_mfma_f32_32x32x2_f32 at hd 128,
+//     A = K from LDS, B = Q^T from registers;
+//   online softmax: each lane owns one row (lane % 32) and 16 of the tile's
+//     positions, its partner lane ^ 32 the other 16;
+//   O^T (hd x 32 rows) += V^T P^T: hd / 32 blocks of 16 MFMA steps, step i
+//     taking the positions the lanes hold in accumulator register i.
+// Every row keeps its own running max / sum, so the rescale of O^T is one
+// factor per lane.  fp32 throughout (products exact, sums in MFMA order);
+// positions after a row's token are masked to -inf.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const float* __restrict__ q,
+                                                           const float* __restrict__ gate, float* __restrict__ out,
+                                                           float* __restrict__ part, uint32_t n_head, uint32_t group,
+                                                           uint32_t tq, uint32_t pos0, uint32_t batch) {
+  constexpr uint32_t TP = 32, KS = HD + 1, NS = HD / 2, NB = HD / 32;
+  constexpr uint32_t NCH = TP * HD / 16;                // 16-value pieces per tile and plane
+  constexpr uint32_t PER = (NCH + 255) / 256;           // pieces per thread
+  __shared__ float s_k[TP * KS];
+  __shared__ __attribute__((aligned(16))) float s_v[TP * HD];
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, h = lane >> 5, col = lane & 31u;
+  const uint32_t kvh = blockIdx.x, tb = blockIdx.y * tq;
+  const uint32_t t_end = min(batch, tb + tq);
+  const uint32_t r = wave * 32u + col;
+  const uint32_t tk = tb + r / group, g = r % group;
+  const bool live = r < tq * group && tk < batch;
+  const uint32_t tkc = live ? tk : tb;                  // spare rows shadow the block's first token
+  const uint32_t my_pos = pos0 + tkc;
+  const uint32_t head = kvh * group + g;
+  const uint32_t last = pos0 + t_end - 1u;              // the largest position any row reads
+  // segment blockIdx.z of kSegTiles tiles (gridDim.z == 1: every position)
+  const uint32_t tile0 = blockIdx.z * kSegTiles;
+  if (tile0 * TP > last) return;                        // past this block's positions
+  const uint32_t n_tiles = gridDim.z == 1 ? last / TP + 1u : min(last / TP + 1u, tile0 + kSegTiles);
+  const uint32_t row_q = c.n_kv * HD, row_d = c.n_kv * (HD / 32);
+  const float scale = 1.0f / sqrtf((float)HD);
+
+  float qreg[NS];
+  {
+    const float* qr = q + ((size_t)tkc * n_head + head) * HD + h;
+#pragma unroll
+    for (uint32_t st = 0; st < NS; ++st) qreg[st] = qr[2u * st];
+  }
+  float16v o[NB];
+#pragma unroll
+  for (uint32_t b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
+  float m_run = -__builtin_inff(), l_run = 0.0f;
+
+  // bytes of tile 0 in flight
+  u32x4 kq[PER], vq[PER];
+  uint32_t kdb[PER], vdb[PER];
+  auto fetch = [&](uint32_t p0) {
+#pragma unroll
+    for (uint32_t u = 0; u < PER; ++u) {
+      const uint32_t ch = min(tid + 256u * u, NCH - 1u);
+      const uint32_t p = min(p0 + ch / (HD / 16), last), d0 = (ch % (HD / 16)) * 16u;
+      const size_t qo = (size_t)p * row_q + kvh * HD + d0, dof = (size_t)p * row_d + kvh * (HD / 32) + d0 / 32;
+      kq[u] = *reinterpret_cast<const u32x4*>(c.k_qs + qo);
+      vq[u] = *reinterpret_cast<const u32x4*>(c.v_qs + qo);
+      kdb[u] = c.k_d[dof];
+      vdb[u] = c.v_d[dof];
+    }
+  };
+  fetch(tile0 * TP);
+
+  for (uint32_t T = tile0; T < n_tiles; ++T) {
+    const uint32_t p0 = T * TP;
+    // this tile's values into LDS, then the next tile's bytes requested
+#pragma unroll
+    for (uint32_t u = 0; u < PER; ++u) {
+      const uint32_t ch = tid + 256u * u;
+      if (ch < NCH) {
+        const uint32_t pp = ch / (HD / 16), d0 = (ch % (HD / 16)) * 16u;
+        float kf[16], vf[16];
+        unpack16(kq[u], kf);
+        unpack16(vq[u], vf);
+        const float kd = f16_to_f32_exact(kdb[u]), vd = f16_to_f32_exact(vdb[u]);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s_k[pp * KS + d0 + j] = kf[j] * kd;
+#pragma unroll
+        for (int j = 0; j < 16; j += 4)
+          *reinterpret_cast<float4*>(&s_v[pp * HD + d0 + j]) =
+              make_float4(vf[j] * vd, vf[j + 1] * vd, vf[j + 2] * vd, vf[j + 3] * vd);
+      }
+    }
+    if (T + 1u < n_tiles) fetch(p0 + TP);
+    lds_barrier();
+
+    // S^T = K Q^T
+    float16v sacc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
+#pragma unroll
+    for (uint32_t st = 0; st < NS; ++st)
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(s_k[col * KS + 2u * st + h], qreg[st], sacc, 0, 0, 0);
+
+    // online softmax over this tile for the lane's row
+    float pm = -__builtin_inff();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t pos = p0 + 8u * (i >> 2) + 4u * h + (i & 3);
+      const float sv = pos <= my_pos ? sacc[i] * scale : -__builtin_inff();
+      sacc[i] = sv;
+      pm = fmaxf(pm, sv);
+    }
+    pm = xor32_pair(pm, true);
+    const float m_new = fmaxf(m_run, pm);
+    // a row whose token precedes the segment sees only masked positions
+    const bool none = m_new == -__builtin_inff();
+    const float alpha = none ? 1.0f : expf(m_run - m_new);
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float e = none ? 0.0f : expf(sacc[i] - m_new);
+      sacc[i] = e;
+      ps += e;
+    }
+    ps = xor32_pair(ps, false);
+    l_run = l_run * alpha + ps;
+    m_run = m_new;
+
+    // O^T += V^T P^T
+#pragma unroll
+    for (uint32_t b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t pp = 8u * (i >> 2) + 4u * h + (i & 3);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(s_v[pp * HD + 32u * b + col], sacc[i], o[b], 0, 0, 0);
+      }
+    }
+    lds_barrier();
+  }
+
+  if (!live) return;
+  if (gridDim.z > 1) {
+    // this segment's (m, l, unnormalised sum) for the merge
+    float* pr = part + (((size_t)tk * n_head + head) * gridDim.z + blockIdx.z) * (HD + 2);
+    if (h == 0) {
+      pr[0] = m_run;
+      pr[1] = l_run;
+    }
+#pragma unroll
+    for (uint32_t b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pr[2 + 32u * b + 8u * (i >> 2) + 4u * h + (i & 3)] = o[b][i];
+    return;
+  }
+  const float inv = 1.0f / l_run;
+  const size_t base = ((size_t)tk * n_head + head) * HD;
+#pragma unroll
+  for (uint32_t b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const uint32_t d0 = 32u * b + 8u * i4 + 4u * h;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float v = o[b][i4 * 4 + e] * inv;
+        if (gate) v *= 1.0f / (1.0f + expf(-gate[base + d0 + e]));
+        out[base + d0 + e] = v;
+      }
+    }
+}
+
+// Merge of the prefill's position segments: one wave per (token, head);
+// segments in ascending order, exp(m_s - m) rescaling, divide, gate.
+__global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ part, uint32_t hd,
+                                                                 uint32_t n_head, uint32_t n_seg, uint32_t seg_len,
+                                                                 uint32_t pos0, uint32_t batch,
+                                                                 const float* __restrict__ gate,
+                                                                 float* __restrict__ out) {
+#pragma clang fp contract(off)
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t row = blockIdx.x * 4u + (threadIdx.x >> 6);   // token * n_head + head
+  if (row >= batch * n_head) return;
+  const uint32_t tk = row / n_head;
+  const uint32_t ns = min(n_seg, (pos0 + tk) / seg_len + 1u);   // segments holding positions <= the token's
+  const float* pr = part + (size_t)row * n_seg * (hd + 2);
+  float m = -__builtin_inff();
+  for (uint32_t sg = 0; sg < ns; ++sg) m = fmaxf(m, pr[(size_t)sg * (hd + 2)]);
+  for (uint32_t d = lane; d < hd; d += 64u) {
+    float l = 0.0f, acc = 0.0f;
+    for (uint32_t sg = 0; sg < ns; ++sg) {
+      const float* ps = pr + (size_t)sg * (hd + 2);
+      const float e = ps[0] == -__builtin_inff() ? 0.0f : expf(ps[0] - m);
+      l += ps[1] * e;
+      acc += ps[2 + d] * e;
+    }
+    float v = acc / l;
+    if (gate) v *= 1.0f / (1.0f + expf(-gate[(size_t)row * hd + d]));
+    out[(size_t)row * hd + d] = v;
+  }
+}
+
 template <int LPT, bool PREP>
 hipError_t launch_chunks(const KvQ8Dev& c, const float* q, uint32_t group, uint32_t seq0, uint32_t n_chunks,
                          uint32_t batch, float* part, const GqaPrep& pp, const RopeFreq& rf, hipStream_t s) {
@@ -736,6 +942,47 @@ hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32
   hipError_t e = launch_chunks_hd<false>(c, q, group, seq0, n_chunks, batch, part, GqaPrep{}, RopeFreq{}, s);
   if (e != hipSuccess) return e;
   return launch_merge(part, c.hd, n_head, batch, n_chunks, chunk, seq0, gate, c.hd, nullptr, out, s);
+}
+
+// Causal attention of batch prepared queries (q, gate: [batch][n_head][hd])
+// on MFMA: tokens at positions pos0 .. pos0 + batch - 1, every cache row up to
+// the last written.  hd <= 128.  Positions are cut into segments of
+// kSegTiles * 32 when there are more than one; ws then holds
+// attn_prefill_workspace_bytes(...) of partial sums.
+uint32_t prefill_segments(uint32_t pos0, uint32_t batch) {
+  return (pos0 + batch - 1u) / (kSegTiles * 32u) + 1u;
+}
+
+size_t attn_prefill_workspace_bytes(uint32_t n_head, uint32_t hd, uint32_t pos0, uint32_t batch) {
+  const uint32_t ns = prefill_segments(pos0, batch);
+  return ns > 1 ? (size_t)batch * n_head * ns * (hd + 2) * sizeof(float) : 0;
+}
+
+hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* gate, float* out, uint32_t n_head,
+                               uint32_t pos0, uint32_t batch, void* ws, hipStream_t s) {
+  const uint32_t group = n_head / c.n_kv;
+  if (group == 0 || group > kMaxGroup || batch == 0) return hipErrorInvalidValue;
+  const uint32_t tq = 128u / group;
+  const uint32_t blocks = (batch + tq - 1) / tq;
+  const uint32_t ns = prefill_segments(pos0, batch);
+  if (blocks > 65535u || ns > 65535u) return hipErrorInvalidValue;
+  float* part = static_cast<float*>(ws);
+  const dim3 grid(c.n_kv, blocks, ns);
+  switch (c.hd) {
+    case 32: hipLaunchKernelGGL(attn_prefill_kernel<32>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head, group,
+                                tq, pos0, batch); break;
+    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head, group,
+                                tq, pos0, batch); break;
+    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head,
+                                 group, tq, pos0, batch); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || ns == 1) return e;
+  const uint32_t rows = batch * n_head;
+  hipLaunchKernelGGL(attn_prefill_merge_kernel, dim3((rows + 3) / 4), dim3(256), 0, s, part, c.hd, n_head, ns,
+                     kSegTiles * 32u, pos0, batch, gate, out);
+  return hipGetLastError();
 }
 
 // One decode step (a single token at row pp.pos, rope position pp.rope_pos)

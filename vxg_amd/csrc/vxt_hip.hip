@@ -48,6 +48,9 @@ hipError_t launch_attn(const KvQ8Dev& c, const float* q, uint32_t n_head, uint32
                        const float* gate, float* out, void* ws, hipStream_t s);
 hipError_t launch_attn_step(const KvQ8Dev& c, GqaPrep pp, uint32_t rope_dim, float freq_base, float* out, void* ws,
                             hipStream_t s);
+size_t attn_prefill_workspace_bytes(uint32_t n_head, uint32_t hd, uint32_t pos0, uint32_t batch);
+hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* gate, float* out, uint32_t n_head,
+                               uint32_t pos0, uint32_t batch, void* ws, hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
 struct ChainLaunch {
@@ -806,6 +809,9 @@ int vxt_hip_attn_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const float* q, ui
 }
 
 namespace {
+// Batches of at least this many tokens take the MFMA prefill attention.
+constexpr uint32_t kPrefillMfmaMin = 16;
+
 // Checks shared by the prep and the whole step; fills the device arguments
 // (q_out / gate_out left to the caller).
 vxt::GqaPrep gqa_prep_args(const vxt::KvQ8Dev& kc, const VxtGqaParams* p, const float* q_raw, uint32_t q_stride,
@@ -881,10 +887,32 @@ int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaP
       if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention step launch failed: ") + hipGetErrorString(e));
       return;
     }
-    // Workspace: q (and gate) of every token, then the partial sums of one
-    // group of tokens at a time, groups sized to keep that part near 16 MiB.
+    // Workspace: q (and gate) of every token, then (batches below
+    // kPrefillMfmaMin tokens, or head_dim 256) the partial sums of one group
+    // of tokens at a time, groups sized to keep that part near 16 MiB.
     const size_t q_bytes = (size_t)batch_m * n_head * kc.hd * sizeof(float);
     const size_t qg_bytes = (q_bytes * (params->gated_q ? 2u : 1u) + 255u) & ~(size_t)255u;
+    if (batch_m >= kPrefillMfmaMin && kc.hd <= 128) {
+      // prep, then the MFMA attention over position segments, in token
+      // groups whose segment partial sums stay near 256 MiB
+      const size_t per_tok = vxt::attn_prefill_workspace_bytes(n_head, kc.hd, pos, batch_m) / batch_m;
+      const uint32_t group_t = (uint32_t)std::max<size_t>(
+          1, std::min<size_t>(batch_m, ((size_t)256 << 20) / std::max<size_t>(per_tok, 1)));
+      ensure_ws(c, qg_bytes + per_tok * group_t);
+      float* q_ws = static_cast<float*>(c->ws);
+      a.q_out = q_ws;
+      a.gate_out = params->gated_q ? q_ws + (size_t)batch_m * n_head * kc.hd : nullptr;
+      void* part = static_cast<char*>(c->ws) + qg_bytes;
+      hipError_t e = vxt::launch_gqa_prep(kc, a, params->rope_dim, params->rope_freq_base, batch_m, s);
+      const size_t row = (size_t)n_head * kc.hd;
+      for (uint32_t t = 0; t < batch_m && e == hipSuccess; t += group_t) {
+        const uint32_t nb = std::min(group_t, batch_m - t);
+        e = vxt::launch_attn_prefill(kc, q_ws + t * row, a.gate_out ? a.gate_out + t * row : nullptr, out + t * row,
+                                     n_head, pos + t, nb, part, s);
+      }
+      if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("prefill attention launch failed: ") + hipGetErrorString(e));
+      return;
+    }
     const size_t per_tok = vxt::attn_workspace_bytes(n_head, pos + batch_m, kc.n_kv, kc.hd, 1);
     const uint32_t group_m =
         (uint32_t)std::max<size_t>(1, std::min<size_t>(batch_m, ((size_t)16 << 20) / std::max<size_t>(per_tok, 1)));
