@@ -649,11 +649,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
                                                            const float* __restrict__ gate, float* __restrict__ out,
                                                            float* __restrict__ part, uint32_t n_head, uint32_t group,
                                                            uint32_t tq, uint32_t pos0, uint32_t batch) {
-  constexpr uint32_t TP = 32, KS = HD + 1, NS = HD / 2, NB = HD / 32;
+  constexpr uint32_t TP = 32, NS = HD / 2, NB = HD / 32;
+  // LDS layouts read 16 bytes (four MFMA operands) at a time, 16 lanes on
+  // distinct banks: K as [h][position][NS + 4] holding K[position][2 st + h]
+  // at st; V transposed, [dim][TP + 4].
+  constexpr uint32_t KS = NS + 4, VS = TP + 4;
   constexpr uint32_t NCH = TP * HD / 16;                // 16-value pieces per tile and plane
   constexpr uint32_t PER = (NCH + 255) / 256;           // pieces per thread
-  __shared__ float s_k[TP * KS];
-  __shared__ __attribute__((aligned(16))) float s_v[TP * HD];
+  __shared__ __attribute__((aligned(16))) float s_k[2 * TP * KS];
+  __shared__ __attribute__((aligned(16))) float s_v[HD * VS];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, h = lane >> 5, col = lane & 31u;
   const uint32_t kvh = blockIdx.x, tb = blockIdx.y * tq;
   const uint32_t t_end = min(batch, tb + tq);
@@ -669,7 +673,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
   if (tile0 * TP > last) return;                        // past this block's positions
   const uint32_t n_tiles = gridDim.z == 1 ? last / TP + 1u : min(last / TP + 1u, tile0 + kSegTiles);
   const uint32_t row_q = c.n_kv * HD, row_d = c.n_kv * (HD / 32);
-  const float scale = 1.0f / sqrtf((float)HD);
+  // scores in base 2: s * log2(e) / sqrt(hd), weights exp2(s2 - ref)
+  const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
 
   float qreg[NS];
   {
@@ -684,14 +689,15 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
     for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
   float m_run = -__builtin_inff(), l_run = 0.0f;
 
-  // bytes of tile 0 in flight
+  // Piece ch of a tile: position ch % 32, values (ch / 32) * 16 .. + 15, so
+  // the lanes of a wave write consecutive positions.
   u32x4 kq[PER], vq[PER];
   uint32_t kdb[PER], vdb[PER];
   auto fetch = [&](uint32_t p0) {
 #pragma unroll
     for (uint32_t u = 0; u < PER; ++u) {
       const uint32_t ch = min(tid + 256u * u, NCH - 1u);
-      const uint32_t p = min(p0 + ch / (HD / 16), last), d0 = (ch % (HD / 16)) * 16u;
+      const uint32_t p = min(p0 + ch % TP, last), d0 = (ch / TP) * 16u;
       const size_t qo = (size_t)p * row_q + kvh * HD + d0, dof = (size_t)p * row_d + kvh * (HD / 32) + d0 / 32;
       kq[u] = *reinterpret_cast<const u32x4*>(c.k_qs + qo);
       vq[u] = *reinterpret_cast<const u32x4*>(c.v_qs + qo);
@@ -708,17 +714,19 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
     for (uint32_t u = 0; u < PER; ++u) {
       const uint32_t ch = tid + 256u * u;
       if (ch < NCH) {
-        const uint32_t pp = ch / (HD / 16), d0 = (ch % (HD / 16)) * 16u;
+        const uint32_t pp = ch % TP, d0 = (ch / TP) * 16u;
         float kf[16], vf[16];
         unpack16(kq[u], kf);
         unpack16(vq[u], vf);
         const float kd = f16_to_f32_exact(kdb[u]), vd = f16_to_f32_exact(vdb[u]);
+        float* k0 = s_k + pp * KS + d0 / 2;              // h = 0: even values
+        float* k1 = s_k + (TP + pp) * KS + d0 / 2;       // h = 1: odd values
+        *reinterpret_cast<float4*>(k0) = make_float4(kf[0] * kd, kf[2] * kd, kf[4] * kd, kf[6] * kd);
+        *reinterpret_cast<float4*>(k0 + 4) = make_float4(kf[8] * kd, kf[10] * kd, kf[12] * kd, kf[14] * kd);
+        *reinterpret_cast<float4*>(k1) = make_float4(kf[1] * kd, kf[3] * kd, kf[5] * kd, kf[7] * kd);
+        *reinterpret_cast<float4*>(k1 + 4) = make_float4(kf[9] * kd, kf[11] * kd, kf[13] * kd, kf[15] * kd);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s_k[pp * KS + d0 + j] = kf[j] * kd;
-#pragma unroll
-        for (int j = 0; j < 16; j += 4)
-          *reinterpret_cast<float4*>(&s_v[pp * HD + d0 + j]) =
-              make_float4(vf[j] * vd, vf[j + 1] * vd, vf[j + 2] * vd, vf[j + 3] * vd);
+        for (int j = 0; j < 16; ++j) s_v[(d0 + j) * VS + pp] = vf[j] * vd;
       }
     }
     if (T + 1u < n_tiles) fetch(p0 + TP);
@@ -728,44 +736,61 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
     float16v sacc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
+    const float* kr = s_k + (h * TP + col) * KS;
 #pragma unroll
-    for (uint32_t st = 0; st < NS; ++st)
-      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(s_k[col * KS + 2u * st + h], qreg[st], sacc, 0, 0, 0);
+    for (uint32_t st = 0; st < NS; st += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(kr + st);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qreg[st], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qreg[st + 1], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qreg[st + 2], sacc, 0, 0, 0);
+      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qreg[st + 3], sacc, 0, 0, 0);
+    }
 
-    // online softmax over this tile for the lane's row
+    // online softmax over this tile for the lane's row.  The weights are
+    // taken against a reference m_run that moves only when the row's max
+    // passes it by more than 8 (weights stay below 2^8), so O^T and l are
+    // rescaled on few tiles.
     float pm = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const uint32_t pos = p0 + 8u * (i >> 2) + 4u * h + (i & 3);
-      const float sv = pos <= my_pos ? sacc[i] * scale : -__builtin_inff();
+      const float sv = pos <= my_pos ? sacc[i] * scale2 : -__builtin_inff();
       sacc[i] = sv;
       pm = fmaxf(pm, sv);
     }
     pm = xor32_pair(pm, true);
-    const float m_new = fmaxf(m_run, pm);
+    const bool move = pm > m_run + 8.0f;               // -inf reference: any finite score moves it
+    const float m_new = move ? pm : m_run;
+    const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;   // exp2(-inf) = 0
     // a row whose token precedes the segment sees only masked positions
     const bool none = m_new == -__builtin_inff();
-    const float alpha = none ? 1.0f : expf(m_run - m_new);
     float ps = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float e = none ? 0.0f : expf(sacc[i] - m_new);
+      const float e = none ? 0.0f : __builtin_amdgcn_exp2f(sacc[i] - m_new);
       sacc[i] = e;
       ps += e;
     }
     ps = xor32_pair(ps, false);
     l_run = l_run * alpha + ps;
     m_run = m_new;
+    const bool rescale = __builtin_amdgcn_ballot_w64(move) != 0;   // uniform across the wave
 
-    // O^T += V^T P^T
+    // O^T += V^T P^T: step i takes positions 8 (i / 4) + 4 h + i % 4
 #pragma unroll
     for (uint32_t b = 0; b < NB; ++b) {
+      if (rescale) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
+        for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
+      }
+      const float* vr = s_v + (32u * b + col) * VS + 4u * h;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const uint32_t pp = 8u * (i >> 2) + 4u * h + (i & 3);
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(s_v[pp * HD + 32u * b + col], sacc[i], o[b], 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        const float4 a = *reinterpret_cast<const float4*>(vr + 8u * j);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, sacc[4 * j], o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, sacc[4 * j + 1], o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, sacc[4 * j + 2], o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, sacc[4 * j + 3], o[b], 0, 0, 0);
       }
     }
     lds_barrier();
@@ -787,22 +812,27 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
   }
   const float inv = 1.0f / l_run;
   const size_t base = ((size_t)tk * n_head + head) * HD;
+  // gate values loaded together first (from a valid address when there is
+  // no gate), used after
+  float gv[NB * 16];
+  const float* gp = gate ? gate + base : q;
 #pragma unroll
   for (uint32_t b = 0; b < NB; ++b)
 #pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const uint32_t d0 = 32u * b + 8u * i4 + 4u * h;
+    for (int i = 0; i < 16; ++i) gv[b * 16 + i] = gp[32u * b + 8u * (i >> 2) + 4u * h + (i & 3)];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float v = o[b][i4 * 4 + e] * inv;
-        if (gate) v *= 1.0f / (1.0f + expf(-gate[base + d0 + e]));
-        out[base + d0 + e] = v;
-      }
+  for (uint32_t b = 0; b < NB; ++b)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float v = o[b][i] * inv;
+      if (gate) v *= 1.0f / (1.0f + expf(-gv[b * 16 + i]));
+      out[base + 32u * b + 8u * (i >> 2) + 4u * h + (i & 3)] = v;
     }
 }
 
 // Merge of the prefill's position segments: one wave per (token, head);
-// segments in ascending order, exp(m_s - m) rescaling, divide, gate.
+// segments in ascending order, exp2(m_s - m) rescaling (the segments' scores
+// and references are base 2), divide, gate.
 __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __restrict__ part, uint32_t hd,
                                                                  uint32_t n_head, uint32_t n_seg, uint32_t seg_len,
                                                                  uint32_t pos0, uint32_t batch,
@@ -821,7 +851,7 @@ __global__ __launch_bounds__(256) void attn_prefill_merge_kernel(const float* __
     float l = 0.0f, acc = 0.0f;
     for (uint32_t sg = 0; sg < ns; ++sg) {
       const float* ps = pr + (size_t)sg * (hd + 2);
-      const float e = ps[0] == -__builtin_inff() ? 0.0f : expf(ps[0] - m);
+      const float e = ps[0] == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(ps[0] - m);   // base-2 references
       l += ps[1] * e;
       acc += ps[2 + d] * e;
     }
