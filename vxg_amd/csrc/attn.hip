@@ -45,6 +45,7 @@ constexpr uint32_t kThreads = 256;
 constexpr uint32_t kMaxGroup = 8;   // query heads per kv head
 
 typedef float float16v __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr uint32_t kSegTiles = 16;   // prefill: 32-position tiles per position segment
 
@@ -629,35 +630,48 @@ __global__ __launch_bounds__(W * 64) void attn_merge_kernel(const float* __restr
   out[(size_t)h * hd + d] = o;
 }
 
-// ---- prefill: causal attention of a batch of prepared queries on fp32 MFMA
-// Workgroup (kv head, block of tq tokens): 4 waves, 32 query rows each; row
-// r is token tb + r / group, query head kvh * group + r % group.  Positions
-// are walked in tiles of 32 from 0 to the block's last token; K and V of a
-// tile are dequantised into LDS as f32 (int8 x f16 scale is exact in f32),
+// ---- prefill: causal attention of a batch of prepared queries on MFMA ------
+// Workgroup (kv head, block of tq tokens, position segment): 4 waves, 32
+// query rows each; row r is token tb + r / group, query head kvh * group +
+// r % group.  Positions are walked in tiles of 32 up to the block's last
+// token (or the segment's end); K and V of a tile are dequantised into LDS,
 // the next tile's bytes already in flight.  Per wave and tile:
-//   S^T (32 positions x 32 rows) = K Q^T: 64 v_mfma_f32_32x32x2_f32 at hd 128,
-//     A = K from LDS, B = Q^T from registers;
+//   S^T (32 positions x 32 rows) = K Q^T;
 //   online softmax: each lane owns one row (lane % 32) and 16 of the tile's
-//     positions, its partner lane ^ 32 the other 16;
-//   O^T (hd x 32 rows) += V^T P^T: hd / 32 blocks of 16 MFMA steps, step i
-//     taking the positions the lanes hold in accumulator register i.
-// Every row keeps its own running max / sum, so the rescale of O^T is one
-// factor per lane.  fp32 throughout (products exact, sums in MFMA order);
-// positions after a row's token are masked to -inf.
+//     positions, its partner lane ^ 32 the other 16; scores in base 2, the
+//     weights taken against a reference that moves only when the row's max
+//     passes it by more than 8, so O^T and l are rescaled on few tiles;
+//   O^T (hd x 32 rows) += V^T P^T, step s taking the positions the lanes hold
+//     in accumulator registers 8 s .. 8 s + 7.
+// Every row keeps its own running sums, so a rescale is one factor per lane;
+// positions after a row's token are masked to -inf.  The products run on
+// v_mfma_f32_32x32x16_bf16 with split operands:
+//   S^T: A = K's int8 values (exact in bf16), B = Q^T as three bf16 terms
+//     (hi + mid + lo represent an f32 exactly), one fresh accumulator per
+//     32-dim block, then S += d_k[position][block] * T in f32 -- the scores
+//     carry fp32 accuracy;
+//   O^T: A = V dequantised (int8 x f16 scale) as two bf16 terms, B = the
+//     weights as two bf16 terms, hi*hi + hi*lo + lo*hi (relative error
+//     about 2^-17 per product).
+// K tile in LDS as bf16 [position][hd + 8]; V^T hi and lo as bf16
+// [dim][32 + 8] with the positions of each 16 stored in the order the
+// weights sit in the accumulator (bits 2 and 3 of the position swapped), so
+// one 16-byte read gives a lane its 8 operands.  A thread dequantises two
+// adjacent positions x 8 dims of the tile.
 template <int HD>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const float* __restrict__ q,
-                                                           const float* __restrict__ gate, float* __restrict__ out,
-                                                           float* __restrict__ part, uint32_t n_head, uint32_t group,
-                                                           uint32_t tq, uint32_t pos0, uint32_t batch) {
-  constexpr uint32_t TP = 32, NS = HD / 2, NB = HD / 32;
-  // LDS layouts read 16 bytes (four MFMA operands) at a time, 16 lanes on
-  // distinct banks: K as [h][position][NS + 4] holding K[position][2 st + h]
-  // at st; V transposed, [dim][TP + 4].
-  constexpr uint32_t KS = NS + 4, VS = TP + 4;
-  constexpr uint32_t NCH = TP * HD / 16;                // 16-value pieces per tile and plane
-  constexpr uint32_t PER = (NCH + 255) / 256;           // pieces per thread
-  __shared__ __attribute__((aligned(16))) float s_k[2 * TP * KS];
-  __shared__ __attribute__((aligned(16))) float s_v[HD * VS];
+__global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(KvQ8Dev c, const float* __restrict__ q,
+                                                                const float* __restrict__ gate,
+                                                                float* __restrict__ out, float* __restrict__ part,
+                                                                uint32_t n_head, uint32_t group, uint32_t tq,
+                                                                uint32_t pos0, uint32_t batch) {
+  constexpr uint32_t TP = 32, NST = HD / 16, NB = HD / 32;
+  constexpr uint32_t KST = HD + 8, VST = TP + 8;        // bf16 strides
+  constexpr uint32_t NPC = (TP / 2) * (HD / 8);         // pieces: 2 positions x 8 dims
+  constexpr uint32_t PER = (NPC + 255) / 256;
+  __shared__ __attribute__((aligned(16))) uint16_t s_kb[TP * KST];
+  __shared__ __attribute__((aligned(16))) float s_kd[NB * TP];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vh[HD * VST];
+  __shared__ __attribute__((aligned(16))) uint16_t s_vl[HD * VST];
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, h = lane >> 5, col = lane & 31u;
   const uint32_t kvh = blockIdx.x, tb = blockIdx.y * tq;
   const uint32_t t_end = min(batch, tb + tq);
@@ -667,20 +681,32 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
   const uint32_t tkc = live ? tk : tb;                  // spare rows shadow the block's first token
   const uint32_t my_pos = pos0 + tkc;
   const uint32_t head = kvh * group + g;
-  const uint32_t last = pos0 + t_end - 1u;              // the largest position any row reads
-  // segment blockIdx.z of kSegTiles tiles (gridDim.z == 1: every position)
+  const uint32_t last = pos0 + t_end - 1u;
   const uint32_t tile0 = blockIdx.z * kSegTiles;
-  if (tile0 * TP > last) return;                        // past this block's positions
+  if (tile0 * TP > last) return;
   const uint32_t n_tiles = gridDim.z == 1 ? last / TP + 1u : min(last / TP + 1u, tile0 + kSegTiles);
   const uint32_t row_q = c.n_kv * HD, row_d = c.n_kv * (HD / 32);
-  // scores in base 2: s * log2(e) / sqrt(hd), weights exp2(s2 - ref)
   const float scale2 = 1.4426950408889634f / sqrtf((float)HD);
 
-  float qreg[NS];
+  // Q^T operand: lane holds row col's dims 16 st + 8 h .. + 7, three terms
+  bf16x8 q0[NST], q1[NST], q2[NST];
   {
-    const float* qr = q + ((size_t)tkc * n_head + head) * HD + h;
+    const float* qr = q + ((size_t)tkc * n_head + head) * HD + 8u * h;
 #pragma unroll
-    for (uint32_t st = 0; st < NS; ++st) qreg[st] = qr[2u * st];
+    for (uint32_t st = 0; st < NST; ++st) {
+      const float4 a = *reinterpret_cast<const float4*>(qr + 16u * st);
+      const float4 b = *reinterpret_cast<const float4*>(qr + 16u * st + 4u);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const __bf16 t0 = (__bf16)v[j];
+        const float r1 = v[j] - (float)t0;
+        const __bf16 t1 = (__bf16)r1;
+        q0[st][j] = t0;
+        q1[st][j] = t1;
+        q2[st][j] = (__bf16)(r1 - (float)t1);
+      }
+    }
   }
   float16v o[NB];
 #pragma unroll
@@ -689,67 +715,101 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
     for (int i = 0; i < 16; ++i) o[b][i] = 0.0f;
   float m_run = -__builtin_inff(), l_run = 0.0f;
 
-  // Piece ch of a tile: position ch % 32, values (ch / 32) * 16 .. + 15, so
-  // the lanes of a wave write consecutive positions.
-  u32x4 kq[PER], vq[PER];
-  uint32_t kdb[PER], vdb[PER];
+  // piece ch: positions 2 (ch % 16) + {0, 1}, dims 8 (ch / 16) .. + 7
+  uint2 kq[PER][2], vq[PER][2];
+  uint32_t kdb[PER][2], vdb[PER][2];
   auto fetch = [&](uint32_t p0) {
 #pragma unroll
     for (uint32_t u = 0; u < PER; ++u) {
-      const uint32_t ch = min(tid + 256u * u, NCH - 1u);
-      const uint32_t p = min(p0 + ch % TP, last), d0 = (ch / TP) * 16u;
-      const size_t qo = (size_t)p * row_q + kvh * HD + d0, dof = (size_t)p * row_d + kvh * (HD / 32) + d0 / 32;
-      kq[u] = *reinterpret_cast<const u32x4*>(c.k_qs + qo);
-      vq[u] = *reinterpret_cast<const u32x4*>(c.v_qs + qo);
-      kdb[u] = c.k_d[dof];
-      vdb[u] = c.v_d[dof];
+      const uint32_t ch = min(tid + 256u * u, NPC - 1u);
+      const uint32_t dg = ch / 16u;
+#pragma unroll
+      for (uint32_t e = 0; e < 2; ++e) {
+        const uint32_t p = min(p0 + 2u * (ch % 16u) + e, last);
+        const size_t qo = (size_t)p * row_q + kvh * HD + 8u * dg, dof = (size_t)p * row_d + kvh * (HD / 32) + dg / 4u;
+        kq[u][e] = *reinterpret_cast<const uint2*>(c.k_qs + qo);
+        vq[u][e] = *reinterpret_cast<const uint2*>(c.v_qs + qo);
+        kdb[u][e] = c.k_d[dof];
+        vdb[u][e] = c.v_d[dof];
+      }
     }
   };
   fetch(tile0 * TP);
 
   for (uint32_t T = tile0; T < n_tiles; ++T) {
     const uint32_t p0 = T * TP;
-    // this tile's values into LDS, then the next tile's bytes requested
 #pragma unroll
     for (uint32_t u = 0; u < PER; ++u) {
       const uint32_t ch = tid + 256u * u;
-      if (ch < NCH) {
-        const uint32_t pp = ch % TP, d0 = (ch / TP) * 16u;
-        float kf[16], vf[16];
-        unpack16(kq[u], kf);
-        unpack16(vq[u], vf);
-        const float kd = f16_to_f32_exact(kdb[u]), vd = f16_to_f32_exact(vdb[u]);
-        float* k0 = s_k + pp * KS + d0 / 2;              // h = 0: even values
-        float* k1 = s_k + (TP + pp) * KS + d0 / 2;       // h = 1: odd values
-        *reinterpret_cast<float4*>(k0) = make_float4(kf[0] * kd, kf[2] * kd, kf[4] * kd, kf[6] * kd);
-        *reinterpret_cast<float4*>(k0 + 4) = make_float4(kf[8] * kd, kf[10] * kd, kf[12] * kd, kf[14] * kd);
-        *reinterpret_cast<float4*>(k1) = make_float4(kf[1] * kd, kf[3] * kd, kf[5] * kd, kf[7] * kd);
-        *reinterpret_cast<float4*>(k1 + 4) = make_float4(kf[9] * kd, kf[11] * kd, kf[13] * kd, kf[15] * kd);
+      if (ch < NPC) {
+        const uint32_t pq = ch % 16u, dg = ch / 16u;
+        // slot of position 2 pq within its 16: bits 2 and 3 swapped
+        const uint32_t rr = (2u * pq) & 15u;
+        const uint32_t slot = (2u * pq & ~15u) | ((rr & 4u) << 1) | ((rr & 8u) >> 1) | (rr & 3u);
+        uint32_t vh_w[8], vl_w[8];
 #pragma unroll
-        for (int j = 0; j < 16; ++j) s_v[(d0 + j) * VS + pp] = vf[j] * vd;
+        for (uint32_t e = 0; e < 2; ++e) {
+          const uint32_t pp = 2u * pq + e;
+          const uint32_t w2[2] = {kq[u][e].x, kq[u][e].y};
+          uint32_t kb4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float f0 = (float)(int8_t)((w2[j >> 1] >> (16 * (j & 1))) & 0xffu);
+            const float f1 = (float)(int8_t)((w2[j >> 1] >> (16 * (j & 1) + 8)) & 0xffu);
+            kb4[j] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);   // exact
+          }
+          *reinterpret_cast<u32x4*>(s_kb + pp * KST + 8u * dg) = u32x4{kb4[0], kb4[1], kb4[2], kb4[3]};
+          if ((dg & 3u) == 0) s_kd[(dg / 4u) * TP + pp] = f16_to_f32_exact(kdb[u][e]);
+          const float vd = f16_to_f32_exact(vdb[u][e]);
+          const uint32_t v2[2] = {vq[u][e].x, vq[u][e].y};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float v = (float)(int8_t)((v2[j >> 2] >> (8 * (j & 3))) & 0xffu) * vd;
+            const __bf16 hi = (__bf16)v;
+            const __bf16 lo = (__bf16)(v - (float)hi);
+            const uint32_t hb = __builtin_bit_cast(uint16_t, hi), lb = __builtin_bit_cast(uint16_t, lo);
+            vh_w[j] = e ? (vh_w[j] | (hb << 16)) : hb;
+            vl_w[j] = e ? (vl_w[j] | (lb << 16)) : lb;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          *reinterpret_cast<uint32_t*>(s_vh + (8u * dg + j) * VST + slot) = vh_w[j];
+          *reinterpret_cast<uint32_t*>(s_vl + (8u * dg + j) * VST + slot) = vl_w[j];
+        }
       }
     }
     if (T + 1u < n_tiles) fetch(p0 + TP);
     lds_barrier();
 
-    // S^T = K Q^T
+    // S^T = sum over 32-dim blocks of d_k * (K Q^T over the block)
     float16v sacc;
 #pragma unroll
     for (int i = 0; i < 16; ++i) sacc[i] = 0.0f;
-    const float* kr = s_k + (h * TP + col) * KS;
 #pragma unroll
-    for (uint32_t st = 0; st < NS; st += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(kr + st);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qreg[st], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qreg[st + 1], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qreg[st + 2], sacc, 0, 0, 0);
-      sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qreg[st + 3], sacc, 0, 0, 0);
+    for (uint32_t b = 0; b < NB; ++b) {
+      float16v tacc;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) tacc[i] = 0.0f;
+#pragma unroll
+      for (uint32_t t = 0; t < 2; ++t) {
+        const uint32_t st = 2u * b + t;
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(s_kb + col * KST + 16u * st + 8u * h);
+        tacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, q0[st], tacc, 0, 0, 0);
+        tacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, q1[st], tacc, 0, 0, 0);
+        tacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, q2[st], tacc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float4 dk = *reinterpret_cast<const float4*>(s_kd + b * TP + 8u * j + 4u * h);
+        sacc[4 * j] = __builtin_fmaf(dk.x, tacc[4 * j], sacc[4 * j]);
+        sacc[4 * j + 1] = __builtin_fmaf(dk.y, tacc[4 * j + 1], sacc[4 * j + 1]);
+        sacc[4 * j + 2] = __builtin_fmaf(dk.z, tacc[4 * j + 2], sacc[4 * j + 2]);
+        sacc[4 * j + 3] = __builtin_fmaf(dk.w, tacc[4 * j + 3], sacc[4 * j + 3]);
+      }
     }
 
-    // online softmax over this tile for the lane's row.  The weights are
-    // taken against a reference m_run that moves only when the row's max
-    // passes it by more than 8 (weights stay below 2^8), so O^T and l are
-    // rescaled on few tiles.
+    // online softmax (as the fp32 kernel): base 2, lazy reference
     float pm = -__builtin_inff();
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -759,10 +819,9 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
       pm = fmaxf(pm, sv);
     }
     pm = xor32_pair(pm, true);
-    const bool move = pm > m_run + 8.0f;               // -inf reference: any finite score moves it
+    const bool move = pm > m_run + 8.0f;
     const float m_new = move ? pm : m_run;
-    const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;   // exp2(-inf) = 0
-    // a row whose token precedes the segment sees only masked positions
+    const float alpha = move ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
     const bool none = m_new == -__builtin_inff();
     float ps = 0.0f;
 #pragma unroll
@@ -774,23 +833,30 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
     ps = xor32_pair(ps, false);
     l_run = l_run * alpha + ps;
     m_run = m_new;
-    const bool rescale = __builtin_amdgcn_ballot_w64(move) != 0;   // uniform across the wave
+    const bool rescale = __builtin_amdgcn_ballot_w64(move) != 0;
 
-    // O^T += V^T P^T: step i takes positions 8 (i / 4) + 4 h + i % 4
+    // weights as two bf16 terms; step s takes accumulator registers 8 s .. + 7
+    bf16x8 ph[2], pl[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const __bf16 hi = (__bf16)sacc[i];
+      ph[i >> 3][i & 7] = hi;
+      pl[i >> 3][i & 7] = (__bf16)(sacc[i] - (float)hi);
+    }
 #pragma unroll
     for (uint32_t b = 0; b < NB; ++b) {
       if (rescale) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) o[b][i] *= alpha;
       }
-      const float* vr = s_v + (32u * b + col) * VS + 4u * h;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float4 a = *reinterpret_cast<const float4*>(vr + 8u * j);
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, sacc[4 * j], o[b], 0, 0, 0);
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, sacc[4 * j + 1], o[b], 0, 0, 0);
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, sacc[4 * j + 2], o[b], 0, 0, 0);
-        o[b] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, sacc[4 * j + 3], o[b], 0, 0, 0);
+      for (uint32_t t = 0; t < 2; ++t) {
+        const uint32_t off = (32u * b + col) * VST + 16u * t + 8u * h;
+        const bf16x8 ah = *reinterpret_cast<const bf16x8*>(s_vh + off);
+        const bf16x8 al = *reinterpret_cast<const bf16x8*>(s_vl + off);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, ph[t], o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, pl[t], o[b], 0, 0, 0);
+        o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, ph[t], o[b], 0, 0, 0);
       }
     }
     lds_barrier();
@@ -798,7 +864,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
 
   if (!live) return;
   if (gridDim.z > 1) {
-    // this segment's (m, l, unnormalised sum) for the merge
     float* pr = part + (((size_t)tk * n_head + head) * gridDim.z + blockIdx.z) * (HD + 2);
     if (h == 0) {
       pr[0] = m_run;
@@ -812,8 +877,6 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(KvQ8Dev c, const floa
   }
   const float inv = 1.0f / l_run;
   const size_t base = ((size_t)tk * n_head + head) * HD;
-  // gate values loaded together first (from a valid address when there is
-  // no gate), used after
   float gv[NB * 16];
   const float* gp = gate ? gate + base : q;
 #pragma unroll
@@ -999,11 +1062,11 @@ hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* ga
   float* part = static_cast<float*>(ws);
   const dim3 grid(c.n_kv, blocks, ns);
   switch (c.hd) {
-    case 32: hipLaunchKernelGGL(attn_prefill_kernel<32>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head, group,
-                                tq, pos0, batch); break;
-    case 64: hipLaunchKernelGGL(attn_prefill_kernel<64>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head, group,
-                                tq, pos0, batch); break;
-    case 128: hipLaunchKernelGGL(attn_prefill_kernel<128>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head,
+    case 32: hipLaunchKernelGGL(attn_prefill_bf16_kernel<32>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head,
+                                group, tq, pos0, batch); break;
+    case 64: hipLaunchKernelGGL(attn_prefill_bf16_kernel<64>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head,
+                                group, tq, pos0, batch); break;
+    case 128: hipLaunchKernelGGL(attn_prefill_bf16_kernel<128>, grid, dim3(256), 0, s, c, q, gate, out, part, n_head,
                                  group, tq, pos0, batch); break;
     default: return hipErrorInvalidValue;
   }
