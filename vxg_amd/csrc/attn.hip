@@ -92,9 +92,9 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(KvQ8Dev c, const fl
 }
 
 // ---- the step's q / k preparation (llm_prefill.rs:284-313) ----------------
-// One wave per (head, token): blockIdx.x < n_head is query head x, the rest
-// are kv heads; blockIdx.y is the token.  A lane holds the values d = lane +
-// 64 j of its head.  Query head: q_raw slice (+ bias), the gate half copied
+// One workgroup per token; its four waves take the heads in turn (query
+// heads, then kv heads), after the token's rotation angles are tabulated in
+// LDS once.  A lane holds the values d = lane + 64 j of its head.  Query head: q_raw slice (+ bias), the gate half copied
 // out, RMSNorm with q_norm (sum of squares over the wave, then x * scale * w
 // as two roundings), RoPE, q_out.  Kv head: V (+ bias) quantised into the
 // cache; K (+ bias), RMSNorm with k_norm, RoPE, quantised.  RoPE angles are
@@ -107,110 +107,127 @@ struct RopeFreq {
 };
 
 template <int HD>
-__global__ __launch_bounds__(64) void gqa_prep_kernel(KvQ8Dev c, GqaPrep a, RopeFreq rf) {
+__global__ __launch_bounds__(256) void gqa_prep_kernel(KvQ8Dev c, GqaPrep a, RopeFreq rf) {
 #pragma clang fp contract(off)
   constexpr int J = HD >= 64 ? HD / 64 : 1;
-  __shared__ float s_x[HD];
-  const uint32_t lane = threadIdx.x, idx = blockIdx.x, m = blockIdx.y;
-  const bool is_q = idx < a.n_head;
-  const uint32_t kvh = is_q ? 0u : idx - a.n_head;
-  const uint32_t per = c.n_kv * HD;
+  __shared__ float s_x[4][HD];          // a wave's head during the rotation
+  __shared__ float s_cs[HD];            // sin, cos of pair i at 2 i, 2 i + 1
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, m = blockIdx.x;
+  const uint32_t per = c.n_kv * HD, n_units = a.n_head + c.n_kv;
   const size_t row = (size_t)a.pos + m;
-  const uint32_t qoff = idx * (a.gated ? 2u : 1u) * HD;
-  const float* src = is_q ? a.q_raw + (size_t)m * a.q_stride + qoff : a.k_cur + (size_t)m * a.kv_stride + kvh * HD;
-  const float* bias = is_q ? (a.q_bias ? a.q_bias + qoff : nullptr) : (a.k_bias ? a.k_bias + kvh * HD : nullptr);
-  const float* nw = is_q ? a.q_norm : a.k_norm;
+  // the token's rotation angles, once for all its heads
+  if (tid < a.half) {
+    const float theta = (float)(a.rope_pos + m) * rf.f[tid];
+    double sd, cd;
+    sincos((double)theta, &sd, &cd);
+    s_cs[2u * tid] = (float)sd;
+    s_cs[2u * tid + 1u] = (float)cd;
+  }
+  __syncthreads();
+  // wave w takes heads w, w + 4, ... (query heads, then kv heads); every
+  // wave runs the same number of rounds so the barriers line up
+  for (uint32_t base = 0; base < n_units; base += 4u) {
+    const uint32_t idx = base + wave;
+    const bool active = idx < n_units;
+    const uint32_t idc = active ? idx : 0u;
+    const bool is_q = idc < a.n_head;
+    const uint32_t kvh = is_q ? 0u : idc - a.n_head;
+    const uint32_t qoff = idc * (a.gated ? 2u : 1u) * HD;
+    const float* src = is_q ? a.q_raw + (size_t)m * a.q_stride + qoff : a.k_cur + (size_t)m * a.kv_stride + kvh * HD;
+    const float* bias = is_q ? (a.q_bias ? a.q_bias + qoff : nullptr) : (a.k_bias ? a.k_bias + kvh * HD : nullptr);
+    const float* nw = is_q ? a.q_norm : a.k_norm;
+    float* sx = s_x[wave];
 
-  float x[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const uint32_t d = lane + 64u * j;
-    x[j] = 0.0f;
-    if (d < HD) {
-      x[j] = src[d];
-      if (bias) x[j] = x[j] + bias[d];
-    }
-  }
-  if (is_q && a.gated) {
-    float* g = a.gate_out + (size_t)m * a.n_head * HD + (size_t)idx * HD;
+    float x[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
       const uint32_t d = lane + 64u * j;
-      if (d < HD) g[d] = bias ? src[HD + d] + bias[HD + d] : src[HD + d];
-    }
-  }
-  if (!is_q) {
-    const float* vs = a.v_cur + (size_t)m * a.kv_stride + kvh * HD;
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t d = lane + 64u * j;
-      float vv = 0.0f;
+      x[j] = 0.0f;
       if (d < HD) {
-        vv = vs[d];
-        if (a.v_bias) vv = vv + a.v_bias[kvh * HD + d];
-      }
-      uint32_t dh;
-      const int q = q8_lane(vv, dh);
-      if (d < HD) {
-        c.v_qs[row * per + kvh * HD + d] = (int8_t)q;
-        if ((d & 31u) == 0) c.v_d[row * (per / 32) + (kvh * HD + d) / 32] = (uint16_t)dh;
+        x[j] = src[d];
+        if (bias) x[j] = x[j] + bias[d];
       }
     }
-  }
-  if (nw) {
-    float sq = 0.0f;
+    if (active && is_q && a.gated) {
+      float* gt = a.gate_out + (size_t)m * a.n_head * HD + (size_t)idc * HD;
 #pragma unroll
-    for (int j = 0; j < J; ++j) sq = __builtin_fmaf(x[j], x[j], sq);
-    sq = lane_reduce<64>(sq);
-    const float scale = 1.0f / sqrtf(sq / (float)HD + a.eps);
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t d = lane + 64u * j;
-      if (d < HD) x[j] = x[j] * scale * nw[d];
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d < HD) gt[d] = bias ? src[HD + d] + bias[HD + d] : src[HD + d];
+      }
     }
-  }
-  if (a.half) {
+    if (!is_q) {
+      const float* vs = a.v_cur + (size_t)m * a.kv_stride + kvh * HD;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t d = lane + 64u * j;
-      if (d < HD) s_x[d] = x[j];
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        float vv = 0.0f;
+        if (d < HD) {
+          vv = vs[d];
+          if (a.v_bias) vv = vv + a.v_bias[kvh * HD + d];
+        }
+        uint32_t dh;
+        const int qq = q8_lane(vv, dh);
+        if (active && d < HD) {
+          c.v_qs[row * per + kvh * HD + d] = (int8_t)qq;
+          if ((d & 31u) == 0) c.v_d[row * (per / 32) + (kvh * HD + d) / 32] = (uint16_t)dh;
+        }
+      }
     }
-    __syncthreads();
-    const float p = (float)(a.rope_pos + m);
-    for (uint32_t i = lane; i < a.half; i += 64u) {
-      const float theta = p * rf.f[i];
-      double sd, cd;
-      sincos((double)theta, &sd, &cd);
-      const float sn = (float)sd, cs = (float)cd;
-      const uint32_t i0 = a.neox ? i : 2u * i, i1 = a.neox ? i + a.half : 2u * i + 1u;
-      const float x0 = s_x[i0], x1 = s_x[i1];
-      s_x[i0] = x0 * cs - x1 * sn;
-      s_x[i1] = x0 * sn + x1 * cs;
-    }
-    __syncthreads();
+    if (nw) {
+      float sq = 0.0f;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t d = lane + 64u * j;
-      if (d < HD) x[j] = s_x[d];
-    }
-  }
-  if (is_q) {
-    float* qo = a.q_out + (size_t)m * a.n_head * HD + (size_t)idx * HD;
+      for (int j = 0; j < J; ++j) sq = __builtin_fmaf(x[j], x[j], sq);
+      sq = lane_reduce<64>(sq);
+      const float scale = 1.0f / sqrtf(sq / (float)HD + a.eps);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const uint32_t d = lane + 64u * j;
-      if (d < HD) qo[d] = x[j];
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d < HD) x[j] = x[j] * scale * nw[d];
+      }
     }
-    return;
-  }
+    if (a.half) {
 #pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const uint32_t d = lane + 64u * j;
-    uint32_t dh;
-    const int q = q8_lane(x[j], dh);
-    if (d < HD) {
-      c.k_qs[row * per + kvh * HD + d] = (int8_t)q;
-      if ((d & 31u) == 0) c.k_d[row * (per / 32) + (kvh * HD + d) / 32] = (uint16_t)dh;
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d < HD) sx[d] = x[j];
+      }
+      lds_barrier();
+      for (uint32_t i = lane; i < a.half; i += 64u) {
+        const float sn = s_cs[2u * i], cs = s_cs[2u * i + 1u];
+        const uint32_t i0 = a.neox ? i : 2u * i, i1 = a.neox ? i + a.half : 2u * i + 1u;
+        const float x0 = sx[i0], x1 = sx[i1];
+        sx[i0] = x0 * cs - x1 * sn;
+        sx[i1] = x0 * sn + x1 * cs;
+      }
+      lds_barrier();
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        if (d < HD) x[j] = sx[d];
+      }
+      lds_barrier();   // the next round writes sx again
+    }
+    if (is_q) {
+      if (active) {
+        float* qo = a.q_out + (size_t)m * a.n_head * HD + (size_t)idc * HD;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+          const uint32_t d = lane + 64u * j;
+          if (d < HD) qo[d] = x[j];
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const uint32_t d = lane + 64u * j;
+        uint32_t dh;
+        const int qq = q8_lane(x[j], dh);
+        if (active && d < HD) {
+          c.k_qs[row * per + kvh * HD + d] = (int8_t)qq;
+          if ((d & 31u) == 0) c.k_d[row * (per / 32) + (kvh * HD + d) / 32] = (uint16_t)dh;
+        }
+      }
     }
   }
 }
@@ -988,7 +1005,7 @@ uint32_t chunk_of(uint32_t hd) { return 16u * (64u / (hd / 16u)); }
 
 template <int HD>
 void launch_prep(const KvQ8Dev& c, const GqaPrep& a, const RopeFreq& rf, uint32_t batch, hipStream_t s) {
-  hipLaunchKernelGGL(gqa_prep_kernel<HD>, dim3(a.n_head + c.n_kv, batch), dim3(64), 0, s, c, a, rf);
+  hipLaunchKernelGGL(gqa_prep_kernel<HD>, dim3(batch), dim3(256), 0, s, c, a, rf);
 }
 
 }  // namespace
