@@ -31,6 +31,10 @@
 // the optional sigmoid gate.  Token z of a batch attends to positions
 // [0, seq0 + z) (causal prefill).  The sums run in a different order from the
 // CPU loop (fp32, parity by tolerance).
+//
+// Prefill (16 tokens or more): a flash-attention kernel on bf16 MFMA with
+// split operands, 128 query rows per workgroup, position segments merged by
+// a small kernel (see attn_prefill_bf16_kernel).
 #include "common.hpp"
 
 #include <algorithm>
