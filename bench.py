@@ -385,7 +385,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="0,2,3,4,s,a",
+    ap.add_argument("--configs", default="0,g,2,3,4,s,a",
                     help="secondary configurations to run (s: whole decode step on config 4's weights, "
                          "a: KV-Q8 decode attention)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -421,6 +421,20 @@ def main():
                           "kernel_GBps": round(r0["kernel_GBps"], 1),
                           "frac_hbm": round(r0["kernel_GBps"] / HBM_PEAK_GBS, 4)})
         log(f"  {r0['GBps']:.1f} GB/s wall, kernel {r0['kernel_ms']*1e3:.2f} us")
+    if "g" in run:
+        # the headline kernel at larger shapes: how much of config 1's gap to
+        # the HBM roofline is the fixed cost of a 12.6 MB launch
+        for (K, N) in [(2048, 24576), (8192, 6144), (2048, 151936)]:
+            mg = synth.make_g64(N, K, seed=4)
+            st = max(20, min(args.steps, int(2e9 / weight_bytes(mg))))
+            rg = bench_gemv(eng, mg, 1, "bf16", "f32", st, min(args.warmup, 5), seed=0)
+            secondary.append({"config": f"1 at larger shapes: g64 gemv M=1 K={K} N={N}",
+                              "GBps": round(rg["GBps"], 1), "kernel_us": round(rg["kernel_ms"] * 1e3, 3),
+                              "kernel_GBps": round(rg["kernel_GBps"], 1),
+                              "frac_hbm": round(rg["kernel_GBps"] / HBM_PEAK_GBS, 4)})
+            log(f"  g64 GEMV M=1 K={K} N={N}: {rg['kernel_GBps']:.1f} GB/s kernel "
+                f"({rg['kernel_ms']*1e3:.2f} us)")
+            del mg
     if "2" in run:
         for (K, N) in [(2048, 2048), (2048, 6144), (6144, 2048), (2048, 151936)]:
             mq = synth.make_q8(N, K, seed=2)
