@@ -16,7 +16,7 @@
  * lives in tests/test_oracle_*.py; the header of each function names the
  * reference lines it follows.
  *
- * Layout conventions (reference `rows x cols`, BASELINE `N x K`):
+ * Layout conventions (reference `rows x cols`, benchmark notation `N x K`):
  *   rows = N (output features), cols = K (reduction), batch_m = M (tokens).
  */
 #include <math.h>
@@ -247,7 +247,7 @@ VXO_API void vxo_cb4_gemv(const vxo_cb4* m, const float* x, float* y, int thread
 }
 
 /* ------------------------------------------------------------------------- */
-/* cb4-g64: the BASELINE decode layout (groups of 64 along K, one 16-entry    */
+/* cb4-g64: the benchmark's decode layout (groups of 64 along K, one 16-entry */
 /* fp16 codebook per group, no scale, no outliers).  Not a reference type;    */
 /* its GEMV follows the reference cb4 kernel's loop shape (codebook.rs:376-417)*/
 /* with the per-group table in place of sc*centroid.                          */

@@ -112,11 +112,11 @@ def test_gemv_reference_bar_197x544(eng):
         assert np.max(np.abs(y - oracle.gemv(m, x, threads=4))) < 2e-4, kind
 
 
-BASELINE_SHAPES = [(2048, 2048), (2048, 6144), (6144, 2048), (4096, 4096)]
+BENCH_SHAPES = [(2048, 2048), (2048, 6144), (6144, 2048), (4096, 4096)]
 
 
 @pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
-@pytest.mark.parametrize("K,N", BASELINE_SHAPES)
+@pytest.mark.parametrize("K,N", BENCH_SHAPES)
 @pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_gemv_baseline_shapes_bf16(eng, kind, K, N, M):
     m = make(kind, N, K, seed=K + N + M)
