@@ -385,7 +385,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="0,g,2,3,4,s,a",
+    ap.add_argument("--configs", default="0,r,g,2,3,4,s,a",
                     help="secondary configurations to run (s: whole decode step on config 4's weights, "
                          "a: KV-Q8 decode attention)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -421,6 +421,19 @@ def main():
                           "kernel_GBps": round(r0["kernel_GBps"], 1),
                           "frac_hbm": round(r0["kernel_GBps"] / HBM_PEAK_GBS, 4)})
         log(f"  {r0['GBps']:.1f} GB/s wall, kernel {r0['kernel_ms']*1e3:.2f} us")
+    if "r" in run:
+        # config 1's shape on the reference cb4 layout (128-column groups, f16
+        # scales, one f32 centroid table, ~0.74 % CSR outliers)
+        mr = synth.make_cb4(6144, 2048, seed=1)
+        rr = bench_gemv(eng, mr, 1, "bf16", "f32", args.steps, args.warmup, seed=0)
+        secondary.append({"config": f"1 on the reference cb4 layout: cb4-ref gemv M=1 K=2048 N=6144 "
+                                    f"({mr.outliers_packed.size} outliers)",
+                          "GBps": round(rr["GBps"], 1), "kernel_us": round(rr["kernel_ms"] * 1e3, 3),
+                          "kernel_GBps": round(rr["kernel_GBps"], 1),
+                          "frac_hbm": round(rr["kernel_GBps"] / HBM_PEAK_GBS, 4)})
+        log(f"  cb4-ref GEMV M=1 K=2048 N=6144: {rr['kernel_GBps']:.1f} GB/s kernel "
+            f"({rr['kernel_ms']*1e3:.2f} us)")
+        del mr
     if "g" in run:
         # the headline kernel at larger shapes: how much of config 1's gap to
         # the HBM roofline is the fixed cost of a 12.6 MB launch
