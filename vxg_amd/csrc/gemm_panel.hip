@@ -157,36 +157,33 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
 __device__ __forceinline__ float wave_max(float v) { return lane_reduce<64, true>(v); }
 __device__ __forceinline__ float wave_add(float v) { return lane_reduce<64>(v); }
 
-// 32 consecutive f32 weights -> hi (and lo) f16 pieces at column k0 of the row.
+// 8 consecutive f32 weights -> hi (and lo) f16 pieces at column c of the row.
 template <bool SPLIT>
-__device__ __forceinline__ void store32(const float (&w)[32], float s, uint16_t* hi, uint16_t* lo, uint32_t k0) {
-  uint32_t h[16], l[16];
+__device__ __forceinline__ void store8(const float (&w)[8], float s, uint16_t* hi, uint16_t* lo, uint32_t c) {
+  uint32_t h[4], l[4];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < 4; ++j) {
     const float a = w[2 * j] * s, b = w[2 * j + 1] * s;   // exact: s is a power of two
     const _Float16 ha = (_Float16)a, hb = (_Float16)b;
     h[j] = pack_h2(ha, hb);
     if constexpr (SPLIT) l[j] = pack_h2((_Float16)((a - (float)ha) * kLoScale), (_Float16)((b - (float)hb) * kLoScale));
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    *reinterpret_cast<uint4*>(hi + k0 + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
-    if constexpr (SPLIT)
-      *reinterpret_cast<uint4*>(lo + k0 + 8 * i) = make_uint4(l[4 * i], l[4 * i + 1], l[4 * i + 2], l[4 * i + 3]);
-  }
+  *reinterpret_cast<uint4*>(hi + c) = make_uint4(h[0], h[1], h[2], h[3]);
+  if constexpr (SPLIT) *reinterpret_cast<uint4*>(lo + c) = make_uint4(l[0], l[1], l[2], l[3]);
 }
 
-// One wave per (weight row, 2048-column segment): a lane decodes 32
-// consecutive columns with 16-byte loads, as the GEMV does, and writes them
-// as 16-byte f16 pieces.  Rows that need a power-of-two scale (hi/lo modes)
-// derive it in every segment's wave from the row's scales and residuals,
-// requested together with the segment's own weights, so no wave walks a row
-// serially.  cb4 residuals are applied by the wave owning the column's
-// segment, after its dense stores, in CSR order.
+// One wave per (weight row, 2048-column segment).  Lane l decodes the four
+// 8-column pieces seg + 512 i + 8 l (i = 0..3), so each of its loads and each
+// 16-byte store instruction covers a contiguous stretch of the row across the
+// wave (1 KB of f16 per store).  Rows that need a power-of-two scale (hi/lo
+// modes) derive it in every segment's wave from the row's scales and
+// residuals, requested together with the segment's own weights, so no wave
+// walks a row serially.  cb4 residuals are applied by the wave owning the
+// column's segment, after its dense stores, in CSR order.
 template <uint32_t KIND>
 __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, uint32_t qblock, uint32_t nseg, XConv xc) {
-  constexpr uint32_t kPair = 48;   // g64 pair-table stride (bytes) in the per-wave slot
-  __shared__ __attribute__((aligned(64))) uint32_t s_slot[KIND == KIND_G64 ? 4 * 32 * kPair / 4 : 1];
+  constexpr uint32_t kTab = 32;   // g64 table bytes per 64-column group
+  __shared__ __attribute__((aligned(64))) uint32_t s_tab[KIND == KIND_G64 ? 4 * 32 * kTab / 4 : 1];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
   if (blockIdx.x < xc.blocks) {   // uniform per workgroup: the activation conversion's share
     if (xc.x_bf16)
@@ -204,63 +201,94 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
   const uint32_t unit = (blockIdx.x - xc.blocks) * 4 + wave;
   if (unit >= N * nseg) return;
   const uint32_t n = unit / nseg, seg = (unit % nseg) * (64 * 32);
-  const uint32_t k0 = seg + lane * 32;
-  const bool live = k0 < KP;   // KP % 64 == 0: a lane pair is wholly inside or outside
+  // Piece i starts at column c0 + 512 i; KP % 64 == 0, so a piece is wholly
+  // inside or outside the panel row.
+  const uint32_t c0 = seg + 8 * lane;
   uint16_t* hi = p.hi + (size_t)n * KP;
   uint16_t* lo = p.lo + (size_t)n * KP;
   float s = 1.0f;
-  float w[32];
   if constexpr (KIND == KIND_G64) {
-    const uint32_t kc = live ? k0 : 0;
-    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2) + kc / 2);
-    const uint4 lt = *reinterpret_cast<const uint4*>(t.p1 + ((size_t)n * (kp / 64) + kc / 64) * 16 + (lane & 1) * 8);
-    const uint32_t slot = wave * 32 * kPair + (lane >> 1) * kPair;   // bytes
-    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(s_slot) + slot + (lane & 1) * 16) = lt;
-    const uint16_t* tab = reinterpret_cast<const uint16_t*>(reinterpret_cast<const char*>(s_slot) + slot);
-    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
-    uint32_t h[16];
+    // KP <= kp here (kp is a multiple of 64 and at least K).  The segment's
+    // 32 tables go to the wave's LDS slot, lane l holding half of table l / 2;
+    // groups past the row's last are clamped (their columns are >= K).
+    const uint32_t ng = kp / 64;
+    const uint32_t g = std::min(seg / 64 + lane / 2, ng - 1);
+    const uint4 lt = *reinterpret_cast<const uint4*>(t.p1 + ((size_t)n * ng + g) * 16 + (lane & 1) * 8);
+    const uint8_t* qr = static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2);
+    uint32_t wd[4];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const uint32_t c0 = 2 * j, c1 = c0 + 1;
-      const uint32_t e0 = k0 + c0 < K ? tab[(wd[c0 >> 3] >> ((c0 & 7) * 4)) & 0xfu] : 0u;
-      const uint32_t e1 = k0 + c1 < K ? tab[(wd[c1 >> 3] >> ((c1 & 7) * 4)) & 0xfu] : 0u;
-      h[j] = e0 | (e1 << 16);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = c0 + 512 * i;
+      wd[i] = *reinterpret_cast<const uint32_t*>(qr + (c < KP ? c : 0) / 2);
     }
-    if (live) {
+    char* slot = reinterpret_cast<char*>(s_tab) + wave * 32 * kTab;
+    *reinterpret_cast<uint4*>(slot + lane * 16) = lt;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<uint4*>(hi + k0 + 8 * i) = make_uint4(h[4 * i], h[4 * i + 1], h[4 * i + 2], h[4 * i + 3]);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = c0 + 512 * i;
+      if (c >= KP) continue;
+      const uint16_t* tab = reinterpret_cast<const uint16_t*>(slot + (8 * i + lane / 8) * kTab);
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t e0 = c + 2 * j < K ? tab[(wd[i] >> (8 * j)) & 0xfu] : 0u;
+        const uint32_t e1 = c + 2 * j + 1 < K ? tab[(wd[i] >> (8 * j + 4)) & 0xfu] : 0u;
+        h[j] = e0 | (e1 << 16);
+      }
+      *reinterpret_cast<uint4*>(hi + c) = make_uint4(h[0], h[1], h[2], h[3]);
     }
   } else if constexpr (KIND == KIND_Q8) {
-    const uint32_t kc = live ? (k0 < kp ? k0 : kp - 32) : 0;   // kp may be 32 short of KP
-    const int8_t* qp = static_cast<const int8_t*>(t.p0) + (size_t)n * kp + kc;
-    const uint4 a = *reinterpret_cast<const uint4*>(qp), b = *reinterpret_cast<const uint4*>(qp + 16);
+    // kp may be 32 short of KP: pieces past kp read the row's last 8 bytes
+    // (their columns are >= K and come out zero).
+    const int8_t* qr = static_cast<const int8_t*>(t.p0) + (size_t)n * kp;
     const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
-    const float d = qblock ? 1.0f : f16_to_f32_exact(dp[kc / 32]);
+    uint2 q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = c0 + 512 * i;
+      q[i] = *reinterpret_cast<const uint2*>(qr + (c < kp ? c : kp - 8));
+    }
+    float d[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     if (qblock) {   // block scales as f32; blocks past the weights' own are zero
       const uint32_t b0 = seg / 32 + lane;
       if (b0 < KP / 32)
         p.dsc[(size_t)n * (KP / 32) + b0] = b0 < kp / 32 ? f16_to_f32_exact(dp[b0]) : 0.0f;
     } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t c = c0 + 512 * i;
+        d[i] = f16_to_f32_exact(dp[(c < kp ? c : kp - 8) / 32]);
+      }
       float dm = 0.0f;
       for (uint32_t g = lane; g < kp / 32; g += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[g])));
       s = row_scale(127.0f * wave_max(dm));
     }
-    const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int j = 0; j < 32; ++j)
-      w[j] = k0 + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d : 0.0f;   // gguf.rs:223-229
-    if (live) {
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = c0 + 512 * i;
+      if (c >= KP) continue;
+      const uint32_t wd[2] = {q[i].x, q[i].y};
+      float w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)   // gguf.rs:223-229
+        w[j] = c + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d[i] : 0.0f;
       if (qblock)   // the int8 value itself, exact in f16
-        store32<false>(w, 1.0f, hi, lo, k0);
+        store8<false>(w, 1.0f, hi, lo, c);
       else
-        store32<true>(w, s, hi, lo, k0);
+        store8<true>(w, s, hi, lo, c);
     }
   } else {
-    const uint32_t kc = live ? k0 : 0;
-    const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint32_t*>(t.p0) + (size_t)n * (kp / 8) + kc / 8);
+    // KP <= kp here (kp is a multiple of 128 and at least K).
+    const uint32_t* pw = static_cast<const uint32_t*>(t.p0) + (size_t)n * (kp / 8);
     const uint16_t* sp = t.p1 + (size_t)n * (kp / 128);
-    const float sc = f16_to_f32_exact(sp[kc / 128]);
+    uint32_t wd[4];
+    float sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = c0 + 512 * i, cc = c < KP ? c : 0;
+      wd[i] = pw[cc / 8];
+      sc[i] = f16_to_f32_exact(sp[cc / 128]);
+    }
     const uint32_t os = t.row_ptr[n], oe = t.row_ptr[n + 1];
     const float* cent = s_cent + 16u * cent_table(t, n);
     float sm = 0.0f, rs = 0.0f, cm = 0.0f;
@@ -269,10 +297,15 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
 #pragma unroll
     for (int i = 0; i < 16; ++i) cm = fmaxf(cm, fabsf(cent[i]));
     s = row_scale(wave_max(sm) * cm + wave_add(rs));
-    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int j = 0; j < 32; ++j) w[j] = k0 + j < K ? sc * cent[(wd[j >> 3] >> ((j & 7) * 4)) & 0xfu] : 0.0f;
-    if (live) store32<true>(w, s, hi, lo, k0);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = c0 + 512 * i;
+      if (c >= KP) continue;
+      float w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = c + j < K ? sc[i] * cent[(wd[i] >> (4 * j)) & 0xfu] : 0.0f;
+      store8<true>(w, s, hi, lo, c);
+    }
     // CSR residuals of this segment's columns (codebook.rs:316-333): the lane
     // holding a column's first entry rebuilds the column from sc * cent[q] and
     // adds its residuals in CSR order, over the halves stored above.  A row
