@@ -199,6 +199,27 @@ def test_gemv_q8_many_rows_small_batch(eng, cols):
             assert max_rel(y[i], yref, q8_floor(m, X[i])) <= 1e-3, (M, i)
 
 
+@pytest.mark.parametrize("M", [5, 6, 7, 8])
+def test_gemv_q8_mfma_batch_edges(eng, M):
+    """Q8 x bf16 at M = 5..8, cols % 8 == 0 and K <= 2048 (the MFMA kernel):
+    row counts off the 16-row tile, cols off the 32-column block (pieces past
+    cols read as zero), odd block counts (a pair without its second block),
+    and more waves than block pairs (cols <= 96)."""
+    for rows, cols in [(1, 8), (5, 40), (37, 136), (16, 96), (300, 2048), (77, 1032), (4099, 2048)]:
+        m = synth.make_q8(rows, cols, seed=rows + cols + M)
+        t = eng.upload_packed(m)
+        xb = synth.make_x_bf16(M, cols, seed=cols + 7 * M)
+        X = bf16_bits_to_f32(xb).reshape(M, cols)
+        yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+        yref = gemv_ref(m, X)
+        fl = floor_scale(oracle.decode_rows(m), X)
+        assert max_rel(yf, yref, fl) <= 1e-3, (rows, cols)
+        assert_bf16_close(yb, yref, fl)
+        yf2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        assert np.array_equal(yf.view(np.uint32), yf2.view(np.uint32)), "run-to-run bits"
+
+
 def test_gemv_deterministic_and_grouping_invariant(eng):
     for kind in ("cb4", "g64", "q8"):
         m = make(kind, 17, 513, seed=3)

@@ -777,6 +777,183 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_lds_kernel(DevTensor t, co
   }
 }
 
+// ---------------------------------------------------------------------------
+// Q8 weights x bf16 activations at M = 5..8 on MFMA.
+//
+// v_mfma_f32_16x16x32_bf16 with the activations as the A operand (rows =
+// tokens; rows past M are zero) and 16 weight rows as the B operand.  An int8
+// weight is exact in bf16, so every product is exact and two MFMAs sum one
+// Q8 block (32 columns) of 16 rows for every token in fp32; the lane's output
+// column is one weight row, so the block scale is applied per lane as
+// acc += d * block (gguf.rs:223-229: w = q * d).  The dot2 kernels spend one
+// VALU instruction per column pair per token; here a block costs its int8 ->
+// bf16 conversion and four FMAs per lane whatever M is.
+//
+// Lane l (row c = l % 16 of the tile, group g = l / 16) loads 16 weight bytes
+// and 16 activations at column 64 p + 16 g of a block pair p, so each load
+// instruction reads 64 contiguous bytes of 16 weight rows.  Groups 0-1 then
+// hold block 2p, groups 2-3 block 2p + 1: each block's MFMAs take the
+// activations of its own groups and zeros in the others (the k slots of one
+// MFMA must share a block scale).  The tile's block scales are staged in LDS
+// by coalesced loads.  A workgroup is WAVES waves over the same 16 rows, each
+// summing a contiguous range of block pairs with all loads of up to
+// kQ8MfmaPairs pairs issued before the first MFMA; the waves' fragments are
+// added in LDS in wave order, so the result does not depend on timing.
+// D register i holds token 4 g + i of weight row row0 + c.  Requires 16-byte
+// aligned activation rows (cols % 8 == 0 and an aligned x) and at most
+// 4 x DI x WAVES scales per row (kQ8MfmaMaxNb).
+constexpr int kQ8MfmaPairs = 8;
+
+// Block scales per row the staging loop covers: DI loads per thread.
+template <int WAVES, int DI>
+constexpr uint32_t kQ8MfmaMaxNb = (uint32_t)DI * WAVES * 4u;
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// Eight int8 weights (two dwords) as eight bf16 (exact).
+__device__ __forceinline__ bf16x8_t q8_bf16x8(uint32_t a, uint32_t b) {
+  const uint32_t wd[2] = {a, b};
+  u32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t w = wd[j >> 1];
+    const int sh = (j & 1) * 16;
+    const float lo = (float)(int8_t)((w >> sh) & 0xffu);
+    const float hi = (float)(int8_t)((w >> (sh + 8)) & 0xffu);
+    r[j] = __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+  }
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+template <int WAVES, int DI>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma_kernel(DevTensor t, const uint16_t* __restrict__ x,
+                                                                 void* __restrict__ y, uint32_t M_rt,
+                                                                 uint32_t y_bf16) {
+  __shared__ f32x4_t s_red[WAVES][32];
+  __shared__ uint16_t s_d[16 * kQ8MfmaMaxNb<WAVES, DI>];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // in SGPRs: pair ranges and guards are scalar
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t nb = kp / 32, np = (nb + 1) / 2;
+  const uint32_t row0 = blockIdx.x * 16;
+  const uint32_t c16 = lane & 15, grp = lane >> 4;
+  const bool lo_half = grp < 2;   // groups 0-1: first block of a pair
+
+  // The tile's scales (rows row0.., contiguous in the plane), clamped loads first.
+  const uint32_t dn = 16 * nb, dlast = rows * nb - 1;
+  uint16_t dv[DI];
+#pragma unroll
+  for (int i = 0; i < DI; ++i) {
+    const uint32_t j = tid + (uint32_t)i * (WAVES * 64);
+    const uint32_t idx = row0 * nb + j;
+    dv[i] = t.p1[idx < dlast ? idx : dlast];
+  }
+
+  const uint32_t row = row0 + c16 < rows ? row0 + c16 : rows - 1;
+  const bool tok_live = c16 < M_rt;
+  const uint16_t* xr = x + (size_t)(tok_live ? c16 : 0) * cols;
+  const uint8_t* wr = static_cast<const uint8_t*>(t.p0) + (size_t)row * kp;
+  const uint32_t p_begin = wave * np / WAVES, p_end = (wave + 1) * np / WAVES;   // uniform per wave
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  bool staged = false;
+  for (uint32_t p0 = p_begin; p0 < p_end; p0 += kQ8MfmaPairs) {
+    u32x4 wv[kQ8MfmaPairs], xa[kQ8MfmaPairs], xb[kQ8MfmaPairs];
+#pragma unroll
+    for (int i = 0; i < kQ8MfmaPairs; ++i) {   // clamped, unconditional loads
+      const uint32_t p = p0 + i < p_end ? p0 + i : p_end - 1;
+      const uint32_t k = p * 64 + 16 * grp;
+      // A missing second block (odd nb) re-reads the first block's bytes; its
+      // activations are past cols (zero) and its scale is never applied.
+      wv[i] = *reinterpret_cast<const u32x4*>(wr + (k < kp ? k : k - 32));
+      xa[i] = *reinterpret_cast<const u32x4*>(xr + (k < cols ? k : cols - 8));
+      xb[i] = *reinterpret_cast<const u32x4*>(xr + (k + 8 < cols ? k + 8 : cols - 8));
+    }
+    if (!staged) {   // first batch only (uniform): scales to LDS behind the loads above
+#pragma unroll
+      for (int i = 0; i < DI; ++i) {
+        const uint32_t j = tid + (uint32_t)i * (WAVES * 64);
+        if (j < dn) s_d[j] = dv[i];
+      }
+      lds_barrier();
+      staged = true;
+    }
+#pragma unroll
+    for (int i = 0; i < kQ8MfmaPairs; ++i) {
+      const uint32_t p = p0 + i;
+      if (p >= p_end) continue;   // uniform
+      const uint32_t k = p * 64 + 16 * grp;   // activation pieces past cols (or padding tokens) are zero
+      const u32x4 va = tok_live && k < cols ? xa[i] : z, vb = tok_live && k + 8 < cols ? xb[i] : z;
+      const bf16x8_t wlo = q8_bf16x8(wv[i].x, wv[i].y), whi = q8_bf16x8(wv[i].z, wv[i].w);
+      const bf16x8_t a0 = __builtin_bit_cast(bf16x8_t, lo_half ? va : z);
+      const bf16x8_t a1 = __builtin_bit_cast(bf16x8_t, lo_half ? vb : z);
+      const bf16x8_t a2 = __builtin_bit_cast(bf16x8_t, lo_half ? z : va);
+      const bf16x8_t a3 = __builtin_bit_cast(bf16x8_t, lo_half ? z : vb);
+      const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+      f32x4_t b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, wlo, zero, 0, 0, 0);
+      b0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, whi, b0, 0, 0, 0);
+      f32x4_t b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2, wlo, zero, 0, 0, 0);
+      b1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a3, whi, b1, 0, 0, 0);
+      const float d0 = f16_to_f32(s_d[c16 * nb + 2 * p]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += d0 * b0[r];
+      if (2 * p + 1 < nb) {   // uniform
+        const float d1 = f16_to_f32(s_d[c16 * nb + 2 * p + 1]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[r] += d1 * b1[r];
+      }
+    }
+  }
+  if (!staged) {   // a wave with no pairs still takes part in the staging barrier
+#pragma unroll
+    for (int i = 0; i < DI; ++i) {
+      const uint32_t j = tid + (uint32_t)i * (WAVES * 64);
+      if (j < dn) s_d[j] = dv[i];
+    }
+    lds_barrier();
+  }
+  // Lanes 0..31 hold tokens 0..7 (4 g + i for g = 0, 1).
+  if (lane < 32) s_red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && lane < 32) {
+    f32x4_t v = s_red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) {
+      const f32x4_t o = s_red[w][lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] += o[r];
+    }
+    const uint32_t n = row0 + c16;
+    if (n < rows) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t m = 4 * grp + r;
+        if (m < M_rt) {
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * rows + n] = f32_to_bf16(v[r]);
+          else
+            static_cast<float*>(y)[(size_t)m * rows + n] = v[r];
+        }
+      }
+    }
+  }
+}
+
+// Used for M = 5..8 with K <= 2048 (launch_kind).  Measured on MI355X against
+// the dot2 kernels, M = 8: 1570 vs 1113 GB/s at K x N = 2048 x 6144, 3110 vs
+// 2307 for the 151936-row LM head, level at 2048 x 2048; behind at M = 4
+// (the MFMA cost does not shrink with M) and at K = 6144 x N = 2048, where
+// 128 row tiles leave most CUs idle (987 vs 1089 GB/s on 4 waves, 1023 on 8).
+template <int WAVES, int DI>
+hipError_t launch_q8_mfma_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  if (m > 8 || t.cols % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.kp / 32 > kQ8MfmaMaxNb<WAVES, DI>)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_q8_mfma_kernel<WAVES, DI>), dim3((t.rows + 15) / 16), dim3(WAVES * 64), 0, s, t,
+                     static_cast<const uint16_t*>(x), y, m, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
 // Grid for the persistent kernel: enough workgroups to fill every CU at the
 // occupancy the LDS footprint allows, never more than there are row blocks.
 template <int MT, int RPW, int WAVES, int NS>
@@ -867,6 +1044,8 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   if constexpr (KIND == KIND_Q8) {
     if (x_bf16 && m >= 2) {
       if (m == 2) return launch_q8_dot2_m<2>(t, x, m, y, y_bf16, s);
+      if (m > 4 && t.cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.kp / 32 <= kQ8MfmaMaxNb<4, 4>)
+        return launch_q8_mfma_t<4, 4>(t, x, m, y, y_bf16, s);
       if (m <= 4) return launch_q8_dot2_m<4>(t, x, m, y, y_bf16, s);
       if (m <= 8) return launch_q8_dot2_m<8>(t, x, m, y, y_bf16, s);
       return hipErrorInvalidValue;
