@@ -6,7 +6,10 @@
 // + beta * D, both operands K-contiguous.  Column-major, that is
 // D^T (N x M) = op_T(B as K x N) * (A as K x M): hipBLASLt's "TN" case.
 // Handles are per device; the descriptors and the heuristic's first
-// algorithm are cached per shape.  No workspace is offered to the library, so
+// algorithm are cached per shape.  A call can also split K into `batch`
+// equal slices run as one strided batch (slice b of A and B starts b * K
+// columns in, its D is the b-th M x N block), so a product with few output
+// tiles still fills the GPU; the caller adds the blocks.  No workspace is offered to the library, so
 // the algorithms it picks never clear one (a clearing node recorded into a
 // captured graph is not replayed reliably on this platform).
 #include <hip/hip_runtime.h>
@@ -26,7 +29,7 @@ struct Entry {
   hipblasLtMatmulAlgo_t algo{};
 };
 
-using Key = std::tuple<int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;   // device, M, N, K, lda, ldb
+using Key = std::tuple<int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t>;   // device, M, N, K, lda, ldb, batch
 
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
@@ -41,8 +44,8 @@ hipError_t status(hipblasStatus_t st) {
 // The cached entry for this shape on the current device (created on first
 // use, outside any capture: the caller's eager call sizes the workspace
 // before a capture is allowed).
-hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb, hipblasLtHandle_t* h,
-                     const Entry** out) {
+hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, uint32_t ldb, uint32_t batch,
+                     hipblasLtHandle_t* h, const Entry** out) {
   std::lock_guard<std::mutex> lk(g_mu);
   auto hi = g_handles.find(dev);
   if (hi == g_handles.end()) {
@@ -52,7 +55,7 @@ hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, 
     hi = g_handles.emplace(dev, nh).first;
   }
   *h = hi->second;
-  const Key key{dev, M, N, K, lda, ldb};
+  const Key key{dev, M, N, K, lda, ldb, batch};
   auto it = g_entries.find(key);
   if (it != g_entries.end()) {
     *out = &it->second;
@@ -69,6 +72,18 @@ hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, 
   if (e == hipSuccess) e = status(hipblasLtMatrixLayoutCreate(&en.la, HIP_R_16F, K, N, ldb));   // weights
   if (e == hipSuccess) e = status(hipblasLtMatrixLayoutCreate(&en.lb, HIP_R_16F, K, M, lda));   // activations
   if (e == hipSuccess) e = status(hipblasLtMatrixLayoutCreate(&en.ld, HIP_R_32F, N, M, N));
+  if (batch > 1) {
+    const int32_t bc = (int32_t)batch;
+    const int64_t kstride = K, dstride = (int64_t)M * N;
+    for (hipblasLtMatrixLayout_t l : {en.la, en.lb, en.ld}) {
+      const int64_t stride = l == en.ld ? dstride : kstride;
+      if (e == hipSuccess)
+        e = status(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_BATCH_COUNT, &bc, sizeof(bc)));
+      if (e == hipSuccess)
+        e = status(hipblasLtMatrixLayoutSetAttribute(l, HIPBLASLT_MATRIX_LAYOUT_STRIDED_BATCH_OFFSET, &stride,
+                                                     sizeof(stride)));
+    }
+  }
   hipblasLtMatmulPreference_t pref = nullptr;
   if (e == hipSuccess) e = status(hipblasLtMatmulPreferenceCreate(&pref));
   const uint64_t no_ws = 0;
@@ -95,16 +110,17 @@ hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, 
 
 }  // namespace
 
-// D[M][N] (f32, row-major) = alpha * A[M][K] * B[N][K]^T + beta * D; A and B
-// f16 row-major with row strides lda, ldb (elements).
+// D_b[M][N] (f32, row-major; block b at D + b * M * N) = alpha * A_b[M][K] *
+// B_b[N][K]^T + beta * D_b for b < batch, where A_b and B_b are the columns
+// [b K, (b + 1) K) of A and B (f16 row-major, row strides lda, ldb elements).
 hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
-                            uint32_t K, float alpha, float beta, float* D, hipStream_t s) {
+                            uint32_t K, uint32_t batch, float alpha, float beta, float* D, hipStream_t s) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   hipblasLtHandle_t h = nullptr;
   const Entry* en = nullptr;
-  e = entry_for(dev, M, N, K, lda, ldb, &h, &en);
+  e = entry_for(dev, M, N, K, lda, ldb, batch, &h, &en);
   if (e != hipSuccess) return e;
   return status(hipblasLtMatmul(h, en->op, &alpha, B, en->la, A, en->lb, &beta, D, en->ld, D, en->ld, &en->algo,
                                 nullptr, 0, s));

@@ -42,7 +42,7 @@ namespace vxt {
 hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
                               bool y_bf16, hipStream_t s);
 hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
-                            uint32_t K, float alpha, float beta, float* D, hipStream_t s);
+                            uint32_t K, uint32_t batch, float alpha, float beta, float* D, hipStream_t s);
 
 namespace gp {
 
@@ -595,6 +595,7 @@ struct Plan {
   int bm, bn, wmode;
   bool lib;   // dense phase on the vendor library (gemm_blas.cpp)
   uint32_t kp, splits, kt_per_split;
+  uint32_t lib_splits;   // K slices of the library call (one strided batch)
   size_t panel_plane, dsc_bytes, panel_bytes, a_plane, a_bytes, partial_bytes;
 };
 
@@ -623,9 +624,20 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   pl.a_plane = al256((size_t)m * pl.kp * 2);
   pl.a_bytes = pl.a_plane * (x_bf16 ? 1 : 2);
   pl.partial_bytes = pl.splits > 1 ? al256((size_t)pl.splits * m * t.rows * 4) : 0;
-  // Library: fp32 D [M][N] (also room for the own kernel's partial sums, its
+  // Library: for products of fewer than 128 output tiles of 128 x 128, K
+  // slices until ~256 tiles are in flight, each slice at least 1024 columns
+  // and a whole number of K tiles (at 512 x 6144 outputs, 192 tiles, two
+  // slices measured slower than none); fp32 D
+  // [lib_splits][M][N] (also room for the own kernel's partial sums, its
   // fallback when the library offers no algorithm for a shape).
-  if (lib) pl.partial_bytes = std::max(pl.partial_bytes, al256((size_t)m * t.rows * 4));
+  pl.lib_splits = 1;
+  if (lib) {
+    const uint32_t tiles128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
+    while (tiles128 < 128 && tiles128 * pl.lib_splits < 256 && pl.kp / (pl.lib_splits * 2) >= 1024 &&
+           pl.kp % (pl.lib_splits * 2 * BK) == 0)
+      pl.lib_splits *= 2;
+    pl.partial_bytes = std::max(pl.partial_bytes, al256((size_t)pl.lib_splits * m * t.rows * 4));
+  }
   return pl;
 }
 
@@ -667,10 +679,12 @@ hipError_t launch_dense_m(const Panel& p, const uint16_t* ah, const uint16_t* al
 
 // The dense phase on the vendor library: D = sum of f16 GEMMs over the
 // hi/lo planes present (lo terms scaled by 2^-11; lo x lo dropped, as in
-// dense_kernel), then Y = D / s through reduce_kernel with one split.
-// hipErrorNotSupported when the library has no algorithm for the shape.
+// dense_kernel), each as one strided batch over `splits` K slices, then
+// Y = (sum of the slices' D) / s through reduce_kernel (slices added in
+// ascending order).  hipErrorNotSupported when the library has no
+// algorithm for the shape.
 hipError_t library_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, bool split_a, int wmode, uint32_t m,
-                         uint32_t n, void* y, bool y_bf16, float* d, hipStream_t s) {
+                         uint32_t n, uint32_t splits, void* y, bool y_bf16, float* d, hipStream_t s) {
   struct Term { const uint16_t* a; const uint16_t* b; float alpha; };
   Term terms[3];
   int nt = 0;
@@ -678,11 +692,11 @@ hipError_t library_dense(const Panel& p, const uint16_t* ah, const uint16_t* al,
   if (wmode == kWHiLo) terms[nt++] = {ah, p.lo, kLoInv};
   if (split_a) terms[nt++] = {al, p.hi, kLoInv};
   for (int i = 0; i < nt; ++i) {
-    const hipError_t e = blas_gemm_f16_tn(terms[i].a, p.kp, terms[i].b, p.kp, m, n, p.kp, terms[i].alpha,
-                                          i == 0 ? 0.0f : 1.0f, d, s);
+    const hipError_t e = blas_gemm_f16_tn(terms[i].a, p.kp, terms[i].b, p.kp, m, n, p.kp / splits, splits,
+                                          terms[i].alpha, i == 0 ? 0.0f : 1.0f, d, s);
     if (e != hipSuccess) return e;
   }
-  return launch_gemm_reduce(d, 1, p.inv, m, n, y, y_bf16, s);
+  return launch_gemm_reduce(d, splits, p.inv, m, n, y, y_bf16, s);
 }
 
 template <uint32_t KIND>
@@ -716,7 +730,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (pl.lib) {
-    e = library_dense(p, ah, al, !x_bf16, pl.wmode, m, t.rows, y, y_bf16, partial, s);
+    e = library_dense(p, ah, al, !x_bf16, pl.wmode, m, t.rows, pl.lib_splits, y, y_bf16, partial, s);
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();   // no algorithm for this shape: the own dense kernel on the same panel
   }
@@ -764,19 +778,24 @@ static bool fused_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
 
 // Two-phase with the vendor dense GEMM: pinned, or automatically above the
 // fused kernel's batch limit when the product has at least 512 x 6144
-// outputs.  Measured (graph-timed, whole call, config 3): 1.2-1.3x faster
-// than dense_kernel at M = 512 x N = 6144 and M = 2048; slower for the
-// hi/lo kinds at M = 512 x N = 2048, a grid too small for the library
-// without a split-K workspace (none is offered, see gemm_blas.cpp).
+// outputs, or, for g64 (one panel plane), when K is long enough (>= 4096)
+// for the library call to be split into K slices that fill the GPU.
+// Measured (graph-timed, whole call, config 3): 1.2-1.3x faster than
+// dense_kernel at M = 512 x N = 6144 and M = 2048; g64 at 512 x 2048 x 6144
+// 295 -> 342 TFLOP/s with four K slices.  The hi/lo kinds stay on
+// dense_kernel there (two library GEMMs: Q8 223 -> 204, cb4 196 -> 192).
 constexpr size_t kLibMinOutputs = (size_t)512 * 6144;
+constexpr uint32_t kLibMinSplitK = 4096;
 
-static bool library_path(uint32_t m, uint32_t n, int mode) {
-  return mode == kGemmLibrary || (mode == kGemmAuto && m > kFusedMaxM && (size_t)m * n >= kLibMinOutputs);
+static bool library_path(const DevTensor& t, uint32_t m, int mode) {
+  if (mode == kGemmLibrary) return true;
+  if (mode != kGemmAuto || m <= kFusedMaxM) return false;
+  return (size_t)m * t.rows >= kLibMinOutputs || (t.kind == KIND_G64 && t.cols >= kLibMinSplitK);
 }
 
 size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
   if (fused_path(t, m, x_bf16, mode)) return gemm_fused_workspace_bytes(t, m);
-  const gp::Plan pl = gp::plan(t, m, x_bf16, library_path(m, t.rows, mode));
+  const gp::Plan pl = gp::plan(t, m, x_bf16, library_path(t, m, mode));
   return pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
 }
 
@@ -785,7 +804,7 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   if (m == 0 || (size_t)m * t.rows > (size_t)1 << 40) return hipErrorInvalidValue;
   if (fused_path(t, m, x_bf16, mode))
     return launch_gemm_fused(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
-  const bool lib = library_path(m, t.rows, mode);
+  const bool lib = library_path(t, m, mode);
   switch (t.kind) {
     case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
     case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);

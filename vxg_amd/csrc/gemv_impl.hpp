@@ -841,12 +841,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma_kernel(DevTensor t, c
   const bool lo_half = grp < 2;   // groups 0-1: first block of a pair
 
   // The tile's scales (rows row0.., contiguous in the plane), clamped loads first.
-  const uint32_t dn = 16 * nb, dlast = rows * nb - 1;
+  const uint32_t dn = 16 * nb;
+  const size_t dlast = (size_t)rows * nb - 1;
   uint16_t dv[DI];
 #pragma unroll
   for (int i = 0; i < DI; ++i) {
-    const uint32_t j = tid + (uint32_t)i * (WAVES * 64);
-    const uint32_t idx = row0 * nb + j;
+    const size_t idx = (size_t)row0 * nb + tid + (uint32_t)i * (WAVES * 64);
     dv[i] = t.p1[idx < dlast ? idx : dlast];
   }
 
