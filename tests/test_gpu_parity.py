@@ -474,24 +474,29 @@ def test_gemm_library_dense_phase(eng, kind, M, N, K, xdt):
 
 
 def test_gemm_library_in_captured_graph():
-    """The library dense phase records into a graph; every replay (with eager
-    work and synchronisation between replays) matches the eager result."""
+    """The library dense phase (pinned) records into a graph, also as a strided
+    batch over K slices (K = 4096 at 300 x 640: four slices); every replay
+    (with eager work and synchronisation between replays) matches the eager
+    result."""
     e = engine.HipEngine()
+    e.set_gemm_path(engine.GEMM_LIBRARY)
     try:
-        for kind in ("g64", "cb4"):
-            m = make(kind, 640, 1024, seed=12)
+        for kind, cols, M in (("g64", 1024, 512), ("cb4", 1024, 512), ("g64", 4096, 300), ("q8", 4096, 300)):
+            m = make(kind, 640, cols, seed=12)
             t = e.upload_packed(m)
-            xd = e.to_device(synth.make_x_bf16(512, 1024, seed=13))
-            yd = e.alloc(512 * 640 * 2)
-            e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 512, yd.ptr, engine.DTYPE_BF16, e.stream)
+            xd = e.to_device(synth.make_x_bf16(M, cols, seed=13))
+            yd = e.alloc(M * 640 * 2)
+            e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, M, yd.ptr, engine.DTYPE_BF16, e.stream)
             e.synchronize()
-            ref = yd.download(np.uint16, (512, 640))
-            g = e.capture(lambda s: e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 512, yd.ptr, engine.DTYPE_BF16, s))
+            ref = yd.download(np.uint16, (M, 640))
+            X = bf16_bits_to_f32(synth.make_x_bf16(M, cols, seed=13)).reshape(M, cols)
+            assert_bf16_close(ref, gemv_ref(m, X), floor_scale(oracle.decode_rows(m), X))
+            g = e.capture(lambda s: e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, M, yd.ptr, engine.DTYPE_BF16, s))
             for rep in range(3):
-                yd.upload(np.full((512, 640), 0x7FC0, np.uint16))
+                yd.upload(np.full((M, 640), 0x7FC0, np.uint16))
                 g.launch(1)
-                assert np.array_equal(yd.download(np.uint16, (512, 640)), ref), (kind, rep)
-                e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 512, yd.ptr, engine.DTYPE_BF16, e.stream)
+                assert np.array_equal(yd.download(np.uint16, (M, 640)), ref), (kind, cols, rep)
+                e.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, M, yd.ptr, engine.DTYPE_BF16, e.stream)
                 e.synchronize()
             g.free()
             t.free()
