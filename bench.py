@@ -227,12 +227,11 @@ def _free_layers(lw):
 
 
 def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: int = 2048,
-                ffn: int = 6144, seed: int = 40, persistent: bool = False):
+                ffn: int = 6144, seed: int = 40):
     """Config 4: tokens/s of the decode-step linear stack (matmul-only path).
 
     The layers of ``_stack_layers`` then the Q8 LM head.  One token is
-    captured as a HIP graph (or, ``persistent``, recorded as one persistent
-    launch); ``tokens`` replays are timed.
+    captured as a HIP graph; ``tokens`` replays are timed.
     """
     from vxg_amd import stack, synth
     lw, nbytes = _stack_layers(eng, kind, layers, hidden, ffn, seed)
@@ -247,10 +246,10 @@ def bench_stack(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: i
     for _ in range(3):
         st.enqueue()
     eng.synchronize()
-    runner = st.persistent() if persistent else st.capture()
-    (runner.run if persistent else runner.launch)(3)
+    runner = st.capture()
+    runner.launch(3)
     t0 = time.perf_counter()
-    ev_ms = (runner.run if persistent else runner.launch)(tokens)
+    ev_ms = runner.launch(tokens)
     wall = time.perf_counter() - t0
     runner.free()
     st.free()
@@ -475,10 +474,10 @@ def main():
                     log(f"  config 3 {kind} M={M} K={K} N={N}: {rg['TFLOPs']:.1f} TFLOP/s")
     if "4" in run:
         head_m = synth.make_q8(151936, 2048, seed=5)
-        for kind, pers in (("g64", False), ("cb4", False), ("g64", True), ("cb4", True)):
-            how = "one persistent launch per token" if pers else "HIP graph of 97 launches per token"
+        for kind in ("g64", "cb4"):
+            how = "HIP graph of 97 launches per token"
             log(f"config 4: decode stack, 24 layers {kind} + Q8 LM head, {how}")
-            rs = bench_stack(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)), persistent=pers)
+            rs = bench_stack(eng, kind, head_m, tokens=max(20, min(200, args.steps // 2)))
             secondary.append({"config": f"4: decode stack 24x{{[q;k;v],o,[gate;up],down}} {kind} + q8 head, M=1, "
                                         f"{how}",
                               "tokens_per_s": round(rs["tokens_per_s"], 1),

@@ -455,46 +455,6 @@ VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
 #define VXT_GEMM_LIBRARY 3u
 VXT_API int vxt_hip_set_gemm_path(void* ctx, uint32_t path);
 
-/* ---- decode-step chain: one persistent launch per token ------------------ */
-
-/* One projection of a chain: y (device, [rows], y_dtype) = W x for x
- * (device, bf16 [cols]).  Ops run in order; an op may read the output of any
- * earlier op. */
-typedef struct VxtHipChainOp {
-    void* tensor;          /* uploaded tensor, padded cols <= 6144          */
-    const void* x;         /* device, bf16                                  */
-    void* y;               /* device                                        */
-    uint32_t y_dtype;      /* VXT_DTYPE_F32 or VXT_DTYPE_BF16               */
-    uint32_t reserved;
-} VxtHipChainOp;
-
-/* Records the matmuls of one decode step for a single cooperative launch per
- * run (the batch-1 step of the reference's device runner,
- * vxt_metal_cb4_fast_step_batch, metal_cb4_fast_ffi.rs:151-162, restricted to
- * its projections).  Pointers are captured: buffers must outlive the chain. */
-VXT_API void* vxt_hip_chain_create(void* ctx, const VxtHipChainOp* ops, uint32_t n_ops, char* err,
-                           size_t err_cap);
-
-/* `runs` back-to-back launches on the context stream; waits, returns the GPU
- * time of all runs, and fails with VXT_E_DEVICE if a wait gave up. */
-VXT_API int vxt_hip_chain_run(void* chain, uint32_t runs, double* gpu_ms, char* err, size_t err_cap);
-
-/* One launch on `stream` (NULL = context stream), asynchronous.  Not
- * capturable.  Replaces vxt_metal_cb4_fast_enqueue_async (:188-197). */
-VXT_API int vxt_hip_chain_enqueue(void* chain, void* stream, char* err, size_t err_cap);
-
-/* Waits for the device; VXT_E_DEVICE if a wait of any launch since the last
- * check gave up (then those outputs are invalid).  Replaces
- * vxt_metal_cb4_fast_wait_cmd (:198-199). */
-VXT_API int vxt_hip_chain_status(void* chain, char* err, size_t err_cap);
-
-/* Polls (about 1 us each) before a wait gives up; default 2,000,000.  No
- * counterpart in the reference: a host-side bound on the kernel's waits. */
-VXT_API int vxt_hip_chain_set_spin_limit(void* chain, uint32_t polls, char* err, size_t err_cap);
-
-/* Frees the chain (after waiting for the device). */
-VXT_API void vxt_hip_chain_free(void* chain);
-
 #ifdef __cplusplus
 }
 #endif

@@ -299,116 +299,3 @@ def test_decode_step_shape_checks(eng):
     other.free()
     w.free()
     st.free()
-
-
-# ---------------------------------------------------------------- persistent chain
-
-@pytest.mark.parametrize("kind", ["cb4", "g64"])
-def test_chain_matches_per_projection_launches(eng, kind):
-    """One persistent launch per token gives the per-projection results bit for bit."""
-    st, _, head = small_stack(eng, kind, 3, seed=11)
-    st.set_input(synth.make_x_bf16(1, st.hidden, seed=6)[0])
-    st.enqueue()
-    eng.synchronize()
-    ref = st.logits.download(np.float32, head.rows)
-    ref_dn = st.dn_out.download(np.uint16, st.hidden)
-    ch = st.persistent()
-    for runs in (1, 1, 5):
-        st.logits.upload(np.full(head.rows, np.nan, np.float32))
-        ch.run(runs)
-        assert np.array_equal(st.logits.download(np.float32, head.rows).view(np.uint32), ref.view(np.uint32))
-        assert np.array_equal(st.dn_out.download(np.uint16, st.hidden), ref_dn)
-    ch.free()
-    st.free()
-
-
-def test_chain_ragged_ops(eng):
-    """Independent and dependent ops of every kind at ragged shapes, vs per-op launches."""
-    specs = [("cb4", 37, 100), ("q8", 300, 100), ("g64", 129, 300), ("cb4", 64, 2050), ("q8", 5, 6144),
-             ("g64", 1000, 5)]
-    ops, refs, outs = [], [], []
-    bufs = []
-    for i, (kind, rows, cols) in enumerate(specs):
-        m = synth.make_cb4(rows, cols, seed=i, outlier_frac=0.05) if kind == "cb4" else make(kind, rows, cols, seed=i)
-        t = eng.upload_packed(m)
-        xd = eng.to_device(synth.make_x_bf16(1, cols, seed=40 + i)[0])
-        ydt = engine.DTYPE_BF16 if i % 2 else engine.DTYPE_F32
-        yd = eng.alloc(rows * 4)
-        eng.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 1, yd.ptr, ydt, eng.stream)
-        eng.synchronize()
-        dt = np.uint16 if ydt == engine.DTYPE_BF16 else np.float32
-        refs.append(yd.download(dt, rows))
-        outs.append((yd, dt, rows))
-        ops.append((t, xd.ptr, yd.ptr, ydt))
-        bufs += [t, xd, yd]
-    # a dependent tail: reads op 2's f32 output? (bf16 x only) -> read op 1's bf16 output
-    m = synth.make_g64(77, 300, seed=99)
-    t = eng.upload_packed(m)
-    yd = eng.alloc(77 * 4)
-    ops.append((t, outs[1][0].ptr, yd.ptr, engine.DTYPE_F32))
-    eng.matmul_dev(t, outs[1][0].ptr, engine.DTYPE_BF16, 1, yd.ptr, engine.DTYPE_F32, eng.stream)
-    eng.synchronize()
-    refs.append(yd.download(np.float32, 77))
-    outs.append((yd, np.float32, 77))
-    ch = eng.chain(ops)
-    for yd_, dt, rows in outs:
-        yd_.upload(np.full(rows, 0xFFFF if dt == np.uint16 else np.nan, dt))
-    ch.run(3)
-    for (yd_, dt, rows), ref in zip(outs, refs):
-        got = yd_.download(dt, rows)
-        assert np.array_equal(got.view(np.uint16 if dt == np.uint16 else np.uint32),
-                              ref.view(np.uint16 if dt == np.uint16 else np.uint32))
-    ch.free()
-
-
-def test_chain_many_residuals_per_row(eng):
-    """cb4 rows with more than 16 (and 64) residuals, duplicates included."""
-    m = synth.make_cb4(40, 2048, seed=5, outlier_frac=0.05)   # ~100 per row
-    t = eng.upload_packed(m)
-    xd = eng.to_device(synth.make_x_bf16(1, 2048, seed=5)[0])
-    yd = eng.alloc(40 * 4)
-    eng.matmul_dev(t, xd.ptr, engine.DTYPE_BF16, 1, yd.ptr, engine.DTYPE_F32, eng.stream)
-    eng.synchronize()
-    ref = yd.download(np.float32, 40)
-    ch = eng.chain([(t, xd.ptr, yd.ptr, engine.DTYPE_F32)])
-    yd.upload(np.full(40, np.nan, np.float32))
-    ch.run(1)
-    assert np.array_equal(yd.download(np.float32, 40).view(np.uint32), ref.view(np.uint32))
-    ch.free()
-
-
-def test_chain_bounded_wait_gives_up_cleanly(eng):
-    """A spin limit of 0 polls makes a wait give up at once: the run reports an
-    error (or completes if no wait had to spin), every wave exits, and the chain
-    works again afterwards."""
-    st, _, head = small_stack(eng, "g64", 2, seed=3)
-    st.set_input(synth.make_x_bf16(1, st.hidden, seed=2)[0])
-    st.enqueue()
-    eng.synchronize()
-    ref = st.logits.download(np.float32, head.rows)
-    ch = st.persistent()
-    ch.set_spin_limit(0)
-    try:
-        ch.run(2)
-    except engine.BackendError as e:
-        assert e.code == engine.VXT_E_DEVICE and "spin limit" in str(e)
-    ch.set_spin_limit(2_000_000)
-    ch.run(1)
-    assert np.array_equal(st.logits.download(np.float32, head.rows).view(np.uint32), ref.view(np.uint32))
-    ch.free()
-    st.free()
-
-
-def test_chain_errors(eng):
-    big = eng.upload_packed(synth.make_q8(4, 6176, seed=1))   # padded K > 6144
-    xd = eng.alloc(6176 * 2)
-    yd = eng.alloc(16)
-    with pytest.raises(engine.BackendError) as ei:
-        eng.chain([(big, xd.ptr, yd.ptr, engine.DTYPE_F32)])
-    assert ei.value.code == engine.VXT_E_SHAPE
-    ok = eng.upload_packed(synth.make_q8(4, 64, seed=1))
-    ch = eng.chain([(ok, xd.ptr, yd.ptr, engine.DTYPE_F32)])
-    with pytest.raises(engine.BackendError) as ei:
-        eng.capture(lambda s: ch.enqueue(s))
-    assert ei.value.code == engine.VXT_E_UNSUPPORTED
-    ch.free()

@@ -141,14 +141,25 @@ __device__ __forceinline__ void unpack_x(const XChunk<XBF16>& c, float (&xv)[kCh
   }
 }
 
-// Per-wave LDS slot for the g64 codebooks of one row-step: 32 pair tables
-// (32 bytes each) at a 48-byte stride.  64 lanes reading random entries of
-// 32 tables conflict heavily on LDS banks at a 32- or 64-byte stride; 48 is
-// the best of the strides measured (32..144).
-constexpr uint32_t kPairStride = 48;
-constexpr uint32_t kSlotBytes = 32 * kPairStride;
+// g64 codebooks in LDS, laid out so that no lookup conflicts on LDS banks:
+// each wave owns 4 KiB blocks of 16 x 64 words, and entry e of lane l's
+// table is word e * 64 + l of its block (the low half for one row, the high
+// half for the row after it).  The 64 lanes of a wave always read 64
+// different words in 64 different banks, whatever the indices; with one
+// table per pair of lanes at a fixed stride, random indices put up to ~4
+// lanes on one bank.  A table address is then byte 0 = 4 l (+2 for the high
+// half), byte 1 = 16 * block | q, which one v_perm_b32 assembles from the
+// nibble byte and the lane's base: a lookup costs one VALU operation.
+// Blocks must lie below 64 KiB of LDS and start 4 KiB aligned.
+constexpr uint32_t kTabBlock = 4096;
 
-typedef __attribute__((address_space(3))) _Float16 lds_half_t;
+// The g64 tables are stored and read through may_alias types: with plain
+// types (lookups _Float16, stores uint16_t), type-based alias analysis let the
+// compiler move lookups above the stores that fill the table.
+typedef uint16_t __attribute__((may_alias)) u16_alias_t;
+typedef uint32_t __attribute__((may_alias)) u32_alias_t;
+typedef __attribute__((address_space(3))) u16_alias_t lds_u16_t;
+typedef __attribute__((address_space(3))) u32_alias_t lds_u32a_t;
 typedef __attribute__((address_space(3))) float lds_float_t;
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -175,14 +186,47 @@ __device__ __forceinline__ void dequant_chunk(const WChunk<KIND>& c, uint32_t cb
       w[j] = *(lds_float_t*)(size_t)(base | off);
     }
   } else {
+    // slot = the lane's table address for this row: block + 4 lane (+2).
+    (void)lane;
     const uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
-    const uint32_t base = slot + (lane >> 1) * kPairStride;   // 16-byte aligned, low 5 bits clear below
+    const uint32_t lbyte = slot & 0xffu;
+    const uint32_t rep = ((slot >> 8) & 0xffu) * 0x01010101u;
 #pragma unroll
-    for (int j = 0; j < kChunk; ++j) {
-      const int sh = (j & 7) * 4 - 1;
-      const uint32_t off = sh < 0 ? ((wd[j >> 3] << 1) & 0x1eu) : ((wd[j >> 3] >> sh) & 0x1eu);
-      w[j] = (float)*(lds_half_t*)(size_t)(base + off);
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t we = (wd[i] & 0x0F0F0F0Fu) | rep;          // nibbles 0, 2, 4, 6 | block
+      const uint32_t wo = ((wd[i] >> 4) & 0x0F0F0F0Fu) | rep;   // nibbles 1, 3, 5, 7 | block
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t sel = 0x0c0c0000u | ((4u + k) << 8);   // [lane byte, nibble byte k, 0, 0]
+        w[8 * i + 2 * k] = f16_to_f32(*(lds_u16_t*)(size_t)__builtin_amdgcn_perm(we, lbyte, sel));
+        w[8 * i + 2 * k + 1] = f16_to_f32(*(lds_u16_t*)(size_t)__builtin_amdgcn_perm(wo, lbyte, sel));
+      }
     }
+  }
+}
+
+// Stores the g64 tables of one row (low halves) or two rows (`b`: high
+// halves) into block `blk`.  The two lanes of a 64-group each hold half of
+// the group's table (entries 8 (l & 1) ..) and each writes its half into both
+// lanes' columns, so no lane exchange is needed.
+__device__ __forceinline__ void store_g64_tables(uint32_t blk, uint32_t lane, const WChunk<KIND_G64>& a,
+                                                 const WChunk<KIND_G64>* b) {
+  const uint32_t half = (lane & 1u) * 2048u;                          // entries 8 (l & 1) .. : words 512 (l & 1) ..
+  lds_u32a_t* own = (lds_u32a_t*)(size_t)(blk + lane * 4u + half);    // word e of the column: own[64 e]
+  lds_u32a_t* other = (lds_u32a_t*)(size_t)(blk + (lane ^ 1u) * 4u + half);
+  const uint32_t A[4] = {a.lut.x, a.lut.y, a.lut.z, a.lut.w};
+  uint32_t B[4] = {0, 0, 0, 0};
+  if (b) {
+    B[0] = b->lut.x; B[1] = b->lut.y; B[2] = b->lut.z; B[3] = b->lut.w;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {   // entry 2j: low halves of A, B; entry 2j + 1: high halves
+    const uint32_t ev = b ? __builtin_amdgcn_perm(B[j], A[j], 0x05040100u) : A[j];
+    const uint32_t od = b ? __builtin_amdgcn_perm(B[j], A[j], 0x07060302u) : A[j] >> 16;
+    own[(2 * j) * 64] = ev;
+    own[(2 * j + 1) * 64] = od;
+    other[(2 * j) * 64] = ev;
+    other[(2 * j + 1) * 64] = od;
   }
 }
 
@@ -298,7 +342,9 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   static_assert(!NORM || (MT == 1 && XBF16), "the norm prologue serves one token with bf16 x");
   extern __shared__ __attribute__((aligned(16))) uint16_t s_xn[];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
-  __shared__ __attribute__((aligned(64))) uint4 s_slot[KIND == KIND_G64 ? kWaves * S * RPW * kSlotBytes / 16 : 1];
+  constexpr int NB = (RPW + 1) / 2;   // g64 table blocks per wave
+  static_assert(kWaves * NB * kTabBlock + kTabBlock <= 65536u, "g64 table blocks must stay below 64 KiB of LDS");
+  __shared__ __attribute__((aligned(KIND == KIND_G64 ? 4096 : 16))) uint32_t s_tab[KIND == KIND_G64 ? kWaves * NB * kTabBlock / 4 : 1];
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = threadIdx.x >> 6;
@@ -315,7 +361,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
     if (threadIdx.x < 48) s_cent[threadIdx.x] = t.cent[threadIdx.x];
     __syncthreads();
   }
-  const uint32_t slot = lds_addr(s_slot) + (KIND == KIND_G64 ? wave * S * RPW * kSlotBytes : 0);
+  const uint32_t tab = lds_addr(s_tab) + (KIND == KIND_G64 ? wave * NB * kTabBlock : 0);
 
   // cb4 residuals: each row's CSR bounds are requested before anything else
   // and each lane's first entry right after the first batch of weights, so
@@ -414,12 +460,14 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
             load_x_scalar<XBF16>(x, cols, (uint32_t)m < M_rt ? m : 0, k0, xv[m]);
         }
       }
+      if constexpr (KIND == KIND_G64) {   // this step's tables; a wave's LDS operations run in
+#pragma unroll                         // order, so the previous step's lookups are done first
+        for (int p = 0; p < NB; ++p)
+          store_g64_tables(tab + p * kTabBlock, lane, wc[s][2 * p], 2 * p + 1 < RPW ? &wc[s][2 * p + 1] : nullptr);
+      }
 #pragma unroll
       for (int r = 0; r < RPW; ++r) {
-        const uint32_t sl = slot + (s * RPW + r) * kSlotBytes;
-        if constexpr (KIND == KIND_G64)   // lane l holds half (l & 1) of pair table l >> 1
-          *(__attribute__((address_space(3))) u32x4*)(size_t)(sl + (lane >> 1) * kPairStride + (lane & 1) * 16) =
-              u32x4{wc[s][r].lut.x, wc[s][r].lut.y, wc[s][r].lut.z, wc[s][r].lut.w};
+        const uint32_t sl = tab + (r / 2) * kTabBlock + lane * 4u + (r & 1) * 2u;
         uint32_t cbase = 0;
         if constexpr (KIND == KIND_CB4) cbase = lds_addr(s_cent) + 64u * cent_table(t, rr[r]);
         float w[kChunk];

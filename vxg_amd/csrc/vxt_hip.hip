@@ -53,18 +53,6 @@ hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* ga
                                uint32_t pos0, uint32_t batch, void* ws, hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
-struct ChainLaunch {
-  const void* ops;
-  uint32_t n_ops;
-  uint32_t* counters;
-  uint32_t* status;
-};
-size_t chain_op_bytes();
-size_t chain_counter_bytes(uint32_t n_ops);
-uint32_t chain_max_k();
-void chain_fill_op(void* dst, const DevTensor& t, uint32_t nnz, const void* x, void* y, bool y_bf16);
-hipError_t chain_grid(uint32_t* grid);
-hipError_t chain_launch(const ChainLaunch& l, uint32_t grid, uint32_t epoch, uint32_t spin_limit, hipStream_t s);
 }  // namespace vxt
 
 namespace {
@@ -126,18 +114,6 @@ struct Graph {
   Ctx* ctx = nullptr;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-};
-
-// A decode-step chain: device op records, completion counters, status word.
-struct Chain {
-  Ctx* ctx = nullptr;
-  void* ops = nullptr;
-  uint32_t n_ops = 0;
-  uint32_t* counters = nullptr;
-  uint32_t* status = nullptr;
-  uint32_t grid = 0;
-  uint32_t epoch = 0;
-  uint32_t spin_limit = 2000000;   // polls of about 1 us: a wait gives up after ~2 s
 };
 
 // ---- error plumbing ---------------------------------------------------------
@@ -1114,138 +1090,5 @@ int vxt_hip_set_gemm_path(void* ctx, uint32_t path) {
   return VXT_OK;
 }
 
-
-// ---- decode-step chain -------------------------------------------------------
-
-namespace {
-
-void chain_reset(Chain* ch) {
-  VXT_HIP_CHECK(hipMemset(ch->counters, 0, vxt::chain_counter_bytes(ch->n_ops)));
-  VXT_HIP_CHECK(hipMemset(ch->status, 0, 4));
-  ch->epoch = 0;
-}
-
-void chain_enqueue_one(Chain* ch, hipStream_t s) {
-  if (ch->ctx->capturing) fail(VXT_E_UNSUPPORTED, "a chain launch cannot be captured into a graph");
-  if (ch->epoch >= (1u << 20)) {   // keep (epoch + 1) * counters-per-slot far from 2^32
-    VXT_HIP_CHECK(hipStreamSynchronize(s));
-    chain_reset(ch);
-  }
-  vxt::ChainLaunch l{ch->ops, ch->n_ops, ch->counters, ch->status};
-  const hipError_t e = vxt::chain_launch(l, ch->grid, ch->epoch, ch->spin_limit, s);
-  if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("chain launch failed: ") + hipGetErrorString(e));
-  ++ch->epoch;
-}
-
-}  // namespace
-
-void* vxt_hip_chain_create(void* ctx, const VxtHipChainOp* ops, uint32_t n_ops, char* err, size_t err_cap) {
-  Chain* out = nullptr;
-  guarded(err, err_cap, [&] {
-    Ctx* c = as_ctx(ctx);
-    if (!ops || n_ops == 0) fail(VXT_E_ARG, "a chain needs at least one op");
-    use_device(c);
-    int coop = 0;
-    VXT_HIP_CHECK(hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, c->device));
-    if (!coop) fail(VXT_E_UNSUPPORTED, "device does not support cooperative launches");
-    const size_t rec = vxt::chain_op_bytes();
-    std::vector<char> h(rec * n_ops, 0);
-    for (uint32_t i = 0; i < n_ops; ++i) {
-      Tensor* t = as_tensor(ops[i].tensor);
-      if (t->ctx != c) fail(VXT_E_ARG, "tensor belongs to another context");
-      if (!ops[i].x || !ops[i].y) fail(VXT_E_ARG, "null activation or output pointer");
-      if (!dtype_ok(ops[i].y_dtype)) fail(VXT_E_ARG, "unknown dtype");
-      if (t->kp > vxt::chain_max_k()) fail(VXT_E_SHAPE, "chain ops take at most 6144 (padded) input columns");
-      vxt::chain_fill_op(h.data() + rec * i, t->dev(), t->nnz, ops[i].x, ops[i].y,
-                         ops[i].y_dtype == VXT_DTYPE_BF16);
-    }
-    Chain* ch = new Chain();
-    ch->ctx = c;
-    ch->n_ops = n_ops;
-    try {
-      VXT_HIP_CHECK(hipMalloc(&ch->ops, h.size()));
-      VXT_HIP_CHECK(hipMemcpy(ch->ops, h.data(), h.size(), hipMemcpyHostToDevice));
-      VXT_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&ch->counters), vxt::chain_counter_bytes(n_ops)));
-      VXT_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&ch->status), 256));
-      chain_reset(ch);
-      const hipError_t e = vxt::chain_grid(&ch->grid);
-      if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("chain occupancy query failed: ") + hipGetErrorString(e));
-    } catch (...) {
-      if (ch->ops) (void)hipFree(ch->ops);
-      if (ch->counters) (void)hipFree(ch->counters);
-      if (ch->status) (void)hipFree(ch->status);
-      delete ch;
-      throw;
-    }
-    out = ch;
-  });
-  return out;
-}
-
-int vxt_hip_chain_run(void* chain, uint32_t runs, double* gpu_ms, char* err, size_t err_cap) {
-  return guarded(err, err_cap, [&] {
-    if (!chain) fail(VXT_E_ARG, "null chain handle");
-    Chain* ch = static_cast<Chain*>(chain);
-    Ctx* c = ch->ctx;
-    if (runs == 0) fail(VXT_E_ARG, "runs must be >= 1");
-    use_device(c);
-    VXT_HIP_CHECK(hipEventRecord(c->ev0, c->stream));
-    for (uint32_t i = 0; i < runs; ++i) chain_enqueue_one(ch, c->stream);
-    VXT_HIP_CHECK(hipEventRecord(c->ev1, c->stream));
-    VXT_HIP_CHECK(hipEventSynchronize(c->ev1));
-    float ms = 0.0f;
-    VXT_HIP_CHECK(hipEventElapsedTime(&ms, c->ev0, c->ev1));
-    c->last_ms = ms;
-    if (gpu_ms) *gpu_ms = ms;
-    uint32_t st = 0;
-    VXT_HIP_CHECK(hipMemcpy(&st, ch->status, 4, hipMemcpyDeviceToHost));
-    if (st != 0) {
-      chain_reset(ch);
-      fail(VXT_E_DEVICE, "a chain wait ran past its spin limit (outputs of that run are invalid)");
-    }
-  });
-}
-
-int vxt_hip_chain_enqueue(void* chain, void* stream, char* err, size_t err_cap) {
-  return guarded(err, err_cap, [&] {
-    if (!chain) fail(VXT_E_ARG, "null chain handle");
-    Chain* ch = static_cast<Chain*>(chain);
-    use_device(ch->ctx);
-    chain_enqueue_one(ch, stream ? static_cast<hipStream_t>(stream) : ch->ctx->stream);
-  });
-}
-
-int vxt_hip_chain_status(void* chain, char* err, size_t err_cap) {
-  return guarded(err, err_cap, [&] {
-    if (!chain) fail(VXT_E_ARG, "null chain handle");
-    Chain* ch = static_cast<Chain*>(chain);
-    use_device(ch->ctx);
-    VXT_HIP_CHECK(hipDeviceSynchronize());
-    uint32_t st = 0;
-    VXT_HIP_CHECK(hipMemcpy(&st, ch->status, 4, hipMemcpyDeviceToHost));
-    if (st != 0) {
-      chain_reset(ch);
-      fail(VXT_E_DEVICE, "a chain wait ran past its spin limit (outputs since the last check are invalid)");
-    }
-  });
-}
-
-int vxt_hip_chain_set_spin_limit(void* chain, uint32_t polls, char* err, size_t err_cap) {
-  return guarded(err, err_cap, [&] {
-    if (!chain) fail(VXT_E_ARG, "null chain handle");
-    static_cast<Chain*>(chain)->spin_limit = polls;
-  });
-}
-
-void vxt_hip_chain_free(void* chain) {
-  if (!chain) return;
-  Chain* ch = static_cast<Chain*>(chain);
-  (void)hipSetDevice(ch->ctx->device);
-  (void)hipDeviceSynchronize();
-  (void)hipFree(ch->ops);
-  (void)hipFree(ch->counters);
-  (void)hipFree(ch->status);
-  delete ch;
-}
 
 }  // extern "C"

@@ -62,8 +62,7 @@ ABI_SYMBOLS = (
     "vxt_hip_kv_q8_append_dev", "vxt_hip_attn_q8_dev", "vxt_hip_attn_prep_q8_dev", "vxt_hip_attn_step_q8_dev",
     "vxt_hip_last_kernel_ms", "vxt_hip_set_gemm_path", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
-    "vxt_hip_graph_launch", "vxt_hip_graph_free", "vxt_hip_chain_create", "vxt_hip_chain_run",
-    "vxt_hip_chain_enqueue", "vxt_hip_chain_status", "vxt_hip_chain_set_spin_limit", "vxt_hip_chain_free",
+    "vxt_hip_graph_launch", "vxt_hip_graph_free",
 )
 
 
@@ -94,11 +93,6 @@ class Cb4G64View(C.Structure):
                 ("reserved", C.c_uint32),
                 ("idx", C.c_void_p), ("n_idx", C.c_size_t),
                 ("lut_f16", C.c_void_p), ("n_lut", C.c_size_t)]
-
-
-class ChainOpView(C.Structure):
-    _fields_ = [("tensor", C.c_void_p), ("x", C.c_void_p), ("y", C.c_void_p), ("y_dtype", C.c_uint32),
-                ("reserved", C.c_uint32)]
 
 
 class VxtArchiveEntry(C.Structure):
@@ -230,18 +224,6 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_graph_launch.argtypes = [vp, vp, u32, C.POINTER(C.c_double), cp, sz]
     L.vxt_hip_graph_free.restype = None
     L.vxt_hip_graph_free.argtypes = [vp]
-    L.vxt_hip_chain_create.restype = vp
-    L.vxt_hip_chain_create.argtypes = [vp, C.POINTER(ChainOpView), u32, cp, sz]
-    L.vxt_hip_chain_run.restype = i32
-    L.vxt_hip_chain_run.argtypes = [vp, u32, C.POINTER(C.c_double), cp, sz]
-    L.vxt_hip_chain_enqueue.restype = i32
-    L.vxt_hip_chain_enqueue.argtypes = [vp, vp, cp, sz]
-    L.vxt_hip_chain_status.restype = i32
-    L.vxt_hip_chain_status.argtypes = [vp, cp, sz]
-    L.vxt_hip_chain_set_spin_limit.restype = i32
-    L.vxt_hip_chain_set_spin_limit.argtypes = [vp, u32, cp, sz]
-    L.vxt_hip_chain_free.restype = None
-    L.vxt_hip_chain_free.argtypes = [vp]
     _lib = L
     return L
 
@@ -429,46 +411,6 @@ class Graph:
             self.handle = None
 
 
-class Chain:
-    """The matmuls of one decode step as one persistent launch (``vxt_hip_chain_*``)."""
-
-    def __init__(self, engine: "HipEngine", handle: int, keep):
-        self._engine = engine
-        self.handle = handle
-        self._keep = keep   # tensors and buffers the chain points at
-
-    def run(self, runs: int = 1) -> float:
-        """``runs`` launches back to back; waits; returns total GPU ms."""
-        ms = C.c_double()
-        buf = _errbuf()
-        _check(load_library().vxt_hip_chain_run(self.handle, int(runs), C.byref(ms), buf, len(buf)), buf)
-        return ms.value
-
-    def enqueue(self, stream: int = 0) -> None:
-        buf = _errbuf()
-        _check(load_library().vxt_hip_chain_enqueue(self.handle, stream or None, buf, len(buf)), buf)
-
-    def status(self) -> None:
-        buf = _errbuf()
-        _check(load_library().vxt_hip_chain_status(self.handle, buf, len(buf)), buf)
-
-    def set_spin_limit(self, polls: int) -> None:
-        buf = _errbuf()
-        _check(load_library().vxt_hip_chain_set_spin_limit(self.handle, int(polls), buf, len(buf)), buf)
-
-    def free(self) -> None:
-        if self.handle:
-            load_library().vxt_hip_chain_free(self.handle)
-            self.handle = None
-
-    def __del__(self):
-        try:
-            if self.handle and self._engine.ctx:
-                self.free()
-        except Exception:
-            pass
-
-
 class HipEngine:
     """HIP compute engine for fused compressed-domain GEMV / GEMM (one GPU)."""
 
@@ -647,23 +589,6 @@ class HipEngine:
 
     def kv_q8_cache(self, max_seq: int, n_kv: int, head_dim: int) -> KvQ8Cache:
         return KvQ8Cache(self, max_seq, n_kv, head_dim)
-
-    def chain(self, ops: Sequence) -> Chain:
-        """A persistent decode-step chain of ``(tensor, x_ptr, y_ptr, y_dtype)``
-        ops (bf16 x, device pointers); an op may read any earlier op's output."""
-        ops = list(ops)
-        arr = (ChainOpView * len(ops))()
-        for i, (t, xp, yp, ydt) in enumerate(ops):
-            arr[i] = ChainOpView(t.handle, xp, yp, ydt, 0)
-        buf = _errbuf()
-        h = load_library().vxt_hip_chain_create(self.ctx, arr, len(ops), buf, len(buf))
-        if not h:
-            msg = buf.value
-            code = (VXT_E_SHAPE if b"columns" in msg else VXT_E_UNSUPPORTED if b"support" in msg
-                    else VXT_E_ARG if (b"null" in msg or b"context" in msg or b"least" in msg or b"dtype" in msg)
-                    else VXT_E_DEVICE)
-            _raise(code, buf)
-        return Chain(self, h, [t for t, *_ in ops])
 
     # -- device-pointer calls (asynchronous on `stream`) ----------------------
     def matmul_dev(self, t: GpuPackedTensor, x_ptr: int, x_dtype: int, batch_m: int, y_ptr: int,

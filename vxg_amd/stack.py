@@ -18,8 +18,7 @@ Only the matmuls run (the "matmul-only path"): attention, norms and the
 activation function are outside this module, so each projection reads a
 slice of the previous one's output instead.  The dependency chain between
 launches is the real one.  One token is 4 * layers + 1 launches; captured
-once into a HIP graph, it replays with no per-launch host work;
-:meth:`DecodeStack.persistent` runs the same token as one persistent launch.
+once into a HIP graph, it replays with no per-launch host work.
 """
 from __future__ import annotations
 
@@ -93,11 +92,6 @@ class DecodeStack:
             x = self.dn_out.ptr
         out.append((self.lm_head, x, self.logits.ptr, f32))
         return out
-
-    def persistent(self) -> engine.Chain:
-        """The same token as one persistent launch (``HipEngine.chain``): each
-        projection's weights stream in while the one before it finishes."""
-        return self.eng.chain(self.ops())
 
     def enqueue(self, stream=None) -> None:
         """Queue one token's projections on ``stream`` (default: the engine's)."""
