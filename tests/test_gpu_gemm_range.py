@@ -1,0 +1,116 @@
+"""Prefill GEMM with activations of any magnitude.
+
+The reference's gemm_cpu takes f32 X of any magnitude
+(crates/vxg-tensor/src/llm_prefill.rs:156-255); the device multiplies f16
+operands, so every activation row carries a power-of-two scale that puts its
+largest magnitude in [2^14, 2^15) and the epilogue undoes it.  These tests
+drive rows from 2^-30 to 2^100 (bf16, about 1e30) and 2^-30 to 2^90 (f32)
+through every GEMM path (fused, two-phase with the own dense kernel, two-phase
+with the library dense phase), each pinned, at the GEMM bars.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from vxg_amd import engine, synth
+from vxg_amd.formats import bf16_bits_to_f32, f32_to_bf16_bits
+
+from parity_util import THREADS, assert_bf16_close, floor_scale, make, max_rel, run_dev
+
+pytestmark = pytest.mark.gpu
+
+PATHS = {"fused": engine.GEMM_FUSED, "panel": engine.GEMM_PANEL, "library": engine.GEMM_LIBRARY}
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = engine.HipEngine(0)
+    yield e
+    e.close()
+
+
+def ranged_rows(M, cols, lo, hi, seed):
+    """N(0,1) rows, row i scaled by 2^p_i with p_i spread over [lo, hi]; one
+    row mixes magnitudes within 2^20 (elements scaled by 2^0..2^19)."""
+    g = np.random.default_rng(seed)
+    X = g.standard_normal((M, cols)).astype(np.float64)
+    p = np.round(np.linspace(lo, hi, M)).astype(np.int64)
+    X *= np.exp2(p)[:, None]
+    X[M // 2] *= np.exp2(g.integers(0, 20, size=cols))
+    return X
+
+
+def check(y, yref, W, X, bf16):
+    fl = floor_scale(W, X)
+    assert np.all(np.isfinite(yref))
+    if bf16:
+        assert_bf16_close(y, yref, fl)
+    else:
+        err = max_rel(y, yref, fl)
+        assert err <= 1e-3, err
+
+
+@pytest.mark.parametrize("path", list(PATHS))
+@pytest.mark.parametrize("kind", ["g64", "q8", "cb4"])
+@pytest.mark.parametrize("M", [24, 130])
+def test_gemm_bf16_activations_any_magnitude(eng, path, kind, M):
+    print(f"gemm range bf16 path={path} kind={kind} M={M}", flush=True)
+    m = make(kind, 70, 320, seed=M + 17)
+    t = eng.upload_packed(m)
+    xb = f32_to_bf16_bits(ranged_rows(M, 320, -30, 100, seed=M).astype(np.float32))
+    X = bf16_bits_to_f32(xb).reshape(M, 320)
+    yref = oracle.gemm(m, X, threads=THREADS)
+    W = oracle.decode_rows(m)
+    eng.set_gemm_path(PATHS[path])
+    try:
+        check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32), yref, W, X, False)
+        check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16), yref, W, X, True)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
+    t.free()
+
+
+@pytest.mark.parametrize("path", ["panel", "library"])
+@pytest.mark.parametrize("kind", ["g64", "q8", "cb4"])
+def test_gemm_f32_activations_any_magnitude(eng, path, kind):
+    print(f"gemm range f32 path={path} kind={kind}", flush=True)
+    M = 40
+    m = make(kind, 70, 320, seed=41)
+    t = eng.upload_packed(m)
+    X = ranged_rows(M, 320, -30, 90, seed=5).astype(np.float32)
+    yref = oracle.gemm(m, X, threads=THREADS)
+    W = oracle.decode_rows(m)
+    eng.set_gemm_path(PATHS[path])
+    try:
+        check(run_dev(eng, t, X, engine.DTYPE_F32, M, engine.DTYPE_F32), yref, W, X, False)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
+    t.free()
+
+
+def test_gemm_host_api_large_activations(eng):
+    """vxt_hip_gemm (f32 in and out, the reference's gemm_cpu signature) with
+    activations above the f16 range."""
+    m = make("cb4", 50, 300, seed=3)
+    t = eng.upload_packed(m)
+    X = (synth.make_x_f32(12, 300, seed=3) * np.float32(1e6)).astype(np.float32)
+    Y = eng.gemm(t, X)
+    check(Y, oracle.gemm(m, X, threads=THREADS), oracle.decode_rows(m), X, False)
+    t.free()
+
+
+def test_gemm_nonfinite_activation_row_propagates(eng):
+    """An Inf in one activation row gives non-finite outputs in that row only,
+    as the reference's f32 arithmetic does; other rows keep the bar."""
+    m = make("g64", 40, 256, seed=8)
+    t = eng.upload_packed(m)
+    X = synth.make_x_f32(16, 256, seed=8)
+    X[3, 17] = np.inf
+    xb = f32_to_bf16_bits(X)
+    Xq = bf16_bits_to_f32(xb).reshape(16, 256)
+    y = run_dev(eng, t, xb, engine.DTYPE_BF16, 16, engine.DTYPE_F32)
+    assert not np.all(np.isfinite(y[3]))
+    keep = np.r_[0:3, 4:16]
+    yref = oracle.gemm(m, Xq[keep], threads=THREADS)
+    check(y[keep], yref, oracle.decode_rows(m), Xq[keep], False)
+    t.free()

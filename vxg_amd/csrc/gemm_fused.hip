@@ -22,8 +22,11 @@
 //       g64: the f16 table entries themselves (exact), looked up in a 48-byte
 //            LDS slot per row holding the group's table (two slots per row,
 //            alternating); v_mfma_f32_32x32x16_f16, with the chunk's
-//            activations converted to f16 once, in place (v_cvt_pk_f16_f32,
-//            round to nearest even: exact in the f16 normal range);
+//            activations converted to f16 once, in place, after a power-of-
+//            two scale per activation row (xe, from xscale_kernel) that puts
+//            the row's largest magnitude in [2^14, 2^15): exact for every
+//            element within 2^28 of it, whatever the row's magnitude; the
+//            epilogue (or the split-K reduction) undoes the scale;
 //       Q8:  the int8 values, exact in bf16, against the bf16 activations
 //            as they are (v_mfma_f32_32x32x16_bf16: the products are exact in
 //            fp32); each 32-column block is two MFMA steps into a fresh
@@ -120,25 +123,30 @@ __device__ __forceinline__ void issue_a(const uint16_t* __restrict__ x, uint32_t
   }
 }
 
-// 8 bf16 -> 8 f16 (two per v_cvt_pk_f16_f32).
-__device__ __forceinline__ u32x4 bf16x8_to_f16(u32x4 raw) {
+// 8 bf16 times 2^e -> 8 f16 (two per v_cvt_pk_f16_f32; the scaling is exact).
+__device__ __forceinline__ u32x4 bf16x8_to_f16(u32x4 raw, int e) {
   u32x4 out;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float2v f = {__uint_as_float(raw[j] << 16), __uint_as_float(raw[j] & 0xffff0000u)};
+    const float2v f = {ldexpf(__uint_as_float(raw[j] << 16), e), ldexpf(__uint_as_float(raw[j] & 0xffff0000u), e)};
     out[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, half2v));
   }
   return out;
 }
 
-// The chunk's activation blocks, bf16 -> f16 in place (all threads; the
-// caller brackets it with barriers).
+// The chunk's activation blocks, bf16 -> f16 in place with the row scales
+// 2^xe (all threads; the caller brackets it with barriers).  Piece i is lane
+// i % 64 of block i / 64, which holds activation row m0 + g * 32 + lane % 32
+// (g = block / 4 % FI; rows past M repeat row M - 1).
 template <int FI, int KW>
-__device__ __forceinline__ void convert_a(char* abuf, uint32_t tiles) {
+__device__ __forceinline__ void convert_a(char* abuf, uint32_t tiles, uint32_t m0, uint32_t M,
+                                          const int32_t* __restrict__ xe) {
   const uint32_t pieces = tiles * FI * 4 * (FRAG / 16);
   for (uint32_t i = threadIdx.x; i < pieces; i += 256 * KW) {
+    const uint32_t g = (i / 64 / 4) % FI;
+    const int e = xe[std::min(m0 + g * 32 + (i & 31), M - 1)];
     u32x4* p = reinterpret_cast<u32x4*>(abuf + i * 16);
-    *p = bf16x8_to_f16(*p);
+    *p = bf16x8_to_f16(*p, e);
   }
 }
 
@@ -279,7 +287,7 @@ template <uint32_t KIND, int FI, int KW>
 __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint16_t* __restrict__ x, uint32_t M,
                                                          uint32_t x_vec, void* __restrict__ y, uint32_t y_bf16,
                                                          float* __restrict__ partial, uint32_t chunks_per_split,
-                                                         uint32_t tiles_m) {
+                                                         uint32_t tiles_m, const int32_t* __restrict__ xe) {
   constexpr uint32_t BM = 32 * FI;
   constexpr uint32_t AB = a_bytes<FI>();
   constexpr int NT = KC / KW;
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
     wait_vm0();        // chunk c has landed (nothing else is in flight)
     __syncthreads();   // ... for every wave; and the other buffer is free
     if constexpr (KIND == KIND_G64) {
-      convert_a<FI, KW>(buf0, std::min<uint32_t>(KC, KT - c * KC));
+      convert_a<FI, KW>(buf0, std::min<uint32_t>(KC, KT - c * KC), m0, M, xe);
       __syncthreads();
     }
     if (c + 1 < c1)
@@ -323,7 +331,7 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
     wait_vm0();
     __syncthreads();
     if constexpr (KIND == KIND_G64) {
-      convert_a<FI, KW>(buf1, std::min<uint32_t>(KC, KT - (c + 1) * KC));
+      convert_a<FI, KW>(buf1, std::min<uint32_t>(KC, KT - (c + 1) * KC), m0, M, xe);
       __syncthreads();
     }
     if (c + 2 < c1)
@@ -362,7 +370,10 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
     for (int r = 0; r < 16; ++r) {
       const uint32_t m = m0 + i * 32 + h * 4 + 8 * (r >> 2) + (r & 3);
       if (m >= M) continue;
-      const float v = acc[i][r];
+      float v = acc[i][r];
+      if constexpr (KIND == KIND_G64) {
+        if (!to_partial) v = ldexpf(v, -xe[m]);
+      }
       if (to_partial)
         partial[((size_t)blockIdx.y * M + m) * N + ncol] = v;
       else if (y_bf16)
@@ -396,53 +407,56 @@ inline Plan plan(const DevTensor& t, uint32_t m) {
 
 template <uint32_t KIND, int FI, int KW>
 hipError_t launch(const DevTensor& t, const uint16_t* x, uint32_t m, uint32_t x_vec, void* y, bool y_bf16,
-                  const Plan& p, float* partial, hipStream_t s) {
+                  const Plan& p, float* partial, const int32_t* xe, hipStream_t s) {
   constexpr size_t lds = lds_bytes<KIND, FI, KW>();
   static_assert(lds <= 160 * 1024, "LDS budget");
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&fused_kernel<KIND, FI, KW>),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
   hipLaunchKernelGGL((fused_kernel<KIND, FI, KW>), dim3(p.tiles_m * p.tiles_n, p.splits), dim3(256 * KW), lds, s,
-                     t, x, m, x_vec, y, (uint32_t)y_bf16, partial, p.cps, p.tiles_m);
+                     t, x, m, x_vec, y, (uint32_t)y_bf16, partial, p.cps, p.tiles_m, xe);
   return hipGetLastError();
 }
 
 template <uint32_t KIND>
 hipError_t launch_kind(const DevTensor& t, const uint16_t* x, uint32_t m, uint32_t x_vec, void* y, bool y_bf16,
-                       const Plan& p, float* partial, hipStream_t s) {
-  if (p.fi == 1) return launch<KIND, 1, 2>(t, x, m, x_vec, y, y_bf16, p, partial, s);
-  if (p.fi == 2) return launch<KIND, 2, 2>(t, x, m, x_vec, y, y_bf16, p, partial, s);
+                       const Plan& p, float* partial, const int32_t* xe, hipStream_t s) {
+  if (p.fi == 1) return launch<KIND, 1, 2>(t, x, m, x_vec, y, y_bf16, p, partial, xe, s);
+  if (p.fi == 2) return launch<KIND, 2, 2>(t, x, m, x_vec, y, y_bf16, p, partial, xe, s);
   // Q8 at 4 fragments holds a second accumulator set per block: one K way
   // keeps it within the registers of 2 waves per SIMD (measured equal speed).
-  return launch<KIND, 4, KIND == KIND_Q8 ? 1 : 2>(t, x, m, x_vec, y, y_bf16, p, partial, s);
+  return launch<KIND, 4, KIND == KIND_Q8 ? 1 : 2>(t, x, m, x_vec, y, y_bf16, p, partial, xe, s);
 }
 
 }  // namespace fz
 
-hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
-                              bool y_bf16, hipStream_t s);
+hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, const int32_t* xe, uint32_t m,
+                              uint32_t n, void* y, bool y_bf16, hipStream_t s);
 
 bool gemm_fused_supported(const DevTensor& t, bool x_bf16) {
   return x_bf16 && (t.kind == KIND_G64 || t.kind == KIND_Q8);
 }
 
+// g64 multiplies f16 activations (row-scaled); Q8 the bf16 activations as they are.
+bool gemm_fused_scales_x(const DevTensor& t) { return t.kind == KIND_G64; }
+
 size_t gemm_fused_workspace_bytes(const DevTensor& t, uint32_t m) { return fz::plan(t, m).partial_bytes; }
 
 hipError_t launch_gemm_fused(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
-                             size_t ws_bytes, hipStream_t s) {
+                             size_t ws_bytes, const int32_t* xe, hipStream_t s) {
   const fz::Plan p = fz::plan(t, m);
   if (ws_bytes < p.partial_bytes) return hipErrorInvalidValue;
   float* partial = static_cast<float*>(ws);
   const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (t.cols % 8 == 0);
   hipError_t e;
   if (t.kind == KIND_G64)
-    e = fz::launch_kind<KIND_G64>(t, x, m, x_vec, y, y_bf16, p, partial, s);
+    e = fz::launch_kind<KIND_G64>(t, x, m, x_vec, y, y_bf16, p, partial, xe, s);
   else if (t.kind == KIND_Q8)
-    e = fz::launch_kind<KIND_Q8>(t, x, m, x_vec, y, y_bf16, p, partial, s);
+    e = fz::launch_kind<KIND_Q8>(t, x, m, x_vec, y, y_bf16, p, partial, nullptr, s);
   else
     return hipErrorInvalidValue;
   if (e != hipSuccess || p.splits == 1) return e;
-  return launch_gemm_reduce(partial, p.splits, nullptr, m, t.rows, y, y_bf16, s);
+  return launch_gemm_reduce(partial, p.splits, nullptr, t.kind == KIND_G64 ? xe : nullptr, m, t.rows, y, y_bf16, s);
 }
 
 }  // namespace vxt

@@ -16,9 +16,13 @@
 //          exact for Q8 (q * d has <= 18), within 2^-22 relative for cb4.
 //   2. dense_kernel: Y = X * W^T on v_mfma_f32_32x32x16_f16 from LDS tiles,
 //      fp32 accumulation; lo products go to a second accumulator folded in
-//      as acc + accl * 2^-11, then scaled by 1/s.  bf16 X becomes f16 while it
-//      is staged (exact for |x| in the f16 normal range); f32 X is split into
-//      hi + lo like the weights, with one more MFMA (lo * lo dropped).
+//      as acc + accl * 2^-11, then scaled by 1/s.  Activations get a
+//      power-of-two scale per row too (xscale_kernel: the row's largest
+//      magnitude in [2^14, 2^15)), undone in the epilogue, so X of any
+//      magnitude converts to f16 without overflow: bf16 X exactly (8
+//      significant bits) for elements within 2^28 of the row's largest; f32
+//      X is split into hi + lo like the weights, with one more MFMA (lo * lo
+//      dropped).
 //      Small M*N grids split K across workgroups; reduce_kernel then adds the
 //      partial sums in a fixed order (results do not depend on timing).
 //      For large products the dense phase runs on hipBLASLt instead
@@ -39,8 +43,8 @@
 
 namespace vxt {
 
-hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
-                              bool y_bf16, hipStream_t s);
+hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, const int32_t* xe, uint32_t m,
+                              uint32_t n, void* y, bool y_bf16, hipStream_t s);
 hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
                             uint32_t K, uint32_t batch, float alpha, float beta, float* D, hipStream_t s);
 
@@ -99,6 +103,7 @@ struct XConv {
   const void* x;
   uint16_t* ah;
   uint16_t* al;
+  const int32_t* xe;   // per-row exponent: X[m] * 2^xe[m] is converted
   uint32_t m, cols, x_bf16, x_vec, blocks;
 };
 
@@ -141,6 +146,9 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
         v[j] = f;
       }
     }
+    const int e = c.xe[m];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ldexpf(v[j], e);   // exact (a power of two)
     uint32_t h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -156,6 +164,34 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
 
 __device__ __forceinline__ float wave_max(float v) { return lane_reduce<64, true>(v); }
 __device__ __forceinline__ float wave_add(float v) { return lane_reduce<64>(v); }
+
+// Per activation row m: xe[m] such that the row's largest magnitude times
+// 2^xe[m] lies in [2^14, 2^15), so the f16 operands neither overflow nor
+// (for bf16 X) round; 0 for a row that is all zero or holds Inf or NaN (those
+// propagate as in the reference's f32 arithmetic).  One workgroup per row.
+__global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict__ x, uint32_t x_bf16, uint32_t M,
+                                                         uint32_t K, int32_t* __restrict__ xe) {
+  __shared__ float s_max[THREADS / 64];
+  for (uint32_t m = blockIdx.x; m < M; m += gridDim.x) {
+    float mx = 0.0f;
+    for (uint32_t k = threadIdx.x; k < K; k += THREADS) {
+      const float v = x_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k])
+                             : static_cast<const float*>(x)[(size_t)m * K + k];
+      const float a = fabsf(v);
+      mx = fmaxf(mx, a != a ? __builtin_inff() : a);   // NaN counts as non-finite
+    }
+    mx = wave_max(mx);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      float b = s_max[0];
+#pragma unroll
+      for (int w = 1; w < THREADS / 64; ++w) b = fmaxf(b, s_max[w]);
+      xe[m] = (b > 0.0f && b <= 3.4028234663852886e38f) ? 14 - ilogbf(b) : 0;
+    }
+    __syncthreads();
+  }
+}
 
 // 8 consecutive f32 weights -> hi (and lo) f16 pieces at column c of the row.
 template <bool SPLIT>
@@ -386,7 +422,7 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
                                                         const uint16_t* __restrict__ al, uint32_t M, uint32_t N,
                                                         void* __restrict__ y, uint32_t y_bf16,
                                                         float* __restrict__ partial, uint32_t kt_per_split,
-                                                        uint32_t tiles_m) {
+                                                        uint32_t tiles_m, const int32_t* __restrict__ xe) {
   constexpr bool SPLIT = WMODE == kWHiLo;
   constexpr bool QBLK = WMODE == kWQBlock;
   static_assert(!(QBLK && SPLIT_A), "block-scaled weights take f16 activations");
@@ -541,7 +577,7 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
         if (to_partial) {
           partial[((size_t)blockIdx.y * M + m) * N + n] = v;
         } else {
-          v *= inv;
+          v = ldexpf(v * inv, -xe[m]);
           if (y_bf16)
             static_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(v);
           else
@@ -551,10 +587,12 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
   }
 }
 
-// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n] (no scaling when
-// inv is null); four outputs per thread when N % 4 == 0.
+// Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n] * 2^-xe[m] (no
+// weight scaling when inv is null, no activation scaling when xe is null);
+// four outputs per thread when N % 4 == 0.
 __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict__ partial, uint32_t splits,
-                                                         const float* __restrict__ inv, uint32_t M, uint32_t N,
+                                                         const float* __restrict__ inv,
+                                                         const int32_t* __restrict__ xe, uint32_t M, uint32_t N,
                                                          void* __restrict__ y, uint32_t y_bf16) {
   const size_t total = (size_t)M * N;
   if (N % 4u == 0u) {
@@ -568,6 +606,10 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
     if (inv) {
       const float4 iv = *reinterpret_cast<const float4*>(inv + i % N);
       v.x *= iv.x; v.y *= iv.y; v.z *= iv.z; v.w *= iv.w;
+    }
+    if (xe) {   // the four outputs share a row (N % 4 == 0)
+      const int e = -xe[i / N];
+      v.x = ldexpf(v.x, e); v.y = ldexpf(v.y, e); v.z = ldexpf(v.z, e); v.w = ldexpf(v.w, e);
     }
     if (y_bf16) {
       const uint32_t lo = f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
@@ -583,6 +625,7 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
   float v = 0.0f;
   for (uint32_t z = 0; z < splits; ++z) v += partial[(size_t)z * total + i];
   if (inv) v *= inv[i % N];
+  if (xe) v = ldexpf(v, -xe[i / N]);
   if (y_bf16)
     static_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
   else
@@ -643,7 +686,7 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
 
 template <int BM, int BN, int WMODE, bool SPLIT_A>
 hipError_t launch_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, uint32_t m, uint32_t n, void* y,
-                        bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
+                        bool y_bf16, const Plan& pl, float* partial, const int32_t* xe, hipStream_t s) {
   constexpr size_t lds = (size_t)(2 * BM * LDK + 2 * BN * LDK + (SPLIT_A ? 2 * BM * LDK : 0) +
                                   (WMODE == kWHiLo ? 2 * BN * LDK : 0)) * 2 +
                          (WMODE == kWQBlock ? 2 * 2 * BN * 4 : 0);
@@ -655,26 +698,28 @@ hipError_t launch_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, 
   const uint32_t tiles_m = (m + BM - 1) / BM;
   const dim3 grid(tiles_m * ((n + BN - 1) / BN), pl.splits);
   hipLaunchKernelGGL((dense_kernel<BM, BN, WMODE, SPLIT_A>), grid, dim3(THREADS), lds, s, p, ah, al, m, n, y,
-                     (uint32_t)y_bf16, partial, pl.kt_per_split, tiles_m);
+                     (uint32_t)y_bf16, partial, pl.kt_per_split, tiles_m, xe);
   return hipGetLastError();
 }
 
 template <int BM, int WMODE>
 hipError_t launch_dense_x(const Panel& p, const uint16_t* ah, const uint16_t* al, bool x_bf16, uint32_t m,
-                          uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
-  if (x_bf16) return launch_dense<BM, BM, WMODE, false>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+                          uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, const int32_t* xe,
+                          hipStream_t s) {
+  if (x_bf16) return launch_dense<BM, BM, WMODE, false>(p, ah, al, m, n, y, y_bf16, pl, partial, xe, s);
   if constexpr (WMODE == kWQBlock) {
     return hipErrorInvalidValue;   // f32 activations use the hi/lo panel
   } else {
-    return launch_dense<BM, BM, WMODE, true>(p, ah, al, m, n, y, y_bf16, pl, partial, s);
+    return launch_dense<BM, BM, WMODE, true>(p, ah, al, m, n, y, y_bf16, pl, partial, xe, s);
   }
 }
 
 template <int WMODE>
 hipError_t launch_dense_m(const Panel& p, const uint16_t* ah, const uint16_t* al, bool x_bf16, uint32_t m,
-                          uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, hipStream_t s) {
-  if (pl.bm == 128) return launch_dense_x<128, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, s);
-  return launch_dense_x<64, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, s);
+                          uint32_t n, void* y, bool y_bf16, const Plan& pl, float* partial, const int32_t* xe,
+                          hipStream_t s) {
+  if (pl.bm == 128) return launch_dense_x<128, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, xe, s);
+  return launch_dense_x<64, WMODE>(p, ah, al, x_bf16, m, n, y, y_bf16, pl, partial, xe, s);
 }
 
 // The dense phase on the vendor library: D = sum of f16 GEMMs over the
@@ -684,7 +729,8 @@ hipError_t launch_dense_m(const Panel& p, const uint16_t* ah, const uint16_t* al
 // ascending order).  hipErrorNotSupported when the library has no
 // algorithm for the shape.
 hipError_t library_dense(const Panel& p, const uint16_t* ah, const uint16_t* al, bool split_a, int wmode, uint32_t m,
-                         uint32_t n, uint32_t splits, void* y, bool y_bf16, float* d, hipStream_t s) {
+                         uint32_t n, uint32_t splits, void* y, bool y_bf16, float* d, const int32_t* xe,
+                         hipStream_t s) {
   struct Term { const uint16_t* a; const uint16_t* b; float alpha; };
   Term terms[3];
   int nt = 0;
@@ -696,12 +742,12 @@ hipError_t library_dense(const Panel& p, const uint16_t* ah, const uint16_t* al,
                                           terms[i].alpha, i == 0 ? 0.0f : 1.0f, d, s);
     if (e != hipSuccess) return e;
   }
-  return launch_gemm_reduce(d, splits, p.inv, m, n, y, y_bf16, s);
+  return launch_gemm_reduce(d, splits, p.inv, xe, m, n, y, y_bf16, s);
 }
 
 template <uint32_t KIND>
 hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
-               size_t ws_bytes, hipStream_t s, bool lib) {
+               size_t ws_bytes, const int32_t* xe, hipStream_t s, bool lib) {
   const Plan pl = plan(t, m, x_bf16, lib);
   if (ws_bytes < pl.panel_bytes + pl.a_bytes + pl.partial_bytes) return hipErrorInvalidValue;
   char* base = static_cast<char*>(ws);
@@ -721,7 +767,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   // One launch: the activation conversion's workgroups first, then one
   // wave per (weight row, 2048-column segment) of the panel decode.
   const size_t pieces = (size_t)m * (pl.kp / 8);
-  XConv xc{x, ah, al, m, t.cols, (uint32_t)x_bf16, x_vec,
+  XConv xc{x, ah, al, xe, m, t.cols, (uint32_t)x_bf16, x_vec,
            (uint32_t)std::min<size_t>((pieces + THREADS - 1) / THREADS, 1024)};
   const uint32_t nseg = (p.kp + 64 * 32 - 1) / (64 * 32);
   const uint32_t pgrid = (uint32_t)(((size_t)t.rows * nseg + 3) / 4);
@@ -730,39 +776,47 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (pl.lib) {
-    e = library_dense(p, ah, al, !x_bf16, pl.wmode, m, t.rows, pl.lib_splits, y, y_bf16, partial, s);
+    e = library_dense(p, ah, al, !x_bf16, pl.wmode, m, t.rows, pl.lib_splits, y, y_bf16, partial, xe, s);
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();   // no algorithm for this shape: the own dense kernel on the same panel
   }
   if constexpr (KIND == KIND_G64) {
-    e = launch_dense_m<kWPlain>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+    e = launch_dense_m<kWPlain>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
   } else if constexpr (KIND == KIND_Q8) {
     if (pl.wmode == kWQBlock)
-      e = launch_dense_m<kWQBlock>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+      e = launch_dense_m<kWQBlock>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
     else
-      e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+      e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
   } else {
-    e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, s);
+    e = launch_dense_m<kWHiLo>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
   }
   if (e != hipSuccess || pl.splits == 1) return e;
-  return launch_gemm_reduce(partial, pl.splits, p.inv, m, t.rows, y, y_bf16, s);
+  return launch_gemm_reduce(partial, pl.splits, p.inv, xe, m, t.rows, y, y_bf16, s);
 }
 
 }  // namespace gp
 
-hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, uint32_t m, uint32_t n, void* y,
-                              bool y_bf16, hipStream_t s) {
+hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, const int32_t* xe, uint32_t m,
+                              uint32_t n, void* y, bool y_bf16, hipStream_t s) {
   const size_t total = (size_t)m * n;
   const size_t threads = n % 4u == 0u ? total / 4 : total;
   hipLaunchKernelGGL(gp::reduce_kernel, dim3((uint32_t)((threads + gp::THREADS - 1) / gp::THREADS)),
-                     dim3(gp::THREADS), 0, s, partial, splits, inv, m, n, y, (uint32_t)y_bf16);
+                     dim3(gp::THREADS), 0, s, partial, splits, inv, xe, m, n, y, (uint32_t)y_bf16);
+  return hipGetLastError();
+}
+
+// Per-row activation exponents (xscale_kernel) into xe[m].
+hipError_t launch_xscale(const void* x, bool x_bf16, uint32_t m, uint32_t k, int32_t* xe, hipStream_t s) {
+  hipLaunchKernelGGL(gp::xscale_kernel, dim3(std::min<uint32_t>(m, 4096u)), dim3(gp::THREADS), 0, s, x,
+                     (uint32_t)x_bf16, m, k, xe);
   return hipGetLastError();
 }
 
 bool gemm_fused_supported(const DevTensor& t, bool x_bf16);
+bool gemm_fused_scales_x(const DevTensor& t);
 size_t gemm_fused_workspace_bytes(const DevTensor& t, uint32_t m);
 hipError_t launch_gemm_fused(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
-                             size_t ws_bytes, hipStream_t s);
+                             size_t ws_bytes, const int32_t* xe, hipStream_t s);
 
 // Path choice: the fused kernel where it applies (g64 and Q8 weights, bf16
 // activations) and batch_m is at most kFusedMaxM, unless the caller pins a
@@ -793,22 +847,36 @@ static bool library_path(const DevTensor& t, uint32_t m, int mode) {
   return (size_t)m * t.rows >= kLibMinOutputs || (t.kind == KIND_G64 && t.cols >= kLibMinSplitK);
 }
 
+// Workspace: the per-row activation exponents first, then the path's own.
+static size_t xe_bytes(uint32_t m) { return gp::al256((size_t)m * 4); }
+
 size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
-  if (fused_path(t, m, x_bf16, mode)) return gemm_fused_workspace_bytes(t, m);
+  if (fused_path(t, m, x_bf16, mode)) return xe_bytes(m) + gemm_fused_workspace_bytes(t, m);
   const gp::Plan pl = gp::plan(t, m, x_bf16, library_path(t, m, mode));
-  return pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
+  return xe_bytes(m) + pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
 }
 
 hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
                        size_t ws_bytes, hipStream_t s, int mode) {
   if (m == 0 || (size_t)m * t.rows > (size_t)1 << 40) return hipErrorInvalidValue;
-  if (fused_path(t, m, x_bf16, mode))
-    return launch_gemm_fused(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
+  if (ws_bytes < xe_bytes(m)) return hipErrorInvalidValue;
+  int32_t* xe = static_cast<int32_t*>(ws);
+  void* rest = static_cast<char*>(ws) + xe_bytes(m);
+  const size_t rest_bytes = ws_bytes - xe_bytes(m);
+  const bool fused = fused_path(t, m, x_bf16, mode);
+  // f16 operands need the activations' row scales (the fused Q8 kernel
+  // multiplies bf16 activations as they are).
+  if (!fused || gemm_fused_scales_x(t)) {
+    const hipError_t e = launch_xscale(x, x_bf16, m, t.cols, xe, s);
+    if (e != hipSuccess) return e;
+  }
+  if (fused)
+    return launch_gemm_fused(t, static_cast<const uint16_t*>(x), m, y, y_bf16, rest, rest_bytes, xe, s);
   const bool lib = library_path(t, m, mode);
   switch (t.kind) {
-    case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
-    case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
-    case KIND_CB4: return gp::run<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, ws, ws_bytes, s, lib);
+    case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
+    case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
+    case KIND_CB4: return gp::run<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
     default: return hipErrorInvalidValue;
   }
 }
