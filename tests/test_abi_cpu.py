@@ -65,6 +65,25 @@ def test_null_handles_are_rejected_without_a_device():
     assert lib.vxt_hip_last_kernel_ms(None, C.byref(ms)) == engine.VXT_E_ARG
 
 
+def test_stale_handles_are_rejected_without_a_device():
+    """Handles the library never issued (or already released) are looked up,
+    not dereferenced: releases are no-ops, calls fail with VXT_E_ARG."""
+    lib = engine.load_library()
+    buf = C.create_string_buffer(256)
+    bogus = C.c_void_p(0x1000)
+    lib.vxt_hip_free_tensor(bogus)
+    lib.vxt_hip_graph_free(bogus)
+    lib.vxt_hip_destroy(bogus)
+    lib.vxt_hip_device_free(bogus, bogus)
+    assert lib.vxt_hip_stream(bogus) is None
+    assert lib.vxt_hip_tensor_info(bogus, None, None, None, None) == engine.VXT_E_ARG
+    assert lib.vxt_hip_set_gemm_path(bogus, 0) == engine.VXT_E_ARG
+    rc = lib.vxt_hip_matmul_dev(bogus, bogus, bogus, 0, 1, bogus, 0, None, buf, len(buf))
+    assert rc == engine.VXT_E_ARG and b"context" in buf.value
+    rc = lib.vxt_hip_graph_launch(bogus, bogus, 1, None, buf, len(buf))
+    assert rc == engine.VXT_E_ARG
+
+
 def test_codebook_validation_mirrors_archive_reader():
     m = synth.make_cb4(7, 300, seed=3)
     m.validate()

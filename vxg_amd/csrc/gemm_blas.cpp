@@ -34,7 +34,15 @@ using Key = std::tuple<int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, ui
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<Key, Entry> g_entries;
+std::map<int, int> g_users;   // contexts alive per device
 constexpr size_t kMaxEntries = 512;
+
+void destroy_entry(Entry& en) {
+  if (en.ld) hipblasLtMatrixLayoutDestroy(en.ld);
+  if (en.lb) hipblasLtMatrixLayoutDestroy(en.lb);
+  if (en.la) hipblasLtMatrixLayoutDestroy(en.la);
+  if (en.op) hipblasLtMatmulDescDestroy(en.op);
+}
 
 hipError_t status(hipblasStatus_t st) {
   if (st == HIPBLAS_STATUS_SUCCESS) return hipSuccess;
@@ -97,10 +105,7 @@ hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, 
   if (pref) hipblasLtMatmulPreferenceDestroy(pref);
   if (e == hipSuccess && nres < 1) e = hipErrorNotSupported;
   if (e != hipSuccess) {
-    if (en.ld) hipblasLtMatrixLayoutDestroy(en.ld);
-    if (en.lb) hipblasLtMatrixLayoutDestroy(en.lb);
-    if (en.la) hipblasLtMatrixLayoutDestroy(en.la);
-    if (en.op) hipblasLtMatmulDescDestroy(en.op);
+    destroy_entry(en);
     return e;
   }
   en.algo = res.algo;
@@ -109,6 +114,38 @@ hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, 
 }
 
 }  // namespace
+
+// The library handle and cached descriptors of a device live while a
+// context on that device does: contexts register here, and the last one to
+// go releases them (the handle is shared by the device's contexts).
+void blas_acquire_device(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  ++g_users[dev];
+}
+
+void blas_release_device(int dev) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  auto u = g_users.find(dev);
+  if (u == g_users.end() || --u->second > 0) return;
+  g_users.erase(u);
+  for (auto it = g_entries.begin(); it != g_entries.end();) {
+    if (std::get<0>(it->first) == dev) {
+      destroy_entry(it->second);
+      it = g_entries.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  auto h = g_handles.find(dev);
+  if (h != g_handles.end()) {
+    int cur = 0;
+    const bool restore = hipGetDevice(&cur) == hipSuccess;
+    (void)hipSetDevice(dev);
+    hipblasLtDestroy(h->second);
+    g_handles.erase(h);
+    if (restore) (void)hipSetDevice(cur);
+  }
+}
 
 // D_b[M][N] (f32, row-major; block b at D + b * M * N) = alpha * A_b[M][K] *
 // B_b[N][K]^T + beta * D_b for b < batch, where A_b and B_b are the columns

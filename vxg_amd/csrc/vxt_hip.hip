@@ -17,6 +17,7 @@
 #include <new>
 #include <set>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/vxt_hip.h"
@@ -53,6 +54,8 @@ hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* ga
                                uint32_t pos0, uint32_t batch, void* ws, hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
+void blas_acquire_device(int dev);
+void blas_release_device(int dev);
 }  // namespace vxt
 
 namespace {
@@ -91,6 +94,8 @@ struct Tensor {
   }
 };
 
+struct Graph;
+
 struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -100,13 +105,15 @@ struct Ctx {
   size_t d_x_cap = 0;
   void* d_y = nullptr;
   size_t d_y_cap = 0;
-  void* ws = nullptr;      // GEMM workspace: weight panel + split-K partial sums
+  void* ws = nullptr;           // workspace: GEMM panel, partial sums, staging
   size_t ws_cap = 0;
+  std::vector<void*> retired;   // replaced workspaces, kept until destroy
   void* greedy = nullptr;  // greedy-selection state words (zero between calls)
   int gemm_mode = vxt::kGemmAuto;
   std::mutex mu;
   std::set<Tensor*> tensors;
   std::set<void*> buffers;
+  std::set<Graph*> graphs;
   bool capturing = false;
 };
 
@@ -115,6 +122,26 @@ struct Graph {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 };
+
+// Live handles (contexts, tensors, graphs).  A handle is checked here before
+// use, so releasing a tensor or graph after its context was destroyed (which
+// already released it), or releasing twice, is a no-op instead of a use
+// after free.
+std::mutex g_reg_mu;
+std::unordered_set<const void*> g_live;
+
+void reg_add(const void* p) {
+  std::lock_guard<std::mutex> g(g_reg_mu);
+  g_live.insert(p);
+}
+bool reg_live(const void* p) {
+  std::lock_guard<std::mutex> g(g_reg_mu);
+  return g_live.count(p) != 0;
+}
+bool reg_take(const void* p) {   // removes; true if it was live
+  std::lock_guard<std::mutex> g(g_reg_mu);
+  return g_live.erase(p) != 0;
+}
 
 // ---- error plumbing ---------------------------------------------------------
 
@@ -200,18 +227,32 @@ Tensor* new_tensor(Ctx* c, uint32_t kind, uint32_t rows, uint32_t cols, uint32_t
 }
 
 void register_tensor(Ctx* c, Tensor* t) {
-  std::lock_guard<std::mutex> g(c->mu);
-  c->tensors.insert(t);
+  {
+    std::lock_guard<std::mutex> g(c->mu);
+    c->tensors.insert(t);
+  }
+  reg_add(t);
 }
 
 Tensor* as_tensor(void* p) {
   if (!p) fail(VXT_E_ARG, "null tensor handle");
+  if (!reg_live(p)) fail(VXT_E_ARG, "released or unknown tensor handle");
   return static_cast<Tensor*>(p);
 }
 
 Ctx* as_ctx(void* p) {
   if (!p) fail(VXT_E_ARG, "null context handle");
+  if (!reg_live(p)) fail(VXT_E_ARG, "destroyed or unknown context handle");
   return static_cast<Ctx*>(p);
+}
+
+// Releases one graph (its context's lock held by the caller or unneeded).
+void release_graph(Graph* g) {
+  (void)hipSetDevice(g->ctx->device);
+  (void)hipStreamSynchronize(g->ctx->stream);
+  (void)hipGraphExecDestroy(g->exec);
+  (void)hipGraphDestroy(g->graph);
+  delete g;
 }
 
 // Plane checks of one CodebookMatrix view, as the archive reader does
@@ -249,19 +290,24 @@ void check_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m
 }
 
 // The context workspace (GEMM weight panel and split-K partial sums, gated-FFN
-// staging) is shared by every call of this context (calls are ordered on one
-// stream, or the caller orders them).  It only grows outside a capture: a
-// captured graph keeps the pointer it recorded.
-void ensure_ws(Ctx* c, size_t need) {
+// staging, attention partial sums) is shared by every call of this context
+// (calls are ordered on one stream, or the caller orders them).  It grows only
+// outside a capture, at least doubling, and a replaced buffer is kept until
+// the context is destroyed: any graph captured earlier -- through
+// vxt_hip_capture_begin or the caller's own stream capture -- recorded that
+// buffer's address and may replay it later.  (Doubling bounds the kept
+// buffers by the current one.)
+void ensure_ws(Ctx* c, size_t need, hipStream_t s) {
   if (need <= c->ws_cap) return;
-  if (c->capturing)
-    fail(VXT_E_ARG, "GEMM workspace too small inside a capture: run this shape once before capturing");
-  VXT_HIP_CHECK(hipDeviceSynchronize());   // earlier calls may still read the old workspace
-  if (c->ws) VXT_HIP_CHECK(hipFree(c->ws));
-  c->ws = nullptr;
-  c->ws_cap = 0;
-  VXT_HIP_CHECK(hipMalloc(&c->ws, need));
-  c->ws_cap = need;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (c->capturing || (hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone))
+    fail(VXT_E_ARG, "workspace too small inside a capture: run this shape once before capturing");
+  const size_t n = std::max(need, 2 * c->ws_cap);
+  void* p = nullptr;
+  VXT_HIP_CHECK(hipMalloc(&p, n));
+  if (c->ws) c->retired.push_back(c->ws);
+  c->ws = p;
+  c->ws_cap = n;
 }
 
 void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, void* y,
@@ -276,7 +322,7 @@ void run_matmul(Ctx* c, Tensor* t, const void* x, uint32_t x_dtype, uint32_t m, 
     e = vxt::launch_gemv(d, x, xb, x_vec, m, y, yb, s);
   } else {
     const size_t need = vxt::gemm_workspace_bytes(d, m, xb, c->gemm_mode);
-    ensure_ws(c, need);
+    ensure_ws(c, need, s);
     e = vxt::launch_gemm(d, x, xb, m, y, yb, c->ws, c->ws_cap, s, c->gemm_mode);
   }
   if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
@@ -328,17 +374,27 @@ void* vxt_hip_create(int32_t device, char* dev_name, size_t dev_name_cap, char* 
       std::snprintf(dev_name, dev_name_cap, "%s (%s)", prop.name, prop.gcnArchName);
   });
   if (rc != VXT_OK) return nullptr;
+  vxt::blas_acquire_device(c->device);
+  reg_add(c);
   return c;
 }
 
 void vxt_hip_destroy(void* ctx) {
-  if (!ctx) return;
+  if (!ctx || !reg_take(ctx)) return;   // null, unknown or already destroyed
   Ctx* c = static_cast<Ctx*>(ctx);
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
   {
+    // Everything the context handed out goes with it; those handles become
+    // stale (their release calls are then no-ops).
     std::lock_guard<std::mutex> g(c->mu);
+    for (Graph* gr : c->graphs) {
+      reg_take(gr);
+      release_graph(gr);
+    }
+    c->graphs.clear();
     for (Tensor* t : c->tensors) {
+      reg_take(t);
       (void)hipFree(t->arena);
       delete t;
     }
@@ -349,10 +405,12 @@ void vxt_hip_destroy(void* ctx) {
   if (c->d_x) (void)hipFree(c->d_x);
   if (c->d_y) (void)hipFree(c->d_y);
   if (c->ws) (void)hipFree(c->ws);
+  for (void* b : c->retired) (void)hipFree(b);
   if (c->greedy) (void)hipFree(c->greedy);
   (void)hipEventDestroy(c->ev0);
   (void)hipEventDestroy(c->ev1);
   (void)hipStreamDestroy(c->stream);
+  vxt::blas_release_device(c->device);
   delete c;
 }
 
@@ -513,7 +571,7 @@ void* vxt_hip_clone_tensor(void* tensor, char* err, size_t err_cap) {
 }
 
 void vxt_hip_free_tensor(void* tensor) {
-  if (!tensor) return;
+  if (!tensor || !reg_take(tensor)) return;   // released already (or with its context)
   Tensor* t = static_cast<Tensor*>(tensor);
   Ctx* c = t->ctx;
   (void)hipSetDevice(c->device);
@@ -529,7 +587,7 @@ void vxt_hip_free_tensor(void* tensor) {
 
 int vxt_hip_tensor_info(void* tensor, uint32_t* kind, uint32_t* rows, uint32_t* cols,
                         uint64_t* device_bytes) {
-  if (!tensor) return VXT_E_ARG;
+  if (!tensor || !reg_live(tensor)) return VXT_E_ARG;
   Tensor* t = static_cast<Tensor*>(tensor);
   if (kind) *kind = t->kind;
   if (rows) *rows = t->rows;
@@ -704,7 +762,7 @@ int vxt_hip_ffn_glu_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype
       const size_t gemm_ws =
           batch_m > 8 ? (vxt::gemm_workspace_bytes(d, batch_m, xb, c->gemm_mode) + 255) / 256 * 256 : 0;
       const size_t stage = (size_t)batch_m * t->rows * sizeof(float);
-      ensure_ws(c, gemm_ws + stage);
+      ensure_ws(c, gemm_ws + stage, s);
       float* gu = reinterpret_cast<float*>(static_cast<char*>(c->ws) + gemm_ws);
       if (batch_m <= 8) {
         e = vxt::launch_gemv(d, x, xb, false, batch_m, gu, false, s);
@@ -778,7 +836,7 @@ int vxt_hip_attn_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const float* q, ui
     if (seq_len == 0 || seq_len > kc.max_seq) fail(VXT_E_SHAPE, "need 1 <= seq_len <= max_seq");
     if (n_head == 0 || n_head % kc.n_kv != 0) fail(VXT_E_SHAPE, "n_head must be a multiple of n_kv");
     if (n_head / kc.n_kv > 8) fail(VXT_E_UNSUPPORTED, "at most 8 query heads per kv head");
-    ensure_ws(c, vxt::attn_workspace_bytes(n_head, seq_len, kc.n_kv, kc.hd, 1));
+    ensure_ws(c, vxt::attn_workspace_bytes(n_head, seq_len, kc.n_kv, kc.hd, 1), static_cast<hipStream_t>(stream));
     hipError_t e = vxt::launch_attn(kc, q, n_head, seq_len, 1, gate, out, c->ws, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention launch failed: ") + hipGetErrorString(e));
   });
@@ -858,7 +916,7 @@ int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaP
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (batch_m == 1) {
       // decode: the prep runs inside the attention's chunk kernel
-      ensure_ws(c, vxt::attn_workspace_bytes(n_head, pos + 1, kc.n_kv, kc.hd, 1));
+      ensure_ws(c, vxt::attn_workspace_bytes(n_head, pos + 1, kc.n_kv, kc.hd, 1), s);
       hipError_t e = vxt::launch_attn_step(kc, a, params->rope_dim, params->rope_freq_base, out, c->ws, s);
       if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("attention step launch failed: ") + hipGetErrorString(e));
       return;
@@ -874,7 +932,7 @@ int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaP
       const size_t per_tok = vxt::attn_prefill_workspace_bytes(n_head, kc.hd, pos, batch_m) / batch_m;
       const uint32_t group_t = (uint32_t)std::max<size_t>(
           1, std::min<size_t>(batch_m, ((size_t)256 << 20) / std::max<size_t>(per_tok, 1)));
-      ensure_ws(c, qg_bytes + per_tok * group_t);
+      ensure_ws(c, qg_bytes + per_tok * group_t, s);
       float* q_ws = static_cast<float*>(c->ws);
       a.q_out = q_ws;
       a.gate_out = params->gated_q ? q_ws + (size_t)batch_m * n_head * kc.hd : nullptr;
@@ -892,7 +950,8 @@ int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const VxtGqaP
     const size_t per_tok = vxt::attn_workspace_bytes(n_head, pos + batch_m, kc.n_kv, kc.hd, 1);
     const uint32_t group_m =
         (uint32_t)std::max<size_t>(1, std::min<size_t>(batch_m, ((size_t)16 << 20) / std::max<size_t>(per_tok, 1)));
-    ensure_ws(c, qg_bytes + vxt::attn_workspace_bytes(n_head, pos + batch_m - group_m + 1, kc.n_kv, kc.hd, group_m));
+    ensure_ws(c, qg_bytes + vxt::attn_workspace_bytes(n_head, pos + batch_m - group_m + 1, kc.n_kv, kc.hd, group_m),
+              s);
     float* q_ws = static_cast<float*>(c->ws);
     float* g_ws = params->gated_q ? q_ws + (size_t)batch_m * n_head * kc.hd : nullptr;
     void* part = static_cast<char*>(c->ws) + qg_bytes;
@@ -976,7 +1035,7 @@ void* vxt_hip_device_alloc(void* ctx, size_t bytes, char* err, size_t err_cap) {
 }
 
 void vxt_hip_device_free(void* ctx, void* dev_ptr) {
-  if (!ctx || !dev_ptr) return;
+  if (!ctx || !dev_ptr || !reg_live(ctx)) return;   // a destroyed context freed its buffers
   Ctx* c = static_cast<Ctx*>(ctx);
   (void)hipSetDevice(c->device);
   (void)hipStreamSynchronize(c->stream);
@@ -1004,7 +1063,7 @@ int vxt_hip_memcpy(void* ctx, void* dst, const void* src, size_t bytes, uint32_t
 }
 
 void* vxt_hip_stream(void* ctx) {
-  if (!ctx) return nullptr;
+  if (!ctx || !reg_live(ctx)) return nullptr;
   return static_cast<Ctx*>(ctx)->stream;
 }
 
@@ -1043,6 +1102,11 @@ void* vxt_hip_capture_end(void* ctx, char* err, size_t err_cap) {
       fail(VXT_E_DEVICE, std::string("hipGraphInstantiate failed: ") + hipGetErrorString(e));
     }
     out = new Graph{c, g, ex};
+    {
+      std::lock_guard<std::mutex> lk(c->mu);
+      c->graphs.insert(out);
+    }
+    reg_add(out);
   });
   return out;
 }
@@ -1052,6 +1116,7 @@ int vxt_hip_graph_launch(void* ctx, void* graph, uint32_t replays, double* gpu_m
   return guarded(err, err_cap, [&] {
     Ctx* c = as_ctx(ctx);
     if (!graph) fail(VXT_E_ARG, "null graph");
+    if (!reg_live(graph)) fail(VXT_E_ARG, "released or unknown graph handle");
     Graph* g = static_cast<Graph*>(graph);
     if (g->ctx != c) fail(VXT_E_ARG, "graph belongs to another context");
     use_device(c);
@@ -1067,23 +1132,23 @@ int vxt_hip_graph_launch(void* ctx, void* graph, uint32_t replays, double* gpu_m
 }
 
 void vxt_hip_graph_free(void* graph) {
-  if (!graph) return;
+  if (!graph || !reg_take(graph)) return;   // released already (or with its context)
   Graph* g = static_cast<Graph*>(graph);
-  (void)hipSetDevice(g->ctx->device);
-  (void)hipStreamSynchronize(g->ctx->stream);
-  (void)hipGraphExecDestroy(g->exec);
-  (void)hipGraphDestroy(g->graph);
-  delete g;
+  {
+    std::lock_guard<std::mutex> lk(g->ctx->mu);
+    g->ctx->graphs.erase(g);
+  }
+  release_graph(g);
 }
 
 int vxt_hip_last_kernel_ms(void* ctx, double* ms) {
-  if (!ctx || !ms) return VXT_E_ARG;
+  if (!ctx || !ms || !reg_live(ctx)) return VXT_E_ARG;
   *ms = static_cast<Ctx*>(ctx)->last_ms;
   return VXT_OK;
 }
 
 int vxt_hip_set_gemm_path(void* ctx, uint32_t path) {
-  if (!ctx || path > VXT_GEMM_LIBRARY) return VXT_E_ARG;
+  if (!ctx || path > VXT_GEMM_LIBRARY || !reg_live(ctx)) return VXT_E_ARG;
   Ctx* c = static_cast<Ctx*>(ctx);
   std::lock_guard<std::mutex> lk(c->mu);
   c->gemm_mode = (int)path;

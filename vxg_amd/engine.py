@@ -282,14 +282,15 @@ class GpuPackedTensor:
         return GpuPackedTensor(self._engine, h)
 
     def free(self) -> None:
-        if self.handle:
+        """Release the device copy (a no-op once the engine is closed:
+        closing released it)."""
+        if self.handle and self._engine.ctx:
             load_library().vxt_hip_free_tensor(self.handle)
-            self.handle = None
+        self.handle = None
 
     def __del__(self):
         try:
-            if self.handle and self._engine.ctx:
-                self.free()
+            self.free()
         except Exception:
             pass
 
@@ -406,9 +407,11 @@ class Graph:
         return ms.value
 
     def free(self) -> None:
-        if self.handle:
+        """Release the graph (a no-op once its engine is closed: closing
+        released it)."""
+        if self.handle and self._engine.ctx:
             load_library().vxt_hip_graph_free(self.handle)
-            self.handle = None
+        self.handle = None
 
 
 class HipEngine:
