@@ -179,11 +179,13 @@ VXT_API int vxt_hip_dequant_rows(void* ctx, void* tensor, uint32_t row0, uint32_
 
 /* y[batch_m * rows] (y_dtype) = W x for x[batch_m * cols] (x_dtype).
  * batch_m 1..8 runs the GEMV kernels; larger batch_m the GEMM kernels, which
- * use the context's workspace (weight panel, converted activations, split-K
- * partial sums).  The workspace grows only outside a capture: inside one, a
- * shape that needs more than an earlier eager call allocated fails with
- * VXT_E_ARG.  GEMMs of one context share it; callers order GEMMs they put on
- * different streams. */
+ * use the context's workspace (activation row scales, weight panel,
+ * converted activations, split-K partial sums).  The workspace grows only
+ * outside any stream capture: inside one, a shape that needs more than an
+ * earlier eager call allocated fails with VXT_E_ARG.  A workspace that is
+ * replaced by a larger one stays allocated until vxt_hip_destroy, so graphs
+ * captured earlier keep replaying.  GEMMs of one context share it; callers
+ * order GEMMs they put on different streams. */
 VXT_API int vxt_hip_matmul_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype,
                        uint32_t batch_m, void* y, uint32_t y_dtype, void* stream, char* err,
                        size_t err_cap);
