@@ -190,6 +190,24 @@ VXT_API int vxt_hip_matmul_dev(void* ctx, void* tensor, const void* x, uint32_t 
                        uint32_t batch_m, void* y, uint32_t y_dtype, void* stream, char* err,
                        size_t err_cap);
 
+/* Allocation-free form of vxt_hip_matmul_dev (same arguments, same kernels,
+ * same results).  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory -- code under stream capture whose first
+ * call would otherwise size the workspace, tight serving loops, harnesses
+ * that forbid hipMalloc.  It never calls hipMalloc, hipFree or the vendor
+ * library (a GEMM the context would send to the library's dense phase runs
+ * the own dense kernel instead); its GEMM workspace is a fixed 32 MiB array
+ * in device memory, one per GPU, allocated when the library's code is
+ * loaded on that GPU and held until the process ends.  A GEMM that needs
+ * more (e.g. the two-phase path at batch_m >= 512 on 6144 x 2048) fails
+ * with VXT_E_SHAPE.  Every call on one GPU shares that array: calls that can
+ * overlap on one GPU (different streams, or different contexts on the same
+ * device) race and must be ordered by the caller.  batch_m 1..8 uses no
+ * workspace at all. */
+VXT_API int vxt_hip_matmul_noalloc_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype,
+                                       uint32_t batch_m, void* y, uint32_t y_dtype, void* stream, char* err,
+                                       size_t err_cap);
+
 /* Several tensors sharing one x (forward_multi, llm_cpu.rs:51-71): tensors[i]
  * writes ys[i].  All tensors must have the same cols. */
 VXT_API int vxt_hip_matmul_multi_dev(void* ctx, void* const* tensors, uint32_t n, const void* x,

@@ -37,7 +37,9 @@ struct DevTensor {
 };
 
 // Prefill GEMM path (batch_m > 8): chosen per call, or pinned by the caller.
-enum GemmMode : int { kGemmAuto = 0, kGemmPanel = 1, kGemmFused = 2, kGemmLibrary = 3 };
+// kGemmAutoOwn chooses like kGemmAuto but never the vendor library (whose
+// first call for a shape allocates descriptors).
+enum GemmMode : int { kGemmAuto = 0, kGemmPanel = 1, kGemmFused = 2, kGemmLibrary = 3, kGemmAutoOwn = 4 };
 
 // Centroid table serving `row` (rows of up to 3 concatenated sub-matrices).
 __device__ __forceinline__ uint32_t cent_table(const DevTensor& t, uint32_t row) {

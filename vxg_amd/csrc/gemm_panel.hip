@@ -843,7 +843,7 @@ constexpr uint32_t kLibMinSplitK = 4096;
 
 static bool library_path(const DevTensor& t, uint32_t m, int mode) {
   if (mode == kGemmLibrary) return true;
-  if (mode != kGemmAuto || m <= kFusedMaxM) return false;
+  if (mode != kGemmAuto || m <= kFusedMaxM) return false;   // kGemmAutoOwn: never
   return (size_t)m * t.rows >= kLibMinOutputs || (t.kind == KIND_G64 && t.cols >= kLibMinSplitK);
 }
 

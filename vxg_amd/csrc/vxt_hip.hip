@@ -58,6 +58,14 @@ void blas_acquire_device(int dev);
 void blas_release_device(int dev);
 }  // namespace vxt
 
+// Scratch memory of the allocation-free matmul entry point
+// (vxt_hip_matmul_noalloc_dev): one array per GPU, in the code object, so
+// calls through that entry point never allocate.  Host code reaches it only
+// through the device address hipGetSymbolAddress returns for the current
+// device (kept per context); the name itself is a host-side stand-in.
+constexpr size_t kScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
 namespace {
 
 using vxt::DevTensor;
@@ -109,6 +117,7 @@ struct Ctx {
   size_t ws_cap = 0;
   std::vector<void*> retired;   // replaced workspaces, kept until destroy
   void* greedy = nullptr;  // greedy-selection state words (zero between calls)
+  void* scratch = nullptr; // device address of `scratch` on this context's device
   int gemm_mode = vxt::kGemmAuto;
   std::mutex mu;
   std::set<Tensor*> tensors;
@@ -361,6 +370,7 @@ void* vxt_hip_create(int32_t device, char* dev_name, size_t dev_name_cap, char* 
       VXT_HIP_CHECK(hipEventCreate(&c->ev1));
       VXT_HIP_CHECK(hipMalloc(&c->greedy, vxt::greedy_state_bytes()));
       VXT_HIP_CHECK(hipMemset(c->greedy, 0, vxt::greedy_state_bytes()));
+      VXT_HIP_CHECK(hipGetSymbolAddress(&c->scratch, HIP_SYMBOL(scratch)));   // with `dev` current
     } catch (...) {
       if (c->greedy) (void)hipFree(c->greedy);
       if (c->ev1) (void)hipEventDestroy(c->ev1);
@@ -603,6 +613,37 @@ int vxt_hip_matmul_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype,
     Tensor* t = as_tensor(tensor);
     check_matmul(c, t, x, x_dtype, batch_m, y, y_dtype);
     run_matmul(c, t, x, x_dtype, batch_m, y, y_dtype, static_cast<hipStream_t>(stream));
+  });
+}
+
+int vxt_hip_matmul_noalloc_dev(void* ctx, void* tensor, const void* x, uint32_t x_dtype, uint32_t batch_m,
+                               void* y, uint32_t y_dtype, void* stream, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    Tensor* t = as_tensor(tensor);
+    check_matmul(c, t, x, x_dtype, batch_m, y, y_dtype);
+    const DevTensor d = t->dev();
+    const bool xb = x_dtype == VXT_DTYPE_BF16, yb = y_dtype == VXT_DTYPE_BF16;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    if (batch_m <= 8) {   // the GEMV kernels use no workspace
+      const size_t esz = xb ? 2 : 4;
+      const bool x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t->cols * esz) % 16 == 0;
+      e = vxt::launch_gemv(d, x, xb, x_vec, batch_m, y, yb, s);
+    } else {
+      // The context's path choice, with the library's dense phase replaced by
+      // the own kernel (the library allocates descriptors on first use).
+      const int mode = c->gemm_mode == vxt::kGemmAuto    ? vxt::kGemmAutoOwn
+                       : c->gemm_mode == vxt::kGemmLibrary ? vxt::kGemmPanel
+                                                           : c->gemm_mode;
+      const size_t need = vxt::gemm_workspace_bytes(d, batch_m, xb, mode);
+      if (need > kScratchBytes)
+        fail(VXT_E_SHAPE, "this GEMM needs " + std::to_string(need) + " bytes of scratch; the allocation-free entry "
+                          "point has " + std::to_string(kScratchBytes) + " (use vxt_hip_matmul_dev)");
+      e = vxt::launch_gemm(d, x, xb, batch_m, y, yb, c->scratch, kScratchBytes, s, mode);
+    }
+    if (e == hipErrorNotSupported) fail(VXT_E_UNSUPPORTED, "batch_m > 8 GEMM not available for this tensor");
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("kernel launch failed: ") + hipGetErrorString(e));
   });
 }
 
