@@ -219,7 +219,8 @@ def _stack_layers(eng, kind: str, layers: int, hidden: int, ffn: int, seed: int)
     """Per layer [q;k;v] (3 x hidden rows), o, [gate;up] (2 x ffn rows), down;
     every layer's weights drawn separately.  Returns (layers, weight bytes)."""
     from vxg_amd import stack, synth
-    gen = {"g64": synth.make_g64, "cb4": synth.make_cb4}[kind]
+    # cb4: centred centroid tables keep a 24-layer chain with no norms in range
+    gen = {"g64": synth.make_g64, "cb4": lambda r, c, seed: synth.make_cb4(r, c, seed=seed, centred=True)}[kind]
     lw, nbytes = [], 0
     for li in range(layers):
         s = seed + 10 * li

@@ -530,3 +530,41 @@ def test_gemm_in_captured_graph():
         g.free()
     finally:
         e.close()
+
+@pytest.mark.parametrize("M", [1, 3, 24])
+def test_cb4_zero_scale_group_with_nonfinite_x(eng, M):
+    """codebook.rs:384-386: the CPU GEMV skips a 128-group whose scale is
+    zero, so Inf / NaN activations inside such a group leave the row finite;
+    batch_m <= 8 follows that per token.  The GEMM (batch_m > 8) follows
+    gemm_cpu (llm_prefill.rs:156-255), which decodes the group to zeros and
+    multiplies them: 0 * Inf is NaN there too."""
+    m = synth.make_cb4(40, 512, seed=21, outlier_frac=0.0)
+    sc = m.scales_f16.reshape(40, 4).copy()
+    sc[::2, 1] = 0          # even rows: group 1 (columns 128..255) has scale 0
+    sc[5, 1] = 0x8000       # row 5: -0, which is zero too
+    m.scales_f16 = sc.reshape(-1)
+    t = eng.upload_packed(m)
+    X = synth.make_x_f32(M, 512, seed=M)
+    X[:, 130] = np.inf      # both inside group 1
+    X[:, 200] = np.nan
+    xb = f32_to_bf16_bits(X)
+    Xq = bf16_bits_to_f32(xb).reshape(M, 512)
+    y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    if M <= 8:
+        ref = np.stack([oracle.gemv(m, Xq[i], threads=THREADS) for i in range(M)])
+    else:
+        ref = oracle.gemm(m, Xq, threads=THREADS)
+    fin = np.isfinite(ref)
+    skipped = np.zeros(40, bool)
+    skipped[::2] = True
+    skipped[5] = True
+    if M <= 8:
+        assert np.array_equal(fin, np.broadcast_to(skipped, fin.shape))
+    else:
+        assert not fin.any()
+    assert np.array_equal(np.isfinite(y), fin)
+    W = oracle.decode_rows(m)
+    Xf = np.where(np.isfinite(Xq), Xq, 0)
+    fl = floor_scale(W, Xf)
+    err = np.abs(y[fin].astype(np.float64) - ref[fin]) / np.maximum(np.abs(ref[fin]), fl[fin])
+    assert err.size == 0 or err.max() <= 1e-3

@@ -53,10 +53,18 @@ def make_g64(rows: int, cols: int, seed: int = 1) -> Cb4G64Matrix:
 
 
 def make_cb4(rows: int, cols: int, seed: int = 2, outlier_frac: float = 0.0074,
-             pad_to: int = 256) -> CodebookMatrix:
+             pad_to: int = 256, centred: bool = False) -> CodebookMatrix:
+    """Reference cb4 layout.  ``centred``: subtract the table's mean from the
+    16 centroids.  A shared table with a non-zero mean gives every row the same
+    bias, so a long chain of projections with no norms between them (the
+    matmul-only decode stack) grows the activations' common part by about
+    0.01 * mean * K per projection until it overflows; a centred table keeps
+    such a chain in range."""
     g = rng(seed)
     kp = (cols + pad_to - 1) // pad_to * pad_to
     cent = np.sort(g.normal(0.0, 1.0, size=16).astype(np.float32))
+    if centred:
+        cent = np.sort((cent - cent.mean()).astype(np.float32))
     scales = f32_to_f16_bits(g.uniform(0.002, 0.02, size=rows * (kp // 128)).astype(np.float32))
     words = g.integers(0, 2**32, size=rows * kp // 8, dtype=np.uint64).astype(np.uint32)
     counts = g.binomial(cols, outlier_frac, size=rows).astype(np.int64)
