@@ -568,3 +568,26 @@ def test_cb4_zero_scale_group_with_nonfinite_x(eng, M):
     fl = floor_scale(W, Xf)
     err = np.abs(y[fin].astype(np.float64) - ref[fin]) / np.maximum(np.abs(ref[fin]), fl[fin])
     assert err.size == 0 or err.max() <= 1e-3
+
+
+@pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
+@pytest.mark.parametrize("rows,cols", [(7, 4100), (300, 6144), (65, 9000)])
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_gemv_split_k_shapes(eng, kind, rows, cols, xdt):
+    """M = 1 with K of two or more 2048-column steps and at most 4096 rows
+    takes the split-K kernel (the K steps of a row on separate waves, summed
+    in wave order): ragged K, a few rows, cb4 residuals anywhere in the row."""
+    m = make(kind, rows, cols, seed=rows + cols)
+    t = eng.upload_packed(m)
+    if xdt == "bf16":
+        xh = synth.make_x_bf16(1, cols, seed=3)
+        X = bf16_bits_to_f32(xh).reshape(1, cols)
+        y = run_dev(eng, t, xh, engine.DTYPE_BF16, 1, engine.DTYPE_F32)
+    else:
+        X = synth.make_x_f32(1, cols, seed=3)
+        y = run_dev(eng, t, X, engine.DTYPE_F32, 1, engine.DTYPE_F32)
+    ref = gemv_ref(m, X)
+    assert max_rel(y, ref, floor_scale(oracle.decode_rows(m), X)) <= 1e-3
+    y2 = run_dev(eng, t, xh if xdt == "bf16" else X, engine.DTYPE_BF16 if xdt == "bf16" else engine.DTYPE_F32, 1,
+                 engine.DTYPE_F32)
+    assert_bits_equal(y2, y)   # deterministic: the waves' sums are added in a fixed order

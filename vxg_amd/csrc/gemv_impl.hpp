@@ -26,6 +26,7 @@
 // to fp32 rounding (the parity bar is relative error, not bits).
 #pragma once
 #include <algorithm>
+#include <cstdlib>
 
 #include "act.hpp"
 #include "common.hpp"
@@ -332,14 +333,19 @@ __device__ __forceinline__ void read_x_lds(const uint16_t* s_xn, uint32_t k0, fl
 // wave, up to S steps per batch.  Gated epilogues take n_ff and the output
 // row stride; the plain epilogue ignores both.  NORM: the norm prologue above
 // (MT = 1, bf16 x staged in dynamic LDS of nsteps * kStep elements).
+// KS > 1 (split K): the workgroup's KS waves share its RPW rows, wave w
+// taking the K steps w, w + KS, ...; their sums are added through LDS in
+// wave order (deterministic), so a matrix of few rows and long K spreads over
+// KS times more waves, each with a KS times shorter chain after its data.
 template <uint32_t KIND, int MT, int RPW, int S, bool XBF16, int EPI = kEpiPlain, bool NORM = false,
-          uint32_t NP = kNormPer>
+          uint32_t NP = kNormPer, int KS = 1>
 __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const void* __restrict__ x,
                                                           void* __restrict__ y, uint32_t M_rt,
                                                           uint32_t y_bf16, uint32_t x_vec, uint32_t n_ff = 0,
                                                           uint32_t y_stride = 0, NormIn nin = {}) {
   static_assert(EPI == kEpiPlain || RPW % 2 == 0, "gated rows come in gate/up pairs");
   static_assert(!NORM || (MT == 1 && XBF16), "the norm prologue serves one token with bf16 x");
+  static_assert(KS == 1 || (S == 1 && EPI == kEpiPlain && !NORM && KS <= kWaves), "split K: plain, one step a batch");
   extern __shared__ __attribute__((aligned(16))) uint16_t s_xn[];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
   constexpr int NB = (RPW + 1) / 2;   // g64 table blocks per wave
@@ -349,7 +355,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = threadIdx.x >> 6;
   constexpr uint32_t kOut = EPI == kEpiPlain ? RPW : RPW / 2;   // outputs per wave
-  const uint32_t first = (blockIdx.x * kWaves + wave) * kOut;
+  const uint32_t first = KS > 1 ? blockIdx.x * kOut : (blockIdx.x * kWaves + wave) * kOut;
   const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
   const uint32_t nsteps = (kp + kStep - 1) / kStep;
   constexpr bool kLateX = MT >= 4;
@@ -401,7 +407,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
-  for (uint32_t s0 = 0; s0 < nsteps; s0 += S) {
+  for (uint32_t s0 = KS > 1 ? wave : 0u; s0 < nsteps; s0 += KS > 1 ? (uint32_t)KS : (uint32_t)S) {
     const uint32_t ns = nsteps - s0 < (uint32_t)S ? nsteps - s0 : (uint32_t)S;   // uniform
     // ---- issue: activations, then weights, for every step of the batch
     XChunk<XBF16> xc[kLateX ? 1 : S][kLateX ? 1 : MT];
@@ -427,10 +433,10 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
       }
     }
     if constexpr (KIND == KIND_CB4) {
-      if (s0 == 0) {   // clamped, unconditional (the CSR stream holds at least one word)
+      if (s0 == (KS > 1 ? wave : 0u)) {   // clamped, unconditional (the CSR stream holds at least one word)
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-          const uint32_t i = os[r] + lane;
+          const uint32_t i = os[r] + (KS > 1 ? wave * 64u : 0u) + lane;
           const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
           pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
         }
@@ -507,15 +513,17 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
 
   if constexpr (KIND == KIND_CB4) {
     // CSR residuals (codebook.rs:409-415): y += f16(res) * x[col]; lane l
-    // takes entries l, l + 64, ... of the row, in that order.
+    // takes entries l, l + 64, ... of the row, in that order (split K: wave
+    // w takes entries 64 w + l, stepping by 64 KS).
+    const uint32_t r_first = KS > 1 ? wave * 64u : 0u;
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       if (!rv[r]) {
         if constexpr (EPI == kEpiPlain) break;   // later rows are past the end too
         continue;
       }
-      for (uint32_t i = os[r] + lane; i < oe[r]; i += 64) {
-        const uint32_t pk = i < os[r] + 64 ? pk0[r] : t.outliers[i];
+      for (uint32_t i = os[r] + r_first + lane; i < oe[r]; i += 64u * KS) {
+        const uint32_t pk = i < os[r] + r_first + 64 ? pk0[r] : t.outliers[i];
         const uint32_t col = pk & 0xffffu;
         if (col >= cols) continue;
         const float val = f16_to_f32(pk >> 16);
@@ -535,7 +543,32 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
     }
   }
 
-  if constexpr (EPI == kEpiPlain) {
+  if constexpr (KS > 1) {   // the waves' sums, added in wave order
+    __shared__ float s_part[KS > 1 ? KS * RPW * MT : 1];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        const float v = wave_sum(acc[r][m]);
+        if (lane == 0) s_part[(wave * RPW + r) * MT + m] = v;
+      }
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) {
+        float v = s_part[r * MT + m];
+#pragma unroll
+        for (int w = 1; w < KS; ++w) v += s_part[(w * RPW + r) * MT + m];
+        if (lane == 0 && rv[r] && (uint32_t)m < M_rt) {
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * rows + rr[r]] = f32_to_bf16(v);
+          else
+            static_cast<float*>(y)[(size_t)m * rows + rr[r]] = v;
+        }
+      }
+  } else if constexpr (EPI == kEpiPlain) {
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
 #pragma unroll
@@ -1068,7 +1101,49 @@ hipError_t launch_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool
   return hipGetLastError();
 }
 
+// Split K over KS waves per workgroup (rows shared, one step per wave).
+template <uint32_t KIND, int MT, int RPW, bool XBF16, int KS>
+hipError_t launch_ks(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  const dim3 grid((t.rows + RPW - 1) / RPW);
+  const size_t esz = XBF16 ? 2 : 4;
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && t.cols % 8 == 0 &&
+                         ((size_t)t.cols * esz) % 16 == 0;
+  hipLaunchKernelGGL((gemv_kernel<KIND, MT, RPW, 1, XBF16, kEpiPlain, false, kNormPer, KS>), grid, dim3(KS * 64), 0,
+                     s, t, x, y, m, (uint32_t)(y_bf16 ? 1u : 0u), x_vec);
+  return hipGetLastError();
+}
+
+// Split K pays where a matrix has few rows for its K and at least two K
+// steps: one wave per step of every row, up to 4.  Measured (M = 1, bf16 x):
+// 2048 x 6144 g64 6.27 -> 5.61 us, Q8 6.20 -> 5.96; 1024 x 8192 g64 6.09 ->
+// 4.18; 2048 x 4096 Q8 with f32 x 9.9 -> 9.7; at 4096 rows it was level or
+// slower (and slower for Q8 with f32 x, whose one-row waves lose the
+// four-row waves' reuse of x).
+template <uint32_t KIND, int MT, bool XBF16>
+bool try_split_k(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s,
+                 hipError_t* e) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (nsteps < 2 || t.rows > 2048) return false;
+  // cb4: each workgroup stages its centroid tables behind a barrier, which
+  // costs more with three times the workgroups; measured slower at 2048 rows
+  // (6.2 -> 7.1 us at K = 6144), faster at 1024 x 8192 (6.3 -> 4.9 us).
+  if (KIND == KIND_CB4 && (t.rows > 1024 || nsteps < 4)) return false;
+  if (nsteps == 2) *e = launch_ks<KIND, MT, 1, XBF16, 2>(t, x, m, y, y_bf16, s);
+  else if (nsteps == 3) *e = launch_ks<KIND, MT, 1, XBF16, 3>(t, x, m, y, y_bf16, s);
+  else *e = launch_ks<KIND, MT, 1, XBF16, 4>(t, x, m, y, y_bf16, s);
+  return true;
+}
+
 // Steps per batch: all of K at once up to 3 steps (K <= 6144), else 2.
+// VXT_GEMV_SPLIT_K=0 in the environment turns split K off (for comparisons).
+inline bool split_k_enabled() {
+  static const bool on = [] {
+    const char* v = getenv("VXT_GEMV_SPLIT_K");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 template <uint32_t KIND, int MT, int RPW, bool XBF16>
 hipError_t launch_s(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
   const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
@@ -1098,6 +1173,12 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
       if (m <= 8) return launch_q8_dot2_m<8>(t, x, m, y, y_bf16, s);
       return hipErrorInvalidValue;
     }
+  }
+  if (m == 1 && split_k_enabled()) {
+    hipError_t e = hipSuccess;
+    if (x_bf16 ? try_split_k<KIND, 1, true>(t, x, m, y, y_bf16, s, &e)
+               : try_split_k<KIND, 1, false>(t, x, m, y, y_bf16, s, &e))
+      return e;
   }
   if (m == 1) {
     // Q8 with f32 activations: four rows per wave halve the activation bytes
