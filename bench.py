@@ -37,6 +37,7 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0       # dense bf16 / fp16 MFMA
 MALL_BYTES = 256 << 20          # Infinity Cache
 METRIC = "decode GEMV HBM GB/s (% of peak) + prefill GEMM TFLOP/s, 1×MI355X"
+EAGER = False   # --eager: plain launches instead of graph replays, for profilers
 
 # HBM bytes per launch of the headline kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
@@ -131,6 +132,8 @@ def time_graph(eng, enqueue, steps: int, warmup: int, n_copies: int = 1):
 
     Returns (wall seconds, GPU ms from the hipEvent pair on the launch stream).
     """
+    if EAGER:
+        return time_eager(eng, enqueue, steps, warmup, n_copies)
     s = eng.stream
     for i in range(max(warmup, 1)):                   # eager warm-up
         enqueue(i, s)
@@ -188,6 +191,43 @@ def bench_gemv(eng, m, M: int, x_dtype: str, y_dtype: str, steps: int, warmup: i
         "GBps": nbytes * steps / wall_s / 1e9, "kernel_GBps": nbytes / (kern_ms * 1e-3) / 1e9,
         "flops_per_call": 2 * M * m.rows * m.cols,
     }
+
+
+def bench_floor(eng, nbytes: int, steps: int, warmup: int):
+    """The HBM floor of one launch that reads `nbytes` (vxt_hip_read_probe_dev:
+    the GEMV's access pattern, no arithmetic), over rotating buffers as the
+    GEMV lines rotate weight copies."""
+    nbytes = (nbytes + 15) // 16 * 16
+    n_copies = max(2, math.ceil(2.5 * MALL_BYTES / nbytes))
+    bufs = [eng.alloc(nbytes) for _ in range(n_copies)]
+    for b in bufs:
+        b.upload(np.full(nbytes // 4, 0x3c003c00, np.uint32))
+
+    def enqueue(i, stream):   # one repeated word: every lane's xor fold is 0, never the key 1
+        eng.read_probe_dev(bufs[i % n_copies].ptr, nbytes, 1, stream)
+
+    wall_s, ev_ms = time_graph(eng, enqueue, steps, warmup, n_copies)
+    for b in bufs:
+        b.free()
+    kern_ms = ev_ms / steps
+    return {"bytes": nbytes, "kernel_ms": kern_ms, "GBps": nbytes / (kern_ms * 1e-3) / 1e9}
+
+
+def time_eager(eng, enqueue, steps: int, warmup: int, n_copies: int = 1):
+    """time_graph's protocol with plain launches (for profilers that do not
+    follow graph replays): wall seconds for both returns."""
+    s = eng.stream
+    for i in range(max(warmup, 1)):
+        enqueue(i, s)
+    for i in range(n_copies):
+        enqueue(i, s)
+    eng.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        enqueue(i, s)
+    eng.synchronize()
+    t1 = time.perf_counter()
+    return (t1 - t0), (t1 - t0) * 1e3
 
 
 def bench_gemm(eng, m, M: int, steps: int, warmup: int, seed: int = 0):
@@ -398,14 +438,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="0,r,g,2,3,4,s,a",
-                    help="secondary configurations to run (s: whole decode step on config 4's weights, "
-                         "a: KV-Q8 decode attention)")
+    ap.add_argument("--configs", default="f,0,r,g,2,3,4,s,a",
+                    help="secondary configurations to run (f: HBM streaming floor at the configs' sizes, "
+                         "s: whole decode step on config 4's weights, a: KV-Q8 decode attention)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
-                    help="time configs s and a with plain launches instead of graph replays (for profilers)")
+                    help="time with plain launches instead of graph replays (for profilers: rocprofv3's kernel "
+                         "tracer has crashed inside hipGraphLaunch after many GEMM graphs; `value` is then not "
+                         "the graph-timed number)")
     args = ap.parse_args()
 
+    global EAGER
+    EAGER = args.eager
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build runs on a single MI355X and has no "
               f"multi-GPU path (asked for --gpus {args.gpus}); run with --gpus 1.", file=sys.stderr)
@@ -426,6 +470,17 @@ def main():
 
     secondary = []
     run = set() if args.quick else {c.strip() for c in args.configs.split(",")}
+    if "f" in run:
+        # the streaming floor at the headline's and other configs' sizes
+        for label, nb in (("config 1 (g64 6144x2048)", 12611584), ("config 1 cb4-ref", 6905860),
+                          ("config 0 (Q8 4096x4096)", 17858560), ("config 2 Q8 2048x2048", 4456448),
+                          ("config 2 Q8 2048x6144", 13369344), ("50 MB", 50331648),
+                          ("config 2 LM head", 330612736)):
+            rf = bench_floor(eng, nb, max(20, min(args.steps, int(3e9 / nb))), min(args.warmup, 5))
+            secondary.append({"config": f"streaming floor (read-only probe) at {label}: {rf['bytes']} B",
+                              "kernel_us": round(rf["kernel_ms"] * 1e3, 3), "GBps": round(rf["GBps"], 1),
+                              "frac_hbm": round(rf["GBps"] / HBM_PEAK_GBS, 4)})
+            log(f"  floor {label}: {rf['kernel_ms']*1e3:.2f} us ({rf['GBps']:.1f} GB/s)")
     if "0" in run:
         m0 = synth.make_q8(4096, 4096, seed=0)
         log("config 0: Q8 GEMV M=1 K=N=4096 x f32")

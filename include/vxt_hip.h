@@ -420,6 +420,15 @@ VXT_API int vxt_hip_embed_dev(void* ctx, void* tensor, const uint32_t* tokens, u
 VXT_API int vxt_hip_greedy_dev(void* ctx, const float* logits, uint32_t n, uint32_t* out, void* stream,
                                char* err, size_t err_cap);
 
+/* Measurement only, no counterpart in the reference: reads [p, p + bytes)
+ * (device memory, bytes a multiple of 16) once with the decode GEMV's access
+ * pattern and no arithmetic -- the HBM floor of a single launch that size.
+ * Each lane folds its words by xor; `key` must be a value no lane's fold of
+ * the buffer gives (e.g. 1 for a buffer of one repeated 32-bit word, whose
+ * folds are 0). */
+VXT_API int vxt_hip_read_probe_dev(void* ctx, const void* p, size_t bytes, uint32_t key, void* stream, char* err,
+                                   size_t err_cap);
+
 /* ---- device memory, stream and graphs ---------------------------------- */
 /* What a host without another GPU runtime (the Rust engine, C callers) needs
  * to keep activations resident and to replay a decode loop without per-launch

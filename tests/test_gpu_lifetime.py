@@ -101,3 +101,20 @@ def test_workspace_growth_inside_capture_is_refused():
         g.free()
     finally:
         eng.close()
+
+
+def test_read_probe_runs_and_checks_sizes():
+    """The streaming-floor probe reads a buffer and rejects sizes that are not
+    a positive multiple of 16."""
+    eng = engine.HipEngine(0)
+    try:
+        b = eng.alloc(1 << 20)
+        eng.read_probe_dev(b.ptr, 1 << 20, 1, eng.stream)
+        eng.synchronize()
+        for bad in (0, 100):
+            with pytest.raises(engine.BackendError) as ei:
+                eng.read_probe_dev(b.ptr, bad, 1, eng.stream)
+            assert ei.value.code == engine.VXT_E_SHAPE
+        b.free()
+    finally:
+        eng.close()

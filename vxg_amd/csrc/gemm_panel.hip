@@ -97,68 +97,104 @@ __device__ __forceinline__ void split_write(float w, float s, uint16_t* hi, uint
 // ---- phase 1: activations and panel -----------------------------------------
 
 // Activation conversion, run by the first `blocks` workgroups of the panel
-// launch: X [M][K] (bf16 or f32) -> A [M][kp] f16, zero for k >= K; f32 X
-// also gets the lo plane (x - hi) * 2^11.  One thread per 8 columns.
+// launch, one activation row per workgroup at a time: the row's largest
+// magnitude first (its exponent xe[m] puts it in [2^14, 2^15): 0 for a row
+// that is all zero or holds Inf / NaN), then X[m] * 2^xe[m] -> A [M][kp] f16,
+// zero for k >= K; f32 X also gets the lo plane (x - hi) * 2^11.  One thread
+// per 8 columns.
 struct XConv {
   const void* x;
   uint16_t* ah;
   uint16_t* al;
-  const int32_t* xe;   // per-row exponent: X[m] * 2^xe[m] is converted
+  int32_t* xe;   // per-row exponent, written here
   uint32_t m, cols, x_bf16, x_vec, blocks;
 };
 
+// 8 activations at column k of row m (zero past K).
+template <bool XBF16>
+__device__ __forceinline__ void load8(const void* __restrict__ x, uint32_t K, uint32_t x_vec, uint32_t m, uint32_t k,
+                                      float (&v)[8]) {
+  if (x_vec && k + 8 <= K) {
+    if constexpr (XBF16) {
+      const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + (size_t)m * K + k);
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[2 * j] = __uint_as_float(w[j] << 16);
+        v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    } else {
+      const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + (size_t)m * K + k);
+      const float4 f0 = f[0], f1 = f[1];
+      v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
+      v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float f = 0.0f;
+      if (k + j < K) {
+        if constexpr (XBF16)
+          f = bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k + j]);
+        else
+          f = static_cast<const float*>(x)[(size_t)m * K + k + j];
+      }
+      v[j] = f;
+    }
+  }
+}
+
+// Exponent that puts `b` (a row's largest magnitude; Inf for non-finite
+// rows) in [2^14, 2^15), or 0.
+__device__ __forceinline__ int row_exponent(float b) {
+  return (b > 0.0f && b <= 3.4028234663852886e38f) ? 14 - ilogbf(b) : 0;
+}
+
+__device__ __forceinline__ float abs_or_inf(float v) {
+  const float a = fabsf(v);
+  return a != a ? __builtin_inff() : a;   // NaN counts as non-finite
+}
+
 template <bool XBF16>
 __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
+  __shared__ float s_max[THREADS / 64];
   const void* __restrict__ x = c.x;
   uint16_t* __restrict__ ah = c.ah;
   uint16_t* __restrict__ al = c.al;
   const uint32_t K = c.cols, x_vec = c.x_vec;
-  const uint32_t ppr = kp / 8;
-  const size_t pieces = (size_t)c.m * ppr;
-  for (size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x; i < pieces; i += (size_t)c.blocks * THREADS) {
-    const uint32_t m = (uint32_t)(i / ppr), k = (uint32_t)(i % ppr) * 8;
-    float v[8];
-    if (x_vec && k + 8 <= K) {
-      if constexpr (XBF16) {
-        const uint4 u = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + (size_t)m * K + k);
-        const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+  for (uint32_t m = blockIdx.x; m < c.m; m += c.blocks) {
+    float mx = 0.0f;
+    for (uint32_t k = threadIdx.x * 8; k < K; k += THREADS * 8) {
+      float v[8];
+      load8<XBF16>(x, K, x_vec, m, k, v);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[2 * j] = __uint_as_float(w[j] << 16);
-          v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
-        }
-      } else {
-        const float4* f = reinterpret_cast<const float4*>(static_cast<const float*>(x) + (size_t)m * K + k);
-        const float4 f0 = f[0], f1 = f[1];
-        v[0] = f0.x; v[1] = f0.y; v[2] = f0.z; v[3] = f0.w;
-        v[4] = f1.x; v[5] = f1.y; v[6] = f1.z; v[7] = f1.w;
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float f = 0.0f;
-        if (k + j < K) {
-          if constexpr (XBF16)
-            f = bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k + j]);
-          else
-            f = static_cast<const float*>(x)[(size_t)m * K + k + j];
-        }
-        v[j] = f;
-      }
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
     }
-    const int e = c.xe[m];
+    mx = lane_reduce<64, true>(mx);
+    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = mx;
+    __syncthreads();
+    float b = s_max[0];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = ldexpf(v[j], e);   // exact (a power of two)
-    uint32_t h[4], l[4];
+    for (int w = 1; w < THREADS / 64; ++w) b = fmaxf(b, s_max[w]);
+    const int e = row_exponent(b);
+    if (threadIdx.x == 0) c.xe[m] = e;
+    __syncthreads();   // s_max is reused by the next row
+    for (uint32_t k = threadIdx.x * 8; k < kp; k += THREADS * 8) {
+      float v[8];
+      load8<XBF16>(x, K, x_vec, m, k, v);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
-      h[j] = pack_h2(h0, h1);
-      if constexpr (!XBF16)
-        l[j] = pack_h2((_Float16)((v[2 * j] - (float)h0) * kLoScale), (_Float16)((v[2 * j + 1] - (float)h1) * kLoScale));
+      for (int j = 0; j < 8; ++j) v[j] = ldexpf(v[j], e);   // exact (a power of two)
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
+        h[j] = pack_h2(h0, h1);
+        if constexpr (!XBF16)
+          l[j] = pack_h2((_Float16)((v[2 * j] - (float)h0) * kLoScale), (_Float16)((v[2 * j + 1] - (float)h1) * kLoScale));
+      }
+      *reinterpret_cast<uint4*>(ah + (size_t)m * kp + k) = make_uint4(h[0], h[1], h[2], h[3]);
+      if constexpr (!XBF16) *reinterpret_cast<uint4*>(al + (size_t)m * kp + k) = make_uint4(l[0], l[1], l[2], l[3]);
     }
-    *reinterpret_cast<uint4*>(ah + (size_t)m * kp + k) = make_uint4(h[0], h[1], h[2], h[3]);
-    if constexpr (!XBF16) *reinterpret_cast<uint4*>(al + (size_t)m * kp + k) = make_uint4(l[0], l[1], l[2], l[3]);
   }
 }
 
@@ -168,29 +204,21 @@ __device__ __forceinline__ float wave_add(float v) { return lane_reduce<64>(v); 
 // Per activation row m: xe[m] such that the row's largest magnitude times
 // 2^xe[m] lies in [2^14, 2^15), so the f16 operands neither overflow nor
 // (for bf16 X) round; 0 for a row that is all zero or holds Inf or NaN (those
-// propagate as in the reference's f32 arithmetic).  One workgroup per row.
-__global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict__ x, uint32_t x_bf16, uint32_t M,
-                                                         uint32_t K, int32_t* __restrict__ xe) {
-  __shared__ float s_max[THREADS / 64];
-  for (uint32_t m = blockIdx.x; m < M; m += gridDim.x) {
-    float mx = 0.0f;
-    for (uint32_t k = threadIdx.x; k < K; k += THREADS) {
-      const float v = x_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k])
-                             : static_cast<const float*>(x)[(size_t)m * K + k];
-      const float a = fabsf(v);
-      mx = fmaxf(mx, a != a ? __builtin_inff() : a);   // NaN counts as non-finite
-    }
-    mx = wave_max(mx);
-    if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = mx;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      float b = s_max[0];
+// propagate as in the reference's f32 arithmetic).  One wave per row.
+template <bool XBF16>
+__global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict__ x, uint32_t M, uint32_t K,
+                                                         uint32_t x_vec, int32_t* __restrict__ xe) {
+  const uint32_t m = blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (m >= M) return;
+  float mx = 0.0f;
+  for (uint32_t k = lane * 8; k < K; k += 64 * 8) {
+    float v[8];
+    load8<XBF16>(x, K, x_vec, m, k, v);
 #pragma unroll
-      for (int w = 1; w < THREADS / 64; ++w) b = fmaxf(b, s_max[w]);
-      xe[m] = (b > 0.0f && b <= 3.4028234663852886e38f) ? 14 - ilogbf(b) : 0;
-    }
-    __syncthreads();
+    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
   }
+  mx = lane_reduce<64, true>(mx);
+  if (lane == 0) xe[m] = row_exponent(mx);
 }
 
 // 8 consecutive f32 weights -> hi (and lo) f16 pieces at column c of the row.
@@ -766,9 +794,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t.cols * esz) % 16 == 0;
   // One launch: the activation conversion's workgroups first, then one
   // wave per (weight row, 2048-column segment) of the panel decode.
-  const size_t pieces = (size_t)m * (pl.kp / 8);
-  XConv xc{x, ah, al, xe, m, t.cols, (uint32_t)x_bf16, x_vec,
-           (uint32_t)std::min<size_t>((pieces + THREADS - 1) / THREADS, 1024)};
+  XConv xc{x, ah, al, const_cast<int32_t*>(xe), m, t.cols, (uint32_t)x_bf16, x_vec, std::min<uint32_t>(m, 1024u)};
   const uint32_t nseg = (p.kp + 64 * 32 - 1) / (64 * 32);
   const uint32_t pgrid = (uint32_t)(((size_t)t.rows * nseg + 3) / 4);
   hipLaunchKernelGGL((panel_kernel<KIND>), dim3(xc.blocks + pgrid), dim3(THREADS), 0, s, t, p,
@@ -807,8 +833,13 @@ hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float
 
 // Per-row activation exponents (xscale_kernel) into xe[m].
 hipError_t launch_xscale(const void* x, bool x_bf16, uint32_t m, uint32_t k, int32_t* xe, hipStream_t s) {
-  hipLaunchKernelGGL(gp::xscale_kernel, dim3(std::min<uint32_t>(m, 4096u)), dim3(gp::THREADS), 0, s, x,
-                     (uint32_t)x_bf16, m, k, xe);
+  const size_t esz = x_bf16 ? 2 : 4;
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)k * esz) % 16 == 0;
+  const dim3 grid((m + gp::THREADS / 64 - 1) / (gp::THREADS / 64));
+  if (x_bf16)
+    hipLaunchKernelGGL(gp::xscale_kernel<true>, grid, dim3(gp::THREADS), 0, s, x, m, k, x_vec, xe);
+  else
+    hipLaunchKernelGGL(gp::xscale_kernel<false>, grid, dim3(gp::THREADS), 0, s, x, m, k, x_vec, xe);
   return hipGetLastError();
 }
 
@@ -864,9 +895,11 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   void* rest = static_cast<char*>(ws) + xe_bytes(m);
   const size_t rest_bytes = ws_bytes - xe_bytes(m);
   const bool fused = fused_path(t, m, x_bf16, mode);
-  // f16 operands need the activations' row scales (the fused Q8 kernel
-  // multiplies bf16 activations as they are).
-  if (!fused || gemm_fused_scales_x(t)) {
+  // f16 operands need the activations' row scales: the two-phase path's
+  // activation conversion finds them itself; the fused g64 kernel takes
+  // them from this pre-pass (the fused Q8 kernel multiplies bf16 activations
+  // as they are).
+  if (fused && gemm_fused_scales_x(t)) {
     const hipError_t e = launch_xscale(x, x_bf16, m, t.cols, xe, s);
     if (e != hipSuccess) return e;
   }

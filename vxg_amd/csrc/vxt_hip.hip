@@ -54,6 +54,7 @@ hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* ga
                                uint32_t pos0, uint32_t batch, void* ws, hipStream_t s);
 size_t greedy_state_bytes();
 hipError_t launch_greedy(const float* logits, uint32_t n, void* state, uint32_t* out, hipStream_t s);
+hipError_t launch_read_probe(const void* p, size_t bytes, uint32_t* sink, uint32_t key, hipStream_t s);
 void blas_acquire_device(int dev);
 void blas_release_device(int dev);
 }  // namespace vxt
@@ -1058,6 +1059,19 @@ int vxt_hip_greedy_dev(void* ctx, const float* logits, uint32_t n, uint32_t* out
     if (n > 0x7fffffffu) fail(VXT_E_SHAPE, "more than 2^31 - 1 logits");
     hipError_t e = vxt::launch_greedy(logits, n, c->greedy, out, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("greedy launch failed: ") + hipGetErrorString(e));
+  });
+}
+
+int vxt_hip_read_probe_dev(void* ctx, const void* p, size_t bytes, uint32_t key, void* stream, char* err,
+                           size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!p) fail(VXT_E_ARG, "null pointer");
+    if (bytes < 16 || bytes % 16 != 0) fail(VXT_E_SHAPE, "bytes must be a positive multiple of 16");
+    // the sink word: the greedy state's last word, never written by the probe
+    uint32_t* sink = reinterpret_cast<uint32_t*>(static_cast<char*>(c->greedy) + vxt::greedy_state_bytes()) - 1;
+    const hipError_t e = vxt::launch_read_probe(p, bytes, sink, key, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) fail(VXT_E_DEVICE, std::string("probe launch failed: ") + hipGetErrorString(e));
   });
 }
 

@@ -60,7 +60,7 @@ ABI_SYMBOLS = (
     "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
     "vxt_hip_vxt_parse", "vxt_hip_upload_vxt_entry", "vxt_hip_gguf_parse", "vxt_hip_upload_gguf_q8_0",
     "vxt_hip_kv_q8_append_dev", "vxt_hip_attn_q8_dev", "vxt_hip_attn_prep_q8_dev", "vxt_hip_attn_step_q8_dev",
-    "vxt_hip_matmul_noalloc_dev", "vxt_hip_last_kernel_ms", "vxt_hip_set_gemm_path", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
+    "vxt_hip_matmul_noalloc_dev", "vxt_hip_read_probe_dev", "vxt_hip_last_kernel_ms", "vxt_hip_set_gemm_path", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free",
 )
@@ -168,6 +168,8 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_dequant_rows.argtypes = [vp, vp, u32, u32, vp, cp, sz]
     L.vxt_hip_matmul_dev.restype = C.c_int
     L.vxt_hip_matmul_dev.argtypes = [vp, vp, vp, u32, u32, vp, u32, vp, cp, sz]
+    L.vxt_hip_read_probe_dev.restype = C.c_int
+    L.vxt_hip_read_probe_dev.argtypes = [vp, vp, sz, u32, vp, cp, sz]
     L.vxt_hip_matmul_noalloc_dev.restype = C.c_int
     L.vxt_hip_matmul_noalloc_dev.argtypes = [vp, vp, vp, u32, u32, vp, u32, vp, cp, sz]
     L.vxt_hip_matmul_multi_dev.restype = C.c_int
@@ -601,6 +603,12 @@ class HipEngine:
         buf = _errbuf()
         _check(load_library().vxt_hip_matmul_dev(self.ctx, t.handle, x_ptr, x_dtype, batch_m,
                                                  y_ptr, y_dtype, stream or None, buf, len(buf)), buf)
+
+    def read_probe_dev(self, ptr: int, nbytes: int, key: int = 1, stream: int = 0) -> None:
+        """``vxt_hip_read_probe_dev``: read nbytes at ptr once (HBM floor probe)."""
+        buf = _errbuf()
+        _check(load_library().vxt_hip_read_probe_dev(self.ctx, ptr, int(nbytes), int(key), stream or None, buf,
+                                                     len(buf)), buf)
 
     def matmul_noalloc_dev(self, t: GpuPackedTensor, x_ptr: int, x_dtype: int, batch_m: int, y_ptr: int,
                            y_dtype: int, stream: int = 0) -> None:
