@@ -211,11 +211,38 @@ __global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict_
   const uint32_t m = blockIdx.x * (THREADS / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (m >= M) return;
   float mx = 0.0f;
-  for (uint32_t k = lane * 8; k < K; k += 64 * 8) {
-    float v[8];
-    load8<XBF16>(x, K, x_vec, m, k, v);
+  // four 8-column pieces per lane in flight before any is used (a round
+  // covers 2048 columns, one round trip); the loads are unconditional from
+  // clamped addresses and columns past K are masked after them
+  if (x_vec) {   // uniform: 16-byte rows pieces (K % 8 == 0 for bf16, % 4 for f32)
+    constexpr uint32_t EPP = XBF16 ? 8 : 4;   // elements per 16-byte piece
+    const uint32_t np = K / EPP;
+    const uint4* row = reinterpret_cast<const uint4*>(static_cast<const char*>(x) + (size_t)m * K * (XBF16 ? 2 : 4));
+    for (uint32_t p0 = 0; p0 < np; p0 += 4 * 64) {
+      uint4 u[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
+      for (int i = 0; i < 4; ++i) u[i] = row[std::min(p0 + i * 64 + lane, np - 1)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (p0 + i * 64 + lane >= np) continue;
+        const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (XBF16) {
+            mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] << 16)));
+            mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] & 0xffff0000u)));
+          } else {
+            mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j])));
+          }
+        }
+      }
+    }
+  } else {
+    for (uint32_t k = lane; k < K; k += 64) {
+      const float v = XBF16 ? bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k])
+                            : static_cast<const float*>(x)[(size_t)m * K + k];
+      mx = fmaxf(mx, abs_or_inf(v));
+    }
   }
   mx = lane_reduce<64, true>(mx);
   if (lane == 0) xe[m] = row_exponent(mx);
@@ -834,7 +861,7 @@ hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float
 // Per-row activation exponents (xscale_kernel) into xe[m].
 hipError_t launch_xscale(const void* x, bool x_bf16, uint32_t m, uint32_t k, int32_t* xe, hipStream_t s) {
   const size_t esz = x_bf16 ? 2 : 4;
-  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)k * esz) % 16 == 0;
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)k * esz) % 16 == 0 && k > 0;
   const dim3 grid((m + gp::THREADS / 64 - 1) / (gp::THREADS / 64));
   if (x_bf16)
     hipLaunchKernelGGL(gp::xscale_kernel<true>, grid, dim3(gp::THREADS), 0, s, x, m, k, x_vec, xe);
