@@ -140,6 +140,17 @@ VXT_API void* vxt_hip_upload_cb4_g64(void* ctx, const VxtCb4G64View* view, char*
 VXT_API void* vxt_hip_upload_q8_0(void* ctx, uint32_t rows, uint32_t cols, const uint8_t* blocks,
                           size_t n_bytes, char* err, size_t err_cap);
 
+/* Q4_0Matrix planes (q4_0.rs:7-14): padded_cols = ceil(cols/32)*32,
+ * scales_f16[rows * padded_cols/32], qs_words[rows * padded_cols/32 * 4]
+ * (byte j of a block: column j low nibble, column j + 16 high nibble).
+ * Replaces upload_q4_0 (metal.rs:179-187); plane rules as format.rs:453-462.
+ * The device holds the values (q - 8) widened to int8 next to the same f16
+ * scales, so the tensor runs on the Q8_0 kernels (kind VXT_KIND_Q8_0 in
+ * vxt_hip_tensor_info): dequant bit-exact with decode_row (q4_0.rs:77-97). */
+VXT_API void* vxt_hip_upload_q4_0(void* ctx, uint32_t rows, uint32_t cols, uint32_t padded_cols,
+                                  const uint16_t* scales_f16, size_t n_scales, const uint32_t* qs_words,
+                                  size_t n_words, char* err, size_t err_cap);
+
 /* Device-to-device copy of an uploaded tensor (same layout, new memory). */
 VXT_API void* vxt_hip_clone_tensor(void* tensor, char* err, size_t err_cap);
 
@@ -344,7 +355,8 @@ VXT_API int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const
  * pointer after returning.  Offsets below are byte offsets into those bytes. */
 
 /* One tensor section of a .vxt (VXT1) archive (format.rs:178-294 layout).
- * The plane fields are filled for kind 2 (KIND_CODEBOOK) only. */
+ * The plane fields are filled for kind 2 (KIND_CODEBOOK) and, for kind 3
+ * (KIND_Q4_0), scales_off / n_scales and words_off / n_words. */
 typedef struct VxtArchiveEntry {
     uint64_t name_off, name_len;    /* UTF-8 name                            */
     uint32_t kind, sub;             /* kind 2 = codebook, sub = bits         */
@@ -359,16 +371,18 @@ typedef struct VxtArchiveEntry {
 
 /* Parse and verify a .vxt archive (read_vxt_model, format.rs:301-451): the
  * archive and per-section FNV-1a64 tags, the codebook header and plane
- * rules (bits 3 or 4, padded_cols = ceil(cols/256)*256, plane lengths) and
- * the outlier CSR rules (format.rs:565-574).  Call with entries = NULL to
+ * rules (bits 3 or 4, padded_cols = ceil(cols/256)*256, plane lengths), the
+ * outlier CSR rules (format.rs:565-574) and the Q4_0 header and plane rules
+ * (padded_cols = ceil(cols/32)*32, plane lengths; format.rs:453-462).  Call with entries = NULL to
  * get *count, then with an array of `cap` >= *count.  *meta_count receives
  * the metadata entry count (values are stepped over).  Sections of kind 7
  * (entropy-coded TurboWht) stop the walk with VXT_E_UNSUPPORTED. */
 VXT_API int vxt_hip_vxt_parse(const uint8_t* bytes, size_t len, VxtArchiveEntry* entries, uint32_t cap,
                               uint32_t* count, uint32_t* meta_count, char* err, size_t err_cap);
 
-/* Upload a parsed 4-bit codebook entry of the same bytes to the device (the
- * path upload_packed takes for PackedTensor::Codebook, metal.rs:162-177). */
+/* Upload a parsed 4-bit codebook or Q4_0 entry of the same bytes to the
+ * device (the paths upload_packed takes for PackedTensor::Codebook and
+ * PackedTensor::Q4_0, metal.rs:162-187). */
 VXT_API void* vxt_hip_upload_vxt_entry(void* ctx, const uint8_t* bytes, size_t len, const VxtArchiveEntry* e,
                                        char* err, size_t err_cap);
 

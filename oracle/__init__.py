@@ -23,7 +23,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "liboracle_vxt.so")
 
-KIND_CB4, KIND_G64, KIND_Q8 = 1, 2, 3
+KIND_CB4, KIND_G64, KIND_Q8, KIND_Q40 = 1, 2, 3, 4
 
 _lib = None
 
@@ -52,6 +52,11 @@ class _Q8(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("blocks", C.c_void_p)]
 
 
+class _Q40(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("padded_cols", C.c_uint32),
+                ("scales_f16", C.c_void_p), ("qs_words", C.c_void_p)]
+
+
 def lib():
     global _lib
     if _lib is None:
@@ -68,12 +73,14 @@ def lib():
         for n in ("vxo_f16_to_f32_n", "vxo_f32_to_f16_n", "vxo_bf16_to_f32_n", "vxo_f32_to_bf16_n"):
             getattr(L, n).argtypes = [vp, vp, sz]
             getattr(L, n).restype = None
-        for n in ("vxo_cb4_decode_row", "vxo_g64_decode_row", "vxo_q8_decode_row"):
+        for n in ("vxo_cb4_decode_row", "vxo_g64_decode_row", "vxo_q8_decode_row", "vxo_q40_decode_row"):
             getattr(L, n).argtypes = [vp, sz, vp]
             getattr(L, n).restype = None
-        for n in ("vxo_cb4_gemv", "vxo_g64_gemv", "vxo_q8_gemv"):
+        for n in ("vxo_cb4_gemv", "vxo_g64_gemv", "vxo_q8_gemv", "vxo_q40_gemv"):
             getattr(L, n).argtypes = [vp, vp, vp, i32]
             getattr(L, n).restype = None
+        L.vxo_q40_encode.argtypes = [C.c_uint32, C.c_uint32, vp, vp, vp]
+        L.vxo_q40_encode.restype = None
         L.vxo_q8_quantize.argtypes = [vp, vp]
         L.vxo_q8_quantize.restype = None
         L.vxo_q8_dot_f32.argtypes = [vp, vp]
@@ -187,11 +194,16 @@ def view(m) -> _View:
         arrs = [np.ascontiguousarray(m.blocks, dtype=np.uint8)]
         s = _Q8(m.rows, m.cols, _ptr(arrs[0]))
         return _View(KIND_Q8, s, arrs)
+    if k == "q4_0":
+        arrs = [np.ascontiguousarray(m.scales_f16, dtype=np.uint16),
+                np.ascontiguousarray(m.qs_words, dtype=np.uint32)]
+        s = _Q40(m.rows, m.cols, m.padded_cols, _ptr(arrs[0]), _ptr(arrs[1]))
+        return _View(KIND_Q40, s, arrs)
     raise TypeError(f"unknown matrix kind {k!r}")
 
 
 _DECODE = {KIND_CB4: "vxo_cb4_decode_row", KIND_G64: "vxo_g64_decode_row",
-           KIND_Q8: "vxo_q8_decode_row"}
+           KIND_Q8: "vxo_q8_decode_row", KIND_Q40: "vxo_q40_decode_row"}
 
 
 def decode_rows(m, row0: int = 0, nrows: int | None = None) -> np.ndarray:
@@ -228,6 +240,21 @@ def gemm(m, X, threads: int = 1) -> np.ndarray:
     Y = np.empty((X.shape[0], m.rows), dtype=np.float32)
     lib().vxo_gemm(v.kind, v.ptr, _ptr(X), X.shape[0], _ptr(Y), int(threads))
     return Y
+
+
+# --------------------------------------------------------------------------
+# Q4_0 encoder
+# --------------------------------------------------------------------------
+
+def q40_encode(rows: int, cols: int, w):
+    """``Q4_0Matrix::encode`` (``q4_0.rs:17-64``) of f32 weights [rows, cols]."""
+    from vxg_amd.formats import Q4_0Matrix
+    ww = np.ascontiguousarray(w, dtype=np.float32).reshape(rows, cols)
+    bpr = (cols + 31) // 32
+    sc = np.empty(rows * bpr, dtype=np.uint16)
+    qs = np.empty(rows * bpr * 4, dtype=np.uint32)
+    lib().vxo_q40_encode(rows, cols, _ptr(ww), _ptr(sc), _ptr(qs))
+    return Q4_0Matrix(rows, cols, bpr * 32, sc, qs)
 
 
 # --------------------------------------------------------------------------

@@ -400,21 +400,137 @@ VXO_API void vxo_q8_gemv(const vxo_q8* m, const float* x, float* y, int threads)
 }
 
 /* ------------------------------------------------------------------------- */
+/* Q4_0: Q4_0Matrix (q4_0.rs:7-14) -- blocks of 32 columns, one f16 scale and */
+/* 16 bytes per block (4 little-endian u32 words); byte j holds column j in   */
+/* its low nibble and column j + 16 in its high nibble; value (q - 8) * d.    */
+/* ------------------------------------------------------------------------- */
+
+typedef struct {
+    uint32_t rows, cols, padded_cols;   /* padded_cols = roundup(cols, 32) */
+    const uint16_t* scales_f16;         /* [rows * padded_cols/32] */
+    const uint32_t* qs_words;           /* [rows * padded_cols/32 * 4] */
+} vxo_q40;
+
+/* Rust `f as i32`: saturating, NaN -> 0. */
+static int32_t vxo_f32_as_i32(float f) {
+    if (isnan(f)) return 0;
+    if (f >= 2147483648.0f) return INT32_MAX;
+    if (f < -2147483648.0f) return INT32_MIN;
+    return (int32_t)f;
+}
+
+/* q4_0.rs:17-64 Q4_0Matrix::encode: per block amax (NaN never compares
+ * greater), d = f16(amax / 7), id = 1 / f32(d) (0 when d is 0), q =
+ * clamp(floor(v * id + 8.5) as i32, 0, 15); columns past `cols` count as 0. */
+VXO_API void vxo_q40_encode(uint32_t rows, uint32_t cols, const float* w, uint16_t* scales_f16,
+                            uint32_t* qs_words) {
+    const size_t bpr = ((size_t)cols + 31) / 32;
+    for (size_t r = 0; r < rows; ++r) {
+        const float* row_w = w + r * cols;
+        for (size_t b = 0; b < bpr; ++b) {
+            const size_t blk = r * bpr + b, c0 = b * 32;
+            float amax = 0.0f, vals[32];
+            for (size_t l = 0; l < 32; ++l) {
+                vals[l] = 0.0f;
+                if (c0 + l < cols) {
+                    const float v = row_w[c0 + l];
+                    vals[l] = v;
+                    if (fabsf(v) > amax) amax = fabsf(v);
+                }
+            }
+            const float d = amax / 7.0f;
+            const uint16_t df16 = vxo_f32_to_f16(d);
+            scales_f16[blk] = df16;
+            const float d_eff = vxo_f16_to_f32(df16);
+            const float id = d_eff != 0.0f ? 1.0f / d_eff : 0.0f;
+            uint8_t bytes[16];
+            for (int j = 0; j < 16; ++j) {
+                int32_t q0 = vxo_f32_as_i32(floorf(vals[j] * id + 8.5f));
+                int32_t q1 = vxo_f32_as_i32(floorf(vals[j + 16] * id + 8.5f));
+                q0 = q0 < 0 ? 0 : (q0 > 15 ? 15 : q0);
+                q1 = q1 < 0 ? 0 : (q1 > 15 ? 15 : q1);
+                bytes[j] = (uint8_t)(q0 | (q1 << 4));
+            }
+            for (int wd = 0; wd < 4; ++wd)
+                qs_words[blk * 4 + wd] = (uint32_t)bytes[wd * 4] | ((uint32_t)bytes[wd * 4 + 1] << 8) |
+                                         ((uint32_t)bytes[wd * 4 + 2] << 16) | ((uint32_t)bytes[wd * 4 + 3] << 24);
+        }
+    }
+}
+
+/* q4_0.rs:77-97 Q4_0Matrix::decode_row: ((nibble as i32) - 8) as f32 * d. */
+VXO_API void vxo_q40_decode_row(const vxo_q40* m, size_t r, float* dst) {
+    const size_t bpr = m->padded_cols / 32;
+    for (size_t b = 0; b < bpr; ++b) {
+        const size_t bi = r * bpr + b, c0 = b * 32;
+        const float d = vxo_f16_to_f32(m->scales_f16[bi]);
+        for (size_t wd = 0; wd < 4; ++wd) {
+            const uint32_t word = m->qs_words[bi * 4 + wd];
+            for (size_t k = 0; k < 4; ++k) {
+                const uint32_t byte = (word >> (8 * k)) & 0xffu;
+                const size_t j = wd * 4 + k;
+                if (c0 + j < m->cols) dst[c0 + j] = (float)((int32_t)(byte & 0x0fu) - 8) * d;
+                if (c0 + j + 16 < m->cols) dst[c0 + j + 16] = (float)((int32_t)(byte >> 4) - 8) * d;
+            }
+        }
+    }
+}
+
+/* q4_0.rs:109-145 Q4_0Matrix::gemv_cpu, per row: blk_acc is one FMA chain
+ * over the block in the order (j, j + 16) for j = 0..15, then
+ * sum = fma(d, blk_acc, sum), blocks in order; x is zero-padded. */
+static void vxo_q40_rows(const void* mp, const float* x_pad, float* y, size_t r0, size_t r1) {
+    const vxo_q40* m = (const vxo_q40*)mp;
+    const size_t bpr = m->padded_cols / 32;
+    for (size_t r = r0; r < r1; ++r) {
+        float sum = 0.0f;
+        for (size_t b = 0; b < bpr; ++b) {
+            const size_t bi = r * bpr + b;
+            const float d = vxo_f16_to_f32(m->scales_f16[bi]);
+            const float* xv = x_pad + b * 32;
+            float blk_acc = 0.0f;
+            for (size_t wd = 0; wd < 4; ++wd) {
+                const uint32_t word = m->qs_words[bi * 4 + wd];
+                const size_t j = wd * 4;
+                for (size_t k = 0; k < 4; ++k) {
+                    const uint32_t byte = (word >> (8 * k)) & 0xffu;
+                    const float q0 = (float)((int32_t)(byte & 0x0fu) - 8);
+                    const float q1 = (float)((int32_t)(byte >> 4) - 8);
+                    blk_acc = fmaf(q0, xv[j + k], blk_acc);
+                    blk_acc = fmaf(q1, xv[j + k + 16], blk_acc);
+                }
+            }
+            sum = fmaf(d, blk_acc, sum);
+        }
+        y[r] = sum;
+    }
+}
+
+VXO_API void vxo_q40_gemv(const vxo_q40* m, const float* x, float* y, int threads) {
+    float* x_pad = (float*)calloc(m->padded_cols ? m->padded_cols : 1, sizeof(float));
+    memcpy(x_pad, x, (size_t)m->cols * sizeof(float));
+    vxo_run_rows(vxo_q40_rows, m, x_pad, y, m->rows, threads);
+    free(x_pad);
+}
+
+/* ------------------------------------------------------------------------- */
 /* Prefill GEMM: PackedTensor::gemm_cpu (llm_prefill.rs:156-255) with the      */
 /* scalar dense_tile_gemm (llm_prefill.rs:139-153).                           */
 /* ------------------------------------------------------------------------- */
 
-enum { VXO_KIND_CB4 = 1, VXO_KIND_G64 = 2, VXO_KIND_Q8 = 3 };
+enum { VXO_KIND_CB4 = 1, VXO_KIND_G64 = 2, VXO_KIND_Q8 = 3, VXO_KIND_Q40 = 4 };
 
 static void vxo_decode_row_any(int kind, const void* m, size_t r, float* dst) {
     if (kind == VXO_KIND_CB4) vxo_cb4_decode_row((const vxo_cb4*)m, r, dst);
     else if (kind == VXO_KIND_G64) vxo_g64_decode_row((const vxo_g64*)m, r, dst);
+    else if (kind == VXO_KIND_Q40) vxo_q40_decode_row((const vxo_q40*)m, r, dst);
     else vxo_q8_decode_row((const vxo_q8*)m, r, dst);
 }
 
 static void vxo_dims(int kind, const void* m, size_t* rows, size_t* cols) {
     if (kind == VXO_KIND_CB4) { *rows = ((const vxo_cb4*)m)->rows; *cols = ((const vxo_cb4*)m)->cols; }
     else if (kind == VXO_KIND_G64) { *rows = ((const vxo_g64*)m)->rows; *cols = ((const vxo_g64*)m)->cols; }
+    else if (kind == VXO_KIND_Q40) { *rows = ((const vxo_q40*)m)->rows; *cols = ((const vxo_q40*)m)->cols; }
     else { *rows = ((const vxo_q8*)m)->rows; *cols = ((const vxo_q8*)m)->cols; }
 }
 
@@ -508,6 +624,7 @@ VXO_API void vxo_gemm(int kind, const void* m, const float* x_batch, size_t batc
 VXO_API void vxo_gemv_any(int kind, const void* m, const float* x, float* y, int threads) {
     if (kind == VXO_KIND_CB4) vxo_cb4_gemv((const vxo_cb4*)m, x, y, threads);
     else if (kind == VXO_KIND_G64) vxo_g64_gemv((const vxo_g64*)m, x, y, threads);
+    else if (kind == VXO_KIND_Q40) vxo_q40_gemv((const vxo_q40*)m, x, y, threads);
     else vxo_q8_gemv((const vxo_q8*)m, x, y, threads);
 }
 

@@ -42,9 +42,12 @@ def raw_f32_section(a) -> tuple:
     return (5, 0, a.shape[0], a.shape[1], a.shape[1], _vec(a.reshape(-1), np.float32))
 
 
-def q4_0_section(rows, cols) -> tuple:
+def q4_0_section(rows, cols, m=None) -> tuple:
+    """A Q4_0 section (format.rs:243-247): all-zero planes, or those of Q4_0Matrix m."""
     pc = (cols + 31) // 32 * 32
     blocks = rows * pc // 32
+    if m is not None:
+        return (3, 0, m.rows, m.cols, m.padded_cols, _vec(m.scales_f16, np.uint16) + _vec(m.qs_words, np.uint32))
     return (3, 0, rows, cols, pc, _vec(np.zeros(blocks, np.uint16), np.uint16)
             + _vec(np.zeros(blocks * 4, np.uint32), np.uint32))
 

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from vxg_amd import engine, loaders, synth
-from vxg_amd.formats import CodebookMatrix, FormatError, q8_from_planes
+from vxg_amd.formats import CodebookMatrix, FormatError, Q4_0Matrix, q8_from_planes
 from archive_util import (codebook_section, lossless_section, q4_0_section, raw_f32_section, wht2_section,
                           write_gguf, write_vxt)
 
@@ -178,3 +178,39 @@ def test_gguf_errors():
         loaders.GgufFile(write_gguf([("w", tuple([1] * 9), 0, b"\x00" * 4)]))
     with pytest.raises(FormatError, match="truncated|larger"):
         loaders.GgufFile(good[:30])
+
+
+def _q40(rows, cols, seed):
+    g = np.random.default_rng(seed)
+    kb = (cols + 31) // 32
+    sc = g.integers(0, 0x7C00, rows * kb, dtype=np.uint16)
+    qw = g.integers(0, 2**32, rows * kb * 4, dtype=np.uint64).astype(np.uint32)
+    return Q4_0Matrix(rows, cols, kb * 32, sc, qw)
+
+
+def test_vxt_q4_0_planes_and_rules():
+    m = _q40(3, 70, 4)
+    with loaders.VxtArchive(write_vxt([("q", q4_0_section(0, 0, m))])) as ar:
+        e = ar["q"]
+        assert (e.kind, e.rows, e.cols, e.padded_cols) == (3, 3, 70, 96)
+        got = ar.q4_0("q")
+        assert np.array_equal(got.scales_f16, m.scales_f16) and np.array_equal(got.qs_words, m.qs_words)
+        with pytest.raises(engine.UnsupportedError):
+            ar.codebook("q")
+    kind, sub, rows, cols, pcols, payload = q4_0_section(0, 0, m)
+    with pytest.raises(FormatError, match="invalid VXT Q4_0 padded_cols"):
+        loaders.VxtArchive(write_vxt([("q", (kind, sub, rows, cols, 128, payload))]))
+    short = Q4_0Matrix(m.rows, m.cols, m.padded_cols, m.scales_f16[:-1], m.qs_words)
+    with pytest.raises(FormatError, match="corrupt VXT Q4_0 plane lengths"):
+        loaders.VxtArchive(write_vxt([("q", q4_0_section(0, 0, short))]))
+
+
+def test_gguf_q4_0_blocks_to_planes():
+    m = _q40(4, 64, 5)
+    data = write_gguf([("w", (64, 4), 2, m.gguf_blocks().tobytes())])
+    with loaders.GgufFile(data) as gf:
+        got = gf.q4_0("w")
+        assert (got.rows, got.cols, got.padded_cols) == (4, 64, 64)
+        assert np.array_equal(got.scales_f16, m.scales_f16) and np.array_equal(got.qs_words, m.qs_words)
+        with pytest.raises(engine.UnsupportedError):
+            gf.q8("w")

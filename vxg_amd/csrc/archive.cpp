@@ -190,10 +190,15 @@ void parse_vxt(const uint8_t* bytes, size_t len, std::vector<VxtArchiveEntry>* o
         r.plane(4, &n);
         r.plane(1, &n);
         break;
-      case kKindQ40:
-        r.plane(2, &n);
-        r.plane(4, &n);
+      case kKindQ40: {
+        // format.rs:453-462
+        if (e.padded_cols != (e.cols + 31) / 32 * 32) fail(VXT_E_FORMAT, "invalid VXT Q4_0 padded_cols");
+        e.scales_off = r.plane(2, &e.n_scales);
+        e.words_off = r.plane(4, &e.n_words);
+        const uint64_t blocks = e.rows * (e.padded_cols / 32);
+        if (e.n_scales != blocks || e.n_words != blocks * 4u) fail(VXT_E_FORMAT, "corrupt VXT Q4_0 plane lengths");
         break;
+      }
       case kKindWht2:
         r.take(64);
         r.plane(2, &n);
@@ -352,10 +357,22 @@ void* vxt_hip_upload_vxt_entry(void* ctx, const uint8_t* bytes, size_t len, cons
   void* out = nullptr;
   int rc = guarded(err, err_cap, [&] {
     if (!bytes || !e) fail(VXT_E_ARG, "null archive or entry");
-    if (e->kind != kKindCodebook) fail(VXT_E_UNSUPPORTED, "only codebook (KIND_CODEBOOK) entries upload");
-    if (e->sub != 4) fail(VXT_E_UNSUPPORTED, "only 4-bit codebooks run on the device");
+    if (e->kind != kKindCodebook && e->kind != kKindQ40)
+      fail(VXT_E_UNSUPPORTED, "only codebook (KIND_CODEBOOK) and Q4_0 entries upload");
     if (e->rows > 0xffffffffu || e->cols > 0xffffffffu || e->padded_cols > 0xffffffffu)
       fail(VXT_E_SHAPE, "matrix too large");
+    if (e->kind == kKindQ40) {
+      if (e->scales_off + 2 * e->n_scales > len || e->words_off + 4 * e->n_words > len)
+        fail(VXT_E_ARG, "entry does not describe this archive");
+      const auto sc = copy_plane<uint16_t>(bytes, e->scales_off, e->n_scales);
+      const auto wd = copy_plane<uint32_t>(bytes, e->words_off, e->n_words);
+      char e2[512];
+      out = vxt_hip_upload_q4_0(ctx, (uint32_t)e->rows, (uint32_t)e->cols, (uint32_t)e->padded_cols, sc.data(),
+                                sc.size(), wd.data(), wd.size(), e2, sizeof(e2));
+      if (!out) fail(VXT_E_FORMAT, e2);
+      return;
+    }
+    if (e->sub != 4) fail(VXT_E_UNSUPPORTED, "only 4-bit codebooks run on the device");
     const uint64_t ends[] = {e->centroids_off + 64, e->scales_off + 2 * e->n_scales, e->words_off + 4 * e->n_words,
                              e->row_ptr_off + 4 * e->n_row_ptr, e->outliers_off + 4 * e->n_outliers};
     for (uint64_t x : ends)

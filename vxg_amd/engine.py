@@ -38,7 +38,7 @@ from typing import Iterable, Sequence
 
 import numpy as np
 
-from .formats import Cb4G64Matrix, CodebookMatrix, Q8Matrix
+from .formats import Cb4G64Matrix, CodebookMatrix, Q4_0Matrix, Q8Matrix
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libvxt_hip.so")
@@ -54,7 +54,7 @@ KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
 ABI_SYMBOLS = (
     "vxt_hip_create", "vxt_hip_destroy", "vxt_hip_upload_cb4", "vxt_hip_upload_cb4_concat",
     "vxt_hip_upload_cb4_g64",
-    "vxt_hip_upload_q8_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
+    "vxt_hip_upload_q8_0", "vxt_hip_upload_q4_0", "vxt_hip_clone_tensor", "vxt_hip_free_tensor",
     "vxt_hip_tensor_info", "vxt_hip_run_multi", "vxt_hip_gemm", "vxt_hip_dequant_rows",
     "vxt_hip_matmul_dev", "vxt_hip_matmul_multi_dev", "vxt_hip_dequant_rows_dev", "vxt_hip_greedy_dev",
     "vxt_hip_embed_dev", "vxt_hip_ffn_glu_dev", "vxt_hip_rms_norm_dev", "vxt_hip_norm_matmul_dev",
@@ -152,6 +152,8 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_upload_cb4_g64.argtypes = [vp, C.POINTER(Cb4G64View), cp, sz]
     L.vxt_hip_upload_q8_0.restype = vp
     L.vxt_hip_upload_q8_0.argtypes = [vp, u32, u32, vp, sz, cp, sz]
+    L.vxt_hip_upload_q4_0.restype = vp
+    L.vxt_hip_upload_q4_0.argtypes = [vp, u32, u32, u32, vp, sz, vp, sz, cp, sz]
     L.vxt_hip_clone_tensor.restype = vp
     L.vxt_hip_clone_tensor.argtypes = [vp, cp, sz]
     L.vxt_hip_free_tensor.restype = None
@@ -464,6 +466,12 @@ class HipEngine:
         elif isinstance(m, Q8Matrix):
             b = np.ascontiguousarray(m.blocks, np.uint8)
             h = L.vxt_hip_upload_q8_0(self.ctx, m.rows, m.cols, b.ctypes.data, b.size, buf, len(buf))
+        elif isinstance(m, Q4_0Matrix):
+            # runs on the Q8_0 kernels: (q - 8) widened to int8, same f16 scales
+            sc = np.ascontiguousarray(m.scales_f16, np.uint16)
+            qw = np.ascontiguousarray(m.qs_words, np.uint32)
+            h = L.vxt_hip_upload_q4_0(self.ctx, m.rows, m.cols, m.padded_cols, sc.ctypes.data, sc.size,
+                                      qw.ctypes.data, qw.size, buf, len(buf))
         else:
             raise UnsupportedError(VXT_E_UNSUPPORTED, f"no device path for {type(m).__name__}")
         if not h:

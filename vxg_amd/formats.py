@@ -17,6 +17,11 @@ holding a ``CodebookMatrix`` (or raw GGUF ``Q8_0`` bytes) can hand it to
   byte layout of ``KvQ8Block`` (``llm_prefill.rs:17-24``) and of GGUF
   ``Q8_0`` (``gguf.rs:223-229``), as ``GgufView::tensor_bytes``
   (``gguf.rs:160-172``) returns them.
+* :class:`Q4_0Matrix` -- ``crates/vxg-tensor/src/q4_0.rs:7-14``: blocks of 32
+  columns, one f16 scale and four little-endian ``u32`` words (16 bytes) per
+  block; byte j holds column j in its low nibble and column j + 16 in its
+  high nibble, value ``(q - 8) * d``.  GGUF ``Q4_0`` blocks (``gguf.rs:211-221``)
+  carry the same bytes as ``{f16 d; u8 qs[16]}``.
 
 Everything here is plain numpy; no device work happens in this module.
 """
@@ -185,7 +190,56 @@ class Q8Matrix:
         return "q8"
 
 
-PackedTensor = Union[CodebookMatrix, Cb4G64Matrix, Q8Matrix]
+@dataclass
+class Q4_0Matrix:
+    """``Q4_0Matrix`` (``q4_0.rs:7-14``): f16 scale + 4 words per 32-column block."""
+
+    rows: int
+    cols: int
+    padded_cols: int
+    scales_f16: np.ndarray   # u16[rows * padded_cols/32]
+    qs_words: np.ndarray     # u32[rows * padded_cols/32 * 4]
+
+    @property
+    def blocks_per_row(self) -> int:
+        return self.padded_cols // 32
+
+    def validate(self) -> None:
+        """The archive reader's checks (``format.rs:453-462``)."""
+        if self.rows <= 0 or self.cols <= 0:
+            raise FormatError("rows and cols must be positive")
+        if self.padded_cols != (self.cols + 31) // 32 * 32:
+            raise FormatError("invalid VXT Q4_0 padded_cols")
+        blocks = self.rows * self.blocks_per_row
+        if np.asarray(self.scales_f16).size != blocks or np.asarray(self.qs_words).size != blocks * 4:
+            raise FormatError("corrupt VXT Q4_0 plane lengths")
+
+    @classmethod
+    def from_gguf_blocks(cls, rows: int, cols: int, blocks: np.ndarray) -> "Q4_0Matrix":
+        """Split GGUF ``Q4_0`` 18-byte blocks (``gguf.rs:211-221``; cols % 32 == 0)."""
+        if cols % 32:
+            raise FormatError("GGUF Q4_0 rows need cols % 32 == 0")
+        b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1, 18)
+        if b.shape[0] != rows * (cols // 32):
+            raise FormatError("corrupt GGUF Q4_0 byte length")
+        sc = b[:, 0:2].copy().view(np.uint16).reshape(-1)
+        qs = b[:, 2:18].copy().view(np.uint32).reshape(-1)
+        return cls(rows, cols, cols, sc, qs)
+
+    def gguf_blocks(self) -> np.ndarray:
+        """The same blocks as GGUF ``Q4_0`` bytes (18 per block)."""
+        n = self.rows * self.blocks_per_row
+        out = np.empty((n, 18), dtype=np.uint8)
+        out[:, 0:2] = np.asarray(self.scales_f16, np.uint16).reshape(n, 1).view(np.uint8)
+        out[:, 2:18] = np.asarray(self.qs_words, np.uint32).reshape(n, 4).view(np.uint8)
+        return out.reshape(-1)
+
+    @property
+    def kind(self) -> str:
+        return "q4_0"
+
+
+PackedTensor = Union[CodebookMatrix, Cb4G64Matrix, Q8Matrix, Q4_0Matrix]
 
 
 def q8_from_planes(rows: int, cols: int, qs: np.ndarray, d_f16: np.ndarray) -> Q8Matrix:

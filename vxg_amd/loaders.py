@@ -22,7 +22,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import engine
-from .formats import CodebookMatrix, FormatError, Q8Matrix
+from .formats import CodebookMatrix, FormatError, Q4_0Matrix, Q8Matrix
 
 KIND_LOSSLESS, KIND_CODEBOOK, KIND_Q4_0, KIND_WHT2, KIND_RAW_F32, KIND_TURBO_WHT, KIND_TURBO_WHT_EC = range(1, 8)
 GGML_F32, GGML_F16, GGML_Q4_0, GGML_Q8_0, GGML_Q4_K, GGML_BF16 = 0, 1, 2, 8, 12, 30
@@ -123,8 +123,17 @@ class VxtArchive:
                               b.view(r.row_ptr_off, np.uint32, r.n_row_ptr),
                               b.view(r.outliers_off, np.uint32, r.n_outliers), bits=e.sub)
 
+    def q4_0(self, name: str) -> Q4_0Matrix:
+        """A Q4_0 entry as a host ``Q4_0Matrix`` (views of the mapped bytes)."""
+        e = self[name]
+        if e.kind != KIND_Q4_0:
+            raise engine.UnsupportedError(engine.VXT_E_UNSUPPORTED, f"{name}: kind {e.kind} is not Q4_0")
+        r = e.raw
+        return Q4_0Matrix(e.rows, e.cols, e.padded_cols, self._b.view(r.scales_off, np.uint16, r.n_scales),
+                          self._b.view(r.words_off, np.uint32, r.n_words))
+
     def upload(self, eng: engine.HipEngine, name: str) -> engine.GpuPackedTensor:
-        """Upload a 4-bit codebook entry from the archive bytes."""
+        """Upload a 4-bit codebook or Q4_0 entry from the archive bytes."""
         e = self[name]
         buf = C.create_string_buffer(512)
         h = engine.load_library().vxt_hip_upload_vxt_entry(eng.ctx, self._b.ptr, self._b.len, C.byref(e.raw),
@@ -205,9 +214,23 @@ class GgufFile:
         rows, cols = dims
         return Q8Matrix(rows, cols, self.tensor_bytes(name))
 
-    def upload(self, eng: engine.HipEngine, name: str) -> engine.GpuPackedTensor:
-        """Upload a Q8_0 matrix from the file bytes (no f32 expansion)."""
+    def q4_0(self, name: str) -> Q4_0Matrix:
+        """A Q4_0 matrix (gguf.rs:211-221 blocks) as a host ``Q4_0Matrix``."""
         t = self[name]
+        if t.ggml_type != GGML_Q4_0:
+            raise engine.UnsupportedError(engine.VXT_E_UNSUPPORTED, f"{name} is not Q4_0")
+        dims = t.matrix_dims()
+        if dims is None:
+            raise FormatError(f"{name} is not a matrix")
+        rows, cols = dims
+        return Q4_0Matrix.from_gguf_blocks(rows, cols, self.tensor_bytes(name))
+
+    def upload(self, eng: engine.HipEngine, name: str) -> engine.GpuPackedTensor:
+        """Upload a Q8_0 matrix from the file bytes (no f32 expansion), or a
+        Q4_0 matrix through its planes (``HipEngine.upload_packed``)."""
+        t = self[name]
+        if t.ggml_type == GGML_Q4_0:
+            return eng.upload_packed(self.q4_0(name))
         buf = C.create_string_buffer(512)
         h = engine.load_library().vxt_hip_upload_gguf_q8_0(eng.ctx, self._b.ptr, self._b.len, C.byref(t.raw), buf,
                                                            len(buf))
