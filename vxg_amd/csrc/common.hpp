@@ -34,6 +34,7 @@ struct DevTensor {
   const uint32_t* outliers;  // CB4 only
   uint32_t split0, split1;   // CB4: first rows served by tables 1 and 2
   float cent[48];            // CB4 only: 3 centroid tables of 16
+  uint32_t tail_nonfinite;   // G64: cols % 64 != 0 and some row's last table holds Inf/NaN
 };
 
 // Prefill GEMM path (batch_m > 8): chosen per call, or pinned by the caller.

@@ -47,6 +47,9 @@ hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float
                               uint32_t n, void* y, bool y_bf16, hipStream_t s);
 hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
                             uint32_t K, uint32_t batch, float alpha, float beta, float* D, hipStream_t s);
+hipError_t launch_dense2(int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* dsc,
+                         const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial,
+                         uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s);
 
 namespace gp {
 
@@ -833,7 +836,12 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();   // no algorithm for this shape: the own dense kernel on the same panel
   }
-  if constexpr (KIND == KIND_G64) {
+  if (x_bf16 && pl.bm == 128) {
+    // 128 x 128 tiles with bf16 (exact f16) activations: the interleaved
+    // dense kernel (gemm_dense.hip), any weight mode
+    e = launch_dense2(pl.wmode, ah, p.hi, p.lo, p.dsc, p.inv, m, t.rows, pl.kp, y, y_bf16, partial, pl.splits,
+                      pl.kt_per_split, xe, s);
+  } else if constexpr (KIND == KIND_G64) {
     e = launch_dense_m<kWPlain>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
   } else if constexpr (KIND == KIND_Q8) {
     if (pl.wmode == kWQBlock)
@@ -876,63 +884,76 @@ size_t gemm_fused_workspace_bytes(const DevTensor& t, uint32_t m);
 hipError_t launch_gemm_fused(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
                              size_t ws_bytes, const int32_t* xe, hipStream_t s);
 
-// Path choice: the fused kernel where it applies (g64 and Q8 weights, bf16
-// activations) and batch_m is at most kFusedMaxM, unless the caller pins a
-// path.  Measured on MI355X (6144 x 2048 and 2048 x 6144): the fused kernel
-// is 1.5-3x faster up to M = 128 and level at M = 512, where the dense
-// kernel's 128 x 128 tiles reuse each decoded weight 4x more.
+bool gemm_tile_supported(const DevTensor& t, bool x_bf16);
+size_t gemm_tile_workspace_bytes(const DevTensor& t, uint32_t m);
+hipError_t launch_gemm_tile(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
+                            size_t ws_bytes, hipStream_t s);
+
+// Path choice, unless the caller pins one (every path runs every kind):
+//   * g64 weights, bf16 activations: the fused kernel up to batch 64, the
+//     decode-in-registers tile kernel (gemm_tile.hip) above;
+//   * Q8 weights, bf16 activations: the fused kernel up to batch 256;
+//   * everything else: the two-phase path with the own dense kernel.
+// The vendor dense GEMM runs only when pinned (kGemmLibrary), as a
+// comparison.  Measured on MI355X (config 3): the tile kernel beats the
+// panel + vendor GEMM path for g64 from M = 128 to 512 and is level at
+// M = 2048; the fused kernels are 1.5-3x faster than the two-phase path up
+// to M = 128 and level at M = 512 for Q8.
 constexpr uint32_t kFusedMaxM = 256;
+constexpr uint32_t kTileMinM = 65;
 
-static bool fused_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
-  if (mode == kGemmPanel || mode == kGemmLibrary || !gemm_fused_supported(t, x_bf16)) return false;
-  return mode == kGemmFused || m <= kFusedMaxM;
+enum class Path { Fused, Tile, Panel };
+
+static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
+  if (mode == kGemmPanel || mode == kGemmLibrary) return Path::Panel;
+  const bool tile_ok = gemm_tile_supported(t, x_bf16) && m >= kTileMinM;
+  if (mode == kGemmFused) {
+    if (tile_ok) return Path::Tile;
+    return gemm_fused_supported(t, x_bf16) ? Path::Fused : Path::Panel;
+  }
+  if (tile_ok) return Path::Tile;
+  if (gemm_fused_supported(t, x_bf16) && m <= kFusedMaxM) return Path::Fused;
+  return Path::Panel;
 }
 
-// Two-phase with the vendor dense GEMM: pinned, or automatically above the
-// fused kernel's batch limit when the product has at least 512 x 6144
-// outputs, or, for g64 (one panel plane), when K is long enough (>= 4096)
-// for the library call to be split into K slices that fill the GPU.
-// Measured (graph-timed, whole call, config 3): 1.2-1.3x faster than
-// dense_kernel at M = 512 x N = 6144 and M = 2048; g64 at 512 x 2048 x 6144
-// 295 -> 342 TFLOP/s with four K slices.  The hi/lo kinds stay on
-// dense_kernel there (two library GEMMs: Q8 223 -> 204, cb4 196 -> 192).
-constexpr size_t kLibMinOutputs = (size_t)512 * 6144;
-constexpr uint32_t kLibMinSplitK = 4096;
+static bool library_path(int mode) { return mode == kGemmLibrary; }
 
-static bool library_path(const DevTensor& t, uint32_t m, int mode) {
-  if (mode == kGemmLibrary) return true;
-  if (mode != kGemmAuto || m <= kFusedMaxM) return false;   // kGemmAutoOwn: never
-  return (size_t)m * t.rows >= kLibMinOutputs || (t.kind == KIND_G64 && t.cols >= kLibMinSplitK);
-}
-
-// Workspace: the per-row activation exponents first, then the path's own.
+// Workspace: the per-row activation exponents first, then the path's own
+// (the tile path keeps its exponents in its own block).
 static size_t xe_bytes(uint32_t m) { return gp::al256((size_t)m * 4); }
 
 size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
-  if (fused_path(t, m, x_bf16, mode)) return xe_bytes(m) + gemm_fused_workspace_bytes(t, m);
-  const gp::Plan pl = gp::plan(t, m, x_bf16, library_path(t, m, mode));
+  switch (choose_path(t, m, x_bf16, mode)) {
+    case Path::Tile: return gemm_tile_workspace_bytes(t, m);
+    case Path::Fused: return xe_bytes(m) + gemm_fused_workspace_bytes(t, m);
+    default: break;
+  }
+  const gp::Plan pl = gp::plan(t, m, x_bf16, library_path(mode));
   return xe_bytes(m) + pl.panel_bytes + pl.a_bytes + pl.partial_bytes;
 }
 
 hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16, void* ws,
                        size_t ws_bytes, hipStream_t s, int mode) {
   if (m == 0 || (size_t)m * t.rows > (size_t)1 << 40) return hipErrorInvalidValue;
+  const Path path = choose_path(t, m, x_bf16, mode);
+  if (path == Path::Tile)
+    return launch_gemm_tile(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
   if (ws_bytes < xe_bytes(m)) return hipErrorInvalidValue;
   int32_t* xe = static_cast<int32_t*>(ws);
   void* rest = static_cast<char*>(ws) + xe_bytes(m);
   const size_t rest_bytes = ws_bytes - xe_bytes(m);
-  const bool fused = fused_path(t, m, x_bf16, mode);
-  // f16 operands need the activations' row scales: the two-phase path's
-  // activation conversion finds them itself; the fused g64 kernel takes
-  // them from this pre-pass (the fused Q8 kernel multiplies bf16 activations
-  // as they are).
-  if (fused && gemm_fused_scales_x(t)) {
-    const hipError_t e = launch_xscale(x, x_bf16, m, t.cols, xe, s);
-    if (e != hipSuccess) return e;
-  }
-  if (fused)
+  if (path == Path::Fused) {
+    // f16 operands need the activations' row scales: the fused g64 kernel
+    // takes them from this pre-pass (the fused Q8 kernel multiplies bf16
+    // activations as they are; the two-phase path's activation conversion
+    // finds them itself).
+    if (gemm_fused_scales_x(t)) {
+      const hipError_t e = launch_xscale(x, x_bf16, m, t.cols, xe, s);
+      if (e != hipSuccess) return e;
+    }
     return launch_gemm_fused(t, static_cast<const uint16_t*>(x), m, y, y_bf16, rest, rest_bytes, xe, s);
-  const bool lib = library_path(t, m, mode);
+  }
+  const bool lib = library_path(mode);
   switch (t.kind) {
     case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
     case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);

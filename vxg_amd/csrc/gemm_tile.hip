@@ -1,0 +1,568 @@
+// gemm_tile.hip -- prefill GEMM (batch_m > 64) for cb4-g64 weights and bf16
+// activations, the weights decoded in registers inside the MFMA loop.
+//
+// Reference behaviour: PackedTensor::gemm_cpu (llm_prefill.rs:156-255)
+// decodes weight tiles to f32 and multiplies them densely; every g64 weight
+// is an f16 table entry, so an f16 MFMA operand holds it exactly, and the
+// products are exact in the fp32 accumulator.
+//
+// Two launches (plus the split-K reduction when K is split):
+//   1. xprep_kernel: per activation row, the power-of-two exponent xe[m]
+//      that puts the row's largest magnitude in [2^14, 2^15) (0 for rows that
+//      are all zero or hold Inf/NaN), then X[m] * 2^xe[m] as f16 (exact for
+//      bf16 X within 2^28 of the row's largest), padded with zeros to kp and
+//      stored with each aligned group of 8 columns in the order
+//      0 2 4 6 1 3 5 7 -- the order in which the weight decode below
+//      produces f16 pairs.
+//   2. tile_kernel: a workgroup computes 128 activation rows x 128 weight
+//      rows over a K range, with KW K-ways of 4 waves (K-way g takes the
+//      range's K tiles g, g + KW, ...; the ways are summed through LDS in
+//      ascending order at the end).  Wave w of a way owns weight rows
+//      32w..32w+31 and all 128 activation rows: four 32x32x16 MFMA fragments
+//      per 16-deep step, the activation fragments read from LDS and the
+//      weight fragment decoded by the lane itself.
+//        * activations: register-staged, two tiles ahead, into two LDS
+//          stages of 128 rows x 128 B; 16-byte chunk c of row r is stored at
+//          chunk c ^ ((r >> 1) & 7) so the fragment reads of 16 lanes (rows
+//          r..r+15 at one chunk) and the row writes touch distinct banks;
+//        * weights: lane (w, l) loads its row's 32 nibbles of the tile (16 B,
+//          columns 32h.. of the tile, h = l / 32) and the group's whole
+//          16-entry table (32 B), two tiles ahead.  Lookups are v_perm_b32
+//          byte selects from the table held in registers: the low and high
+//          bytes of entries 0-7 and 8-15 form four 8-byte sources; a perm
+//          picks four bytes by nibble & 7, a second perm takes the 8-15 half
+//          where bit 3 is set, and two more interleave low and high bytes
+//          into f16 pairs (columns 0,2 / 4,6 / 1,3 / 5,7 of each group of 8);
+//        * the loop body has no conditional memory operation, so the
+//          compiler keeps the next tile's loads in flight across the LDS
+//          stores (its waits are counted per static load order).
+//      Columns past K are zero in the activations, so the padding weights
+//      add nothing (decode_row stops at `cols`) unless an entry they index
+//      is Inf/NaN; tensors where that can happen take the panel path (the
+//      upload records it), so the loop body has no branch.  With gridDim.y > 1
+//      the workgroup writes fp32 partial sums of its K slice and
+//      reduce_kernel adds them in slice order, then applies 2^-xe[m].
+#include <algorithm>
+#include <type_traits>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace vxt {
+
+hipError_t launch_gemm_reduce(const float* partial, uint32_t splits, const float* inv, const int32_t* xe, uint32_t m,
+                              uint32_t n, void* y, bool y_bf16, hipStream_t s);
+
+namespace gt {
+
+constexpr int BM = 128;   // activation rows per workgroup
+constexpr int BN = 128;   // weight rows per workgroup (4 waves x 32)
+constexpr int BK = 64;    // K tile = one g64 group
+constexpr int NT = 256;   // threads of one K-way
+constexpr uint32_t kStageBytes = BM * BK * 2;   // one activation stage
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+
+// ---- activation preparation --------------------------------------------------
+
+__device__ __forceinline__ float abs_or_inf(float v) {
+  const float a = fabsf(v);
+  return a != a ? __builtin_inff() : a;   // NaN counts as non-finite
+}
+
+__device__ __forceinline__ int row_exponent(float b) {
+  return (b > 0.0f && b <= 3.4028234663852886e38f) ? 14 - ilogbf(b) : 0;
+}
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)a) |
+         ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)b) << 16);
+}
+
+// One wave per activation row.  x_vec: rows are 16-byte aligned and K % 8 == 0.
+__global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__ x, uint32_t M, uint32_t K,
+                                                    uint32_t kp, uint32_t x_vec, uint16_t* __restrict__ xh,
+                                                    int32_t* __restrict__ xe) {
+  const uint32_t m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (m >= M) return;
+  const uint16_t* row = x + (size_t)m * K;
+  float mx = 0.0f;
+  if (x_vec) {
+    const uint32_t np = K / 8;
+    const uint4* rv = reinterpret_cast<const uint4*>(row);
+    for (uint32_t p0 = 0; p0 < np; p0 += 4 * 64) {
+      uint4 u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = rv[std::min(p0 + i * 64 + lane, np - 1)];   // clamped, masked after
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (p0 + i * 64 + lane >= np) continue;
+        const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] << 16)));
+          mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] & 0xffff0000u)));
+        }
+      }
+    }
+  } else {
+    for (uint32_t k = lane; k < K; k += 64) mx = fmaxf(mx, abs_or_inf(bf16_to_f32(row[k])));
+  }
+  mx = lane_reduce<64, true>(mx);
+  const int e = row_exponent(mx);
+  if (lane == 0) xe[m] = e;
+  // 16-byte pieces of 8 columns; four per lane in flight before any is used
+  // (unconditional loads from clamped addresses, columns past K zeroed after)
+  const uint32_t np = kp / 8;
+  for (uint32_t p0 = 0; p0 < np; p0 += 4 * 64) {
+    float v[4][8];
+    if (x_vec) {
+      const uint32_t nv = K / 8;   // pieces that lie inside the row
+      uint4 u[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) u[i] = reinterpret_cast<const uint4*>(row)[std::min(p0 + i * 64 + lane, nv - 1)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool in = p0 + i * 64 + lane < nv;
+        const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          v[i][2 * j] = in ? __uint_as_float(w[j] << 16) : 0.0f;
+          v[i][2 * j + 1] = in ? __uint_as_float(w[j] & 0xffff0000u) : 0.0f;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t k = (p0 + i * 64 + lane) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[i][j] = k + j < K ? bf16_to_f32(row[k + j]) : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t pc = p0 + i * 64 + lane;
+      if (pc >= np) continue;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[i][j] = ldexpf(v[i][j], e);   // exact (a power of two)
+      // columns 0 2 4 6 1 3 5 7 of the group
+      *reinterpret_cast<uint4*>(xh + (size_t)m * kp + pc * 8) =
+          make_uint4(pack2(v[i][0], v[i][2]), pack2(v[i][4], v[i][6]), pack2(v[i][1], v[i][3]), pack2(v[i][5], v[i][7]));
+    }
+  }
+}
+
+// ---- weight decode -------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+// Byte planes of one 16-entry f16 table: L0..L3 the low bytes of entries
+// 0-3, 4-7, 8-11, 12-15, H0..H3 the high bytes.
+struct Planes {
+  uint32_t L0, L1, L2, L3, H0, H1, H2, H3;
+};
+
+__device__ __forceinline__ Planes make_planes(const u32x4& t0, const u32x4& t1) {
+  Planes p;
+  p.L0 = perm(t0.y, t0.x, 0x06040200u);
+  p.H0 = perm(t0.y, t0.x, 0x07050301u);
+  p.L1 = perm(t0.w, t0.z, 0x06040200u);
+  p.H1 = perm(t0.w, t0.z, 0x07050301u);
+  p.L2 = perm(t1.y, t1.x, 0x06040200u);
+  p.H2 = perm(t1.y, t1.x, 0x07050301u);
+  p.L3 = perm(t1.w, t1.z, 0x06040200u);
+  p.H3 = perm(t1.w, t1.z, 0x07050301u);
+  return p;
+}
+
+// Four nibbles q (one per byte, high nibble of each byte zero) -> table
+// entries as f16 pairs (byte 0, byte 1) and (byte 2, byte 3).
+__device__ __forceinline__ void lookup4(const Planes& p, uint32_t q, uint32_t& p01, uint32_t& p23) {
+  const uint32_t s = q & 0x07070707u;
+  const uint32_t sel = ((q >> 1) & 0x04040404u) | 0x03020100u;   // byte i from the 8-15 half when bit 3 is set
+  const uint32_t la = perm(p.L1, p.L0, s), lb = perm(p.L3, p.L2, s);
+  const uint32_t ha = perm(p.H1, p.H0, s), hb = perm(p.H3, p.H2, s);
+  const uint32_t l = perm(lb, la, sel), h = perm(hb, ha, sel);
+  p01 = perm(h, l, 0x05010400u);
+  p23 = perm(h, l, 0x07030602u);
+}
+
+// 8 nibbles (columns 0..7 of a group of 8, low nibble first) -> f16 pairs
+// (0,2) (4,6) (1,3) (5,7).
+__device__ __forceinline__ u32x4 decode8(const Planes& p, uint32_t w) {
+  uint32_t a, b, c, d;
+  lookup4(p, w & 0x0F0F0F0Fu, a, b);
+  lookup4(p, (w >> 4) & 0x0F0F0F0Fu, c, d);
+  return u32x4{a, b, c, d};
+}
+
+struct Raw {
+  u32x4 nib;      // 32 nibbles: columns 32h .. 32h + 31 of the tile
+  u32x4 t0, t1;   // the group's 16 table entries
+};
+
+__device__ __forceinline__ void bload(const DevTensor& t, uint32_t n, uint32_t kt, uint32_t h, Raw& r) {
+  const uint32_t kp = t.kp;
+  r.nib = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2) + kt * 32 + 16 * h);
+  const u32x4* tab = reinterpret_cast<const u32x4*>(t.p1 + ((size_t)n * (kp / 64) + kt) * 16);
+  r.t0 = tab[0];
+  r.t1 = tab[1];
+}
+
+// ---- activation tiles ------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t c) { return c ^ ((row >> 1) & 7u); }
+
+// 128 rows x 64 columns of xh: 4 pieces of 16 B per thread of the K-way.
+__device__ __forceinline__ void aload(const uint16_t* __restrict__ xh, uint32_t m0, uint32_t M, uint32_t kp,
+                                      uint32_t kt, uint32_t tid, u32x4 (&r)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t i = tid + NT * j;
+    const uint32_t row = std::min(m0 + i / 8, M - 1);   // rows past M repeat row M-1 (never stored)
+    r[j] = *reinterpret_cast<const u32x4*>(xh + (size_t)row * kp + kt * BK + (i % 8) * 8);
+  }
+}
+
+__device__ __forceinline__ void astore(char* stage, uint32_t tid, const u32x4 (&r)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t i = tid + NT * j;
+    const uint32_t row = i / 8, c = i % 8;
+    *reinterpret_cast<u32x4*>(stage + row * 128 + swz(row, c) * 16) = r[j];
+  }
+}
+
+// LDS: the activation stages (reused for the K-way sums at the end), the
+// tile's 128 row exponents, then the bf16 output tile [128][136].
+constexpr uint32_t LDO = BN + 8;
+
+template <int KW>
+constexpr size_t xe_offset() {
+  const size_t stages = (size_t)KW * 2 * kStageBytes;
+  const size_t red = (size_t)(KW - 1) * 4 * 4 * 16 * 64 * 4;   // K-way sums at the end
+  return stages > red ? stages : red;
+}
+
+template <int KW>
+constexpr size_t out_offset() { return xe_offset<KW>() + BM * 4; }
+
+template <int KW>
+constexpr size_t lds_bytes() { return out_offset<KW>() + (size_t)BM * LDO * 2; }
+
+// gridDim.x = tiles_m * tiles_n, gridDim.y = K slices of kt_per_split tiles.
+template <int KW>
+__global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTensor t, const uint16_t* __restrict__ xh,
+                                                                         uint32_t M, const int32_t* __restrict__ xe,
+                                                                         void* __restrict__ y, uint32_t y_bf16,
+                                                                         float* __restrict__ partial,
+                                                                         uint32_t kt_per_split, uint32_t tiles_m) {
+  extern __shared__ __attribute__((aligned(1024))) char smem_all[];
+  const uint32_t lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane((threadIdx.x >> 6) & 3);
+  const uint32_t kg = __builtin_amdgcn_readfirstlane(threadIdx.x >> 8);   // K-way
+  const uint32_t tid = threadIdx.x & (NT - 1);
+  char* const smem = smem_all + kg * (2 * kStageBytes);
+  // Tile order: blocks b, b+8, ... run on one XCD (one L2), so each XCD gets
+  // a contiguous range of tiles, walked in groups of 8 tile rows.
+  uint32_t tm, tn;
+  {
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t bb = (G % 8u == 0u) ? (b % 8u) * (G / 8u) + b / 8u : b;
+    const uint32_t tiles_n = G / tiles_m;
+    constexpr uint32_t GM = 8;
+    const uint32_t in_group = GM * tiles_n;
+    const uint32_t first = bb / in_group * GM;
+    const uint32_t gsz = std::min(tiles_m - first, GM);
+    tm = first + (bb % in_group) % gsz;
+    tn = (bb % in_group) / gsz;
+  }
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint32_t N = t.rows, K = t.cols, kp = t.kp;
+  const uint32_t KTT = kp / BK;
+  const uint32_t kt0 = blockIdx.y * kt_per_split;
+  const uint32_t kt1 = std::min(KTT, kt0 + kt_per_split);
+  const uint32_t ntiles = kt1 - kt0;                 // >= 1 (the plan guarantees it)
+  const uint32_t KT = (ntiles + KW - 1) / KW;        // iterations of every K-way
+  // K-way kg's tile at iteration i (clamped to the slice; only the last
+  // iteration of a way can lie past it, and is then not multiplied)
+  auto ktile = [&](uint32_t i) { return std::min(kt0 + kg + KW * i, kt1 - 1); };
+  const uint32_t n = std::min(n0 + wave * 32 + l32, N - 1);   // rows past N repeat row N-1 (never stored)
+#define STAGE(st) (smem + (st) * kStageBytes)
+
+  float16v acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+  // fragment offsets: fragment i, step t reads row 32i + l32, chunk 4h + t
+  uint32_t offA[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) offA[tt] = l32 * 128 + swz(l32, 4 * h + tt) * 16;   // + 4096 i (same swizzle)
+
+  // Weight tile i is decoded during iteration i - 1 (into bf[i & 1]) from
+  // the raw slot rb[i & 1], which was loaded two iterations before that.
+  u32x4 ra[2][4];
+  Raw rb[2];
+  u32x4 bf[2][4];
+  aload(xh, m0, M, kp, ktile(0), tid, ra[0]);
+  aload(xh, m0, M, kp, ktile(1), tid, ra[1]);
+  bload(t, n, ktile(0), h, rb[0]);
+  bload(t, n, ktile(1), h, rb[1]);
+  astore(STAGE(0), tid, ra[0]);
+  aload(xh, m0, M, kp, ktile(2), tid, ra[0]);
+  {
+    const Planes p0 = make_planes(rb[0].t0, rb[0].t1);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) bf[0][tt] = decode8(p0, rb[0].nib[tt]);
+  }
+  bload(t, n, ktile(2), h, rb[0]);
+  __syncthreads();
+
+  // Iteration i (P = i & 1): multiply stage P by bf[P] (tile i).  Spread
+  // between the 16 MFMAs: the next step's activation fragments; storing
+  // activation tile i+1 (slot P^1) into stage P^1 and loading tile i+3 into
+  // the slot; decoding weight tile i+1 (rb[P^1]) into bf[P^1].  Then the raw
+  // slot is reloaded with tile i+3.  Every memory operation is unconditional
+  // (clamped tiles), so the compiler counts its waits in one static order;
+  // sched_barrier keeps the interleave.
+  auto body = [&](uint32_t i, auto par) {
+    constexpr int P = decltype(par)::value;
+    const char* stage = STAGE(P);
+    char* const next_stage = STAGE(P ^ 1);
+    const uint32_t kn = ktile(i + 3);
+    const Planes pl = make_planes(rb[P ^ 1].t0, rb[P ^ 1].t1);
+    half8 af[2][4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) af[0][f] = *reinterpret_cast<const half8*>(stage + f * 4096 + offA[0]);
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      const int cur = tt & 1, nxt = cur ^ 1;
+      const half8 b = __builtin_bit_cast(half8, bf[P][tt]);
+      const uint32_t w = rb[P ^ 1].nib[tt];
+      uint32_t d0, d1, d2, d3;
+      __builtin_amdgcn_sched_barrier(0);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][0], b, acc[0], 0, 0, 0);
+      if (tt < 3) af[nxt][0] = *reinterpret_cast<const half8*>(stage + 0 * 4096 + offA[tt + 1]);
+      {
+        const uint32_t pi = tid + NT * tt, row = pi / 8, c = pi % 8;
+        *reinterpret_cast<u32x4*>(next_stage + row * 128 + swz(row, c) * 16) = ra[P ^ 1][tt];
+        const uint32_t grow = std::min(m0 + pi / 8, M - 1);
+        ra[P ^ 1][tt] = *reinterpret_cast<const u32x4*>(xh + (size_t)grow * kp + kn * BK + c * 8);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][1], b, acc[1], 0, 0, 0);
+      if (tt < 3) af[nxt][1] = *reinterpret_cast<const half8*>(stage + 1 * 4096 + offA[tt + 1]);
+      lookup4(pl, w & 0x0F0F0F0Fu, d0, d1);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[2] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][2], b, acc[2], 0, 0, 0);
+      if (tt < 3) af[nxt][2] = *reinterpret_cast<const half8*>(stage + 2 * 4096 + offA[tt + 1]);
+      lookup4(pl, (w >> 4) & 0x0F0F0F0Fu, d2, d3);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[3] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[cur][3], b, acc[3], 0, 0, 0);
+      if (tt < 3) af[nxt][3] = *reinterpret_cast<const half8*>(stage + 3 * 4096 + offA[tt + 1]);
+      bf[P ^ 1][tt] = u32x4{d0, d1, d2, d3};
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    bload(t, n, kn, h, rb[P ^ 1]);
+    __syncthreads();
+  };
+  auto last = [&](const char* stage, const u32x4 (&b)[4]) {
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt) {
+      half8 af[4];
+#pragma unroll
+      for (int f = 0; f < 4; ++f) af[f] = *reinterpret_cast<const half8*>(stage + f * 4096 + offA[tt]);
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+        acc[f] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[f], __builtin_bit_cast(half8, b[tt]), acc[f], 0, 0, 0);
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  uint32_t i = 0;
+  for (; i + 2 < KT; i += 2) {
+    body(i, I0{});
+    body(i + 1, I1{});
+  }
+  if (i + 1 < KT) {
+    body(i, I0{});
+    ++i;
+  }
+  // last iteration: stage i&1, weights bf[i&1]; a K-way whose tiles ran out
+  // (kt0 + kg + KW i >= kt1) skips it
+  if (kt0 + kg + KW * i < kt1) {
+    if (i & 1)
+      last(STAGE(1), bf[1]);
+    else
+      last(STAGE(0), bf[0]);
+  }
+#undef STAGE
+
+  // The tile's 128 row exponents go through LDS (one load per thread of
+  // K-way 0): read per output from global memory they cost more than the
+  // last K tiles.  bf16 outputs of a whole tile are transposed through LDS
+  // and written as 16-byte pieces of full rows (2-byte lane stores write
+  // half lines).  Every wave runs every barrier; K-ways > 0 only hand over
+  // their sums.
+  const bool to_partial = gridDim.y > 1;
+  const uint32_t N_ = N;
+  const bool rows_fast = y_bf16 && !to_partial && N_ % 8 == 0 && n0 + BN <= N_ &&
+                         reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  int32_t* s_xe = reinterpret_cast<int32_t*>(smem_all + xe_offset<KW>());
+  uint16_t* s_out = reinterpret_cast<uint16_t*>(smem_all + out_offset<KW>());
+  __syncthreads();   // every way is done with its stages
+  if (kg == 0 && tid < BM && !to_partial) s_xe[tid] = xe[std::min(m0 + tid, M - 1)];
+  if constexpr (KW > 1) {
+    float* red = reinterpret_cast<float*>(smem_all);
+    if (kg > 0) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) red[((((kg - 1) * 4 + wave) * 4 + f) * 16 + r) * 64 + lane] = acc[f][r];
+    }
+  }
+  __syncthreads();
+  if (kg == 0) {
+    if constexpr (KW > 1) {
+      const float* red = reinterpret_cast<const float*>(smem_all);
+#pragma unroll
+      for (uint32_t g = 1; g < (uint32_t)KW; ++g)
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[f][r] += red[((((g - 1) * 4 + wave) * 4 + f) * 16 + r) * 64 + lane];
+    }
+    // Lane owns output column n0 + 32 wave + l32 and rows
+    // m0 + 32 f + 4 h + 8 (r / 4) + r % 4 of fragment f.
+    const uint32_t nl = wave * 32 + l32, ncol = n0 + nl;
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      // this fragment's 16 row exponents, 4 consecutive rows per 16-byte read
+      int xs[16];
+      if (!to_partial) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int4 e4 = *reinterpret_cast<const int4*>(s_xe + f * 32 + h * 4 + 8 * q);
+          xs[4 * q + 0] = e4.x;
+          xs[4 * q + 1] = e4.y;
+          xs[4 * q + 2] = e4.z;
+          xs[4 * q + 3] = e4.w;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t ml = f * 32 + h * 4 + 8 * (r >> 2) + (r & 3), m = m0 + ml;
+        const float v = acc[f][r];
+        if (rows_fast) {
+          s_out[ml * LDO + nl] = f32_to_bf16(ldexpf(v, -xs[r]));
+          continue;
+        }
+        if (m >= M || ncol >= N_) continue;
+        if (to_partial) {
+          partial[((size_t)blockIdx.y * M + m) * N_ + ncol] = v;
+        } else {
+          const float o = ldexpf(v, -xs[r]);
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * N_ + ncol] = f32_to_bf16(o);
+          else
+            static_cast<float*>(y)[(size_t)m * N_ + ncol] = o;
+        }
+      }
+    }
+  }
+  if (rows_fast) {   // uniform
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t idx = tid + NT * k, row = idx / 16, c = idx % 16;
+        if (m0 + row >= M) continue;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(s_out + row * LDO + c * 8);
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(y) + (size_t)(m0 + row) * N_ + n0 + c * 8) = v;
+      }
+    }
+  }
+}
+
+struct Plan {
+  uint32_t tiles_m, tiles_n, kw, splits, kps;
+  size_t xe_off, xh_off, partial_off, bytes;
+};
+
+inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Grid shape.  Two workgroups of 4 waves fit a CU (512 slots): from 384
+// tiles on, one K-way; below, two K-ways (8 waves, one workgroup per CU),
+// and K split across workgroups until the grid has about 256 workgroups,
+// with >= 2 tiles per way in a slice and at most 16 MB of partial sums.
+constexpr size_t kMaxPartialBytes = (size_t)16 << 20;
+
+inline Plan plan(const DevTensor& t, uint32_t m) {
+  Plan p{};
+  p.tiles_m = (m + BM - 1) / BM;
+  p.tiles_n = (t.rows + BN - 1) / BN;
+  const uint32_t ktt = t.kp / BK;
+  const uint32_t tiles = p.tiles_m * p.tiles_n;
+  p.kw = tiles >= 384 ? 1 : 2;
+  uint32_t splits = 1;
+  if (p.kw == 2) {
+    const size_t slice_bytes = (size_t)m * t.rows * 4;
+    splits = (256u + tiles - 1) / tiles;
+    splits = std::min<uint32_t>(splits, std::max<uint32_t>(1u, ktt / (2 * p.kw)));
+    splits = (uint32_t)std::min<size_t>(splits, std::max<size_t>(1, kMaxPartialBytes / slice_bytes));
+  }
+  p.kps = (ktt + splits - 1) / splits;
+  p.splits = (ktt + p.kps - 1) / p.kps;
+  p.xe_off = 0;
+  p.xh_off = al256((size_t)m * 4);
+  p.partial_off = p.xh_off + al256((size_t)m * t.kp * 2);
+  p.bytes = p.partial_off + (p.splits > 1 ? al256((size_t)p.splits * m * t.rows * 4) : 0);
+  return p;
+}
+
+template <int KW>
+hipError_t launch_tile(const DevTensor& t, const uint16_t* xh, uint32_t m, const int32_t* xe, void* y, bool y_bf16,
+                       float* partial, const Plan& p, hipStream_t s) {
+  constexpr size_t lds = lds_bytes<KW>();
+  static_assert(lds <= 160 * 1024, "LDS budget");
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&tile_kernel<KW>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((tile_kernel<KW>), dim3(p.tiles_m * p.tiles_n, p.splits), dim3(NT * KW), lds, s, t, xh, m, xe, y,
+                     (uint32_t)y_bf16, partial, p.kps, p.tiles_m);
+  return hipGetLastError();
+}
+
+}  // namespace gt
+
+bool gemm_tile_supported(const DevTensor& t, bool x_bf16) {
+  return x_bf16 && t.kind == KIND_G64 && t.kp % 64 == 0 && !(t.cols % 64 != 0 && t.tail_nonfinite);
+}
+
+size_t gemm_tile_workspace_bytes(const DevTensor& t, uint32_t m) { return gt::plan(t, m).bytes; }
+
+hipError_t launch_gemm_tile(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
+                            size_t ws_bytes, hipStream_t s) {
+  if (!gemm_tile_supported(t, true) || m == 0) return hipErrorInvalidValue;
+  const gt::Plan p = gt::plan(t, m);
+  if (ws_bytes < p.bytes) return hipErrorInvalidValue;
+  char* base = static_cast<char*>(ws);
+  int32_t* xe = reinterpret_cast<int32_t*>(base + p.xe_off);
+  uint16_t* xh = reinterpret_cast<uint16_t*>(base + p.xh_off);
+  float* partial = reinterpret_cast<float*>(base + p.partial_off);
+  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (t.cols % 8 == 0);
+  hipLaunchKernelGGL(gt::xprep_kernel, dim3((m + 3) / 4), dim3(256), 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  e = p.kw == 1 ? gt::launch_tile<1>(t, xh, m, xe, y, y_bf16, partial, p, s)
+                : gt::launch_tile<2>(t, xh, m, xe, y, y_bf16, partial, p, s);
+  if (e != hipSuccess || p.splits == 1) return e;
+  return launch_gemm_reduce(partial, p.splits, nullptr, xe, m, t.rows, y, y_bf16, s);
+}
+
+}  // namespace vxt

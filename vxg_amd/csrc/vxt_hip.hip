@@ -82,6 +82,7 @@ struct Tensor {
   uint32_t nnz = 0;
   uint32_t split0 = 0, split1 = 0;
   float cent[48] = {};
+  uint32_t tail_nonfinite = 0;   // g64: see DevTensor::tail_nonfinite
 
   DevTensor dev() const {
     DevTensor d{};
@@ -92,6 +93,7 @@ struct Tensor {
     d.kp = kp;
     d.p0 = base + off_p0;
     d.p1 = reinterpret_cast<const uint16_t*>(base + off_p1);
+    d.tail_nonfinite = tail_nonfinite;
     if (kind == VXT_KIND_CB4) {
       d.row_ptr = reinterpret_cast<const uint32_t*>(base + off_rp);
       d.outliers = reinterpret_cast<const uint32_t*>(base + off_out);
@@ -586,9 +588,20 @@ void* vxt_hip_upload_cb4_g64(void* ctx, const VxtCb4G64View* v, char* err, size_
     std::memcpy(h.data(), v->idx, n_idx);
     std::memcpy(h.data() + i_bytes, v->lut_f16, n_lut * 2u);
     use_device(c);
+    // Padding columns multiply zero activations: they add nothing unless the
+    // entry they index is Inf/NaN, which the kernels that do not mask them
+    // must know about.
+    uint32_t tail_nonfinite = 0;
+    if (v->cols % 64u != 0) {
+      const size_t gpr = v->padded_cols / 64u;
+      for (size_t r = 0; r < v->rows && !tail_nonfinite; ++r)
+        for (size_t e = 0; e < 16; ++e)
+          if ((v->lut_f16[(r * gpr + gpr - 1) * 16 + e] & 0x7c00u) == 0x7c00u) tail_nonfinite = 1;
+    }
     Tensor* t = new_tensor(c, VXT_KIND_CB4_G64, v->rows, v->cols, v->padded_cols, h);
     t->off_p0 = 0;
     t->off_p1 = i_bytes;
+    t->tail_nonfinite = tail_nonfinite;
     register_tensor(c, t);
     out = t;
   });
