@@ -1,0 +1,105 @@
+"""GPU parity of the large-batch GEMM kernels: the g64 tile kernel
+(gemm_tile.hip) and the interleaved dense kernel of the two-phase path
+(gemm_dense.hip), at ragged shapes and through every K-way / split / epilogue
+branch, against the oracle's gemm_cpu (llm_prefill.rs:156-255).
+
+Bars as in test_gpu_parity: f32 out within 1e-3 of the oracle relative to
+max(|y|, 2^-10 sum|wx|); bf16 out within 1 ulp of f32_to_bf16(y_ref); bf16
+output equal to the rounding of the f32 output of the same call path.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from vxg_amd import engine, synth
+from vxg_amd.formats import Cb4G64Matrix, bf16_bits_to_f32, f32_to_bf16_bits
+from parity_util import THREADS, assert_bf16_close, floor_scale, make, max_rel, run_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def eng():
+    e = engine.HipEngine()
+    print(f"device: {e.device_name}", flush=True)
+    yield e
+    e.close()
+
+
+def check(eng, m, M, path, sel=None, seed=0):
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(M, m.cols, seed=seed)
+    X = bf16_bits_to_f32(xb).reshape(M, m.cols)
+    sel = np.unique(np.r_[0:3, M // 2, M - 3:M]) if sel is None else sel
+    W = oracle.decode_rows(m)
+    yref = oracle.gemm(m, X[sel], threads=THREADS)
+    eng.set_gemm_path(path)
+    try:
+        yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
+    fl = floor_scale(W, X[sel])
+    assert max_rel(yf[sel], yref, fl) <= 1e-3
+    assert_bf16_close(yb[sel], yref, fl)
+    assert np.array_equal(yb, f32_to_bf16_bits(yf))
+    t.free()
+    return yf
+
+
+# The tile kernel: one K-way from 384 tiles of 128 x 128, two below; split K
+# below ~256 workgroups; ragged M, N and K; N not a multiple of 8 (per-lane
+# epilogue) and of 128 (partial last tile).
+@pytest.mark.parametrize("M,N,K", [(65, 97, 64), (130, 640, 100), (300, 1500, 1000), (129, 2048, 3000),
+                                   (1000, 384, 2048), (2048, 6144, 192), (640, 8200, 448)])
+def test_tile_kernel_shapes(eng, M, N, K):
+    check(eng, synth.make_g64(N, K, seed=M + N), M, engine.GEMM_AUTO, seed=K)
+
+
+def test_tile_kernel_repeatable(eng):
+    """Split-K partial sums are added in slice order: bit-identical reruns."""
+    m = synth.make_g64(256, 6144, seed=5)
+    a = check(eng, m, 200, engine.GEMM_AUTO)
+    b = check(eng, m, 200, engine.GEMM_AUTO)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_g64_nonfinite_padding_table(eng):
+    """Padding columns (>= K) index table entries; decode_row stops at cols, so
+    an Inf entry reached only from padding must not reach the output.  Such
+    tensors take the panel path; the same matrix with a finite entry takes
+    the tile kernel.  Both match the oracle."""
+    m = synth.make_g64(200, 100, seed=11)        # padded to 128: columns 100..127 are padding
+    idx = m.idx.reshape(200, 64).copy()
+    lut = m.lut_f16.reshape(200, 2, 16).copy()
+    # last group: real columns use entries 0..14, padding columns entry 15
+    for r in range(200):
+        nib = np.zeros(64, np.uint8)
+        nib[:36] = np.random.default_rng(r).integers(0, 15, 36)   # columns 64..99
+        nib[36:] = 15                                                # columns 100..127
+        idx[r, 32:] = (nib[0::2] | (nib[1::2] << 4)).astype(np.uint8)
+    for entry in (0x7C00, 0x3C00):   # +Inf (panel path), then 1.0 (tile kernel)
+        lut[:, 1, 15] = entry
+        mm = Cb4G64Matrix(200, 100, 128, idx.reshape(-1).copy(), lut.reshape(-1).copy())
+        y = check(eng, mm, 300, engine.GEMM_AUTO)
+        assert np.isfinite(y).all()
+
+
+# The interleaved dense kernel (two-phase path, 128 x 128 tiles for M >= 256)
+# in each weight mode: g64 plain, Q8 block scales, cb4 hi/lo; ragged shapes;
+# split K on small grids.
+@pytest.mark.parametrize("kind", ["g64", "q8", "cb4"])
+@pytest.mark.parametrize("M,N,K", [(256, 97, 64), (300, 1500, 1000), (1000, 130, 4096), (513, 2048, 2048)])
+def test_dense_kernel_modes(eng, kind, M, N, K):
+    check(eng, make(kind, N, K, seed=M + K), M, engine.GEMM_PANEL, seed=N)
+
+
+def test_dense_kernel_q8_block_scales_extreme(eng):
+    """Block scales spanning subnormal to 2^15 in one row (each block's
+    fragment is scaled on its own)."""
+    q = synth.make_q8(300, 2048, seed=7)
+    b = q.blocks.copy().reshape(-1, 34)
+    b[0::5, 0:2] = np.array([0x7800], np.uint16).view(np.uint8)   # d = 32768
+    b[1::7, 0:2] = np.array([0x0001], np.uint16).view(np.uint8)   # subnormal d
+    q.blocks = b.reshape(-1)
+    check(eng, q, 512, engine.GEMM_PANEL)
