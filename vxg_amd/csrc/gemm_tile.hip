@@ -82,50 +82,40 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 }
 
 // One wave per activation row.  x_vec: rows are 16-byte aligned and K % 8 == 0.
+// NP > 0: the row (at most NP 16-byte pieces per lane, K <= 512 NP) is read
+// once into registers, all loads in flight together, and converted from
+// there; NP == 0: two passes over the row (any K).
+template <int NP>
 __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__ x, uint32_t M, uint32_t K,
                                                     uint32_t kp, uint32_t x_vec, uint16_t* __restrict__ xh,
                                                     int32_t* __restrict__ xe) {
   const uint32_t m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (m >= M) return;
   const uint16_t* row = x + (size_t)m * K;
-  float mx = 0.0f;
-  if (x_vec) {
-    const uint32_t np = K / 8;
-    const uint4* rv = reinterpret_cast<const uint4*>(row);
-    for (uint32_t p0 = 0; p0 < np; p0 += 4 * 64) {
-      uint4 u[4];
+  const uint32_t np = kp / 8;   // 16-byte pieces of the padded row
+  auto store = [&](uint32_t pc, const float (&v)[8], int e) {
+    float w[8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) u[i] = rv[std::min(p0 + i * 64 + lane, np - 1)];   // clamped, masked after
+    for (int j = 0; j < 8; ++j) w[j] = ldexpf(v[j], e);   // exact (a power of two)
+    // columns 0 2 4 6 1 3 5 7 of the group
+    *reinterpret_cast<uint4*>(xh + (size_t)m * kp + pc * 8) =
+        make_uint4(pack2(w[0], w[2]), pack2(w[4], w[6]), pack2(w[1], w[3]), pack2(w[5], w[7]));
+  };
+  auto piece = [&](uint32_t pc, float (&v)[8]) {   // scalar path: columns past K are zero
+    const uint32_t k = pc * 8;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (p0 + i * 64 + lane >= np) continue;
-        const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] << 16)));
-          mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] & 0xffff0000u)));
-        }
-      }
-    }
-  } else {
-    for (uint32_t k = lane; k < K; k += 64) mx = fmaxf(mx, abs_or_inf(bf16_to_f32(row[k])));
-  }
-  mx = lane_reduce<64, true>(mx);
-  const int e = row_exponent(mx);
-  if (lane == 0) xe[m] = e;
-  // 16-byte pieces of 8 columns; four per lane in flight before any is used
-  // (unconditional loads from clamped addresses, columns past K zeroed after)
-  const uint32_t np = kp / 8;
-  for (uint32_t p0 = 0; p0 < np; p0 += 4 * 64) {
-    float v[4][8];
+    for (int j = 0; j < 8; ++j) v[j] = k + j < K ? bf16_to_f32(row[k + j]) : 0.0f;
+  };
+  if constexpr (NP > 0) {
+    float v[NP][8];
     if (x_vec) {
-      const uint32_t nv = K / 8;   // pieces that lie inside the row
-      uint4 u[4];
+      const uint32_t nv = K / 8;   // pieces inside the row
+      uint4 u[NP];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) u[i] = reinterpret_cast<const uint4*>(row)[std::min(p0 + i * 64 + lane, nv - 1)];
+      for (int i = 0; i < NP; ++i) u[i] = reinterpret_cast<const uint4*>(row)[std::min(i * 64 + lane, nv - 1)];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool in = p0 + i * 64 + lane < nv;
+      for (int i = 0; i < NP; ++i) {
+        const bool in = i * 64 + lane < nv;
         const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -135,21 +125,34 @@ __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t k = (p0 + i * 64 + lane) * 8;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[i][j] = k + j < K ? bf16_to_f32(row[k + j]) : 0.0f;
-      }
+      for (int i = 0; i < NP; ++i) piece(i * 64 + lane, v[i]);
     }
+    float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t pc = p0 + i * 64 + lane;
-      if (pc >= np) continue;
+    for (int i = 0; i < NP; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[i][j] = ldexpf(v[i][j], e);   // exact (a power of two)
-      // columns 0 2 4 6 1 3 5 7 of the group
-      *reinterpret_cast<uint4*>(xh + (size_t)m * kp + pc * 8) =
-          make_uint4(pack2(v[i][0], v[i][2]), pack2(v[i][4], v[i][6]), pack2(v[i][1], v[i][3]), pack2(v[i][5], v[i][7]));
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[i][j]));
+    mx = lane_reduce<64, true>(mx);
+    const int e = row_exponent(mx);
+    if (lane == 0) xe[m] = e;
+#pragma unroll
+    for (int i = 0; i < NP; ++i)
+      if (i * 64 + lane < np) store(i * 64 + lane, v[i], e);
+  } else {
+    float mx = 0.0f;
+    for (uint32_t pc = lane; pc < np; pc += 64) {
+      float v[8];
+      piece(pc, v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
+    }
+    mx = lane_reduce<64, true>(mx);
+    const int e = row_exponent(mx);
+    if (lane == 0) xe[m] = e;
+    for (uint32_t pc = lane; pc < np; pc += 64) {
+      float v[8];
+      piece(pc, v);
+      store(pc, v, e);
     }
   }
 }
@@ -556,7 +559,16 @@ hipError_t launch_gemm_tile(const DevTensor& t, const uint16_t* x, uint32_t m, v
   uint16_t* xh = reinterpret_cast<uint16_t*>(base + p.xh_off);
   float* partial = reinterpret_cast<float*>(base + p.partial_off);
   const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (t.cols % 8 == 0);
-  hipLaunchKernelGGL(gt::xprep_kernel, dim3((m + 3) / 4), dim3(256), 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
+  const dim3 xg((m + 3) / 4), xb(256);
+  const uint32_t npl = (t.kp / 8 + 63) / 64;   // 16-byte pieces per lane
+  if (npl <= 4)
+    hipLaunchKernelGGL(gt::xprep_kernel<4>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
+  else if (npl <= 8)
+    hipLaunchKernelGGL(gt::xprep_kernel<8>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
+  else if (npl <= 16)
+    hipLaunchKernelGGL(gt::xprep_kernel<16>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
+  else
+    hipLaunchKernelGGL(gt::xprep_kernel<0>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   e = p.kw == 1 ? gt::launch_tile<1>(t, xh, m, xe, y, y_bf16, partial, p, s)
