@@ -480,18 +480,19 @@ VXT_API void vxt_hip_graph_free(void* graph);
 /* Kernel time of the last synchronous call, in ms (hipEvent pair). */
 VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
 
-/* Prefill GEMM path (batch_m > 8) of this context's later calls.  AUTO (the
- * default): g64 and Q8_0 weights with bf16 activations and batch_m <= 256
- * are decoded inside the MFMA loop (fused); other calls at batch_m <= 256
- * take the two-phase path (decoded f16 panel, then this library's dense MFMA
- * kernel); batch_m > 256 with batch_m * rows >= 512 * 6144 takes the
- * two-phase path with the dense phase on hipBLASLt (smaller products keep the
- * own dense kernel).  PANEL pins the two-phase path with the own dense kernel;
- * FUSED takes the fused kernel at every batch_m it applies to; LIBRARY pins
- * the hipBLASLt dense phase (falling back to the own kernel for a shape the
- * library has no algorithm for).  A tuning and test control with no
- * counterpart in the reference, whose gemm_cpu (llm_prefill.rs:156-255) has a
- * single path.  Returns VXT_E_ARG for an unknown path. */
+/* Prefill GEMM path (batch_m > 8) of this context's later calls.  Every path
+ * runs this library's own kernels except LIBRARY.  AUTO (the default):
+ * g64 weights with bf16 activations decode inside the MFMA loop -- the
+ * 128 x 128 tile kernel from batch_m 65, the fused kernel below; Q8_0 (and
+ * Q4_0) weights with bf16 activations and batch_m <= 256 take the fused
+ * kernel; every other call takes the two-phase path (a decoded f16 weight
+ * panel, then the dense MFMA kernel).  PANEL pins the two-phase path; FUSED
+ * takes the decode-in-loop kernels at every batch_m they apply to; LIBRARY
+ * pins the two-phase path with its dense phase on hipBLASLt, a comparison
+ * only (falling back to the own kernel for a shape the library has no
+ * algorithm for).  A tuning and test control with no counterpart in the
+ * reference, whose gemm_cpu (llm_prefill.rs:156-255) has a single path.
+ * Returns VXT_E_ARG for an unknown path. */
 #define VXT_GEMM_AUTO 0u
 #define VXT_GEMM_PANEL 1u
 #define VXT_GEMM_FUSED 2u

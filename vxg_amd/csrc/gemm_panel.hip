@@ -14,9 +14,12 @@
 //          row's largest magnitude in [2^14, 2^15) (no f16 overflow, lo out
 //          of the subnormal range).  hi + lo carries 22 significant bits:
 //          exact for Q8 (q * d has <= 18), within 2^-22 relative for cb4.
-//   2. dense_kernel: Y = X * W^T on v_mfma_f32_32x32x16_f16 from LDS tiles,
-//      fp32 accumulation; lo products go to a second accumulator folded in
-//      as acc + accl * 2^-11, then scaled by 1/s.  Activations get a
+//   2. dense phase: Y = X * W^T on v_mfma_f32_32x32x16_f16 from LDS tiles,
+//      fp32 accumulation -- the interleaved 128 x 128 kernel of
+//      gemm_dense.hip for bf16 X from M = 256, dense_kernel below (64 x 64
+//      tiles below M = 256, and for f32 X); lo products go to a second
+//      accumulator folded in as acc + accl * 2^-11, then scaled by 1/s.
+//      Activations get a
 //      power-of-two scale per row too (xscale_kernel: the row's largest
 //      magnitude in [2^14, 2^15)), undone in the epilogue, so X of any
 //      magnitude converts to f16 without overflow: bf16 X exactly (8
@@ -25,12 +28,13 @@
 //      dropped).
 //      Small M*N grids split K across workgroups; reduce_kernel then adds the
 //      partial sums in a fixed order (results do not depend on timing).
-//      For large products the dense phase runs on hipBLASLt instead
-//      (library_dense below, gemm_blas.cpp), with reduce_kernel as the
-//      1/s + bf16 epilogue.
+//      Only when a caller pins kGemmLibrary does the dense phase run on
+//      hipBLASLt (library_dense below, gemm_blas.cpp), with reduce_kernel as
+//      the 1/s + bf16 epilogue -- a comparison, never the automatic path.
 //
-// g64 and Q8_0 weights with bf16 activations at small batches take the fused
-// kernel of gemm_fused.hip instead of either phase (launch_gemm chooses).
+// g64 weights with bf16 activations take the tile kernel of gemm_tile.hip
+// (M > 64) or the fused kernel of gemm_fused.hip (M <= 64); Q8_0 with bf16
+// activations takes the fused kernel up to M = 256 (launch_gemm chooses).
 //
 // The panel costs one pass over the packed weights plus one f16 (or 2 x f16)
 // write; the fused alternative re-decodes every weight tile once per M tile
