@@ -1,8 +1,9 @@
 """GPU: prefill GEMM with the weights decoded inside the MFMA loop.
 
-For g64 and Q8_0 tensors with bf16 activations, ``batch_m > 8`` products take
-the fused kernel by default; ``vxt_hip_set_gemm_path(PANEL)`` pins the
-two-phase path (f16 panel, then the dense kernel).  Both must meet the GEMM
+For g64 and Q8_0 tensors with bf16 activations, ``vxt_hip_set_gemm_path(FUSED)``
+pins the kernels that decode inside the MFMA loop (the fused kernel; for g64
+above batch 64 the tile kernel), and ``PANEL`` pins the two-phase path (f16
+panel, then the dense kernel).  Both must meet the GEMM
 bar against the oracle (max relative error <= 1e-3 of
 max(|y_ref|, 2^-10 * sum |w x|); bf16 outputs within 1 bf16 ulp), on shapes
 that cross every tile edge of the fused kernel: M around 32 / 64 / 128 (the
@@ -31,10 +32,14 @@ def eng():
 
 
 def both_paths(eng, t, xb, M):
-    """(f32 out, bf16 out) of the fused path, then f32 out of the panel path."""
-    eng.set_gemm_path(engine.GEMM_AUTO)
-    yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
-    yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+    """(f32 out, bf16 out) of the decode-in-loop path, then f32 out of the
+    panel path."""
+    eng.set_gemm_path(engine.GEMM_FUSED)
+    try:
+        yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
     eng.set_gemm_path(engine.GEMM_PANEL)
     try:
         yp = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
@@ -77,7 +82,11 @@ def test_fused_split_k_deterministic(eng, kind, M, N, K):
     yf, yb, yp = both_paths(eng, t, xb, M)
     sel = np.unique(np.r_[0, M - 1, np.random.default_rng(M).choice(M, min(M, 12), replace=False)])
     check(m, xb, M, yf, yb, yp, sample=sel)
-    y2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    eng.set_gemm_path(engine.GEMM_FUSED)   # the same path again
+    try:
+        y2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
     assert np.array_equal(yf.view(np.uint32), y2.view(np.uint32))
     t.free()
 
@@ -98,7 +107,8 @@ def test_fused_multi_chunk_workgroups(eng, kind, M, N, K):
 
 @pytest.mark.parametrize("kind", ["g64", "q8"])
 def test_fused_path_forced_at_large_batch(eng, kind):
-    """GEMM_FUSED takes the fused kernel past the automatic batch limit."""
+    """GEMM_FUSED decodes inside the MFMA loop past the automatic batch limit
+    (Q8: the fused kernel; g64: the tile kernel)."""
     M, N, K = 512, 640, 1024
     m = make(kind, N, K, seed=77)
     t = eng.upload_packed(m)

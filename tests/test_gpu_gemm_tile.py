@@ -47,20 +47,21 @@ def check(eng, m, M, path, sel=None, seed=0):
     return yf
 
 
-# The tile kernel: one K-way from 384 tiles of 128 x 128, two below; split K
-# below ~256 workgroups; ragged M, N and K; N not a multiple of 8 (per-lane
-# epilogue) and of 128 (partial last tile).
+# The tile kernel (pinned: GEMM_FUSED takes it for g64 above batch 64): one
+# K-way from 384 tiles of 128 x 128, two below; split K below ~256
+# workgroups; ragged M, N and K; N not a multiple of 8 (per-lane epilogue)
+# and of 128 (partial last tile).
 @pytest.mark.parametrize("M,N,K", [(65, 97, 64), (130, 640, 100), (300, 1500, 1000), (129, 2048, 3000),
                                    (1000, 384, 2048), (2048, 6144, 192), (640, 8200, 448)])
 def test_tile_kernel_shapes(eng, M, N, K):
-    check(eng, synth.make_g64(N, K, seed=M + N), M, engine.GEMM_AUTO, seed=K)
+    check(eng, synth.make_g64(N, K, seed=M + N), M, engine.GEMM_FUSED, seed=K)
 
 
 def test_tile_kernel_repeatable(eng):
     """Split-K partial sums are added in slice order: bit-identical reruns."""
     m = synth.make_g64(256, 6144, seed=5)
-    a = check(eng, m, 200, engine.GEMM_AUTO)
-    b = check(eng, m, 200, engine.GEMM_AUTO)
+    a = check(eng, m, 200, engine.GEMM_FUSED)
+    b = check(eng, m, 200, engine.GEMM_FUSED)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 

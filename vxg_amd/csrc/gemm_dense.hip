@@ -112,6 +112,9 @@ __global__ __launch_bounds__(NT, occupancy<MODE>()) void dense2_kernel(const uin
   const uint32_t KT = kt1 - kt0;   // >= 1
   auto ktile = [&](uint32_t i) { return std::min(kt0 + i, kt1 - 1); };
   constexpr bool LO = MODE == kHiLo;
+  // The tile's row exponents are requested now, so the epilogue does not
+  // wait for another round trip to memory.
+  const int32_t xe_pre = xe[std::min(m0 + (tid & (BM - 1)), M - 1)];
 #define SA(st) (smem + (st) * stage_bytes<MODE>())
 #define SB(st) (smem + (st) * stage_bytes<MODE>() + kOpBytes)
 #define SL(st) (smem + (st) * stage_bytes<MODE>() + 2 * kOpBytes)
@@ -278,7 +281,7 @@ __global__ __launch_bounds__(NT, occupancy<MODE>()) void dense2_kernel(const uin
 
   // Lane owns column n0 + wn*64 + j*32 + l32 of fragment (i, j), rows
   // m0 + wm*64 + i*32 + 4h + 8(r/4) + r%4.  The tile's 128 row exponents go
-  // through LDS (one load per thread): read per output from global memory
+  // through LDS (loaded in the prologue): read per output from global memory
   // they cost more than the last K tiles.  bf16 outputs of a whole tile are
   // transposed through LDS and written as 16-byte pieces of full rows (lane
   // stores of 2 bytes write half lines, which costs as much as the last
@@ -291,7 +294,7 @@ __global__ __launch_bounds__(NT, occupancy<MODE>()) void dense2_kernel(const uin
                          reinterpret_cast<uintptr_t>(y) % 16 == 0;
   if (!to_partial) {
     __syncthreads();   // every wave is done with the stages
-    if (tid < BM) s_xe[tid] = xe[std::min(m0 + tid, M - 1)];
+    if (tid < BM) s_xe[tid] = xe_pre;
     __syncthreads();
   }
   // this lane's 32 row exponents, 4 consecutive rows per 16-byte read
@@ -370,7 +373,7 @@ hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, co
 hipError_t launch_dense2(int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* dsc,
                          const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial,
                          uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
-  if (kp % gd::BK != 0) return hipErrorInvalidValue;
+  if (kp % gd::BK != 0 || xe == nullptr) return hipErrorInvalidValue;
   switch (wmode) {
     case gd::kPlain:
       return gd::launch<gd::kPlain>(ah, bh, bl, dsc, inv, m, n, kp, y, y_bf16, partial, splits, kt_per_split, xe, s);

@@ -894,29 +894,41 @@ hipError_t launch_gemm_tile(const DevTensor& t, const uint16_t* x, uint32_t m, v
                             size_t ws_bytes, hipStream_t s);
 
 // Path choice, unless the caller pins one (every path runs every kind):
-//   * g64 weights, bf16 activations: the fused kernel up to batch 64, the
-//     decode-in-registers tile kernel (gemm_tile.hip) above;
-//   * Q8 weights, bf16 activations: the fused kernel up to batch 256;
+//   * g64 weights, bf16 activations: the fused kernel up to batch 64; the
+//     decode-in-registers tile kernel (gemm_tile.hip) from batch 192 to
+//     2047, and beyond when K > N; the two-phase path otherwise;
+//   * Q8 weights, bf16 activations: the fused kernel up to batch 128;
 //   * everything else: the two-phase path with the own dense kernel.
 // The vendor dense GEMM runs only when pinned (kGemmLibrary), as a
-// comparison.  Measured on MI355X (config 3): the tile kernel beats the
-// panel + vendor GEMM path for g64 from M = 128 to 512 and is level at
-// M = 2048; the fused kernels are 1.5-3x faster than the two-phase path up
-// to M = 128 and level at M = 512 for Q8.
-constexpr uint32_t kFusedMaxM = 256;
-constexpr uint32_t kTileMinM = 65;
+// comparison.  Measured on MI355X (whole call, graph of 100 calls, TFLOP/s,
+// K x N = 2048 x 6144 / 6144 x 2048):
+//   g64 M = 64: fused 73 / 61, two-phase 68 / 61; M = 128: tile 109 / 99,
+//   two-phase 118 / 108; M = 512: tile 372 / 316, two-phase 300 / 325;
+//   M = 2048: tile 605 / 603, two-phase 653 / 581; M = 4096: 673 / 761
+//   (2048 x 6144);
+//   Q8 M = 64: fused 81 / 71, two-phase 61 / 54; M = 256: fused 125 / 161,
+//   two-phase 132 / 163.
+constexpr uint32_t kFusedMaxM = 128;
+constexpr uint32_t kG64FusedMaxM = 64;
+constexpr uint32_t kTileMinM = 192;
+constexpr uint32_t kTileMaxM = 2048;   // exclusive, unless K > N
 
 enum class Path { Fused, Tile, Panel };
 
 static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
   if (mode == kGemmPanel || mode == kGemmLibrary) return Path::Panel;
-  const bool tile_ok = gemm_tile_supported(t, x_bf16) && m >= kTileMinM;
-  if (mode == kGemmFused) {
-    if (tile_ok) return Path::Tile;
-    return gemm_fused_supported(t, x_bf16) ? Path::Fused : Path::Panel;
+  const bool tile_ok = gemm_tile_supported(t, x_bf16);
+  const bool fused_ok = gemm_fused_supported(t, x_bf16);
+  if (mode == kGemmFused) {   // decode inside the MFMA loop wherever it applies
+    if (tile_ok && m > kG64FusedMaxM) return Path::Tile;
+    return fused_ok ? Path::Fused : Path::Panel;
   }
-  if (tile_ok) return Path::Tile;
-  if (gemm_fused_supported(t, x_bf16) && m <= kFusedMaxM) return Path::Fused;
+  if (t.kind == KIND_G64 && x_bf16) {
+    if (fused_ok && m <= kG64FusedMaxM) return Path::Fused;
+    if (tile_ok && m >= kTileMinM && (m < kTileMaxM || t.cols > t.rows)) return Path::Tile;
+    return Path::Panel;
+  }
+  if (fused_ok && m <= kFusedMaxM) return Path::Fused;
   return Path::Panel;
 }
 

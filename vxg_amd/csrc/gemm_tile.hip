@@ -295,6 +295,9 @@ __global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTenso
   // iteration of a way can lie past it, and is then not multiplied)
   auto ktile = [&](uint32_t i) { return std::min(kt0 + kg + KW * i, kt1 - 1); };
   const uint32_t n = std::min(n0 + wave * 32 + l32, N - 1);   // rows past N repeat row N-1 (never stored)
+  // The tile's row exponents are requested now, so the epilogue does not
+  // wait for another round trip to memory.
+  const int32_t xe_pre = xe[std::min(m0 + (tid & (BM - 1)), M - 1)];
 #define STAGE(st) (smem + (st) * kStageBytes)
 
   float16v acc[4];
@@ -406,9 +409,9 @@ __global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTenso
   }
 #undef STAGE
 
-  // The tile's 128 row exponents go through LDS (one load per thread of
-  // K-way 0): read per output from global memory they cost more than the
-  // last K tiles.  bf16 outputs of a whole tile are transposed through LDS
+  // The tile's 128 row exponents go through LDS (loaded in the prologue by
+  // the threads of K-way 0): read per output from global memory they cost
+  // more than the last K tiles.  bf16 outputs of a whole tile are transposed through LDS
   // and written as 16-byte pieces of full rows (2-byte lane stores write
   // half lines).  Every wave runs every barrier; K-ways > 0 only hand over
   // their sums.
@@ -419,7 +422,7 @@ __global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTenso
   int32_t* s_xe = reinterpret_cast<int32_t*>(smem_all + xe_offset<KW>());
   uint16_t* s_out = reinterpret_cast<uint16_t*>(smem_all + out_offset<KW>());
   __syncthreads();   // every way is done with its stages
-  if (kg == 0 && tid < BM && !to_partial) s_xe[tid] = xe[std::min(m0 + tid, M - 1)];
+  if (kg == 0 && tid < BM && !to_partial) s_xe[tid] = xe_pre;
   if constexpr (KW > 1) {
     float* red = reinterpret_cast<float*>(smem_all);
     if (kg > 0) {
