@@ -859,6 +859,117 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_lds_kernel(DevTensor t, co
 }
 
 // ---------------------------------------------------------------------------
+// Q8 weights x f32 (or bf16) activations, one token, 1..3 K steps
+// (K <= 6144; config 0 is 4096 x 4096 with f32 activations).  With the activations read straight from L2, every wave
+// of the generic kernel re-reads the whole f32 row (16 KB at K = 4096, as many
+// bytes as its four weight rows) and waits for 30-odd loads at once; a timed
+// trace of that kernel on MI355X showed no wave holding all its data before
+// 4.4 us of an 8 us call.  Here the workgroup stages the row once into LDS
+// (16-byte pieces, zero past `cols` by the raw-buffer bounds), each wave
+// holds RPW rows, every load is unconditional (clamped rows and columns), and
+// step s is multiplied as soon as its own weights have landed.  Lane l reads
+// the 32 columns it multiplies as 8 pieces, piece i of lane l stored at slot
+// 8 l + (i ^ ((l >> 1) & 7)) of its step's block, so 16 consecutive lanes
+// reading piece i touch 16 different 16-byte bank groups.  Products and the
+// order of the sums are those of the generic kernel (two fp32 chains per
+// lane, the block scale on their sum, steps in order, the wave sum).
+template <int RPW, int WAVES, int NS, bool XBF16 = false>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q8_m1_kernel(DevTensor t, const void* __restrict__ x,
+                                                                 void* __restrict__ y, uint32_t y_bf16) {
+  static_assert(NS >= 1 && NS <= 3, "K steps staged in LDS");
+  __shared__ __attribute__((aligned(16))) float s_x[NS * kStep];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
+
+  // Activations first (their wait then leaves the weights in flight).  A
+  // load piece is 16 bytes: 4 f32 or 8 bf16 columns (bf16 is widened to f32,
+  // exactly, as it is stored: two LDS pieces).
+  constexpr uint32_t kCols = XBF16 ? 8 : 4;
+  constexpr uint32_t kPieces = NS * kStep / kCols;
+  constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0,
+                                                                     (int)(cols * (XBF16 ? 2u : 4u)), 0x00020000);
+  u32x4 xv[kPer];
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
+    xv[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, p * 16u, 0, 0);
+  }
+  WChunk<KIND_Q8> wc[NS][RPW];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t k0 = s * kStep + lane * kChunk;
+    const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) load_chunk<KIND_Q8>(t, std::min(row0 + r, rows - 1), k0c, 0, 0, wc[s][r]);
+  }
+  // Nothing that uses a loaded value may be scheduled above the last load:
+  // a conversion hoisted there makes the wave wait for the loads before it.
+  __builtin_amdgcn_sched_barrier(0);
+  auto put = [&](uint32_t p, const u32x4& v) {   // f32 piece p (4 columns) to its slot
+    const uint32_t blk = p / 512u, l = (p % 512u) / 8u, i = p % 8u;
+    *reinterpret_cast<u32x4*>(&s_x[(blk * 512u + 8u * l + (i ^ ((l >> 1) & 7u))) * 4u]) = v;
+  };
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
+    if constexpr (XBF16) {
+      const u32x4 v = xv[j];
+      put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
+      put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
+    } else {
+      put(p, xv[j]);
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
+
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  const uint32_t swl = (lane >> 1) & 7u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool kin = s * kStep + lane * kChunk < kp;
+    float xf[kChunk];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&s_x[(s * 512u + 8u * lane + (i ^ swl)) * 4u]);
+      xf[4 * i] = __uint_as_float(v.x);
+      xf[4 * i + 1] = __uint_as_float(v.y);
+      xf[4 * i + 2] = __uint_as_float(v.z);
+      xf[4 * i + 3] = __uint_as_float(v.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float w[kChunk];
+      dequant_chunk<KIND_Q8>(wc[s][r], 0, 0, lane, w);
+      float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kChunk; j += 2) {
+        p0 = __builtin_fmaf(w[j], xf[j], p0);
+        p1 = __builtin_fmaf(w[j + 1], xf[j + 1], p1);
+      }
+      const float p = (p0 + p1) * f16_to_f32(wc[s][r].d);
+      acc[r] += kin ? p : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const float v = wave_sum(acc[r]);
+    const uint32_t row = row0 + r;
+    if (lane == 0 && row < rows) {
+      if (y_bf16)
+        static_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
+      else
+        static_cast<float*>(y)[row] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q8 weights x bf16 activations at M = 5..8 on MFMA.
 //
 // v_mfma_f32_16x16x32_bf16 with the activations as the A operand (rows =
@@ -1026,6 +1137,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma_kernel(DevTensor t, c
 // 2307 for the 151936-row LM head, level at 2048 x 2048; behind at M = 4
 // (the MFMA cost does not shrink with M) and at K = 6144 x N = 2048, where
 // 128 row tiles leave most CUs idle (987 vs 1089 GB/s on 4 waves, 1023 on 8).
+// Q8 x f32 activations, one token, staged through LDS (gemv_q8_m1_kernel).
+// Requires 16-byte aligned activations, cols % 4 == 0 and NS K steps.
+template <int RPW, int WAVES, int NS, bool XBF16 = false>
+hipError_t launch_q8_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % (XBF16 ? 8 : 4) != 0 ||
+      (t.kp + kStep - 1) / kStep != (uint32_t)NS)
+    return hipErrorInvalidValue;
+  const uint32_t per_block = WAVES * RPW;
+  hipLaunchKernelGGL((gemv_q8_m1_kernel<RPW, WAVES, NS, XBF16>), dim3((t.rows + per_block - 1) / per_block),
+                     dim3(WAVES * 64), 0, s, t, x, y, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
 template <int WAVES, int DI>
 hipError_t launch_q8_mfma_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
   if (m > 8 || t.cols % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.kp / 32 > kQ8MfmaMaxNb<WAVES, DI>)
@@ -1159,6 +1283,21 @@ hipError_t launch_r(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, 
                 : launch_s<KIND, MT, RPW, false>(t, x, m, y, y_bf16, s);
 }
 
+// One token of Q8 weights through the LDS-staged kernel: one row per wave and
+// eight waves per workgroup, four and four at >= 65536 rows (the LM head).
+template <bool XBF16>
+hipError_t launch_q8_x1(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (t.rows >= 65536) {
+    if (nsteps == 1) return launch_q8_m1_t<4, 4, 1, XBF16>(t, x, y, y_bf16, s);
+    if (nsteps == 2) return launch_q8_m1_t<4, 4, 2, XBF16>(t, x, y, y_bf16, s);
+    return launch_q8_m1_t<4, 4, 3, XBF16>(t, x, y, y_bf16, s);
+  }
+  if (nsteps == 1) return launch_q8_m1_t<1, 8, 1, XBF16>(t, x, y, y_bf16, s);
+  if (nsteps == 2) return launch_q8_m1_t<1, 8, 2, XBF16>(t, x, y, y_bf16, s);
+  return launch_q8_m1_t<1, 8, 3, XBF16>(t, x, y, y_bf16, s);
+}
+
 // Rows per wave: more rows per wave (more bytes in flight per wave) once rows
 // are plentiful; one row per wave keeps narrow matrices spread over all CUs.
 template <uint32_t KIND>
@@ -1174,6 +1313,21 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
       return hipErrorInvalidValue;
     }
   }
+  if constexpr (KIND == KIND_Q8) {
+    // f32 activations, one token: the LDS-staged kernel (gemv_q8_m1_kernel).
+    // Measured against the generic kernel (graph-timed, rotated copies):
+    // 4096 x 4096 (config 0) 8.46 -> 5.54 us, 2048 x 4096 7.30 -> 3.81,
+    // 2048 x 2048 4.21 -> 2.89, 6144 x 6144 19.7 -> 9.7; one row per wave and
+    // eight waves per workgroup were best up to 16384 rows, four rows per wave
+    // and four waves at the 151936-row head (79.7 -> 58.8 us).
+    // bf16 activations take the same kernel at one token (widened to f32 as
+    // they are staged): 2048 x 2048 3.15 -> 2.87 us, 6144 x 2048 5.03 ->
+    // 4.64, 2048 x 6144 (split K before) 5.75 -> 4.52, the 151936-row head
+    // 60.5 -> 57.2.
+    const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+    if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
+      return x_bf16 ? launch_q8_x1<true>(t, x, y, y_bf16, s) : launch_q8_x1<false>(t, x, y, y_bf16, s);
+  }
   if (m == 1 && split_k_enabled()) {
     hipError_t e = hipSuccess;
     if (x_bf16 ? try_split_k<KIND, 1, true>(t, x, m, y, y_bf16, s, &e)
@@ -1181,9 +1335,10 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
       return e;
   }
   if (m == 1) {
-    // Q8 with f32 activations: four rows per wave halve the activation bytes
-    // each wave re-reads from L2 per weight byte (config 0, 4096 x 4096:
-    // 8.68 -> 8.24 us against two rows).
+    // Q8 with f32 activations the LDS-staged kernel does not take (x not
+    // 16-byte aligned, K > 6144): four rows per wave halve the activation
+    // bytes each wave re-reads from L2 per weight byte (4096 x 4096: 8.68 ->
+    // 8.24 us against two rows).
     if (t.rows >= 65536 || (KIND == KIND_Q8 && !x_bf16 && t.rows >= 4096))
       return launch_r<KIND, 1, 4>(t, x, x_bf16, m, y, y_bf16, s);
     if (t.rows >= 4096) return launch_r<KIND, 1, 2>(t, x, x_bf16, m, y, y_bf16, s);
