@@ -626,7 +626,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": MEASURED_TRAFFIC_BYTES["config1"],
-                     "kernel": "vxt::gemv_kernel<9,1,..> (g64, M=1)",
+                     "kernel": "vxt::gv::gemv_g64_m1_kernel<1, 4, 1> (g64, M=1)",
                      "bytes_per_launch": r["bytes_per_call"],
                      "kernel_us": round(r["kernel_ms"] * 1e3, 3)},
         "cpu_baseline": None if cpu is None else {k: (round(v, 4) if isinstance(v, float) else v)

@@ -970,6 +970,115 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_m1_kernel(DevTensor t, con
 }
 
 // ---------------------------------------------------------------------------
+// cb4-g64 weights x bf16 activations, one token, 1..3 K steps: the structure
+// of gemv_q8_m1_kernel (activations staged once per workgroup, widened to f32
+// in swizzled LDS; every load unconditional; RPW rows per wave) with the g64
+// decode of gemv_kernel (each wave's transposed table blocks in LDS, one
+// v_perm_b32 address per lookup).  Products and summation order are those of
+// gemv_kernel.
+template <int RPW, int WAVES, int NS>
+__global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, const uint16_t* __restrict__ x,
+                                                                void* __restrict__ y, uint32_t y_bf16) {
+  static_assert(NS >= 1 && NS <= 3, "K steps staged in LDS");
+  constexpr int NB = (RPW + 1) / 2;   // table blocks per wave
+  static_assert(WAVES * NB * kTabBlock <= 65536u, "g64 table blocks must stay below 64 KiB of LDS");
+  // One array, so the table blocks start at LDS offset 0 (a lookup address
+  // keeps only its low 16 bits) and the activations follow them.
+  __shared__ __attribute__((aligned(4096))) uint32_t s_mem[WAVES * NB * kTabBlock / 4 + NS * kStep];
+  uint32_t* const s_tab = s_mem;
+  float* const s_x = reinterpret_cast<float*>(s_mem + WAVES * NB * kTabBlock / 4);
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
+
+  constexpr uint32_t kPieces = NS * kStep / 8;   // 16-byte pieces of bf16 activations
+  constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)(cols * 2u), 0x00020000);
+  u32x4 xv[kPer];
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
+    xv[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, p * 16u, 0, 0);
+  }
+  WChunk<KIND_G64> wc[NS][RPW];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t k0 = s * kStep + lane * kChunk;
+    const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
+    const uint32_t gmax = kp / 64 - 1;
+    const uint32_t g = s * 32 + (lane >> 1);
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+      load_chunk<KIND_G64>(t, std::min(row0 + r, rows - 1), k0c, g < gmax ? g : gmax, lane & 1, wc[s][r]);
+  }
+  // Nothing that uses a loaded value may be scheduled above the last load.
+  __builtin_amdgcn_sched_barrier(0);
+  auto put = [&](uint32_t p, const u32x4& v) {   // f32 piece p (4 columns) to its slot
+    const uint32_t blk = p / 512u, l = (p % 512u) / 8u, i = p % 8u;
+    *reinterpret_cast<u32x4*>(&s_x[(blk * 512u + 8u * l + (i ^ ((l >> 1) & 7u))) * 4u]) = v;
+  };
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
+    const u32x4 v = xv[j];
+    put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
+    put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
+  }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
+
+  const uint32_t tab = lds_addr(s_tab) + wave * NB * kTabBlock;
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  const uint32_t swl = (lane >> 1) & 7u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool kin = s * kStep + lane * kChunk < kp;
+    // this step's tables (the wave's LDS operations run in order, so the
+    // previous step's lookups are done first)
+#pragma unroll
+    for (int p = 0; p < NB; ++p)
+      store_g64_tables(tab + p * kTabBlock, lane, wc[s][2 * p], 2 * p + 1 < RPW ? &wc[s][2 * p + 1] : nullptr);
+    float xf[kChunk];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&s_x[(s * 512u + 8u * lane + (i ^ swl)) * 4u]);
+      xf[4 * i] = __uint_as_float(v.x);
+      xf[4 * i + 1] = __uint_as_float(v.y);
+      xf[4 * i + 2] = __uint_as_float(v.z);
+      xf[4 * i + 3] = __uint_as_float(v.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const uint32_t sl = tab + (r / 2) * kTabBlock + lane * 4u + (r & 1) * 2u;
+      float w[kChunk];
+      dequant_chunk<KIND_G64>(wc[s][r], 0, sl, lane, w);
+      float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kChunk; j += 2) {
+        p0 = __builtin_fmaf(w[j], xf[j], p0);
+        p1 = __builtin_fmaf(w[j + 1], xf[j + 1], p1);
+      }
+      acc[r] += kin ? p0 + p1 : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const float v = wave_sum(acc[r]);
+    const uint32_t row = row0 + r;
+    if (lane == 0 && row < rows) {
+      if (y_bf16)
+        static_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
+      else
+        static_cast<float*>(y)[row] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q8 weights x bf16 activations at M = 5..8 on MFMA.
 //
 // v_mfma_f32_16x16x32_bf16 with the activations as the A operand (rows =
@@ -1137,6 +1246,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma_kernel(DevTensor t, c
 // 2307 for the 151936-row LM head, level at 2048 x 2048; behind at M = 4
 // (the MFMA cost does not shrink with M) and at K = 6144 x N = 2048, where
 // 128 row tiles leave most CUs idle (987 vs 1089 GB/s on 4 waves, 1023 on 8).
+// cb4-g64 x bf16, one token, staged through LDS (gemv_g64_m1_kernel).
+// Requires 16-byte aligned activations, cols % 8 == 0 and NS K steps.
+template <int RPW, int WAVES, int NS>
+hipError_t launch_g64_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % 8 != 0 || (t.kp + kStep - 1) / kStep != (uint32_t)NS)
+    return hipErrorInvalidValue;
+  const uint32_t per_block = WAVES * RPW;
+  hipLaunchKernelGGL((gemv_g64_m1_kernel<RPW, WAVES, NS>), dim3((t.rows + per_block - 1) / per_block),
+                     dim3(WAVES * 64), 0, s, t, static_cast<const uint16_t*>(x), y, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
 // Q8 x f32 activations, one token, staged through LDS (gemv_q8_m1_kernel).
 // Requires 16-byte aligned activations, cols % 4 == 0 and NS K steps.
 template <int RPW, int WAVES, int NS, bool XBF16 = false>
@@ -1327,6 +1448,25 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
     const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
     if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
       return x_bf16 ? launch_q8_x1<true>(t, x, y, y_bf16, s) : launch_q8_x1<false>(t, x, y, y_bf16, s);
+  }
+  if constexpr (KIND == KIND_G64) {
+    // One token: the LDS-staged kernel (gemv_g64_m1_kernel).  Measured
+    // against gemv_kernel (graph-timed, rotated copies): 6144 x 2048 (config
+    // 1) 4.86 -> 4.66 us, 2048 x 2048 3.15 -> 3.09, 2048 x 6144 (split K
+    // before) 5.61 -> 5.33 with one row per wave; 12288 x 2048 7.71 -> 6.85,
+    // 24576 x 2048 12.32 -> 11.59, 151936 x 2048 59.6 -> 52.4 with two; four
+    // waves per workgroup throughout.
+    const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+    if (m == 1 && x_bf16 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % 8 == 0) {
+      if (t.rows > 8192) {
+        if (nsteps == 1) return launch_g64_m1_t<2, 4, 1>(t, x, y, y_bf16, s);
+        if (nsteps == 2) return launch_g64_m1_t<2, 4, 2>(t, x, y, y_bf16, s);
+        return launch_g64_m1_t<2, 4, 3>(t, x, y, y_bf16, s);
+      }
+      if (nsteps == 1) return launch_g64_m1_t<1, 4, 1>(t, x, y, y_bf16, s);
+      if (nsteps == 2) return launch_g64_m1_t<1, 4, 2>(t, x, y, y_bf16, s);
+      return launch_g64_m1_t<1, 4, 3>(t, x, y, y_bf16, s);
+    }
   }
   if (m == 1 && split_k_enabled()) {
     hipError_t e = hipSuccess;
