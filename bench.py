@@ -42,7 +42,7 @@ EAGER = False   # --eager: plain launches instead of graph replays, for profiler
 # HBM bytes per launch of the headline kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, WRITE_SIZE) scaled by what the same counters read for a
 # device-to-device copy of known size; see profiles/gemv_g64_config1.md.
-MEASURED_TRAFFIC_BYTES = {"config1": 12709173}
+MEASURED_TRAFFIC_BYTES = {"config1": 12688655}
 
 
 def log(msg: str) -> None:
