@@ -1079,6 +1079,139 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, co
 }
 
 // ---------------------------------------------------------------------------
+// cb4 (reference layout) weights, one token, 1..3 K steps: the structure of
+// gemv_q8_m1_kernel with the cb4 decode of gemv_kernel (centroid tables in
+// LDS, the group scale on the 32-column partial sum, the zero-scale group
+// skip of codebook.rs:384-386, CSR residuals after the dense part in lane
+// order).  The residuals' activations come from the staged row in LDS, so the
+// call does not end on a dependent global read.  Products and summation order
+// are those of gemv_kernel.
+template <int RPW, int WAVES, int NS, bool XBF16>
+__global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, const void* __restrict__ x,
+                                                                void* __restrict__ y, uint32_t y_bf16) {
+  static_assert(NS >= 1 && NS <= 3, "K steps staged in LDS");
+  __shared__ __attribute__((aligned(64))) float s_cent[48];
+  __shared__ __attribute__((aligned(16))) float s_x[NS * kStep];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
+
+  // Each row's CSR bounds first, then the activations, the weights and each
+  // lane's first residual entry.
+  uint32_t rr[RPW], os[RPW], oe[RPW], pk0[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    rr[r] = std::min(row0 + r, rows - 1);
+    os[r] = t.row_ptr[rr[r]];
+    oe[r] = t.row_ptr[rr[r] + 1];
+  }
+  constexpr uint32_t kCols = XBF16 ? 8 : 4;
+  constexpr uint32_t kPieces = NS * kStep / kCols;
+  constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0,
+                                                                     (int)(cols * (XBF16 ? 2u : 4u)), 0x00020000);
+  u32x4 xv[kPer];
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
+    xv[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, p * 16u, 0, 0);
+  }
+  WChunk<KIND_CB4> wc[NS][RPW];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t k0 = s * kStep + lane * kChunk;
+    const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) load_chunk<KIND_CB4>(t, rr[r], k0c, 0, 0, wc[s][r]);
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {   // clamped, unconditional (the CSR stream holds at least one word)
+    const uint32_t i = os[r] + lane;
+    const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
+    pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
+  }
+  // Nothing that uses a loaded value may be scheduled above the last load.
+  __builtin_amdgcn_sched_barrier(0);
+  if (tid < 48) s_cent[tid] = t.cent[tid];
+  auto put = [&](uint32_t p, const u32x4& v) {   // f32 piece p (4 columns) to its slot
+    const uint32_t blk = p / 512u, l = (p % 512u) / 8u, i = p % 8u;
+    *reinterpret_cast<u32x4*>(&s_x[(blk * 512u + 8u * l + (i ^ ((l >> 1) & 7u))) * 4u]) = v;
+  };
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
+    const u32x4 v = xv[j];
+    if constexpr (XBF16) {
+      put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
+      put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
+    } else {
+      put(p, v);
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
+
+  float acc[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+  const uint32_t swl = (lane >> 1) & 7u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool kin = s * kStep + lane * kChunk < kp;
+    float xf[kChunk];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&s_x[(s * 512u + 8u * lane + (i ^ swl)) * 4u]);
+      xf[4 * i] = __uint_as_float(v.x);
+      xf[4 * i + 1] = __uint_as_float(v.y);
+      xf[4 * i + 2] = __uint_as_float(v.z);
+      xf[4 * i + 3] = __uint_as_float(v.w);
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      float w[kChunk];
+      dequant_chunk<KIND_CB4>(wc[s][r], lds_addr(s_cent) + 64u * cent_table(t, rr[r]), 0, lane, w);
+      float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kChunk; j += 2) {
+        p0 = __builtin_fmaf(w[j], xf[j], p0);
+        p1 = __builtin_fmaf(w[j + 1], xf[j + 1], p1);
+      }
+      float p = p0 + p1;
+      const float sc = f16_to_f32(wc[s][r].sc);   // codebook.rs:384-386: a zero scale skips the group
+      p = sc != 0.0f ? sc * p : 0.0f;
+      acc[r] += kin ? p : 0.0f;
+    }
+  }
+  // CSR residuals (codebook.rs:409-415): lane l takes entries l, l + 64, ...
+  // of the row, in that order; the activation comes from the staged row.
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    if (row0 + r >= rows) break;   // later rows are past the end too
+    for (uint32_t i = os[r] + lane; i < oe[r]; i += 64u) {
+      const uint32_t pk = i < os[r] + 64u ? pk0[r] : t.outliers[i];
+      const uint32_t col = pk & 0xffffu;
+      if (col >= cols) continue;
+      const uint32_t q = col / 4u, blk = q / 512u, l = (q % 512u) / 8u, pi = q % 8u;
+      const float xc = s_x[(blk * 512u + 8u * l + (pi ^ ((l >> 1) & 7u))) * 4u + col % 4u];
+      acc[r] = __builtin_fmaf(f16_to_f32(pk >> 16), xc, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const float v = wave_sum(acc[r]);
+    const uint32_t row = row0 + r;
+    if (lane == 0 && row < rows) {
+      if (y_bf16)
+        static_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
+      else
+        static_cast<float*>(y)[row] = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Q8 weights x bf16 activations at M = 5..8 on MFMA.
 //
 // v_mfma_f32_16x16x32_bf16 with the activations as the A operand (rows =
@@ -1258,6 +1391,20 @@ hipError_t launch_g64_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf
   return hipGetLastError();
 }
 
+// cb4 x bf16 / f32, one token, staged through LDS (gemv_cb4_m1_kernel).
+// Requires 16-byte aligned activations, 16-byte pieces wholly inside or
+// outside the row, and NS K steps.
+template <int RPW, int WAVES, int NS, bool XBF16>
+hipError_t launch_cb4_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % (XBF16 ? 8 : 4) != 0 ||
+      (t.kp + kStep - 1) / kStep != (uint32_t)NS)
+    return hipErrorInvalidValue;
+  const uint32_t per_block = WAVES * RPW;
+  hipLaunchKernelGGL((gemv_cb4_m1_kernel<RPW, WAVES, NS, XBF16>), dim3((t.rows + per_block - 1) / per_block),
+                     dim3(WAVES * 64), 0, s, t, x, y, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
 // Q8 x f32 activations, one token, staged through LDS (gemv_q8_m1_kernel).
 // Requires 16-byte aligned activations, cols % 4 == 0 and NS K steps.
 template <int RPW, int WAVES, int NS, bool XBF16 = false>
@@ -1404,6 +1551,21 @@ hipError_t launch_r(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, 
                 : launch_s<KIND, MT, RPW, false>(t, x, m, y, y_bf16, s);
 }
 
+// One token of cb4 weights through the LDS-staged kernel: one row per wave
+// up to 8192 rows, two above; eight waves per workgroup.
+template <bool XBF16>
+hipError_t launch_cb4_m1(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (t.rows > 8192) {
+    if (nsteps == 1) return launch_cb4_m1_t<2, 8, 1, XBF16>(t, x, y, y_bf16, s);
+    if (nsteps == 2) return launch_cb4_m1_t<2, 8, 2, XBF16>(t, x, y, y_bf16, s);
+    return launch_cb4_m1_t<2, 8, 3, XBF16>(t, x, y, y_bf16, s);
+  }
+  if (nsteps == 1) return launch_cb4_m1_t<1, 8, 1, XBF16>(t, x, y, y_bf16, s);
+  if (nsteps == 2) return launch_cb4_m1_t<1, 8, 2, XBF16>(t, x, y, y_bf16, s);
+  return launch_cb4_m1_t<1, 8, 3, XBF16>(t, x, y, y_bf16, s);
+}
+
 // One token of Q8 weights through the LDS-staged kernel: one row per wave and
 // eight waves per workgroup, four and four at >= 65536 rows (the LM head).
 template <bool XBF16>
@@ -1448,6 +1610,16 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
     const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
     if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
       return x_bf16 ? launch_q8_x1<true>(t, x, y, y_bf16, s) : launch_q8_x1<false>(t, x, y, y_bf16, s);
+  }
+  if constexpr (KIND == KIND_CB4) {
+    // One token: the LDS-staged kernel (gemv_cb4_m1_kernel).  Measured against
+    // gemv_kernel (bf16 x, 0.7 % residuals, graph-timed, rotated copies):
+    // 6144 x 2048 5.11 -> 4.80 us, 2048 x 2048 4.01 -> 3.42, 2048 x 6144
+    // 6.20 -> 5.31 with one row per wave; 12288 x 2048 8.10 -> 7.01 with two;
+    // eight waves per workgroup.
+    const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+    if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
+      return x_bf16 ? launch_cb4_m1<true>(t, x, y, y_bf16, s) : launch_cb4_m1<false>(t, x, y, y_bf16, s);
   }
   if constexpr (KIND == KIND_G64) {
     // One token: the LDS-staged kernel (gemv_g64_m1_kernel).  Measured
