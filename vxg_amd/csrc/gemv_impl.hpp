@@ -1079,6 +1079,120 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, co
 }
 
 // ---------------------------------------------------------------------------
+// Q8 weights x bf16 activations, MT tokens (2..8), 1..3 K steps: the
+// structure of gemv_q8_m1_kernel (every token's row staged once per workgroup
+// in LDS, as packed bf16 pairs; every load unconditional; RPW rows per wave)
+// with the arithmetic of gemv_q8_dot2_kernel (v_dot2_f32_bf16 on int8 pairs
+// widened to bf16, the block scale on the two chains' sum).  Lane l reads its
+// 32 columns of a token as 4 pieces, piece i stored at slot
+// 4 l + (i ^ ((l >> 2) & 3)) of the token's step block, so 16 consecutive
+// lanes reading piece i touch 16 different 16-byte bank groups.
+template <int MT, int RPW, int WAVES, int NS>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q8_mt_kernel(DevTensor t, const uint16_t* __restrict__ x,
+                                                               void* __restrict__ y, uint32_t M_rt, uint32_t y_bf16) {
+  static_assert(NS >= 1 && NS <= 3 && MT >= 2 && MT <= 8, "tokens and K steps staged in LDS");
+  constexpr uint32_t kBlk = kStep / 8;   // 16-byte pieces of one token's step block
+  __shared__ __attribute__((aligned(16))) uint32_t s_x[MT * NS * kStep / 2];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
+
+  constexpr uint32_t kPieces = MT * NS * kBlk;
+  constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
+  u32x4 xv[kPer];
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
+    const uint32_t m = p / (NS * kBlk), q = p % (NS * kBlk);
+    xv[j] = __builtin_amdgcn_raw_buffer_load_b128(x_row_rsrc(x, cols, m < M_rt ? m : 0), q * 16u, 0, 0);
+  }
+  WChunk<KIND_Q8> wc[NS][RPW];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t k0 = s * kStep + lane * kChunk;
+    const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) load_chunk<KIND_Q8>(t, std::min(row0 + r, rows - 1), k0c, 0, 0, wc[s][r]);
+  }
+  // Nothing that uses a loaded value may be scheduled above the last load.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (uint32_t j = 0; j < kPer; ++j) {
+    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
+    const uint32_t mb = p / kBlk, q = p % kBlk, l = q / 4u, i = q % 4u;   // mb = token * NS + step
+    *reinterpret_cast<u32x4*>(&s_x[(mb * kBlk + 4u * l + (i ^ ((l >> 2) & 3u))) * 4u]) = xv[j];
+  }
+  __syncthreads();
+  __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
+
+  float acc[RPW][MT];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+  const uint32_t swl = (lane >> 2) & 3u;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool kin = s * kStep + lane * kChunk < kp;
+    uint32_t qp[RPW][kChunk / 2];
+    float d[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      q8_pairs(wc[s][r], qp[r]);
+      d[r] = f16_to_f32(wc[s][r].d);
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      uint32_t xp[kChunk / 2];
+#pragma unroll
+      for (uint32_t i = 0; i < 4; ++i) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(&s_x[((m * NS + s) * kBlk + 4u * lane + (i ^ swl)) * 4u]);
+        xp[4 * i] = v.x;
+        xp[4 * i + 1] = v.y;
+        xp[4 * i + 2] = v.z;
+        xp[4 * i + 3] = v.w;
+      }
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kChunk / 2; j += 2) {
+          p0 = dot2_bf16(qp[r][j], xp[j], p0);
+          p1 = dot2_bf16(qp[r][j + 1], xp[j + 1], p1);
+        }
+        acc[r][m] += kin ? (p0 + p1) * d[r] : 0.0f;
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const uint32_t row = row0 + r;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+      const float v = wave_sum(acc[r][m]);
+      if (lane == 0 && row < rows && (uint32_t)m < M_rt) {
+        if (y_bf16)
+          static_cast<uint16_t*>(y)[(size_t)m * rows + row] = f32_to_bf16(v);
+        else
+          static_cast<float*>(y)[(size_t)m * rows + row] = v;
+      }
+    }
+  }
+}
+
+template <int MT, int RPW, int WAVES, int NS>
+hipError_t launch_q8_mt_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  if (m > (uint32_t)MT || reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % 8 != 0 ||
+      (t.kp + kStep - 1) / kStep != (uint32_t)NS)
+    return hipErrorInvalidValue;
+  const uint32_t per_block = WAVES * RPW;
+  hipLaunchKernelGGL((gemv_q8_mt_kernel<MT, RPW, WAVES, NS>), dim3((t.rows + per_block - 1) / per_block),
+                     dim3(WAVES * 64), 0, s, t, static_cast<const uint16_t*>(x), y, m, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // cb4 (reference layout) weights, one token, 1..3 K steps: the structure of
 // gemv_q8_m1_kernel with the cb4 decode of gemv_kernel (centroid tables in
 // LDS, the group scale on the 32-column partial sum, the zero-scale group
@@ -1551,6 +1665,22 @@ hipError_t launch_r(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, 
                 : launch_s<KIND, MT, RPW, false>(t, x, m, y, y_bf16, s);
 }
 
+// 2 or 3..4 tokens of Q8 weights through the LDS-staged kernel: one row per
+// wave (eight waves, four for three K steps); two rows and eight waves at
+// >= 65536 rows (the LM head).
+template <int MT>
+hipError_t launch_q8_mt(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (t.rows >= 65536) {
+    if (nsteps == 1) return launch_q8_mt_t<MT, 2, 8, 1>(t, x, m, y, y_bf16, s);
+    if (nsteps == 2) return launch_q8_mt_t<MT, 2, 8, 2>(t, x, m, y, y_bf16, s);
+    return launch_q8_mt_t<MT, 2, 8, 3>(t, x, m, y, y_bf16, s);
+  }
+  if (nsteps == 1) return launch_q8_mt_t<MT, 1, 8, 1>(t, x, m, y, y_bf16, s);
+  if (nsteps == 2) return launch_q8_mt_t<MT, 1, 8, 2>(t, x, m, y, y_bf16, s);
+  return launch_q8_mt_t<MT, 1, 4, 3>(t, x, m, y, y_bf16, s);
+}
+
 // One token of cb4 weights through the LDS-staged kernel: one row per wave
 // up to 8192 rows, two above; eight waves per workgroup.
 template <bool XBF16>
@@ -1587,6 +1717,20 @@ template <uint32_t KIND>
 hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void* y, bool y_bf16,
                        hipStream_t s) {
   if constexpr (KIND == KIND_Q8) {
+    // 2..8 tokens with bf16 activations: the LDS-staged kernel
+    // (gemv_q8_mt_kernel) where it measured faster than the dot2 and MFMA
+    // kernels (graph-timed, rotated copies; 2048 x 2048 / 6144 x 2048 /
+    // 2048 x 6144 / 151936 x 2048): M = 2 3.99 / 5.97 / 6.29 / 64.5 us ->
+    // 3.22 / 4.95 / 5.26 / 63.0; M = 4 4.95 / 7.82 / 8.75 / 84.6 -> 3.81 /
+    // 5.92 / 6.64 / 80.1; M = 8 only at 2048 x 2048, 6.25 -> 4.98 (the MFMA
+    // and persistent kernels keep the others).
+    if (x_bf16 && m >= 2 && m <= 8) {
+      const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+      if (nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % 8 == 0) {
+        if (m <= 4) return m == 2 ? launch_q8_mt<2>(t, x, m, y, y_bf16, s) : launch_q8_mt<4>(t, x, m, y, y_bf16, s);
+        if (t.rows <= 4096 && nsteps == 1) return launch_q8_mt_t<8, 1, 4, 1>(t, x, m, y, y_bf16, s);
+      }
+    }
     if (x_bf16 && m >= 2) {
       if (m == 2) return launch_q8_dot2_m<2>(t, x, m, y, y_bf16, s);
       if (m > 4 && t.cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.kp / 32 <= kQ8MfmaMaxNb<4, 4>)
