@@ -481,18 +481,25 @@ VXT_API void vxt_hip_graph_free(void* graph);
 VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
 
 /* Prefill GEMM path (batch_m > 8) of this context's later calls.  Every path
- * runs this library's own kernels except LIBRARY.  AUTO (the default):
- * g64 weights with bf16 activations decode inside the MFMA loop -- the
- * 128 x 128 tile kernel from batch_m 65, the fused kernel below; Q8_0 (and
- * Q4_0) weights with bf16 activations and batch_m <= 256 take the fused
- * kernel; every other call takes the two-phase path (a decoded f16 weight
- * panel, then the dense MFMA kernel).  PANEL pins the two-phase path; FUSED
- * takes the decode-in-loop kernels at every batch_m they apply to; LIBRARY
- * pins the two-phase path with its dense phase on hipBLASLt, a comparison
- * only (falling back to the own kernel for a shape the library has no
- * algorithm for).  A tuning and test control with no counterpart in the
- * reference, whose gemm_cpu (llm_prefill.rs:156-255) has a single path.
- * Returns VXT_E_ARG for an unknown path. */
+ * runs this library's own kernels except LIBRARY.  AUTO (the default), by
+ * measured speed: g64 weights with bf16 activations decode inside the MFMA
+ * loop -- the fused kernel up to batch_m 64, the 128 x 128 tile kernel from
+ * 192 to 2047 (and beyond when cols > rows); Q8_0 (and Q4_0) weights with
+ * bf16 activations and batch_m <= 128 take the fused kernel; every other call
+ * takes the two-phase path (a decoded f16 weight panel, then the dense MFMA
+ * kernel).  PANEL pins the two-phase path.  FUSED takes the decode-in-loop
+ * kernels wherever they apply: for cb4 weights with bf16 activations the cb4
+ * tile kernel (scale x centroid tables and the CSR residuals decoded inside
+ * the MFMA loop, no weight panel), when the upload found the tensor eligible
+ * (every plane finite, each row's residual columns strictly increasing, at
+ * most 16384 residuals per block of 128 rows); for g64 the tile kernel above
+ * batch_m 64 and the fused kernel below; for Q8_0 / Q4_0 the fused kernel;
+ * the two-phase path otherwise.  LIBRARY pins the two-phase path with its
+ * dense phase on hipBLASLt, a comparison only (falling back to the own
+ * kernel for a shape the library has no algorithm for).  A tuning and test
+ * control with no counterpart in the reference, whose gemm_cpu
+ * (llm_prefill.rs:156-255) has a single path.  Returns VXT_E_ARG for an
+ * unknown path. */
 #define VXT_GEMM_AUTO 0u
 #define VXT_GEMM_PANEL 1u
 #define VXT_GEMM_FUSED 2u

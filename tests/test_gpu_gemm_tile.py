@@ -104,3 +104,83 @@ def test_dense_kernel_q8_block_scales_extreme(eng):
     b[1::7, 0:2] = np.array([0x0001], np.uint16).view(np.uint8)   # subnormal d
     q.blocks = b.reshape(-1)
     check(eng, q, 512, engine.GEMM_PANEL)
+
+
+# ---- the cb4 decode-in-loop tile kernel (GEMM_FUSED pins it for eligible
+# tensors: finite planes, each row's residual columns increasing, at most
+# 4096 residuals per 128-row block) -------------------------------------------
+
+def check_parts(eng, parts, M, path, seed=0):
+    """check() for a row-concatenated tensor of cb4 parts."""
+    t = eng.upload_concat(parts)
+    K = parts[0].cols
+    xb = synth.make_x_bf16(M, K, seed=seed)
+    X = bf16_bits_to_f32(xb).reshape(M, K)
+    sel = np.unique(np.r_[0:3, M // 2, M - 3:M])
+    W = np.concatenate([oracle.decode_rows(p) for p in parts])
+    yref = np.concatenate([oracle.gemm(p, X[sel], threads=THREADS) for p in parts], axis=1)
+    eng.set_gemm_path(path)
+    try:
+        yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
+    fl = floor_scale(W, X[sel])
+    assert max_rel(yf[sel], yref, fl) <= 1e-3
+    assert_bf16_close(yb[sel], yref, fl)
+    assert np.array_equal(yb, f32_to_bf16_bits(yf))
+    t.free()
+    return yf
+
+
+# ragged M, N and K; split K on small grids (M <= 128, short N); a residual
+# density that puts several residuals in one lane's 8-column window
+@pytest.mark.parametrize("M,N,K,frac", [(9, 130, 100, 0.0074), (130, 640, 300, 0.0074), (300, 1500, 1000, 0.0074),
+                                        (129, 2048, 3000, 0.0074), (1000, 384, 2048, 0.0074),
+                                        (2048, 640, 192, 0.0074), (64, 900, 448, 0.05)])
+def test_cb4_tile_kernel_shapes(eng, M, N, K, frac):
+    m = synth.make_cb4(N, K, seed=M + N, outlier_frac=frac)
+    check(eng, m, M, engine.GEMM_FUSED, seed=K)
+
+
+def test_cb4_tile_kernel_repeatable(eng):
+    """Split-K partial sums are added in slice order: bit-identical reruns."""
+    m = synth.make_cb4(256, 6144, seed=5)
+    a = check(eng, m, 200, engine.GEMM_FUSED)
+    b = check(eng, m, 200, engine.GEMM_FUSED)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_cb4_tile_kernel_concatenated_parts(eng):
+    """Three parts with their own centroid tables, split at rows that are not
+    multiples of 32, so lanes of one wave read different tables."""
+    parts = [synth.make_cb4(r, 700, seed=20 + i) for i, r in enumerate((45, 70, 51))]
+    for i, p in enumerate(parts):
+        p.centroids = (p.centroids * (1.0 + 3 * i)).astype(np.float32)
+    check_parts(eng, parts, 150, engine.GEMM_FUSED, seed=3)
+
+
+def test_cb4_tile_kernel_scales_zero_and_extreme(eng):
+    """Zero-scale groups, scales near the f16 maximum and centroids far below
+    one in the same tensor: the per-row exponents keep every hi / lo split in
+    the f16 range."""
+    m = synth.make_cb4(300, 1024, seed=9)
+    sc = m.scales_f16.reshape(300, -1).copy()
+    sc[0::7, 1] = 0
+    sc[3::11, :] = np.array([0x7BFF], np.uint16)        # 65504
+    sc[5::13, 2] = np.array([0x0001], np.uint16)        # smallest subnormal
+    m.scales_f16 = sc.reshape(-1)
+    m.centroids = (m.centroids * 1e-3).astype(np.float32)
+    check(eng, m, 260, engine.GEMM_FUSED, seed=4)
+
+
+def test_cb4_tile_kernel_ineligible_tensor(eng):
+    """A residual column repeated within a row (decode_row adds both) makes
+    the tensor take the two-phase path, which meets the same bar."""
+    m = synth.make_cb4(200, 512, seed=12)
+    rp = m.outlier_row_ptr
+    r = int(np.argmax(np.diff(rp.astype(np.int64)) >= 2))
+    m.outliers_packed = m.outliers_packed.copy()
+    a = int(rp[r])
+    m.outliers_packed[a + 1] = (m.outliers_packed[a + 1] & 0xFFFF0000) | (m.outliers_packed[a] & 0xFFFF)
+    check(eng, m, 150, engine.GEMM_FUSED, seed=6)

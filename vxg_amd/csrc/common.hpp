@@ -35,6 +35,9 @@ struct DevTensor {
   uint32_t split0, split1;   // CB4: first rows served by tables 1 and 2
   float cent[48];            // CB4 only: 3 centroid tables of 16
   uint32_t tail_nonfinite;   // G64: cols % 64 != 0 and some row's last table holds Inf/NaN
+  // CB4 only, null unless the decode-in-loop GEMM takes the tensor: per row,
+  // the exponent e with (the row's largest |w| bound) * 2^e in [2^14, 2^15).
+  const int8_t* rexp;
 };
 
 // Prefill GEMM path (batch_m > 8): chosen per call, or pinned by the caller.

@@ -892,6 +892,10 @@ bool gemm_tile_supported(const DevTensor& t, bool x_bf16);
 size_t gemm_tile_workspace_bytes(const DevTensor& t, uint32_t m);
 hipError_t launch_gemm_tile(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
                             size_t ws_bytes, hipStream_t s);
+bool gemm_tile_cb4_supported(const DevTensor& t, bool x_bf16);
+size_t gemm_tile_cb4_workspace_bytes(const DevTensor& t, uint32_t m);
+hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t m, void* y, bool y_bf16, void* ws,
+                                size_t ws_bytes, hipStream_t s);
 
 // Path choice, unless the caller pins one (every path runs every kind):
 //   * g64 weights, bf16 activations: the fused kernel up to batch 64; the
@@ -913,13 +917,14 @@ constexpr uint32_t kG64FusedMaxM = 64;
 constexpr uint32_t kTileMinM = 192;
 constexpr uint32_t kTileMaxM = 2048;   // exclusive, unless K > N
 
-enum class Path { Fused, Tile, Panel };
+enum class Path { Fused, Tile, TileCb4, Panel };
 
 static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
   if (mode == kGemmPanel || mode == kGemmLibrary) return Path::Panel;
   const bool tile_ok = gemm_tile_supported(t, x_bf16);
   const bool fused_ok = gemm_fused_supported(t, x_bf16);
   if (mode == kGemmFused) {   // decode inside the MFMA loop wherever it applies
+    if (gemm_tile_cb4_supported(t, x_bf16)) return Path::TileCb4;
     if (tile_ok && m > kG64FusedMaxM) return Path::Tile;
     return fused_ok ? Path::Fused : Path::Panel;
   }
@@ -941,6 +946,7 @@ static size_t xe_bytes(uint32_t m) { return gp::al256((size_t)m * 4); }
 size_t gemm_workspace_bytes(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
   switch (choose_path(t, m, x_bf16, mode)) {
     case Path::Tile: return gemm_tile_workspace_bytes(t, m);
+    case Path::TileCb4: return gemm_tile_cb4_workspace_bytes(t, m);
     case Path::Fused: return xe_bytes(m) + gemm_fused_workspace_bytes(t, m);
     default: break;
   }
@@ -954,6 +960,8 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   const Path path = choose_path(t, m, x_bf16, mode);
   if (path == Path::Tile)
     return launch_gemm_tile(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
+  if (path == Path::TileCb4)
+    return launch_gemm_tile_cb4(t, static_cast<const uint16_t*>(x), m, y, y_bf16, ws, ws_bytes, s);
   if (ws_bytes < xe_bytes(m)) return hipErrorInvalidValue;
   int32_t* xe = static_cast<int32_t*>(ws);
   void* rest = static_cast<char*>(ws) + xe_bytes(m);

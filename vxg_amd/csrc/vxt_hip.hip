@@ -10,6 +10,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <limits>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -83,6 +84,7 @@ struct Tensor {
   uint32_t split0 = 0, split1 = 0;
   float cent[48] = {};
   uint32_t tail_nonfinite = 0;   // g64: see DevTensor::tail_nonfinite
+  size_t off_rx = 0;             // cb4: row exponents of the decode-in-loop GEMM (0: not eligible)
 
   DevTensor dev() const {
     DevTensor d{};
@@ -100,6 +102,7 @@ struct Tensor {
       d.split0 = split0;
       d.split1 = split1;
       std::memcpy(d.cent, cent, sizeof(cent));
+      if (off_rx) d.rexp = reinterpret_cast<const int8_t*>(base + off_rx);
     }
     return d;
   }
@@ -501,6 +504,69 @@ void* vxt_hip_upload_q4_0(void* ctx, uint32_t rows, uint32_t cols, uint32_t padd
   return out;
 }
 
+namespace {
+
+float host_f16_to_f32(uint16_t h) {
+  const uint32_t s = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+  if (e == 0x1f) return m ? std::numeric_limits<float>::quiet_NaN() : (s ? -INFINITY : INFINITY);
+  const float v = e ? std::ldexp((float)(m | 0x400u), (int)e - 25) : std::ldexp((float)m, -24);
+  return s ? -v : v;
+}
+
+}  // namespace
+
+// Whether the decode-in-loop GEMM can take a cb4 tensor, and its per-row
+// exponents if so: every centroid, scale and residual finite; each row's
+// residual columns strictly increasing and inside the row; at most
+// kCb4TileResCap residuals per block of 128 rows (the block's list is staged
+// in LDS); e with bound * 2^e in [2^14, 2^15) for bound = largest |scale| x
+// largest |centroid| + largest |residual| of the row (so every w * 2^e, and
+// its hi/lo f16 split, stays inside the f16 range).
+constexpr uint32_t kCb4TileResCap = 16384;
+
+static bool cb4_tile_exponents(const VxtCb4View* subs, uint32_t n_subs, const uint32_t* rp, const uint32_t* outl,
+                               const uint16_t* scales, std::vector<int8_t>& rex) {
+  size_t rows = 0;
+  for (uint32_t i = 0; i < n_subs; ++i) rows += subs[i].rows;
+  const uint32_t cols = subs[0].cols, gpr = subs[0].padded_cols / 128u;
+  rex.assign(rows, 0);
+  size_t r = 0;
+  for (uint32_t i = 0; i < n_subs; ++i) {
+    double cmax = 0.0;
+    for (int q = 0; q < 16; ++q) {
+      const float c = subs[i].centroids[q];
+      if (!std::isfinite(c)) return rex.clear(), false;
+      cmax = std::max(cmax, (double)std::fabs(c));
+    }
+    for (size_t rr = 0; rr < subs[i].rows; ++rr, ++r) {
+      double smax = 0.0, emax = 0.0;
+      for (uint32_t g = 0; g < gpr; ++g) {
+        const float sc = host_f16_to_f32(scales[r * gpr + g]);
+        if (!std::isfinite(sc)) return rex.clear(), false;
+        smax = std::max(smax, (double)std::fabs(sc));
+      }
+      int64_t prev = -1;
+      for (uint32_t k = rp[r]; k < rp[r + 1]; ++k) {
+        const uint32_t col = outl[k] & 0xffffu;
+        const float v = host_f16_to_f32((uint16_t)(outl[k] >> 16));
+        if (col >= cols || (int64_t)col <= prev || !std::isfinite(v)) return rex.clear(), false;
+        prev = col;
+        emax = std::max(emax, (double)std::fabs(v));
+      }
+      const double bound = smax * cmax + emax;
+      int e = 0;
+      if (bound > 0.0) {
+        e = 14 - std::ilogb(bound);
+        if (e < -100 || e > 100) return rex.clear(), false;
+      }
+      rex[r] = (int8_t)e;
+    }
+  }
+  for (size_t b = 0; b < rows; b += 128)
+    if (rp[std::min(rows, b + 128)] - rp[b] > kCb4TileResCap) return rex.clear(), false;
+  return true;
+}
+
 void* vxt_hip_upload_cb4(void* ctx, const VxtCb4View* v, char* err, size_t err_cap) {
   return vxt_hip_upload_cb4_concat(ctx, v, 1u, err, err_cap);
 }
@@ -545,8 +611,19 @@ void* vxt_hip_upload_cb4_concat(void* ctx, const VxtCb4View* subs, uint32_t n_su
       oo += v.n_outliers;
     }
     rp[rows] = (uint32_t)nnz;
+    // Decode-in-loop GEMM (gemm_tile.hip, tile_cb4_kernel): per-row exponents
+    // appended to the arena when the tensor suits it.
+    std::vector<int8_t> rex;
+    if (cb4_tile_exponents(subs, n_subs, rp, reinterpret_cast<const uint32_t*>(h.data() + w_bytes + s_bytes + rp_bytes),
+                           reinterpret_cast<const uint16_t*>(h.data() + w_bytes), rex)) {
+      const size_t at = h.size();
+      h.resize(at + align256(rows));
+      std::memcpy(h.data() + at, rex.data(), rows);
+    }
+    const size_t rx_at = rex.empty() ? 0 : w_bytes + s_bytes + rp_bytes + o_bytes;
     use_device(c);
     Tensor* t = new_tensor(c, VXT_KIND_CB4, (uint32_t)rows, subs[0].cols, subs[0].padded_cols, h);
+    t->off_rx = rx_at;
     t->off_p0 = 0;
     t->off_p1 = w_bytes;
     t->off_rp = w_bytes + s_bytes;
