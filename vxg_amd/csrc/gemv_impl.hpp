@@ -1211,15 +1211,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
   const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
   const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
 
-  // Each row's CSR bounds first, then the activations, the weights and each
-  // lane's first residual entry.
-  uint32_t rr[RPW], os[RPW], oe[RPW], pk0[RPW];
+  // Load order (the vector loads count in one in-order counter, so a wait for
+  // a load also waits for every load issued before it): each row's CSR
+  // bounds first (lane-varying vector loads: a scalar load would share its
+  // counter with the LDS traffic and hold back the activation barrier), then
+  // the activations and the weights; each lane's first residual entry after
+  // the activation barrier, when its bounds have long arrived.
+  uint32_t rr[RPW], rpv[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     rr[r] = std::min(row0 + r, rows - 1);
-    os[r] = t.row_ptr[rr[r]];
-    oe[r] = t.row_ptr[rr[r] + 1];
+    rpv[r] = t.row_ptr[rr[r] + (lane & 1u)];   // lane 0: start, lane 1: end
   }
+  __builtin_amdgcn_sched_barrier(0);   // keeps these loads ahead of the rest
   constexpr uint32_t kCols = XBF16 ? 8 : 4;
   constexpr uint32_t kPieces = NS * kStep / kCols;
   constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
@@ -1239,15 +1243,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
 #pragma unroll
     for (int r = 0; r < RPW; ++r) load_chunk<KIND_CB4>(t, rr[r], k0c, 0, 0, wc[s][r]);
   }
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {   // clamped, unconditional (the CSR stream holds at least one word)
-    const uint32_t i = os[r] + lane;
-    const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
-    pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
-  }
   // Nothing that uses a loaded value may be scheduled above the last load.
   __builtin_amdgcn_sched_barrier(0);
-  if (tid < 48) s_cent[tid] = t.cent[tid];
+  if (tid == 0) {   // the centroid tables come with the kernel arguments (scalar loads)
+#pragma unroll
+    for (int c = 0; c < 48; c += 4)
+      *reinterpret_cast<float4*>(&s_cent[c]) = make_float4(t.cent[c], t.cent[c + 1], t.cent[c + 2], t.cent[c + 3]);
+  }
   auto put = [&](uint32_t p, const u32x4& v) {   // f32 piece p (4 columns) to its slot
     const uint32_t blk = p / 512u, l = (p % 512u) / 8u, i = p % 8u;
     *reinterpret_cast<u32x4*>(&s_x[(blk * 512u + 8u * l + (i ^ ((l >> 1) & 7u))) * 4u]) = v;
@@ -1265,6 +1267,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
   }
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
+
+  uint32_t os[RPW], oe[RPW], pk0[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {   // clamped, unconditional (the CSR stream holds at least one word)
+    os[r] = __builtin_amdgcn_readlane(rpv[r], 0);
+    oe[r] = __builtin_amdgcn_readlane(rpv[r], 1);
+    const uint32_t i = os[r] + lane;
+    const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
+    pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
+  }
 
   float acc[RPW];
 #pragma unroll
