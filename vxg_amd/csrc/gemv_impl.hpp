@@ -1192,6 +1192,95 @@ hipError_t launch_q8_mt_t(const DevTensor& t, const void* x, uint32_t m, void* y
   return hipGetLastError();
 }
 
+// Epilogue of the one-token kernels: plain (y[row] = sum) or gated (the
+// wave's gate / up pair, y[first] = f(gate) * up, and workgroup 0 zeroes the
+// padding columns [n_ff, y_stride)), as gemv_kernel writes them.
+template <int EPI, int RPW, int WAVES>
+__device__ __forceinline__ void m1_epilogue(const float (&acc)[RPW], const uint32_t (&rr)[RPW], const bool (&rv)[RPW],
+                                            uint32_t first, uint32_t lane, uint32_t rows, uint32_t n_ff,
+                                            uint32_t y_stride, void* y, uint32_t y_bf16) {
+  if constexpr (EPI == kEpiPlain) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const float v = wave_sum(acc[r]);
+      if (lane == 0 && rv[r]) {
+        if (y_bf16)
+          static_cast<uint16_t*>(y)[rr[r]] = f32_to_bf16(v);
+        else
+          static_cast<float*>(y)[rr[r]] = v;
+      }
+    }
+  } else {
+    const float g = wave_sum(acc[0]);
+    const float u = wave_sum(acc[1]);
+    if (lane == 0 && rv[0]) {
+      const float v = gated<EPI>(g, u);
+      if (y_bf16)
+        static_cast<uint16_t*>(y)[first] = f32_to_bf16(v);
+      else
+        static_cast<float*>(y)[first] = v;
+    }
+    if (blockIdx.x == 0) {   // zero padding columns [n_ff, y_stride)
+      for (uint32_t c = n_ff + threadIdx.x; c < y_stride; c += WAVES * 64) {
+        if (y_bf16)
+          static_cast<uint16_t*>(y)[c] = 0;
+        else
+          static_cast<float*>(y)[c] = 0.0f;
+      }
+    }
+  }
+  (void)rows;
+}
+
+// ---------------------------------------------------------------------------
+// Norm prologue of the one-token LDS-staged kernels (NORM): x is built by
+// every workgroup as bf16(rms_norm(cur [+ delta]) * w) with the reduction of
+// norm_prologue (threads 0..255, element i = tid + 256 j by FMA in ascending
+// j, the DPP wave sum, the four wave sums in order; the workgroup's other
+// waves add zeros after them), so x is bit-identical to the stand-alone
+// RMSNorm's bf16 output, and is written widened to f32 in the swizzled
+// 4-column slots the kernels read (zero past cols up to xlen).  Workgroup 0
+// also stores cur + delta to cur_out.  Ends with a barrier.
+template <uint32_t NP, int WAVES>
+__device__ __forceinline__ void norm_stage_m1(const NormIn& nin, uint32_t cols, uint32_t xlen, const float (&c)[NP],
+                                              const float (&d)[NP], const float (&w)[NP], float* s_x,
+                                              float* s_part) {
+#pragma clang fp contract(off)
+  const uint32_t tid = threadIdx.x;
+  const bool add = nin.delta != nullptr, mine = tid < 256u;
+  float v[NP];
+  float sq = 0.0f;
+#pragma unroll
+  for (uint32_t j = 0; j < NP; ++j) {
+    v[j] = add ? c[j] + d[j] : c[j];
+    if (mine && tid + 256u * j < cols) sq = __builtin_fmaf(v[j], v[j], sq);
+  }
+  sq = wave_sum(sq);
+  if ((tid & 63u) == 0) s_part[tid >> 6] = sq;
+  __syncthreads();
+  float total = 0.0f;
+#pragma unroll
+  for (int k = 0; k < WAVES; ++k) total += s_part[k];
+  const float scale = 1.0f / sqrtf(total / (float)cols + nin.eps);
+  auto slot = [&](uint32_t i) {   // f32 index of column i
+    const uint32_t q = i / 4u, blk = q / 512u, l = (q % 512u) / 8u, pi = q % 8u;
+    return (blk * 512u + 8u * l + (pi ^ ((l >> 1) & 7u))) * 4u + i % 4u;
+  };
+  if (mine) {
+    const bool store = add && blockIdx.x == 0;
+#pragma unroll
+    for (uint32_t j = 0; j < NP; ++j) {
+      const uint32_t i = tid + 256u * j;
+      if (i < cols) {
+        s_x[slot(i)] = bf16_to_f32(f32_to_bf16(v[j] * scale * w[j]));
+        if (store) nin.cur_out[i] = v[j];
+      }
+    }
+  }
+  for (uint32_t i = cols + tid; i < xlen; i += WAVES * 64u) s_x[slot(i)] = 0.0f;
+  __syncthreads();
+}
+
 // ---------------------------------------------------------------------------
 // cb4 (reference layout) weights, one token, 1..3 K steps: the structure of
 // gemv_q8_m1_kernel with the cb4 decode of gemv_kernel (centroid tables in
@@ -1200,16 +1289,30 @@ hipError_t launch_q8_mt_t(const DevTensor& t, const void* x, uint32_t m, void* y
 // order).  The residuals' activations come from the staged row in LDS, so the
 // call does not end on a dependent global read.  Products and summation order
 // are those of gemv_kernel.
-template <int RPW, int WAVES, int NS, bool XBF16>
+//
+// EPI: the plain or a gated epilogue of gemv_kernel (rows in gate / up pairs,
+// RPW = 2: one output per wave).  NORM: x built by norm_stage_m1 from
+// cur [+ delta] and the norm weight instead of read from memory (bf16; at
+// most 16 elements per thread of the first 256).
+template <int RPW, int WAVES, int NS, bool XBF16, int EPI = kEpiPlain, bool NORM = false, uint32_t NP = 8>
 __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, const void* __restrict__ x,
-                                                                void* __restrict__ y, uint32_t y_bf16) {
+                                                                void* __restrict__ y, uint32_t y_bf16,
+                                                                uint32_t n_ff = 0, uint32_t y_stride = 0,
+                                                                NormIn nin = {}) {
   static_assert(NS >= 1 && NS <= 3, "K steps staged in LDS");
+  static_assert(EPI == kEpiPlain || RPW == 2, "gated: one gate / up row pair per wave");
+  static_assert(!NORM || (XBF16 && NS <= 2 && WAVES >= 4), "the norm prologue: bf16, cols <= 4096");
   __shared__ __attribute__((aligned(64))) float s_cent[48];
   __shared__ __attribute__((aligned(16))) float s_x[NS * kStep];
+  __shared__ float s_part[WAVES];
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
-  const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
+  constexpr uint32_t kOut = EPI == kEpiPlain ? RPW : RPW / 2;   // outputs per wave
+  const uint32_t first = (blockIdx.x * WAVES + wave) * kOut;
+  uint32_t rr[RPW];
+  bool rv[RPW];
+  wave_rows<EPI, RPW>(first, rows, n_ff, rr, rv);
 
   // Load order (the vector loads count in one in-order counter, so a wait for
   // a load also waits for every load issued before it): each row's CSR
@@ -1217,23 +1320,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
   // counter with the LDS traffic and hold back the activation barrier), then
   // the activations and the weights; each lane's first residual entry after
   // the activation barrier, when its bounds have long arrived.
-  uint32_t rr[RPW], rpv[RPW];
+  uint32_t rpv[RPW];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    rr[r] = std::min(row0 + r, rows - 1);
-    rpv[r] = t.row_ptr[rr[r] + (lane & 1u)];   // lane 0: start, lane 1: end
-  }
+  for (int r = 0; r < RPW; ++r) rpv[r] = t.row_ptr[rr[r] + (lane & 1u)];   // lane 0: start, lane 1: end
   __builtin_amdgcn_sched_barrier(0);   // keeps these loads ahead of the rest
   constexpr uint32_t kCols = XBF16 ? 8 : 4;
   constexpr uint32_t kPieces = NS * kStep / kCols;
-  constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0,
-                                                                     (int)(cols * (XBF16 ? 2u : 4u)), 0x00020000);
+  constexpr uint32_t kPer = NORM ? 1 : (kPieces + WAVES * 64 - 1) / (WAVES * 64);
   u32x4 xv[kPer];
+  float n_c[NORM ? NP : 1], n_d[NORM ? NP : 1], n_w[NORM ? NP : 1];
+  if constexpr (NORM) {   // norm inputs (clamped, unconditional), before the weights
 #pragma unroll
-  for (uint32_t j = 0; j < kPer; ++j) {
-    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
-    xv[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, p * 16u, 0, 0);
+    for (uint32_t j = 0; j < NP; ++j) {
+      const uint32_t i = std::min(std::min(tid, 255u) + 256u * j, cols - 1);
+      n_c[j] = nin.cur[i];
+      n_w[j] = nin.w[i];
+      n_d[j] = nin.delta ? nin.delta[i] : 0.0f;
+    }
+  } else {
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0,
+                                                                       (int)(cols * (XBF16 ? 2u : 4u)), 0x00020000);
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; ++j) {
+      const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
+      xv[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, p * 16u, 0, 0);
+    }
   }
   WChunk<KIND_CB4> wc[NS][RPW];
 #pragma unroll
@@ -1250,22 +1361,26 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
     for (int c = 0; c < 48; c += 4)
       *reinterpret_cast<float4*>(&s_cent[c]) = make_float4(t.cent[c], t.cent[c + 1], t.cent[c + 2], t.cent[c + 3]);
   }
-  auto put = [&](uint32_t p, const u32x4& v) {   // f32 piece p (4 columns) to its slot
-    const uint32_t blk = p / 512u, l = (p % 512u) / 8u, i = p % 8u;
-    *reinterpret_cast<u32x4*>(&s_x[(blk * 512u + 8u * l + (i ^ ((l >> 1) & 7u))) * 4u]) = v;
-  };
+  if constexpr (NORM) {
+    norm_stage_m1<NP, WAVES>(nin, cols, NS * kStep, n_c, n_d, n_w, s_x, s_part);
+  } else {
+    auto put = [&](uint32_t p, const u32x4& v) {   // f32 piece p (4 columns) to its slot
+      const uint32_t blk = p / 512u, l = (p % 512u) / 8u, i = p % 8u;
+      *reinterpret_cast<u32x4*>(&s_x[(blk * 512u + 8u * l + (i ^ ((l >> 1) & 7u))) * 4u]) = v;
+    };
 #pragma unroll
-  for (uint32_t j = 0; j < kPer; ++j) {
-    const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
-    const u32x4 v = xv[j];
-    if constexpr (XBF16) {
-      put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
-      put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
-    } else {
-      put(p, v);
+    for (uint32_t j = 0; j < kPer; ++j) {
+      const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
+      const u32x4 v = xv[j];
+      if constexpr (XBF16) {
+        put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
+        put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
+      } else {
+        put(p, v);
+      }
     }
+    __syncthreads();
   }
-  __syncthreads();
   __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
 
   uint32_t os[RPW], oe[RPW], pk0[RPW];
@@ -1314,7 +1429,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
   // of the row, in that order; the activation comes from the staged row.
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
-    if (row0 + r >= rows) break;   // later rows are past the end too
+    if (!rv[r]) continue;
     for (uint32_t i = os[r] + lane; i < oe[r]; i += 64u) {
       const uint32_t pk = i < os[r] + 64u ? pk0[r] : t.outliers[i];
       const uint32_t col = pk & 0xffffu;
@@ -1324,17 +1439,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
       acc[r] = __builtin_fmaf(f16_to_f32(pk >> 16), xc, acc[r]);
     }
   }
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {
-    const float v = wave_sum(acc[r]);
-    const uint32_t row = row0 + r;
-    if (lane == 0 && row < rows) {
-      if (y_bf16)
-        static_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
-      else
-        static_cast<float*>(y)[row] = v;
-    }
-  }
+  m1_epilogue<EPI, RPW, WAVES>(acc, rr, rv, first, lane, rows, n_ff, y_stride, y, y_bf16);
 }
 
 // ---------------------------------------------------------------------------
@@ -1528,6 +1633,19 @@ hipError_t launch_cb4_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf
   const uint32_t per_block = WAVES * RPW;
   hipLaunchKernelGGL((gemv_cb4_m1_kernel<RPW, WAVES, NS, XBF16>), dim3((t.rows + per_block - 1) / per_block),
                      dim3(WAVES * 64), 0, s, t, x, y, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
+// The same kernel with a gated epilogue (outs = n_ff) and / or the norm
+// prologue (x unused), eight waves per workgroup.
+template <int RPW, int NS, bool XBF16, int EPI, bool NORM, uint32_t NP = 8>
+hipError_t launch_cb4_m1_e(const DevTensor& t, const void* x, uint32_t outs, void* y, bool y_bf16, uint32_t n_ff,
+                           uint32_t y_stride, const NormIn& nin, hipStream_t s) {
+  constexpr int WAVES = 8;
+  constexpr uint32_t per_block = WAVES * (EPI == kEpiPlain ? RPW : RPW / 2);
+  hipLaunchKernelGGL((gemv_cb4_m1_kernel<RPW, WAVES, NS, XBF16, EPI, NORM, NP>),
+                     dim3((outs + per_block - 1) / per_block), dim3(WAVES * 64), 0, s, t, x, y,
+                     (uint32_t)(y_bf16 ? 1u : 0u), n_ff, y_stride, nin);
   return hipGetLastError();
 }
 
@@ -1854,9 +1972,33 @@ hipError_t launch_glu_x(const DevTensor& t, const void* x, bool x_bf16, uint32_t
                 : launch_glu_s<KIND, MT, false, EPI>(t, x, m, n_ff, y, y_bf16, y_stride, s);
 }
 
+// cb4, one token: the LDS-staged kernel with the gated epilogue (16-byte
+// aligned activations, cols a multiple of one 16-byte piece, 1..3 K steps).
+template <int EPI>
+bool try_glu_cb4_m1(const DevTensor& t, const void* x, bool x_bf16, uint32_t n_ff, void* y, bool y_bf16,
+                    uint32_t y_stride, hipStream_t s, hipError_t* e) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (nsteps > 3 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % (x_bf16 ? 8 : 4) != 0) return false;
+  const NormIn none{};
+  if (x_bf16) {
+    *e = nsteps == 1 ? launch_cb4_m1_e<2, 1, true, EPI, false>(t, x, n_ff, y, y_bf16, n_ff, y_stride, none, s)
+       : nsteps == 2 ? launch_cb4_m1_e<2, 2, true, EPI, false>(t, x, n_ff, y, y_bf16, n_ff, y_stride, none, s)
+                     : launch_cb4_m1_e<2, 3, true, EPI, false>(t, x, n_ff, y, y_bf16, n_ff, y_stride, none, s);
+  } else {
+    *e = nsteps == 1 ? launch_cb4_m1_e<2, 1, false, EPI, false>(t, x, n_ff, y, y_bf16, n_ff, y_stride, none, s)
+       : nsteps == 2 ? launch_cb4_m1_e<2, 2, false, EPI, false>(t, x, n_ff, y, y_bf16, n_ff, y_stride, none, s)
+                     : launch_cb4_m1_e<2, 3, false, EPI, false>(t, x, n_ff, y, y_bf16, n_ff, y_stride, none, s);
+  }
+  return true;
+}
+
 template <uint32_t KIND, int EPI>
 hipError_t launch_glu_m(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, uint32_t n_ff, void* y,
                         bool y_bf16, uint32_t y_stride, hipStream_t s) {
+  if constexpr (KIND == KIND_CB4) {
+    hipError_t e = hipSuccess;
+    if (m == 1 && try_glu_cb4_m1<EPI>(t, x, x_bf16, n_ff, y, y_bf16, y_stride, s, &e)) return e;
+  }
   if (m == 1) return launch_glu_x<KIND, 1, EPI>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s);
   if (m == 2) return launch_glu_x<KIND, 2, EPI>(t, x, x_bf16, m, n_ff, y, y_bf16, y_stride, s);
   return hipErrorInvalidValue;
@@ -1901,10 +2043,33 @@ hipError_t launch_norm_s(const DevTensor& t, const NormIn& nin, uint32_t outs, v
 
 // epi: kEpiPlain (y = W x, outs = rows) or a gated epilogue (outs = rows / 2).
 // Requires cols <= 256 * kNormPer.
+// cb4: the LDS-staged one-token kernel with the norm prologue (1..2 K steps).
+template <int RPW, int NS, int EPI, uint32_t NP>
+hipError_t launch_norm_cb4_m1(const DevTensor& t, const NormIn& nin, uint32_t outs, void* y, bool y_bf16,
+                              uint32_t y_stride, hipStream_t s) {
+  return launch_cb4_m1_e<RPW, NS, true, EPI, true, NP>(t, nullptr, outs, y, y_bf16, EPI == kEpiPlain ? 0u : outs,
+                                                       y_stride, nin, s);
+}
+
+template <int RPW, int EPI>
+hipError_t launch_norm_cb4_m1_s(const DevTensor& t, const NormIn& nin, uint32_t outs, void* y, bool y_bf16,
+                                uint32_t y_stride, hipStream_t s) {
+  const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+  if (nsteps == 1) return launch_norm_cb4_m1<RPW, 1, EPI, 8>(t, nin, outs, y, y_bf16, y_stride, s);
+  if (t.cols <= 2048) return launch_norm_cb4_m1<RPW, 2, EPI, 8>(t, nin, outs, y, y_bf16, y_stride, s);
+  return launch_norm_cb4_m1<RPW, 2, EPI, 16>(t, nin, outs, y, y_bf16, y_stride, s);
+}
+
 template <uint32_t KIND>
 hipError_t launch_norm_kind(const DevTensor& t, const NormIn& nin, int epi, void* y, bool y_bf16,
                             uint32_t y_stride, hipStream_t s) {
   if (t.cols > 256u * kNormPer) return hipErrorInvalidValue;
+  if constexpr (KIND == KIND_CB4) {   // cols <= 4096: at most two K steps
+    if (epi == kEpiSilu) return launch_norm_cb4_m1_s<2, kEpiSilu>(t, nin, t.rows / 2, y, y_bf16, y_stride, s);
+    if (epi == kEpiGelu) return launch_norm_cb4_m1_s<2, kEpiGelu>(t, nin, t.rows / 2, y, y_bf16, y_stride, s);
+    if (t.rows > 8192) return launch_norm_cb4_m1_s<2, kEpiPlain>(t, nin, t.rows, y, y_bf16, t.rows, s);
+    return launch_norm_cb4_m1_s<1, kEpiPlain>(t, nin, t.rows, y, y_bf16, t.rows, s);
+  }
   if (epi == kEpiSilu) return launch_norm_s<KIND, 2, kEpiSilu>(t, nin, t.rows / 2, y, y_bf16, y_stride, s);
   if (epi == kEpiGelu) return launch_norm_s<KIND, 2, kEpiGelu>(t, nin, t.rows / 2, y, y_bf16, y_stride, s);
   if (t.rows >= 65536) return launch_norm_s<KIND, 4, kEpiPlain>(t, nin, t.rows, y, y_bf16, t.rows, s);
