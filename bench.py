@@ -440,7 +440,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--configs", default="f,0,r,g,2,3,4,s,a",
                     help="secondary configurations to run (f: HBM streaming floor at the configs' sizes, "
-                         "s: whole decode step on config 4's weights, a: KV-Q8 decode attention)")
+                         "s: whole decode step on config 4's weights, a: KV-Q8 decode attention, "
+                         "c: config 3's cb4 lines on the pinned decode-in-loop tile kernel)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
                     help="time with plain launches instead of graph replays (for profilers: rocprofv3's kernel "
@@ -542,6 +543,22 @@ def main():
                                       "kernel_us": round(rg["kernel_ms"] * 1e3, 2),
                                       "frac_mfma": round(rg["TFLOPs"] / BF16_PEAK_TFLOPS, 4)})
                     log(f"  config 3 {kind} M={M} K={K} N={N}: {rg['TFLOPs']:.1f} TFLOP/s")
+    if "c" in run:   # config 3's cb4 lines on the decode-in-loop tile kernel (pinned FUSED path)
+        eng.set_gemm_path(engine.GEMM_FUSED)
+        try:
+            for (K, N) in [(2048, 6144), (6144, 2048)]:
+                mk = synth.make_cb4(N, K, seed=3)
+                for M in (128, 512, 2048):
+                    st = max(10, min(100, int(4e12 / (2.0 * M * N * K))))
+                    rg = bench_gemm(eng, mk, M, st, 3, seed=M)
+                    secondary.append({"config": f"3 on the cb4 decode-in-loop tile kernel (pinned): cb4 gemm M={M} "
+                                                f"K={K} N={N} bf16->bf16",
+                                      "TFLOPs": round(rg["TFLOPs"], 1),
+                                      "kernel_us": round(rg["kernel_ms"] * 1e3, 2),
+                                      "frac_mfma": round(rg["TFLOPs"] / BF16_PEAK_TFLOPS, 4)})
+                    log(f"  config 3 cb4 (tile kernel) M={M} K={K} N={N}: {rg['TFLOPs']:.1f} TFLOP/s")
+        finally:
+            eng.set_gemm_path(engine.GEMM_AUTO)
     if "4" in run:
         head_m = synth.make_q8(151936, 2048, seed=5)
         for kind in ("g64", "cb4"):
