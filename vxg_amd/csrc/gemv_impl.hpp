@@ -1319,7 +1319,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
   // bounds first (lane-varying vector loads: a scalar load would share its
   // counter with the LDS traffic and hold back the activation barrier), then
   // the activations and the weights; each lane's first residual entry after
-  // the activation barrier, when its bounds have long arrived.
+  // them, when its bounds have landed.
   uint32_t rpv[RPW];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) rpv[r] = t.row_ptr[rr[r] + (lane & 1u)];   // lane 0: start, lane 1: end
@@ -1361,6 +1361,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
     for (int c = 0; c < 48; c += 4)
       *reinterpret_cast<float4*>(&s_cent[c]) = make_float4(t.cent[c], t.cent[c + 1], t.cent[c + 2], t.cent[c + 3]);
   }
+  // Each lane's first residual entry: its bounds were the first loads, so
+  // they have landed by the time the activations are waited for below.
+  uint32_t os[RPW], oe[RPW], pk0[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {   // clamped, unconditional (the CSR stream holds at least one word)
+    os[r] = __builtin_amdgcn_readlane(rpv[r], 0);
+    oe[r] = __builtin_amdgcn_readlane(rpv[r], 1);
+    const uint32_t i = os[r] + lane;
+    const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
+    pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
+  }
   if constexpr (NORM) {
     norm_stage_m1<NP, WAVES>(nin, cols, NS * kStep, n_c, n_d, n_w, s_x, s_part);
   } else {
@@ -1382,16 +1393,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_cb4_m1_kernel(DevTensor t, co
     __syncthreads();
   }
   __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
-
-  uint32_t os[RPW], oe[RPW], pk0[RPW];
-#pragma unroll
-  for (int r = 0; r < RPW; ++r) {   // clamped, unconditional (the CSR stream holds at least one word)
-    os[r] = __builtin_amdgcn_readlane(rpv[r], 0);
-    oe[r] = __builtin_amdgcn_readlane(rpv[r], 1);
-    const uint32_t i = os[r] + lane;
-    const uint32_t last = oe[r] > 0 ? oe[r] - 1 : 0;
-    pk0[r] = t.outliers[i < oe[r] ? i : (os[r] < oe[r] ? last : 0)];
-  }
 
   float acc[RPW];
 #pragma unroll
