@@ -969,6 +969,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_m1_kernel(DevTensor t, con
   }
 }
 
+// An empty asm that takes the four words: the compiler cannot move a use of
+// them (or the wait for the load that produced them) above this point.
+__device__ __forceinline__ void opaque4(uint4& v) {
+  uint32_t a = v.x, b = v.y, c = v.z, d = v.w;
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  v = make_uint4(a, b, c, d);
+}
+
 // ---------------------------------------------------------------------------
 // cb4-g64 weights x bf16 activations, one token, 1..3 K steps: the structure
 // of gemv_q8_m1_kernel (activations staged once per workgroup, widened to f32
@@ -1037,11 +1045,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, co
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const bool kin = s * kStep + lane * kChunk < kp;
-    // this step's tables (the wave's LDS operations run in order, so the
-    // previous step's lookups are done first)
-#pragma unroll
-    for (int p = 0; p < NB; ++p)
-      store_g64_tables(tab + p * kTabBlock, lane, wc[s][2 * p], 2 * p + 1 < RPW ? &wc[s][2 * p + 1] : nullptr);
+    // The step's activations first: they are in LDS already, so their reads
+    // go out before the wait for this step's weights.
     float xf[kChunk];
 #pragma unroll
     for (uint32_t i = 0; i < 8; ++i) {
@@ -1051,6 +1056,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, co
       xf[4 * i + 2] = __uint_as_float(v.z);
       xf[4 * i + 3] = __uint_as_float(v.w);
     }
+    // The weights enter the computation only here (an empty asm that takes
+    // them), so nothing derived from them -- and no wait for them -- is
+    // placed above the activation reads.
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      opaque4(wc[s][r].q);
+      opaque4(wc[s][r].lut);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // this step's tables (the wave's LDS operations run in order, so the
+    // previous step's lookups are done first)
+#pragma unroll
+    for (int p = 0; p < NB; ++p)
+      store_g64_tables(tab + p * kTabBlock, lane, wc[s][2 * p], 2 * p + 1 < RPW ? &wc[s][2 * p + 1] : nullptr);
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       const uint32_t sl = tab + (r / 2) * kTabBlock + lane * 4u + (r & 1) * 2u;
