@@ -93,12 +93,15 @@ __device__ __forceinline__ float f16_to_f32(uint32_t h) {
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
 
-// f32 -> bf16 with the reference's rule (fp16.rs:113-120).
+// f32 -> bf16 with the reference's rule (fp16.rs:113-120): NaN keeps its top
+// bits with the quiet bit set, everything else rounds to nearest even.  Both
+// results are formed and one selected, so the compiler emits a compare and a
+// v_cndmask rather than exec-mask control flow around every conversion.
 __device__ __forceinline__ uint16_t f32_to_bf16(float v) {
-  uint32_t b = __float_as_uint(v);
-  if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu) != 0u)
-    return (uint16_t)((b >> 16) | 0x0040u);
-  return (uint16_t)((b + 0x7fffu + ((b >> 16) & 1u)) >> 16);
+  const uint32_t b = __float_as_uint(v);
+  const uint32_t quiet = (b >> 16) | 0x0040u;
+  const uint32_t rounded = (b + 0x7fffu + ((b >> 16) & 1u)) >> 16;
+  return (uint16_t)(__builtin_isnan(v) ? quiet : rounded);
 }
 
 // Inputs of a GEMV whose activations are an RMSNorm of the residual stream

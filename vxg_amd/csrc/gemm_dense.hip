@@ -311,32 +311,62 @@ __global__ __launch_bounds__(NT, occupancy<MODE>()) void dense2_kernel(const uin
         xs[ii][4 * q + 3] = e4.w;
       }
   }
+  // One loop per output mode (a mode test per output compiles to branches
+  // per output).
+  auto row_of = [&](int ii, int r) { return (uint32_t)(wm * 64 + ii * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
+  auto value = [&](int ii, int j, int r) {
+    float v = acc[ii][j][r];
+    if constexpr (LO) v = __builtin_fmaf(accl[ii][j][r], kLoInv, v);
+    return v;
+  };
+  if (rows_fast) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const uint32_t n = n0 + wn * 64 + j * 32 + l32;
-    const float sc = to_partial ? 1.0f : inv[std::min(n, N - 1)];
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t nl = wn * 64 + j * 32 + l32;
+      const float sc = inv[n0 + nl];
 #pragma unroll
-    for (int ii = 0; ii < 2; ++ii)
+      for (int ii = 0; ii < 2; ++ii)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t ml = wm * 64 + ii * 32 + h * 4 + 8 * (r >> 2) + (r & 3), m = m0 + ml;
-        float v = acc[ii][j][r];
-        if constexpr (LO) v = __builtin_fmaf(accl[ii][j][r], kLoInv, v);
-        if (rows_fast) {
-          s_out[ml * LDO + (n - n0)] = f32_to_bf16(ldexpf(v * sc, -xs[ii][r]));
-          continue;
-        }
-        if (m >= M || n >= N) continue;
-        if (to_partial) {
-          partial[((size_t)blockIdx.y * M + m) * N + n] = v;
-        } else {
-          const float o = ldexpf(v * sc, -xs[ii][r]);
+        for (int r = 0; r < 16; ++r)
+          s_out[row_of(ii, r) * LDO + nl] = f32_to_bf16(ldexpf(value(ii, j, r) * sc, -xs[ii][r]));
+    }
+  } else if (to_partial) {
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t n = n0 + wn * 64 + j * 32 + l32;
+      float* const pp = partial + ((size_t)blockIdx.y * M + m0) * N + n;
+      if (full) {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) pp[(size_t)row_of(ii, r) * N] = value(ii, j, r);
+      } else {
+#pragma unroll
+        for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (m0 + row_of(ii, r) < M && n < N) pp[(size_t)row_of(ii, r) * N] = value(ii, j, r);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t n = n0 + wn * 64 + j * 32 + l32;
+      const float sc = inv[std::min(n, N - 1)];
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t m = m0 + row_of(ii, r);
+          if (m >= M || n >= N) continue;
+          const float o = ldexpf(value(ii, j, r) * sc, -xs[ii][r]);
           if (y_bf16)
             static_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(o);
           else
             static_cast<float*>(y)[(size_t)m * N + n] = o;
         }
-      }
+    }
   }
   if (rows_fast) {   // uniform
     __syncthreads();

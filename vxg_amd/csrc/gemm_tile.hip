@@ -444,35 +444,55 @@ __global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTenso
           for (int r = 0; r < 16; ++r) acc[f][r] += red[((((g - 1) * 4 + wave) * 4 + f) * 16 + r) * 64 + lane];
     }
     // Lane owns output column n0 + 32 wave + l32 and rows
-    // m0 + 32 f + 4 h + 8 (r / 4) + r % 4 of fragment f.
+    // m0 + 32 f + 4 h + 8 (r / 4) + r % 4 of fragment f.  Each output mode
+    // has a loop of its own: a mode test per output became a pair of
+    // branches per output, whose cold code cost microseconds per workgroup.
     const uint32_t nl = wave * 32 + l32, ncol = n0 + nl;
+    auto row_of = [&](int f, int r) { return (uint32_t)(f * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
+    // fragment f's 16 row exponents, 4 consecutive rows per 16-byte read
+    auto load_xs = [&](int f, int (&xs)[16]) {
 #pragma unroll
-    for (int f = 0; f < 4; ++f) {
-      // this fragment's 16 row exponents, 4 consecutive rows per 16-byte read
-      int xs[16];
-      if (!to_partial) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int4 e4 = *reinterpret_cast<const int4*>(s_xe + f * 32 + h * 4 + 8 * q);
-          xs[4 * q + 0] = e4.x;
-          xs[4 * q + 1] = e4.y;
-          xs[4 * q + 2] = e4.z;
-          xs[4 * q + 3] = e4.w;
-        }
+      for (int q = 0; q < 4; ++q) {
+        const int4 e4 = *reinterpret_cast<const int4*>(s_xe + f * 32 + h * 4 + 8 * q);
+        xs[4 * q + 0] = e4.x;
+        xs[4 * q + 1] = e4.y;
+        xs[4 * q + 2] = e4.z;
+        xs[4 * q + 3] = e4.w;
       }
+    };
+    const bool full = m0 + BM <= M && n0 + BN <= N_;
+    if (rows_fast) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t ml = f * 32 + h * 4 + 8 * (r >> 2) + (r & 3), m = m0 + ml;
-        const float v = acc[f][r];
-        if (rows_fast) {
-          s_out[ml * LDO + nl] = f32_to_bf16(ldexpf(v, -xs[r]));
-          continue;
-        }
-        if (m >= M || ncol >= N_) continue;
-        if (to_partial) {
-          partial[((size_t)blockIdx.y * M + m) * N_ + ncol] = v;
-        } else {
-          const float o = ldexpf(v, -xs[r]);
+      for (int f = 0; f < 4; ++f) {
+        int xs[16];
+        load_xs(f, xs);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s_out[row_of(f, r) * LDO + nl] = f32_to_bf16(ldexpf(acc[f][r], -xs[r]));
+      }
+    } else if (to_partial) {
+      float* const pp = partial + ((size_t)blockIdx.y * M + m0) * N_ + ncol;
+      if (full) {
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) pp[(size_t)row_of(f, r) * N_] = acc[f][r];
+      } else {
+#pragma unroll
+        for (int f = 0; f < 4; ++f)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (m0 + row_of(f, r) < M && ncol < N_) pp[(size_t)row_of(f, r) * N_] = acc[f][r];
+      }
+    } else {
+#pragma unroll
+      for (int f = 0; f < 4; ++f) {
+        int xs[16];
+        load_xs(f, xs);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t m = m0 + row_of(f, r);
+          if (m >= M || ncol >= N_) continue;
+          const float o = ldexpf(acc[f][r], -xs[r]);
           if (y_bf16)
             static_cast<uint16_t*>(y)[(size_t)m * N_ + ncol] = f32_to_bf16(o);
           else
@@ -928,33 +948,53 @@ __global__ __launch_bounds__(NT, 1) void tile_cb4_kernel(DevTensor t, const uint
   __syncthreads();   // every wave is done with the stages and the residual list
   if (tid < BM && !to_partial) s_xe[tid] = xe_pre;
   __syncthreads();
+  // One loop per output mode (a mode test per output compiles to branches
+  // per output).
   const uint32_t nl = wave * 32 + l32, ncol = n0 + nl;
+  auto row_of = [&](int f, int r) { return (uint32_t)(f * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
+  auto value = [&](int f, int r) { return __builtin_fmaf(accl[f][r], 1.0f / 2048.0f, acc[f][r]); };
+  auto load_xs = [&](int f, int (&xs)[16]) {
 #pragma unroll
-  for (int f = 0; f < 4; ++f) {
-    int xs[16];
-    if (!to_partial) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int4 e4 = *reinterpret_cast<const int4*>(s_xe + f * 32 + h * 4 + 8 * q);
-        xs[4 * q + 0] = e4.x;
-        xs[4 * q + 1] = e4.y;
-        xs[4 * q + 2] = e4.z;
-        xs[4 * q + 3] = e4.w;
-      }
+    for (int q = 0; q < 4; ++q) {
+      const int4 e4 = *reinterpret_cast<const int4*>(s_xe + f * 32 + h * 4 + 8 * q);
+      xs[4 * q + 0] = e4.x;
+      xs[4 * q + 1] = e4.y;
+      xs[4 * q + 2] = e4.z;
+      xs[4 * q + 3] = e4.w;
     }
+  };
+  if (rows_fast) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const uint32_t ml = f * 32 + h * 4 + 8 * (r >> 2) + (r & 3), m = m0 + ml;
-      const float v = __builtin_fmaf(accl[f][r], 1.0f / 2048.0f, acc[f][r]);
-      if (rows_fast) {
-        s_out[ml * LDO + nl] = f32_to_bf16(ldexpf(v, -(xs[r] + er)));
-        continue;
-      }
-      if (m >= M || ncol >= N_) continue;
-      if (to_partial) {
-        partial[((size_t)blockIdx.y * M + m) * N_ + ncol] = ldexpf(v, -er);
-      } else {
-        const float o = ldexpf(v, -(xs[r] + er));
+    for (int f = 0; f < 4; ++f) {
+      int xs[16];
+      load_xs(f, xs);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) s_out[row_of(f, r) * LDO + nl] = f32_to_bf16(ldexpf(value(f, r), -(xs[r] + er)));
+    }
+  } else if (to_partial) {
+    float* const pp = partial + ((size_t)blockIdx.y * M + m0) * N_ + ncol;
+    if (m0 + BM <= M && n0 + BN <= N_) {
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) pp[(size_t)row_of(f, r) * N_] = ldexpf(value(f, r), -er);
+    } else {
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (m0 + row_of(f, r) < M && ncol < N_) pp[(size_t)row_of(f, r) * N_] = ldexpf(value(f, r), -er);
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      int xs[16];
+      load_xs(f, xs);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t m = m0 + row_of(f, r);
+        if (m >= M || ncol >= N_) continue;
+        const float o = ldexpf(value(f, r), -(xs[r] + er));
         if (y_bf16)
           static_cast<uint16_t*>(y)[(size_t)m * N_ + ncol] = f32_to_bf16(o);
         else
