@@ -26,8 +26,9 @@
 //          chunk c ^ ((r >> 1) & 7) so the fragment reads of 16 lanes (rows
 //          r..r+15 at one chunk) and the row writes touch distinct banks;
 //        * weights: lane (w, l) loads its row's 32 nibbles of the tile (16 B,
-//          columns 32h.. of the tile, h = l / 32) and the group's whole
-//          16-entry table (32 B), two tiles ahead.  Lookups are v_perm_b32
+//          columns 32h.. of the tile, h = l / 32) and half of the group's
+//          16-entry table (16 B; v_permlane32_swap with the lane of the other
+//          half completes it), two tiles ahead.  Lookups are v_perm_b32
 //          byte selects from the table held in registers: the low and high
 //          bytes of entries 0-7 and 8-15 form four 8-byte sources; a perm
 //          picks four bytes by nibble & 7, a second perm takes the 8-15 half
@@ -203,17 +204,29 @@ __device__ __forceinline__ u32x4 decode8(const Planes& p, uint32_t w) {
   return u32x4{a, b, c, d};
 }
 
+// Lanes l and l + 32 of a wave take the same weight row (the two 32-column
+// halves of the tile), so each loads one 16-byte half of the row's table and
+// v_permlane32_swap gives both lanes the whole of it.
 struct Raw {
-  u32x4 nib;      // 32 nibbles: columns 32h .. 32h + 31 of the tile
-  u32x4 t0, t1;   // the group's 16 table entries
+  u32x4 nib;   // 32 nibbles: columns 32h .. 32h + 31 of the tile
+  u32x4 th;    // table entries 8h .. 8h + 7 of the group
 };
 
 __device__ __forceinline__ void bload(const DevTensor& t, uint32_t n, uint32_t kt, uint32_t h, Raw& r) {
   const uint32_t kp = t.kp;
   r.nib = *reinterpret_cast<const u32x4*>(static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2) + kt * 32 + 16 * h);
-  const u32x4* tab = reinterpret_cast<const u32x4*>(t.p1 + ((size_t)n * (kp / 64) + kt) * 16);
-  r.t0 = tab[0];
-  r.t1 = tab[1];
+  r.th = reinterpret_cast<const u32x4*>(t.p1 + ((size_t)n * (kp / 64) + kt) * 16)[h];
+}
+
+__device__ __forceinline__ Planes planes_of(const Raw& r) {
+  u32x4 t0, t1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const auto v = __builtin_amdgcn_permlane32_swap(r.th[j], r.th[j], false, false);
+    t0[j] = v[0];   // lanes 0-31 keep entries 0-7, lanes 32-63 receive them
+    t1[j] = v[1];   // lanes 32-63 keep entries 8-15, lanes 0-31 receive them
+  }
+  return make_planes(t0, t1);
 }
 
 // ---- activation tiles ------------------------------------------------------------
@@ -322,7 +335,7 @@ __global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTenso
   astore(STAGE(0), tid, ra[0]);
   aload(xh, m0, M, kp, ktile(2), tid, ra[0]);
   {
-    const Planes p0 = make_planes(rb[0].t0, rb[0].t1);
+    const Planes p0 = planes_of(rb[0]);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) bf[0][tt] = decode8(p0, rb[0].nib[tt]);
   }
@@ -341,7 +354,7 @@ __global__ __launch_bounds__(NT * KW, KW == 1 ? 2 : 1) void tile_kernel(DevTenso
     const char* stage = STAGE(P);
     char* const next_stage = STAGE(P ^ 1);
     const uint32_t kn = ktile(i + 3);
-    const Planes pl = make_planes(rb[P ^ 1].t0, rb[P ^ 1].t1);
+    const Planes pl = planes_of(rb[P ^ 1]);
     half8 af[2][4];
 #pragma unroll
     for (int f = 0; f < 4; ++f) af[0][f] = *reinterpret_cast<const half8*>(stage + f * 4096 + offA[0]);
