@@ -899,22 +899,22 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 
 // Path choice, unless the caller pins one (every path runs every kind):
 //   * g64 weights, bf16 activations: the fused kernel up to batch 64; the
-//     decode-in-registers tile kernel (gemm_tile.hip) from batch 192 to
+//     decode-in-registers tile kernel (gemm_tile.hip) from batch 128 to
 //     2047, and beyond when K > N; the two-phase path otherwise;
 //   * Q8 weights, bf16 activations: the fused kernel up to batch 128;
 //   * everything else: the two-phase path with the own dense kernel.
 // The vendor dense GEMM runs only when pinned (kGemmLibrary), as a
 // comparison.  Measured on MI355X (whole call, graph of 100 calls, TFLOP/s,
 // K x N = 2048 x 6144 / 6144 x 2048):
-//   g64 M = 64: fused 73 / 61, two-phase 68 / 61; M = 128: tile 109 / 99,
-//   two-phase 118 / 108; M = 512: tile 372 / 316, two-phase 300 / 325;
-//   M = 2048: tile 605 / 603, two-phase 653 / 581; M = 4096: 673 / 761
-//   (2048 x 6144);
+//   g64 M = 64: fused 73 / 61, two-phase 68 / 61; M = 96: tile 82, two-phase
+//   89 (2048 x 6144); M = 128: tile 134 / 118, two-phase 115 / 107; M = 512:
+//   tile 407 / 350, two-phase 300 / 325; M = 2048: tile 636 / 637, two-phase
+//   671 / 581; M = 4096: 673 / 761 (2048 x 6144);
 //   Q8 M = 64: fused 81 / 71, two-phase 61 / 54; M = 256: fused 125 / 161,
 //   two-phase 132 / 163.
 constexpr uint32_t kFusedMaxM = 128;
 constexpr uint32_t kG64FusedMaxM = 64;
-constexpr uint32_t kTileMinM = 192;
+constexpr uint32_t kTileMinM = 128;
 constexpr uint32_t kTileMaxM = 2048;   // exclusive, unless K > N
 
 enum class Path { Fused, Tile, TileCb4, Panel };
