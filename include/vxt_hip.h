@@ -484,7 +484,9 @@ VXT_API int vxt_hip_last_kernel_ms(void* ctx, double* ms);
  * runs this library's own kernels except LIBRARY.  AUTO (the default), by
  * measured speed: g64 weights with bf16 activations decode inside the MFMA
  * loop -- the fused kernel up to batch_m 64, the 128 x 128 tile kernel from
- * 128 to 2047 (and beyond when cols > rows); Q8_0 (and Q4_0) weights with
+ * 128 to 2047 (and beyond when cols > rows); cb4 weights with bf16
+ * activations take the cb4 tile kernel described under FUSED from batch_m 128
+ * to 511 when the tensor is eligible for it; Q8_0 (and Q4_0) weights with
  * bf16 activations and batch_m <= 128 take the fused kernel; every other call
  * takes the two-phase path (a decoded f16 weight panel, then the dense MFMA
  * kernel).  PANEL pins the two-phase path.  FUSED takes the decode-in-loop

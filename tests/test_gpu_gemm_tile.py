@@ -184,3 +184,22 @@ def test_cb4_tile_kernel_ineligible_tensor(eng):
     a = int(rp[r])
     m.outliers_packed[a + 1] = (m.outliers_packed[a + 1] & 0xFFFF0000) | (m.outliers_packed[a] & 0xFFFF)
     check(eng, m, 150, engine.GEMM_FUSED, seed=6)
+
+
+@pytest.mark.parametrize("M", [128, 300])
+def test_cb4_tile_kernel_on_auto_path(eng, M):
+    """From batch 128 to 511 the automatic choice takes the cb4 tile kernel
+    for an eligible tensor: the same bits as the pinned kernel, and the
+    oracle bar; an ineligible tensor keeps the two-phase path there."""
+    m = synth.make_cb4(640, 2048, seed=M)
+    a = check(eng, m, M, engine.GEMM_AUTO, seed=1)
+    b = check(eng, m, M, engine.GEMM_FUSED, seed=1)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    rp = m.outlier_row_ptr
+    r = int(np.argmax(np.diff(rp.astype(np.int64)) >= 2))
+    m.outliers_packed = m.outliers_packed.copy()
+    i = int(rp[r])
+    m.outliers_packed[i + 1] = (m.outliers_packed[i + 1] & 0xFFFF0000) | (m.outliers_packed[i] & 0xFFFF)
+    c = check(eng, m, M, engine.GEMM_AUTO, seed=2)
+    d = check(eng, m, M, engine.GEMM_PANEL, seed=2)
+    assert np.array_equal(c.view(np.uint32), d.view(np.uint32))

@@ -901,6 +901,11 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 //   * g64 weights, bf16 activations: the fused kernel up to batch 64; the
 //     decode-in-registers tile kernel (gemm_tile.hip) from batch 128 to
 //     2047, and beyond when K > N; the two-phase path otherwise;
+//   * cb4 weights, bf16 activations, within the tile kernel's limits
+//     (gemm_tile_cb4_supported): its decode-in-loop tile kernel from batch
+//     128 to 511 (M = 128 / 256: 96 / 84 and 137 / 145 TFLOP/s against the
+//     two-phase path's 81 / 77 and 121 / 131; at M = 64 and 512 the
+//     two-phase path is ahead);
 //   * Q8 weights, bf16 activations: the fused kernel up to batch 128;
 //   * everything else: the two-phase path with the own dense kernel.
 // The vendor dense GEMM runs only when pinned (kGemmLibrary), as a
@@ -916,6 +921,7 @@ constexpr uint32_t kFusedMaxM = 128;
 constexpr uint32_t kG64FusedMaxM = 64;
 constexpr uint32_t kTileMinM = 128;
 constexpr uint32_t kTileMaxM = 2048;   // exclusive, unless K > N
+constexpr uint32_t kCb4TileMaxM = 512;  // exclusive
 
 enum class Path { Fused, Tile, TileCb4, Panel };
 
@@ -928,6 +934,8 @@ static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
     if (tile_ok && m > kG64FusedMaxM) return Path::Tile;
     return fused_ok ? Path::Fused : Path::Panel;
   }
+  if (t.kind == KIND_CB4 && m >= kTileMinM && m < kCb4TileMaxM && gemm_tile_cb4_supported(t, x_bf16))
+    return Path::TileCb4;
   if (t.kind == KIND_G64 && x_bf16) {
     if (fused_ok && m <= kG64FusedMaxM) return Path::Fused;
     if (tile_ok && m >= kTileMinM && (m < kTileMaxM || t.cols > t.rows)) return Path::Tile;
