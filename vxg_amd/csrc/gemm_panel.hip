@@ -652,6 +652,29 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
 // Y[m, n] = (sum_z partial[z, m, n], z ascending) / s[n] * 2^-xe[m] (no
 // weight scaling when inv is null, no activation scaling when xe is null);
 // four outputs per thread when N % 4 == 0.
+// sum_z p[z * stride], z = 0 .. splits-1 added in ascending order, with up to
+// 8 loads in flight: the loads of a group of 8 slices (the last group's past
+// `splits` clamped to a valid slice and not added) are issued before any of
+// them is added, so a thread waits for one memory latency per group rather
+// than one per slice.
+template <typename V>
+__device__ __forceinline__ V sum_slices(const V* __restrict__ p, size_t stride, uint32_t splits) {
+  V v{};
+  for (uint32_t z = 0; z < splits; z += 8) {
+    V a[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) a[j] = p[(size_t)std::min(z + j, splits - 1) * stride];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j)
+      if (z + j < splits) v = v + a[j];
+  }
+  return v;
+}
+
+__device__ __forceinline__ float4 operator+(const float4& a, const float4& b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
 __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict__ partial, uint32_t splits,
                                                          const float* __restrict__ inv,
                                                          const int32_t* __restrict__ xe, uint32_t M, uint32_t N,
@@ -660,11 +683,7 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
   if (N % 4u == 0u) {
     const size_t i = ((size_t)blockIdx.x * THREADS + threadIdx.x) * 4;
     if (i >= total) return;
-    float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t z = 0; z < splits; ++z) {
-      const float4 a = *reinterpret_cast<const float4*>(partial + (size_t)z * total + i);
-      v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
-    }
+    float4 v = sum_slices(reinterpret_cast<const float4*>(partial + i), total / 4, splits);
     if (inv) {
       const float4 iv = *reinterpret_cast<const float4*>(inv + i % N);
       v.x *= iv.x; v.y *= iv.y; v.z *= iv.z; v.w *= iv.w;
@@ -684,8 +703,7 @@ __global__ __launch_bounds__(THREADS) void reduce_kernel(const float* __restrict
   }
   const size_t i = (size_t)blockIdx.x * THREADS + threadIdx.x;
   if (i >= total) return;
-  float v = 0.0f;
-  for (uint32_t z = 0; z < splits; ++z) v += partial[(size_t)z * total + i];
+  float v = sum_slices(partial + i, total, splits);
   if (inv) v *= inv[i % N];
   if (xe) v = ldexpf(v, -xe[i / N]);
   if (y_bf16)
