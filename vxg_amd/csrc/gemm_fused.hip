@@ -364,6 +364,36 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
   const uint32_t ncol = n0 + wn * 32 + (lane & 31);
   if (ncol >= N) return;
   const bool to_partial = gridDim.y > 1;
+  if constexpr (FI == 4) {
+    // One loop per output mode (a mode test per output compiles to a pair
+    // of branches per output); the smaller instantiations keep the shared
+    // loop below, whose registers they need.
+    auto row_of = [&](int i, int r) { return (uint32_t)(i * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
+    if (to_partial) {
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t m = m0 + row_of(i, r);
+          if (m < M) partial[((size_t)blockIdx.y * M + m) * N + ncol] = acc[i][r];
+        }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t m = m0 + row_of(i, r);
+          if (m >= M) continue;
+          float v = acc[i][r];
+          if constexpr (KIND == KIND_G64) v = ldexpf(v, -xe[m]);
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * N + ncol] = f32_to_bf16(v);
+          else
+            static_cast<float*>(y)[(size_t)m * N + ncol] = v;
+        }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < FI; ++i)
 #pragma unroll
