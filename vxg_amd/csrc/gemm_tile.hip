@@ -86,12 +86,15 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
 // NP > 0: the row (at most NP 16-byte pieces per lane, K <= 512 NP) is read
 // once into registers, all loads in flight together, and converted from
 // there; NP == 0: two passes over the row (any K).
-template <int NP>
+template <int NPT>
 __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__ x, uint32_t M, uint32_t K,
                                                     uint32_t kp, uint32_t x_vec, uint16_t* __restrict__ xh,
                                                     int32_t* __restrict__ xe) {
-  const uint32_t m = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-  if (m >= M) return;
+  // One workgroup (4 waves) per activation row: thread t takes the row's
+  // 16-byte pieces t, t + 256, ...; the row maximum is combined through LDS
+  // (the maximum does not depend on the order, so neither does xe).
+  __shared__ float s_mx[4];
+  const uint32_t m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint16_t* row = x + (size_t)m * K;
   const uint32_t np = kp / 8;   // 16-byte pieces of the padded row
   auto store = [&](uint32_t pc, const float (&v)[8], int e) {
@@ -107,16 +110,22 @@ __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = k + j < K ? bf16_to_f32(row[k + j]) : 0.0f;
   };
-  if constexpr (NP > 0) {
-    float v[NP][8];
+  auto row_max = [&](float mx) {
+    mx = lane_reduce<64, true>(mx);
+    if (lane == 0) s_mx[wave] = mx;
+    __syncthreads();
+    return fmaxf(fmaxf(s_mx[0], s_mx[1]), fmaxf(s_mx[2], s_mx[3]));
+  };
+  if constexpr (NPT > 0) {
+    float v[NPT][8];
     if (x_vec) {
       const uint32_t nv = K / 8;   // pieces inside the row
-      uint4 u[NP];
+      uint4 u[NPT];
 #pragma unroll
-      for (int i = 0; i < NP; ++i) u[i] = reinterpret_cast<const uint4*>(row)[std::min(i * 64 + lane, nv - 1)];
+      for (int i = 0; i < NPT; ++i) u[i] = reinterpret_cast<const uint4*>(row)[std::min(i * 256 + tid, nv - 1)];
 #pragma unroll
-      for (int i = 0; i < NP; ++i) {
-        const bool in = i * 64 + lane < nv;
+      for (int i = 0; i < NPT; ++i) {
+        const bool in = i * 256 + tid < nv;
         const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -126,31 +135,29 @@ __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < NP; ++i) piece(i * 64 + lane, v[i]);
+      for (int i = 0; i < NPT; ++i) piece(i * 256 + tid, v[i]);
     }
     float mx = 0.0f;
 #pragma unroll
-    for (int i = 0; i < NP; ++i)
+    for (int i = 0; i < NPT; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[i][j]));
-    mx = lane_reduce<64, true>(mx);
-    const int e = row_exponent(mx);
-    if (lane == 0) xe[m] = e;
+    const int e = row_exponent(row_max(mx));
+    if (tid == 0) xe[m] = e;
 #pragma unroll
-    for (int i = 0; i < NP; ++i)
-      if (i * 64 + lane < np) store(i * 64 + lane, v[i], e);
+    for (int i = 0; i < NPT; ++i)
+      if (i * 256 + tid < np) store(i * 256 + tid, v[i], e);
   } else {
     float mx = 0.0f;
-    for (uint32_t pc = lane; pc < np; pc += 64) {
+    for (uint32_t pc = tid; pc < np; pc += 256) {
       float v[8];
       piece(pc, v);
 #pragma unroll
       for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
     }
-    mx = lane_reduce<64, true>(mx);
-    const int e = row_exponent(mx);
-    if (lane == 0) xe[m] = e;
-    for (uint32_t pc = lane; pc < np; pc += 64) {
+    const int e = row_exponent(row_max(mx));
+    if (tid == 0) xe[m] = e;
+    for (uint32_t pc = tid; pc < np; pc += 256) {
       float v[8];
       piece(pc, v);
       store(pc, v, e);
@@ -1114,18 +1121,20 @@ inline hipError_t launch_tile_cb4(const DevTensor& t, const uint16_t* xh, uint32
   return hipGetLastError();
 }
 
-// The activation pre-pass (row exponents, row-scaled permuted f16 rows).
+// The activation pre-pass (row exponents, row-scaled permuted f16 rows):
+// one workgroup per row, up to 4 pieces of 16 bytes per thread in registers
+// (rows up to 8192 columns), longer rows in two passes.
 inline hipError_t launch_xprep(const uint16_t* x, uint32_t m, uint32_t cols, uint32_t kp, uint16_t* xh, int32_t* xe,
                                hipStream_t s) {
   const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (cols % 8 == 0);
-  const dim3 xg((m + 3) / 4), xb(256);
-  const uint32_t npl = (kp / 8 + 63) / 64;   // 16-byte pieces per lane
-  if (npl <= 4)
+  const dim3 xg(m), xb(256);
+  const uint32_t npt = (kp / 8 + 255) / 256;   // 16-byte pieces per thread
+  if (npt <= 1)
+    hipLaunchKernelGGL(xprep_kernel<1>, xg, xb, 0, s, x, m, cols, kp, x_vec, xh, xe);
+  else if (npt <= 2)
+    hipLaunchKernelGGL(xprep_kernel<2>, xg, xb, 0, s, x, m, cols, kp, x_vec, xh, xe);
+  else if (npt <= 4)
     hipLaunchKernelGGL(xprep_kernel<4>, xg, xb, 0, s, x, m, cols, kp, x_vec, xh, xe);
-  else if (npl <= 8)
-    hipLaunchKernelGGL(xprep_kernel<8>, xg, xb, 0, s, x, m, cols, kp, x_vec, xh, xe);
-  else if (npl <= 16)
-    hipLaunchKernelGGL(xprep_kernel<16>, xg, xb, 0, s, x, m, cols, kp, x_vec, xh, xe);
   else
     hipLaunchKernelGGL(xprep_kernel<0>, xg, xb, 0, s, x, m, cols, kp, x_vec, xh, xe);
   return hipGetLastError();
@@ -1148,18 +1157,7 @@ hipError_t launch_gemm_tile(const DevTensor& t, const uint16_t* x, uint32_t m, v
   int32_t* xe = reinterpret_cast<int32_t*>(base + p.xe_off);
   uint16_t* xh = reinterpret_cast<uint16_t*>(base + p.xh_off);
   float* partial = reinterpret_cast<float*>(base + p.partial_off);
-  const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && (t.cols % 8 == 0);
-  const dim3 xg((m + 3) / 4), xb(256);
-  const uint32_t npl = (t.kp / 8 + 63) / 64;   // 16-byte pieces per lane
-  if (npl <= 4)
-    hipLaunchKernelGGL(gt::xprep_kernel<4>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
-  else if (npl <= 8)
-    hipLaunchKernelGGL(gt::xprep_kernel<8>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
-  else if (npl <= 16)
-    hipLaunchKernelGGL(gt::xprep_kernel<16>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
-  else
-    hipLaunchKernelGGL(gt::xprep_kernel<0>, xg, xb, 0, s, x, m, t.cols, t.kp, x_vec, xh, xe);
-  hipError_t e = hipGetLastError();
+  hipError_t e = gt::launch_xprep(x, m, t.cols, t.kp, xh, xe, s);
   if (e != hipSuccess) return e;
   e = p.kw == 1 ? gt::launch_tile<1>(t, xh, m, xe, y, y_bf16, partial, p, s)
                 : gt::launch_tile<2>(t, xh, m, xe, y, y_bf16, partial, p, s);
