@@ -1,0 +1,439 @@
+// gemm_dense3.hip -- large-tile dense phase of the two-phase prefill GEMM:
+// Y = A * W^T with A the row-scaled f16 activations [M][kp] and W the f16
+// weight panel [N][kp] (gemm_panel.hip writes both).
+//
+// Reference behaviour: the dense tile product of PackedTensor::gemm_cpu
+// (llm_prefill.rs:156-255) over decoded weights; MFMA products are exact in
+// the fp32 accumulators.
+//
+// Shape: a workgroup is 4 waves in 2 x 2; wave (wm, wn) owns WM x WN
+// fragments of v_mfma_f32_32x32x16_f16 (32·WM activation rows x 32·WN weight
+// rows), so the workgroup tile is 64·WM x 64·WN.  The wave tile is the
+// lever: every 16-deep step reads WM + WN fragments (1 KB each) from LDS for
+// WM·WN MFMAs, so 4 x 4 fragments need half the LDS reads per MFMA of the
+// 2 x 2 fragments of a 128 x 128 tile.
+//
+// Operands move global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
+// round trip, no ds_write).  A K tile is 32 columns (64 bytes per row); the
+// hardware writes lane l's 16 bytes at LDS base + 16 l, so one instruction
+// fills 16 rows and the bank swizzle is applied on the global side: lane l
+// fetches logical chunk (l % 4) ^ ((l >> 4) & 3) of row l / 4, i.e. chunk c
+// of row r sits at position c ^ ((r >> 2) & 3).  Fragment reads (16 lanes =
+// 16 consecutive rows at one logical chunk) then hit 16 distinct 16-byte
+// bank groups.
+//
+// Pipeline: NS LDS stages (4 or 5, as many as fit), each a separate
+// __shared__ array, so the compiler can tell the loads into one stage from
+// the fragment reads of another and does not wait for the loads before those
+// reads.  Tile t runs in two 16-deep steps:
+//   step 0: its MFMAs, between them the fragment reads of its step 1;
+//   wait for this wave's loads of tile t + 1, then one barrier: every wave
+//     has then finished reading tile t's stage, and tile t + 1 has landed;
+//   step 1: its MFMAs, between them the fragment reads of tile t + 1's step
+//     0 and the loads of tile t + NS into the stage tile t just left.
+// So loads run NS - 1.5 tiles ahead of their use, the barrier sits between
+// two runs of MFMAs, and fragment registers are double-buffered across the
+// tile boundary: the matrix pipe never waits for an LDS read it could have
+// issued earlier.  Each slice (one MFMA, at most one read, at most one load)
+// is fenced with sched_barrier so the compiler keeps that order.
+//
+// Modes (the panel's weight representation, as in gemm_dense.hip):
+//   * plain: f16 values;
+//   * hi/lo: w * s = hi + lo * 2^-11, each product into its own accumulator,
+//     combined as acc + accl * 2^-11 in the epilogue.
+// With gridDim.y > 1 the workgroup writes fp32 partial sums of its K slice;
+// reduce_kernel adds them in slice order and applies the scales.
+#include <algorithm>
+#include <type_traits>
+#include <utility>
+
+#include "common.hpp"
+
+#pragma clang fp contract(off)
+
+namespace vxt {
+
+namespace g3 {
+
+constexpr int BK = 32, NT = 256;
+constexpr float kLoInv = 1.0f / 2048.0f;
+enum : int { kPlain = 0, kHiLo = 1 };
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>), in order.
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_seq(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+template <int WM, int WN, int MODE>
+struct Cfg {
+  static constexpr int BM = 64 * WM, BN = 64 * WN;
+  static constexpr bool LO = MODE == kHiLo;
+  static constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;   // one stage of one operand
+  static constexpr int STAGE = A_BYTES + B_BYTES * (LO ? 2 : 1);
+  static constexpr int NS = std::min(5, (160 * 1024 - 2048) / STAGE);
+  static constexpr int NA = BM / 64, NB = BN / 64, NL = LO ? NB : 0;   // 1 KB loads per wave per tile
+  static constexpr int NLD = NA + NB + NL;
+  static constexpr int NR = WM + WN + (LO ? WN : 0);   // fragment reads per step
+  static constexpr int NM = WM * WN * (LO ? 2 : 1);    // MFMAs per step
+  static_assert(NS >= 4, "stages");
+  static_assert(NR <= NM && NLD <= NM, "one read and one load per MFMA slice");
+  static_assert(32 * (32 * WN + 8) * 2 <= A_BYTES, "epilogue transpose region");
+};
+
+// 16 bytes per lane from buffer `r` at voff + soff into LDS at lds + 16 lane
+// (a __device__ function, not a lambda: the LDS address-space cast must not
+// appear in code the host pass compiles).
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
+// Raw buffer resource over [base, base + bytes): bounds-checked by the
+// hardware (every offset the kernel forms is in range; rows past the end
+// are clamped to the last row).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, size_t bytes) {
+  const int n = (int)std::min<size_t>(bytes, 0x7ffffff0u);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+
+// s_waitcnt with vmcnt(V) and lgkmcnt(0) (expcnt not waited).
+template <int V>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(V >= 0 && V < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4));
+}
+
+template <int WM, int WN, int MODE>
+__global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restrict__ ah, const uint16_t* __restrict__ bh,
+                                                      const uint16_t* __restrict__ bl, const float* __restrict__ inv,
+                                                      uint32_t M, uint32_t N, uint32_t kp, void* __restrict__ y,
+                                                      uint32_t y_bf16, float* __restrict__ partial,
+                                                      uint32_t kt_per_split, uint32_t tiles_m,
+                                                      const int32_t* __restrict__ xe) {
+  using C = Cfg<WM, WN, MODE>;
+  constexpr int BM = C::BM, BN = C::BN, NS = C::NS;
+  constexpr bool LO = C::LO;
+#define VXT_STAGE(k)                                                                  \
+  __shared__ __attribute__((aligned(1024))) char sA##k[k < NS ? C::A_BYTES : 16];     \
+  __shared__ __attribute__((aligned(1024))) char sB##k[k < NS ? C::B_BYTES : 16];     \
+  __shared__ __attribute__((aligned(1024))) char sL##k[k < NS && LO ? C::B_BYTES : 16];
+  VXT_STAGE(0)
+  VXT_STAGE(1)
+  VXT_STAGE(2)
+  VXT_STAGE(3)
+  VXT_STAGE(4)
+#undef VXT_STAGE
+  __shared__ int32_t s_xe[BM];
+  auto stA = [&](auto k_) -> char* {
+    constexpr int k = decltype(k_)::value;
+    if constexpr (k == 0) return sA0; else if constexpr (k == 1) return sA1; else if constexpr (k == 2) return sA2;
+    else if constexpr (k == 3) return sA3; else return sA4;
+  };
+  auto stB = [&](auto k_) -> char* {
+    constexpr int k = decltype(k_)::value;
+    if constexpr (k == 0) return sB0; else if constexpr (k == 1) return sB1; else if constexpr (k == 2) return sB2;
+    else if constexpr (k == 3) return sB3; else return sB4;
+  };
+  auto stL = [&](auto k_) -> char* {
+    constexpr int k = decltype(k_)::value;
+    if constexpr (k == 0) return sL0; else if constexpr (k == 1) return sL1; else if constexpr (k == 2) return sL2;
+    else if constexpr (k == 3) return sL3; else return sL4;
+  };
+
+  const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave >> 1, wn = wave & 1;
+  // Tile order: blocks b, b+8, ... run on one XCD (one L2), so each XCD gets
+  // a contiguous range of tiles, walked in groups of 8 tile rows.
+  uint32_t tm, tn;
+  {
+    const uint32_t G = gridDim.x, b = blockIdx.x;
+    const uint32_t bb = (G % 8u == 0u) ? (b % 8u) * (G / 8u) + b / 8u : b;
+    const uint32_t tiles_n = G / tiles_m;
+    constexpr uint32_t GM = 8;
+    const uint32_t in_group = GM * tiles_n;
+    const uint32_t first = bb / in_group * GM;
+    const uint32_t gsz = std::min(tiles_m - first, GM);
+    tm = first + (bb % in_group) % gsz;
+    tn = (bb % in_group) / gsz;
+  }
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const uint32_t KTT = kp / BK;
+  const uint32_t kt0 = blockIdx.y * kt_per_split;
+  const uint32_t kt1 = std::min(KTT, kt0 + kt_per_split);
+  const uint32_t KT = kt1 - kt0;   // >= 1
+
+  const __amdgpu_buffer_rsrc_t ra = rsrc(ah, (size_t)M * kp * 2);
+  const __amdgpu_buffer_rsrc_t rb = rsrc(bh, (size_t)N * kp * 2);
+  const __amdgpu_buffer_rsrc_t rl = rsrc(LO ? bl : bh, (size_t)N * kp * 2);
+
+  // Per-lane byte offsets of the load instructions (tile 0 of the slice):
+  // instruction j of this wave fills rows 16 (wave + 4 j) .. + 15.
+  uint32_t va[C::NA], vb[C::NB];
+  {
+    const uint32_t r16 = lane >> 2, chunk = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+    for (int j = 0; j < C::NA; ++j) {
+      const uint32_t g = std::min(m0 + 16 * (wave + 4 * j) + r16, M - 1);
+      va[j] = g * kp * 2 + chunk * 16 + kt0 * (BK * 2);
+    }
+#pragma unroll
+    for (int j = 0; j < C::NB; ++j) {
+      const uint32_t g = std::min(n0 + 16 * (wave + 4 * j) + r16, N - 1);
+      vb[j] = g * kp * 2 + chunk * 16 + kt0 * (BK * 2);
+    }
+  }
+  // Load piece j (A pieces, then W, then W's lo plane) of slice tile t into
+  // stage k.
+  auto load_piece = [&](auto k_, int j, uint32_t t) {
+    const uint32_t so = t * (BK * 2);
+    if (j < C::NA) {
+      dma16(ra, stA(k_) + 1024 * (wave + 4 * j), va[j], so);
+    } else if (j < C::NA + C::NB) {
+      const int q = j - C::NA;
+      dma16(rb, stB(k_) + 1024 * (wave + 4 * q), vb[q], so);
+    } else {
+      const int q = j - C::NA - C::NB;
+      dma16(rl, stL(k_) + 1024 * (wave + 4 * q), vb[q], so);
+    }
+  };
+
+  if (tid < BM) s_xe[tid] = xe[std::min(m0 + tid, M - 1)];
+
+  float16v acc[WM][WN];
+  float16v accl[LO ? WM : 1][LO ? WN : 1];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int j = 0; j < WN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        acc[i][j][r] = 0.0f;
+        if constexpr (LO) accl[i][j][r] = 0.0f;
+      }
+
+  // fragment (i, step s): operand rows base + 32 i + l32, logical chunk 2 s + h
+  uint32_t offA[2], offB[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const uint32_t pos = ((2 * s + h) ^ ((l32 >> 2) & 3u)) * 16;   // + 32 i keeps the swizzle
+    offA[s] = (wm * (32 * WM) + l32) * 64 + pos;
+    offB[s] = (wn * (32 * WN) + l32) * 64 + pos;
+  }
+
+  half8 af[2][WM], bf[2][WN], lf[2][LO ? WN : 1];
+  // fragment read q of step s from stage k into register set `set`, in the
+  // order the step's MFMAs need them: A0, B0 .. B(WN-1) (each with its lo
+  // plane), A1 .. A(WM-1)
+  auto read = [&](auto k_, auto s_, auto set_, auto q_) {
+    constexpr int s = decltype(s_)::value, set = decltype(set_)::value, q = decltype(q_)::value;
+    constexpr int NBL = WN * (LO ? 2 : 1);
+    if constexpr (q == 0) {
+      af[set][0] = *reinterpret_cast<const half8*>(stA(k_) + offA[s]);
+    } else if constexpr (q <= NBL) {
+      constexpr int j = (q - 1) / (LO ? 2 : 1);
+      if constexpr (LO && (q - 1) % 2 == 1)
+        lf[set][j] = *reinterpret_cast<const half8*>(stL(k_) + j * 2048 + offB[s]);
+      else
+        bf[set][j] = *reinterpret_cast<const half8*>(stB(k_) + j * 2048 + offB[s]);
+    } else {
+      constexpr int i = q - NBL;
+      af[set][i] = *reinterpret_cast<const half8*>(stA(k_) + i * 2048 + offA[s]);
+    }
+  };
+  auto mma = [&](auto set_, auto q_) {
+    constexpr int set = decltype(set_)::value, q = decltype(q_)::value;
+    constexpr int p = LO ? q / 2 : q;
+    constexpr int i = p / WN, j = p % WN;
+    if constexpr (LO && q % 2 == 1)
+      accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[set][i], lf[set][j], accl[i][j], 0, 0, 0);
+    else
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[set][i], bf[set][j], acc[i][j], 0, 0, 0);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  // prologue: tiles 0 .. NS-1 into stages 0 .. NS-1, wait for tile 0, read
+  // its step-0 fragments
+  static_for<NS>([&](auto k_) {
+    constexpr int k = decltype(k_)::value;
+#pragma unroll
+    for (int j = 0; j < C::NLD; ++j) load_piece(k_, j, std::min<uint32_t>(k, KT - 1));
+  });
+  wait_vm_lgkm0<(NS - 1) * C::NLD>();
+  __builtin_amdgcn_s_barrier();
+  static_for<C::NR>([&](auto q_) { read(I0{}, I0{}, I0{}, q_); });
+
+  // Tile t from stage k (= t mod NS).
+  auto tile = [&](auto k_, uint32_t t) {
+    constexpr int k = decltype(k_)::value;
+    using KN = std::integral_constant<int, (k + 1) % NS>;
+    // step 0: MFMAs on set 0, reads of step 1 into set 1
+    static_for<C::NM>([&](auto q_) {
+      constexpr int q = decltype(q_)::value;
+      mma(I0{}, q_);
+      if constexpr (q < C::NR) read(k_, I1{}, I1{}, q_);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    // tile t + 1 landed (this wave's loads; the barrier covers the others)
+    // and every wave is done reading stage k
+    wait_vm_lgkm0<(NS - 2) * C::NLD>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    // step 1: MFMAs on set 1, reads of tile t + 1's step 0 into set 0, loads
+    // of tile t + NS into stage k
+    const uint32_t tl = std::min(t + NS, KT - 1);
+    static_for<C::NM>([&](auto q_) {
+      constexpr int q = decltype(q_)::value;
+      mma(I1{}, q_);
+      if constexpr (q < C::NR) read(KN{}, I0{}, I0{}, q_);
+      if constexpr (q < C::NLD) load_piece(k_, q, tl);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  uint32_t t = 0;
+  for (; t + NS <= KT; t += NS) {
+    static_for<NS>([&](auto k_) { tile(k_, t + decltype(k_)::value); });
+  }
+  {
+    const uint32_t rem = KT - t;
+    static_for<NS - 1>([&](auto k_) {
+      if (decltype(k_)::value < rem) tile(k_, t + decltype(k_)::value);
+    });
+  }
+  __syncthreads();   // drains the clamped tail loads too: the epilogue reuses stages
+
+  // Epilogue.  Lane owns column n0 + wn*32*WN + j*32 + l32 of fragment
+  // (i, j), rows m0 + wm*32*WM + i*32 + 4h + 8(r/4) + r%4.
+  const bool to_partial = gridDim.y > 1;
+  auto value = [&](int i, int j, int r) {
+    float v = acc[i][j][r];
+    if constexpr (LO) v = __builtin_fmaf(accl[i][j][r], kLoInv, v);
+    return v;
+  };
+  auto row_of = [&](int i, int r) { return (uint32_t)(wm * 32 * WM + i * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
+  const bool rows_fast = y_bf16 && !to_partial && N % 8 == 0 && n0 + BN <= N &&
+                         reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  if (rows_fast) {
+    // Each wave transposes its 32·WM x 32·WN block through its own LDS
+    // region (stage wave's A array), 32 rows at a time, and writes whole-row
+    // 16-byte pieces.  Rows r and r + 1 of a lane are converted as one pair
+    // (one v_cvt_pk_bf16_f32) and stored as the pair's two halves.
+    constexpr uint32_t LDO = 32 * WN + 8;   // bf16 elements per LDS row
+    uint16_t* reg = reinterpret_cast<uint16_t*>(wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : sA3);
+    float sc[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) sc[j] = inv[n0 + wn * 32 * WN + j * 32 + l32];
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+      // this lane's 16 row exponents (4 consecutive rows per 16-byte read)
+      int nxe[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int4 e4 = *reinterpret_cast<const int4*>(s_xe + wm * 32 * WM + i * 32 + h * 4 + 8 * q);
+        nxe[4 * q + 0] = -e4.x;
+        nxe[4 * q + 1] = -e4.y;
+        nxe[4 * q + 2] = -e4.z;
+        nxe[4 * q + 3] = -e4.w;
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const uint32_t rr = h * 4 + 8 * (r >> 2) + (r & 3);
+          const uint32_t p = bf16x2_pack(ldexpf(value(i, j, r) * sc[j], nxe[r]),
+                                         ldexpf(value(i, j, r + 1) * sc[j], nxe[r + 1]));
+          reg[rr * LDO + j * 32 + l32] = (uint16_t)p;
+          reg[(rr + 1) * LDO + j * 32 + l32] = (uint16_t)(p >> 16);
+        }
+      // 32 rows x 32·WN columns: 4·WN lanes per row, 16 bytes each (LDS
+      // operations of one wave complete in order: no barrier needed)
+      constexpr uint32_t LPR = 4 * WN, ROWS_PER = 64 / LPR;
+#pragma unroll
+      for (uint32_t q = 0; q < (32 + ROWS_PER - 1) / ROWS_PER; ++q) {
+        const uint32_t rr = q * ROWS_PER + lane / LPR, c = lane % LPR;
+        const uint32_t m = m0 + wm * 32 * WM + i * 32 + rr;
+        if (rr < 32 && lane < ROWS_PER * LPR && m < M) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(reg + rr * LDO + c * 8);
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(y) + (size_t)m * N + n0 + wn * 32 * WN + c * 8) = v;
+        }
+      }
+    }
+  } else if (to_partial) {
+    const bool full = m0 + BM <= M && n0 + BN <= N;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const uint32_t n = n0 + wn * 32 * WN + j * 32 + l32;
+      float* const pp = partial + ((size_t)blockIdx.y * M + m0) * N + n;
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (full || (m0 + row_of(i, r) < M && n < N)) pp[(size_t)row_of(i, r) * N] = value(i, j, r);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const uint32_t n = n0 + wn * 32 * WN + j * 32 + l32;
+      const float sc = inv[std::min(n, N - 1)];
+#pragma unroll
+      for (int i = 0; i < WM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t m = m0 + row_of(i, r);
+          if (m >= M || n >= N) continue;
+          const float o = ldexpf(value(i, j, r) * sc, -s_xe[row_of(i, r)]);
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(o);
+          else
+            static_cast<float*>(y)[(size_t)m * N + n] = o;
+        }
+    }
+  }
+}
+
+template <int WM, int WN, int MODE>
+hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* inv, uint32_t m,
+                  uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial, uint32_t splits,
+                  uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
+  using C = Cfg<WM, WN, MODE>;
+  const uint32_t tiles_m = (m + C::BM - 1) / C::BM;
+  hipLaunchKernelGGL((dense3_kernel<WM, WN, MODE>), dim3(tiles_m * ((n + C::BN - 1) / C::BN), splits), dim3(NT), 0,
+                     s, ah, bh, bl, inv, m, n, kp, y, (uint32_t)y_bf16, partial, kt_per_split, tiles_m, xe);
+  return hipGetLastError();
+}
+
+}  // namespace g3
+
+// Large-tile dense phase.  cfg selects the wave tile (WM x WN fragments):
+// 0 = 4 x 4 (workgroup tile 256 x 256), 1 = 4 x 3 (256 x 192), 2 = 4 x 2
+// (256 x 128), 3 = 2 x 2 (128 x 128).  wmode 0 = plain f16 panel, 1 = hi/lo
+// panel (bh + bl * 2^-11; cfg 2 and 3).  kt_per_split counts 32-column K
+// tiles; kp % 32 == 0.
+hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl,
+                         const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
+                         float* partial, uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
+  if (kp % g3::BK != 0 || xe == nullptr || m == 0 || n == 0 || kt_per_split == 0) return hipErrorInvalidValue;
+#define VXT_D3(WM, WN, MODE) \
+  return g3::launch<WM, WN, MODE>(ah, bh, bl, inv, m, n, kp, y, y_bf16, partial, splits, kt_per_split, xe, s)
+  switch (wmode * 16 + cfg) {
+    case g3::kPlain * 16 + 0: VXT_D3(4, 4, g3::kPlain);
+    case g3::kPlain * 16 + 1: VXT_D3(4, 3, g3::kPlain);
+    case g3::kPlain * 16 + 2: VXT_D3(4, 2, g3::kPlain);
+    case g3::kPlain * 16 + 3: VXT_D3(2, 2, g3::kPlain);
+    case g3::kHiLo * 16 + 2: VXT_D3(4, 2, g3::kHiLo);
+    case g3::kHiLo * 16 + 3: VXT_D3(2, 2, g3::kHiLo);
+    default: return hipErrorInvalidValue;
+  }
+#undef VXT_D3
+}
+
+}  // namespace vxt

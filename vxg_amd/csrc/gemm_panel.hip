@@ -54,6 +54,9 @@ hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, 
 hipError_t launch_dense2(int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* dsc,
                          const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial,
                          uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s);
+hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl,
+                         const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
+                         float* partial, uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s);
 
 namespace gp {
 
@@ -719,6 +722,7 @@ struct Plan {
   bool lib;   // dense phase on the vendor library (gemm_blas.cpp)
   uint32_t kp, splits, kt_per_split;
   uint32_t lib_splits;   // K slices of the library call (one strided batch)
+  int d3cfg;             // >= 0: the dense phase on dense3_kernel (gemm_dense3.hip) with this wave tile
   size_t panel_plane, dsc_bytes, panel_bytes, a_plane, a_bytes, partial_bytes;
 };
 
@@ -741,6 +745,24 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   while (tiles * splits < 512 && ktiles / (splits * 2) >= 16) splits *= 2;
   pl.kt_per_split = (ktiles + splits - 1) / splits;
   pl.splits = (ktiles + pl.kt_per_split - 1) / pl.kt_per_split;
+  // Large batches of bf16 activations over a plain f16 panel: the
+  // large-tile kernel, one K range per workgroup.  256 x 192 tiles where the
+  // rows divide (at 2048 x 6144 outputs, one tile per CU), 128 x 128
+  // otherwise.  Measured (lab, graph-free, realistic operands), dense phase
+  // alone: 2048 x 2048 -> 6144 51-61 us against 60-63 us for dense2_kernel;
+  // 2048 x 6144 -> 2048 59 us (128 x 128, no split) against 58-59 us
+  // (dense2_kernel, two K slices and the reduction).
+  pl.d3cfg = -1;
+  if (x_bf16 && !lib && pl.wmode == kWPlain && m >= 1024) {
+    const uint32_t t192 = ((m + 255) / 256) * (t.rows / 192);
+    const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
+    if (t.rows % 192 == 0 && t192 >= 224) pl.d3cfg = 1;
+    else if (t128 >= 224) pl.d3cfg = 3;
+    if (pl.d3cfg >= 0) {
+      pl.splits = 1;
+      pl.kt_per_split = pl.kp / 32;
+    }
+  }
   pl.panel_plane = al256((size_t)t.rows * pl.kp * 2);
   pl.dsc_bytes = pl.wmode == kWQBlock ? al256((size_t)t.rows * (pl.kp / 32) * 4) : 0;
   pl.panel_bytes = pl.panel_plane * (pl.wmode == kWHiLo ? 2 : 1) + pl.dsc_bytes + al256((size_t)t.rows * 4);
@@ -858,7 +880,10 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
     if (e != hipErrorNotSupported) return e;
     (void)hipGetLastError();   // no algorithm for this shape: the own dense kernel on the same panel
   }
-  if (x_bf16 && pl.bm == 128) {
+  if (pl.d3cfg >= 0) {
+    e = launch_dense3(pl.d3cfg, 0, ah, p.hi, p.lo, p.inv, m, t.rows, pl.kp, y, y_bf16, partial, pl.splits,
+                      pl.kt_per_split, xe, s);
+  } else if (x_bf16 && pl.bm == 128) {
     // 128 x 128 tiles with bf16 (exact f16) activations: the interleaved
     // dense kernel (gemm_dense.hip), any weight mode
     e = launch_dense2(pl.wmode, ah, p.hi, p.lo, p.dsc, p.inv, m, t.rows, pl.kp, y, y_bf16, partial, pl.splits,
