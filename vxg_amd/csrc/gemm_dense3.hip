@@ -22,7 +22,7 @@
 // 16 consecutive rows at one logical chunk) then hit 16 distinct 16-byte
 // bank groups.
 //
-// Pipeline: NS LDS stages (4 or 5, as many as fit), each a separate
+// Pipeline: NS LDS stages (3 to 5, as many as fit), each a separate
 // __shared__ array, so the compiler can tell the loads into one stage from
 // the fragment reads of another and does not wait for the loads before those
 // reads.  Tile t runs in two 16-deep steps:
@@ -40,7 +40,16 @@
 // Modes (the panel's weight representation, as in gemm_dense.hip):
 //   * plain: f16 values;
 //   * hi/lo: w * s = hi + lo * 2^-11, each product into its own accumulator,
-//     combined as acc + accl * 2^-11 in the epilogue.
+//     combined as acc + accl * 2^-11 in the epilogue;
+//   * Q8 block: int8 values as f16 and one f32 scale per (row, 32-column
+//     block).  A K tile is exactly one block: its two steps' MFMAs go into a
+//     fresh fragment set, and acc += d * fragment (the lane's output column
+//     is fixed, so one scale per fragment) -- for tile t in tile t + 1's
+//     step 0, fragment q's sixteen FMAs just before the MFMA that restarts
+//     fragment q.  Two workgroups per CU (two waves per SIMD), so one wave's
+//     scale FMAs run in the VALU while the other wave's MFMAs keep the
+//     matrix pipe busy.  The tile's scales travel with it: a 4-byte-per-lane
+//     LDS load of the scales of the tile's weight rows.
 // With gridDim.y > 1 the workgroup writes fp32 partial sums of its K slice;
 // reduce_kernel adds them in slice order and applies the scales.
 #include <algorithm>
@@ -57,7 +66,7 @@ namespace g3 {
 
 constexpr int BK = 32, NT = 256;
 constexpr float kLoInv = 1.0f / 2048.0f;
-enum : int { kPlain = 0, kHiLo = 1 };
+enum : int { kPlain = 0, kHiLo = 1, kQBlock = 2 };
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float float16v __attribute__((ext_vector_type(16)));
@@ -73,20 +82,28 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
+// 128 x 128 tiles run two workgroups per CU (the LDS budget halves)
+constexpr int occupancy(int wm, int wn) { return (wm == 2 && wn == 2) ? 2 : 1; }
+
 template <int WM, int WN, int MODE>
 struct Cfg {
   static constexpr int BM = 64 * WM, BN = 64 * WN;
-  static constexpr bool LO = MODE == kHiLo;
+  static constexpr bool LO = MODE == kHiLo, QB = MODE == kQBlock;
   static constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;   // one stage of one operand
-  static constexpr int STAGE = A_BYTES + B_BYTES * (LO ? 2 : 1);
-  static constexpr int NS = std::min(5, (160 * 1024 - 2048) / STAGE);
+  static constexpr int D_BYTES = QB ? BN * 4 : 16;             // Q8 block: the tile's scales
+  static constexpr int STAGE = A_BYTES + B_BYTES * (LO ? 2 : 1) + (QB ? D_BYTES : 0);
+  static constexpr int OCC = occupancy(WM, WN);
+  static constexpr int NS = std::min(5, (160 * 1024 / OCC - 2048) / STAGE);
   static constexpr int NA = BM / 64, NB = BN / 64, NL = LO ? NB : 0;   // 1 KB loads per wave per tile
-  static constexpr int NLD = NA + NB + NL;
+  static constexpr int ND = QB ? 1 : 0;   // one 4-byte-per-lane scale load per wave per tile
+  static constexpr int NLD = NA + NB + NL + ND;
   static constexpr int NR = WM + WN + (LO ? WN : 0);   // fragment reads per step
   static constexpr int NM = WM * WN * (LO ? 2 : 1);    // MFMAs per step
-  static_assert(NS >= 4, "stages");
-  static_assert(NR <= NM && NLD <= NM, "one read and one load per MFMA slice");
+  static_assert(NS >= 3, "stages");
+  static constexpr int LPS = (NLD + NM - 1) / NM;   // loads per MFMA slice of step 1
+  static_assert(NR <= NM && LPS <= 2, "one read and at most two loads per MFMA slice");
   static_assert(32 * (32 * WN + 8) * 2 <= A_BYTES, "epilogue transpose region");
+  static_assert(!QB || (BN == 128 && OCC == 2), "Q8 block mode: 128 x 128 tiles");
 };
 
 // 16 bytes per lane from buffer `r` at voff + soff into LDS at lds + 16 lane
@@ -94,6 +111,10 @@ struct Cfg {
 // appear in code the host pass compiles).
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, char* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 4, voff, soff, 0, 0);
 }
 
 // Raw buffer resource over [base, base + bytes): bounds-checked by the
@@ -112,19 +133,21 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 }
 
 template <int WM, int WN, int MODE>
-__global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restrict__ ah, const uint16_t* __restrict__ bh,
-                                                      const uint16_t* __restrict__ bl, const float* __restrict__ inv,
+__global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uint16_t* __restrict__ ah, const uint16_t* __restrict__ bh,
+                                                      const uint16_t* __restrict__ bl, const float* __restrict__ dsc,
+                                                      const float* __restrict__ inv,
                                                       uint32_t M, uint32_t N, uint32_t kp, void* __restrict__ y,
                                                       uint32_t y_bf16, float* __restrict__ partial,
                                                       uint32_t kt_per_split, uint32_t tiles_m,
                                                       const int32_t* __restrict__ xe) {
   using C = Cfg<WM, WN, MODE>;
   constexpr int BM = C::BM, BN = C::BN, NS = C::NS;
-  constexpr bool LO = C::LO;
+  constexpr bool LO = C::LO, QB = C::QB;
 #define VXT_STAGE(k)                                                                  \
   __shared__ __attribute__((aligned(1024))) char sA##k[k < NS ? C::A_BYTES : 16];     \
   __shared__ __attribute__((aligned(1024))) char sB##k[k < NS ? C::B_BYTES : 16];     \
-  __shared__ __attribute__((aligned(1024))) char sL##k[k < NS && LO ? C::B_BYTES : 16];
+  __shared__ __attribute__((aligned(1024))) char sL##k[k < NS && LO ? C::B_BYTES : 16]; \
+  __shared__ __attribute__((aligned(256))) char sD##k[k < NS ? C::D_BYTES : 16];
   VXT_STAGE(0)
   VXT_STAGE(1)
   VXT_STAGE(2)
@@ -146,6 +169,11 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
     constexpr int k = decltype(k_)::value;
     if constexpr (k == 0) return sL0; else if constexpr (k == 1) return sL1; else if constexpr (k == 2) return sL2;
     else if constexpr (k == 3) return sL3; else return sL4;
+  };
+  auto stD = [&](auto k_) -> char* {
+    constexpr int k = decltype(k_)::value;
+    if constexpr (k == 0) return sD0; else if constexpr (k == 1) return sD1; else if constexpr (k == 2) return sD2;
+    else if constexpr (k == 3) return sD3; else return sD4;
   };
 
   const uint32_t tid = threadIdx.x, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
@@ -173,10 +201,14 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
   const __amdgpu_buffer_rsrc_t ra = rsrc(ah, (size_t)M * kp * 2);
   const __amdgpu_buffer_rsrc_t rb = rsrc(bh, (size_t)N * kp * 2);
   const __amdgpu_buffer_rsrc_t rl = rsrc(LO ? bl : bh, (size_t)N * kp * 2);
+  const uint32_t nblk = kp / BK;   // Q8 block scales per weight row
+  const __amdgpu_buffer_rsrc_t rd = rsrc(QB ? (const void*)dsc : (const void*)bh, QB ? (size_t)N * nblk * 4 : 16);
 
   // Per-lane byte offsets of the load instructions (tile 0 of the slice):
   // instruction j of this wave fills rows 16 (wave + 4 j) .. + 15.
-  uint32_t va[C::NA], vb[C::NB];
+  uint32_t va[C::NA], vb[C::NB], vd = 0;
+  if constexpr (QB)   // wave w loads the scales of weight rows 64 (w % 2) .. + 63 (waves 2, 3 repeat 0, 1)
+    vd = std::min(n0 + 64 * (wave & 1) + lane, N - 1) * nblk * 4 + kt0 * 4;
   {
     const uint32_t r16 = lane >> 2, chunk = (lane & 3) ^ ((lane >> 4) & 3);
 #pragma unroll
@@ -194,7 +226,9 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
   // stage k.
   auto load_piece = [&](auto k_, int j, uint32_t t) {
     const uint32_t so = t * (BK * 2);
-    if (j < C::NA) {
+    if (QB && j == C::NLD - 1) {
+      dma4(rd, stD(k_) + 256 * (wave & 1), vd, t * 4);
+    } else if (j < C::NA) {
       dma16(ra, stA(k_) + 1024 * (wave + 4 * j), va[j], so);
     } else if (j < C::NA + C::NB) {
       const int q = j - C::NA;
@@ -209,6 +243,21 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
 
   float16v acc[WM][WN];
   float16v accl[LO ? WM : 1][LO ? WN : 1];
+  // Q8 block mode: the block's fragments, and the scales of this lane's
+  // output columns for the tile being multiplied (set t & 1) and the one
+  // being scaled
+  float16v tmp[QB ? WM : 1][QB ? WN : 1];
+  float dreg[QB ? 2 : 1][QB ? WN : 1];
+  if constexpr (QB) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int j = 0; j < WN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) tmp[i][j][r] = 0.0f;   // "tile -1": adds 0 * 0
+#pragma unroll
+    for (int j = 0; j < WN; ++j) dreg[1][j] = 0.0f;
+  }
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
@@ -248,14 +297,24 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
       af[set][i] = *reinterpret_cast<const half8*>(stA(k_) + i * 2048 + offA[s]);
     }
   };
-  auto mma = [&](auto set_, auto q_) {
-    constexpr int set = decltype(set_)::value, q = decltype(q_)::value;
+  auto mma = [&](auto set_, auto q_, auto par_) {
+    constexpr int set = decltype(set_)::value, q = decltype(q_)::value, par = decltype(par_)::value;
     constexpr int p = LO ? q / 2 : q;
     constexpr int i = p / WN, j = p % WN;
     if constexpr (LO && q % 2 == 1)
       accl[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[set][i], lf[set][j], accl[i][j], 0, 0, 0);
+    else if constexpr (QB)   // step 0 (set 0) starts the block's fragment
+      tmp[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[set][i], bf[set][j], set == 0 ? float16v{} : tmp[i][j],
+                                                         0, 0, 0);
     else
       acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[set][i], bf[set][j], acc[i][j], 0, 0, 0);
+  };
+  // Q8 block: acc += d * fragment q of the previous tile (scales set par)
+  auto scale = [&](auto par_, auto q_) {
+    constexpr int par = decltype(par_)::value, q = decltype(q_)::value;
+    constexpr int i = q / WN, j = q % WN;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(dreg[par][j], tmp[i][j][r], acc[i][j][r]);
   };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
@@ -275,11 +334,16 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
   auto tile = [&](auto k_, uint32_t t) {
     constexpr int k = decltype(k_)::value;
     using KN = std::integral_constant<int, (k + 1) % NS>;
+    using PAR = std::integral_constant<int, k & 1>;          // this tile's fragment set (Q8 block)
+    using PPAR = std::integral_constant<int, (k & 1) ^ 1>;   // the previous tile's
     // step 0: MFMAs on set 0, reads of step 1 into set 1
     static_for<C::NM>([&](auto q_) {
       constexpr int q = decltype(q_)::value;
-      mma(I0{}, q_);
+      if constexpr (QB) scale(PPAR{}, q_);   // the previous block's fragment q, before the MFMA restarts it
+      mma(I0{}, q_, PAR{});
       if constexpr (q < C::NR) read(k_, I1{}, I1{}, q_);
+      if constexpr (QB && q < WN)   // this tile's scales, before its stage is released
+        dreg[PAR::value][q] = *reinterpret_cast<const float*>(stD(k_) + 4 * (wn * (32 * WN) + q * 32 + l32));
       __builtin_amdgcn_sched_barrier(0);
     });
     // tile t + 1 landed (this wave's loads; the barrier covers the others)
@@ -292,9 +356,12 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
     const uint32_t tl = std::min(t + NS, KT - 1);
     static_for<C::NM>([&](auto q_) {
       constexpr int q = decltype(q_)::value;
-      mma(I1{}, q_);
+      mma(I1{}, q_, PAR{});
       if constexpr (q < C::NR) read(KN{}, I0{}, I0{}, q_);
-      if constexpr (q < C::NLD) load_piece(k_, q, tl);
+      static_for<C::LPS>([&](auto u_) {
+        constexpr int j = q * C::LPS + decltype(u_)::value;
+        if constexpr (j < C::NLD) load_piece(k_, j, tl);
+      });
       __builtin_amdgcn_sched_barrier(0);
     });
   };
@@ -308,6 +375,12 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
     static_for<NS - 1>([&](auto k_) {
       if (decltype(k_)::value < rem) tile(k_, t + decltype(k_)::value);
     });
+    if constexpr (QB) {   // the last tile's scaling: its scales are set (KT - 1) & 1
+      if (((KT - 1) & 1) == 0)
+        static_for<C::NM>([&](auto q_) { scale(I0{}, q_); });
+      else
+        static_for<C::NM>([&](auto q_) { scale(I1{}, q_); });
+    }
   }
   __syncthreads();   // drains the clamped tail loads too: the epilogue reuses stages
 
@@ -324,11 +397,14 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
                          reinterpret_cast<uintptr_t>(y) % 16 == 0;
   if (rows_fast) {
     // Each wave transposes its 32·WM x 32·WN block through its own LDS
-    // region (stage wave's A array), 32 rows at a time, and writes whole-row
-    // 16-byte pieces.  Rows r and r + 1 of a lane are converted as one pair
-    // (one v_cvt_pk_bf16_f32) and stored as the pair's two halves.
+    // region (stage wave's A array; with three stages wave 3 takes stage 0's
+    // W array), 32 rows at a time, and writes whole-row 16-byte pieces.  Rows
+    // r and r + 1 of a lane are converted as one pair (one v_cvt_pk_bf16_f32)
+    // and stored as the pair's two halves.
     constexpr uint32_t LDO = 32 * WN + 8;   // bf16 elements per LDS row
-    uint16_t* reg = reinterpret_cast<uint16_t*>(wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : sA3);
+    static_assert(NS >= 4 || 32 * LDO * 2 <= C::B_BYTES, "epilogue region of wave 3");
+    char* const reg3 = NS >= 4 ? sA3 : sB0;
+    uint16_t* reg = reinterpret_cast<uint16_t*>(wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : reg3);
     float sc[WN];
 #pragma unroll
     for (int j = 0; j < WN; ++j) sc[j] = inv[n0 + wn * 32 * WN + j * 32 + l32];
@@ -401,13 +477,13 @@ __global__ __launch_bounds__(NT, 1) void dense3_kernel(const uint16_t* __restric
 }
 
 template <int WM, int WN, int MODE>
-hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* inv, uint32_t m,
+hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* dsc, const float* inv, uint32_t m,
                   uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial, uint32_t splits,
                   uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
   using C = Cfg<WM, WN, MODE>;
   const uint32_t tiles_m = (m + C::BM - 1) / C::BM;
   hipLaunchKernelGGL((dense3_kernel<WM, WN, MODE>), dim3(tiles_m * ((n + C::BN - 1) / C::BN), splits), dim3(NT), 0,
-                     s, ah, bh, bl, inv, m, n, kp, y, (uint32_t)y_bf16, partial, kt_per_split, tiles_m, xe);
+                     s, ah, bh, bl, dsc, inv, m, n, kp, y, (uint32_t)y_bf16, partial, kt_per_split, tiles_m, xe);
   return hipGetLastError();
 }
 
@@ -416,14 +492,15 @@ hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, co
 // Large-tile dense phase.  cfg selects the wave tile (WM x WN fragments):
 // 0 = 4 x 4 (workgroup tile 256 x 256), 1 = 4 x 3 (256 x 192), 2 = 4 x 2
 // (256 x 128), 3 = 2 x 2 (128 x 128).  wmode 0 = plain f16 panel, 1 = hi/lo
-// panel (bh + bl * 2^-11; cfg 2 and 3).  kt_per_split counts 32-column K
+// panel (bh + bl * 2^-11; cfg 2 and 3), 2 = Q8 block (int8 values as f16 in
+// bh, f32 scales dsc [n][kp / 32]; cfg 3).  kt_per_split counts 32-column K
 // tiles; kp % 32 == 0.
 hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl,
-                         const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
+                         const float* dsc, const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
                          float* partial, uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
   if (kp % g3::BK != 0 || xe == nullptr || m == 0 || n == 0 || kt_per_split == 0) return hipErrorInvalidValue;
 #define VXT_D3(WM, WN, MODE) \
-  return g3::launch<WM, WN, MODE>(ah, bh, bl, inv, m, n, kp, y, y_bf16, partial, splits, kt_per_split, xe, s)
+  return g3::launch<WM, WN, MODE>(ah, bh, bl, dsc, inv, m, n, kp, y, y_bf16, partial, splits, kt_per_split, xe, s)
   switch (wmode * 16 + cfg) {
     case g3::kPlain * 16 + 0: VXT_D3(4, 4, g3::kPlain);
     case g3::kPlain * 16 + 1: VXT_D3(4, 3, g3::kPlain);
@@ -431,6 +508,7 @@ hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t*
     case g3::kPlain * 16 + 3: VXT_D3(2, 2, g3::kPlain);
     case g3::kHiLo * 16 + 2: VXT_D3(4, 2, g3::kHiLo);
     case g3::kHiLo * 16 + 3: VXT_D3(2, 2, g3::kHiLo);
+    case g3::kQBlock * 16 + 3: VXT_D3(2, 2, g3::kQBlock);
     default: return hipErrorInvalidValue;
   }
 #undef VXT_D3

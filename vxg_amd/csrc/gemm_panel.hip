@@ -55,7 +55,7 @@ hipError_t launch_dense2(int wmode, const uint16_t* ah, const uint16_t* bh, cons
                          const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial,
                          uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s);
 hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl,
-                         const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
+                         const float* dsc, const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
                          float* partial, uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s);
 
 namespace gp {
@@ -723,6 +723,7 @@ struct Plan {
   uint32_t kp, splits, kt_per_split;
   uint32_t lib_splits;   // K slices of the library call (one strided batch)
   int d3cfg;             // >= 0: the dense phase on dense3_kernel (gemm_dense3.hip) with this wave tile
+  int d3mode;            // its weight mode (0 plain, 2 Q8 block)
   size_t panel_plane, dsc_bytes, panel_bytes, a_plane, a_bytes, partial_bytes;
 };
 
@@ -752,16 +753,42 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   // alone: 2048 x 2048 -> 6144 51-61 us against 60-63 us for dense2_kernel;
   // 2048 x 6144 -> 2048 59 us (128 x 128, no split) against 58-59 us
   // (dense2_kernel, two K slices and the reduction).
+  //
+  // Q8 block mode where 128 x 128 tiles alone fill both workgroup slots of
+  // every CU: each block's scale FMAs run while the other workgroup's MFMAs
+  // keep the matrix pipe busy.  Measured (whole call, graph-timed): M = 2048
+  // x 2048 -> 6144 480 vs 444 TFLOP/s on dense2_kernel's block mode, 6144 ->
+  // 2048 level; with fewer tiles the K slices its grid needs cost more
+  // (M = 512 x 6144 -> 2048 239 vs 273), so dense2_kernel keeps those.
+  //
+  // hi/lo panels (cb4) at large batches of the wide projections: 256 x 128
+  // tiles (lab, dense phase alone, M = 2048 x 2048 -> 6144: 122.6 vs 128.4
+  // us; M = 4096: 226 vs 278 us).
   pl.d3cfg = -1;
+  pl.d3mode = 0;
+  const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
   if (x_bf16 && !lib && pl.wmode == kWPlain && m >= 1024) {
     const uint32_t t192 = ((m + 255) / 256) * (t.rows / 192);
-    const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
     if (t.rows % 192 == 0 && t192 >= 224) pl.d3cfg = 1;
     else if (t128 >= 224) pl.d3cfg = 3;
-    if (pl.d3cfg >= 0) {
-      pl.splits = 1;
-      pl.kt_per_split = pl.kp / 32;
-    }
+  } else if (x_bf16 && !lib && pl.wmode == kWQBlock && t128 >= 256) {
+    pl.d3cfg = 3;
+    pl.d3mode = 2;
+  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && m >= 2048 && t.rows >= 4096) {
+    pl.d3cfg = 2;
+    pl.d3mode = 1;
+  }
+  if (pl.d3cfg >= 0) {
+    // K slices until the grid fills the CUs (one workgroup per CU at 256 x
+    // 192, two at 128 x 128), each slice at least 8 tiles of 32 columns
+    const uint32_t bm = pl.d3cfg == 3 ? 128 : 256, bn = pl.d3cfg == 1 ? 192 : 128;
+    const uint32_t slots = pl.d3cfg == 3 ? 512 : 256;
+    const uint32_t tiles3 = ((m + bm - 1) / bm) * ((t.rows + bn - 1) / bn);
+    const uint32_t kt32 = pl.kp / 32;
+    uint32_t sp = 1;
+    while (tiles3 * sp * 2 <= slots && kt32 / (sp * 2) >= 8) sp *= 2;
+    pl.kt_per_split = (kt32 + sp - 1) / sp;
+    pl.splits = (kt32 + pl.kt_per_split - 1) / pl.kt_per_split;
   }
   pl.panel_plane = al256((size_t)t.rows * pl.kp * 2);
   pl.dsc_bytes = pl.wmode == kWQBlock ? al256((size_t)t.rows * (pl.kp / 32) * 4) : 0;
@@ -881,7 +908,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
     (void)hipGetLastError();   // no algorithm for this shape: the own dense kernel on the same panel
   }
   if (pl.d3cfg >= 0) {
-    e = launch_dense3(pl.d3cfg, 0, ah, p.hi, p.lo, p.inv, m, t.rows, pl.kp, y, y_bf16, partial, pl.splits,
+    e = launch_dense3(pl.d3cfg, pl.d3mode, ah, p.hi, p.lo, p.dsc, p.inv, m, t.rows, pl.kp, y, y_bf16, partial, pl.splits,
                       pl.kt_per_split, xe, s);
   } else if (x_bf16 && pl.bm == 128) {
     // 128 x 128 tiles with bf16 (exact f16) activations: the interleaved
