@@ -109,6 +109,8 @@ def weight_bytes(m) -> int:
         return m.rows * m.padded_cols // 2 + m.rows * (m.padded_cols // 64) * 32
     if k == "q8":
         return m.rows * m.blocks_per_row * 34
+    if k == "q4_0":
+        return m.rows * m.blocks_per_row * 18
     return (m.rows * m.padded_cols // 2 + m.rows * (m.padded_cols // 128) * 2
             + (m.rows + 1) * 4 + m.outliers_packed.size * 4)
 
@@ -438,10 +440,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="f,0,r,g,2,3,4,s,a",
+    ap.add_argument("--configs", default="f,0,r,q,g,2,3,4,s,a",
                     help="secondary configurations to run (f: HBM streaming floor at the configs' sizes, "
                          "s: whole decode step on config 4's weights, a: KV-Q8 decode attention, "
-                         "c: config 3's cb4 lines on the pinned decode-in-loop tile kernel)")
+                         "c: config 3's cb4 lines on the pinned decode-in-loop tile kernel, q: Q4_0 GEMV at config 1's shape)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
                     help="time with plain launches instead of graph replays (for profilers: rocprofv3's kernel "
@@ -504,6 +506,18 @@ def main():
         log(f"  cb4-ref GEMV M=1 K=2048 N=6144: {rr['kernel_GBps']:.1f} GB/s kernel "
             f"({rr['kernel_ms']*1e3:.2f} us)")
         del mr
+    if "q" in run:
+        # config 1's shape in Q4_0 (4.5 bits per weight streamed from the
+        # resident nibble plane, q4_0.rs:109-147 / vxt_gemv.metal:461-520)
+        m4 = synth.make_q40(6144, 2048, seed=3)
+        r4 = bench_gemv(eng, m4, 1, "bf16", "f32", args.steps, args.warmup, seed=0)
+        secondary.append({"config": "Q4_0 gemv M=1 K=2048 N=6144 (4.5 bits per weight)",
+                          "GBps": round(r4["GBps"], 1), "kernel_us": round(r4["kernel_ms"] * 1e3, 3),
+                          "kernel_GBps": round(r4["kernel_GBps"], 1),
+                          "frac_hbm": round(r4["kernel_GBps"] / HBM_PEAK_GBS, 4)})
+        log(f"  Q4_0 GEMV M=1 K=2048 N=6144: {r4['kernel_GBps']:.1f} GB/s kernel "
+            f"({r4['kernel_ms']*1e3:.2f} us)")
+        del m4
     if "g" in run:
         # the headline kernel at larger shapes: how much of config 1's gap to
         # the HBM roofline is the fixed cost of a 12.6 MB launch

@@ -62,6 +62,7 @@ extern "C" {
 /* ---- tensor kinds (kind 2 = codebook, as VxtMetalOp.kind in
  *      native/metal_internal.h:14) ---------------------------------------- */
 #define VXT_KIND_CB4 2u     /* CodebookMatrix, bits = 4 (codebook.rs:9-24)   */
+#define VXT_KIND_Q4_0 4u    /* Q4_0Matrix blocks of 32 (q4_0.rs:7-14)        */
 #define VXT_KIND_Q8_0 8u    /* GGUF Q8_0 / KvQ8Block rows (llm_prefill.rs:17) */
 #define VXT_KIND_CB4_G64 9u /* cb4 with a per-64-group fp16 codebook         */
 
@@ -144,9 +145,11 @@ VXT_API void* vxt_hip_upload_q8_0(void* ctx, uint32_t rows, uint32_t cols, const
  * scales_f16[rows * padded_cols/32], qs_words[rows * padded_cols/32 * 4]
  * (byte j of a block: column j low nibble, column j + 16 high nibble).
  * Replaces upload_q4_0 (metal.rs:179-187); plane rules as format.rs:453-462.
- * The device holds the values (q - 8) widened to int8 next to the same f16
- * scales, so the tensor runs on the Q8_0 kernels (kind VXT_KIND_Q8_0 in
- * vxt_hip_tensor_info): dequant bit-exact with decode_row (q4_0.rs:77-97). */
+ * The device holds both planes as given (4.5 bits per weight, kind
+ * VXT_KIND_Q4_0 in vxt_hip_tensor_info): the GEMV streams the nibbles
+ * (the reference's vxt_gemv_q4_0, vxt_gemv.metal:461-520), prefill
+ * decodes them into the GEMM's weight panel; dequant bit-exact with
+ * decode_row (q4_0.rs:77-97). */
 VXT_API void* vxt_hip_upload_q4_0(void* ctx, uint32_t rows, uint32_t cols, uint32_t padded_cols,
                                   const uint16_t* scales_f16, size_t n_scales, const uint32_t* qs_words,
                                   size_t n_words, char* err, size_t err_cap);

@@ -1,7 +1,9 @@
 """GPU parity of Q4_0 weights (q4_0.rs) through the C ABI.
 
-The device keeps a Q4_0 matrix as (q - 8) widened to int8 next to its f16
-block scales and runs it on the Q8_0 kernels.  Bars as in test_gpu_parity:
+The device keeps a Q4_0 matrix in its own planes (16 nibble bytes and one f16
+scale per block of 32: 4.5 bits per weight) and streams the nibbles in the
+GEMV (vxt_gemv.metal:461-520); prefill decodes them into the GEMM's weight
+panel.  Bars as in test_gpu_parity:
 dequant bit-exact against decode_row (q4_0.rs:77-97); GEMV and GEMM within
 1e-3 of the oracle (gemv_cpu, q4_0.rs:109-145, and gemm_cpu over decode_row)
 relative to max(|y|, 2^-10 sum|wx|); bf16 outputs within 1 ulp.
@@ -42,7 +44,9 @@ def test_q40_dequant_bit_exact(eng, rows, cols):
     t = eng.upload_packed(m)
     got = eng.dequant_rows(t)
     assert_bits_equal(got, oracle.decode_rows(m))
-    assert (t.kind, t.rows, t.cols) == (engine.KIND_Q8_0, rows, cols)
+    assert (t.kind, t.rows, t.cols) == (engine.KIND_Q4_0, rows, cols)
+    kb = (cols + 31) // 32   # 18 bytes per block resident, each plane 256-byte aligned
+    assert t.device_bytes <= rows * kb * 18 + 512
     t.free()
 
 

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvxt_hip.so")
-SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip", "gemm_tile.hip", "gemm_dense.hip", "gemm_dense3.hip",
+SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_q40.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip", "gemm_tile.hip", "gemm_dense.hip", "gemm_dense3.hip",
            "gemm_blas.cpp", "dequant.hip", "greedy.hip", "probe.hip", "ffn.hip", "attn.hip", "archive.cpp"]
 
 # hipBLASLt runs the dense phase of large-batch prefill GEMMs (gemm_blas.cpp).

@@ -12,6 +12,11 @@
 //          CSR   row_ptr u32[rows+1], outliers u32[nnz] (col | f16 << 16)
 //   G64    idx   u8    [rows][kp/2]      low nibble = even column
 //          lut   f16   [rows][kp/64][16]
+//   Q4_0   qs    u8    [rows][kp/2]      kp = 32 * ceil(cols/32); block b of a
+//                                      row is bytes 16 b .. 16 b + 15, byte j
+//                                      holding column 32 b + j (low nibble) and
+//                                      32 b + j + 16 (high nibble), value q - 8
+//          d     f16   [rows][kp/32]
 //
 // Every plane starts 256-byte aligned inside one arena allocation per tensor.
 #pragma once
@@ -21,15 +26,15 @@
 
 namespace vxt {
 
-enum Kind : uint32_t { KIND_CB4 = 2u, KIND_Q8 = 8u, KIND_G64 = 9u };
+enum Kind : uint32_t { KIND_CB4 = 2u, KIND_Q40 = 4u, KIND_Q8 = 8u, KIND_G64 = 9u };
 
 struct DevTensor {
   uint32_t kind;
   uint32_t rows;
   uint32_t cols;
   uint32_t kp;          // padded cols of the resident layout
-  const void* p0;       // Q8: qs      CB4: words     G64: idx
-  const uint16_t* p1;   // Q8: d       CB4: scales    G64: lut
+  const void* p0;       // Q8: qs      CB4: words     G64: idx   Q4_0: nibbles
+  const uint16_t* p1;   // Q8: d       CB4: scales    G64: lut   Q4_0: d
   const uint32_t* row_ptr;   // CB4 only
   const uint32_t* outliers;  // CB4 only
   uint32_t split0, split1;   // CB4: first rows served by tables 1 and 2

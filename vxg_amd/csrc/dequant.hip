@@ -7,6 +7,7 @@
 //        the row's CSR residuals added in CSR order for col < cols
 //        (codebook.rs:285-337);
 //   Q8:  dst[c] = (float)q * f32(d)                (gguf.rs:223-229, exact);
+//   Q4_0: dst[c] = (float)(q - 8) * f32(d)         (q4_0.rs:89-93, exact);
 //   G64: dst[c] = f32(lut[q])                      (exact).
 // f16 scales and tables are widened with the integer rule of fp16.rs:6-29 so
 // NaN payloads match as well.
@@ -25,6 +26,10 @@ __global__ __launch_bounds__(256) void dequant_dense_kernel(DevTensor t, uint32_
   float v;
   if (t.kind == KIND_Q8) {
     const int8_t q = static_cast<const int8_t*>(t.p0)[row * t.kp + c];
+    v = (float)q * f16_to_f32_exact(t.p1[row * (t.kp / 32) + c / 32]);
+  } else if (t.kind == KIND_Q40) {   // q4_0.rs:89-93: ((nibble as i32) - 8) as f32 * d
+    const uint8_t b = static_cast<const uint8_t*>(t.p0)[row * (t.kp / 2) + (c / 32) * 16 + c % 16];
+    const int32_t q = (int32_t)((c % 32 < 16 ? b : b >> 4) & 0xfu) - 8;
     v = (float)q * f16_to_f32_exact(t.p1[row * (t.kp / 32) + c / 32]);
   } else if (t.kind == KIND_CB4) {
     const uint32_t w = static_cast<const uint32_t*>(t.p0)[row * (t.kp / 8) + c / 8];
@@ -76,6 +81,10 @@ __global__ __launch_bounds__(256) void embed_kernel(DevTensor t, const uint32_t*
   float v;
   if (t.kind == KIND_Q8) {
     const int8_t q = static_cast<const int8_t*>(t.p0)[row * t.kp + c];
+    v = (float)q * f16_to_f32_exact(t.p1[row * (t.kp / 32) + c / 32]);
+  } else if (t.kind == KIND_Q40) {   // q4_0.rs:89-93: ((nibble as i32) - 8) as f32 * d
+    const uint8_t b = static_cast<const uint8_t*>(t.p0)[row * (t.kp / 2) + (c / 32) * 16 + c % 16];
+    const int32_t q = (int32_t)((c % 32 < 16 ? b : b >> 4) & 0xfu) - 8;
     v = (float)q * f16_to_f32_exact(t.p1[row * (t.kp / 32) + c / 32]);
   } else if (t.kind == KIND_CB4) {
     const uint32_t w = static_cast<const uint32_t*>(t.p0)[row * (t.kp / 8) + c / 8];

@@ -338,16 +338,31 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
       }
       *reinterpret_cast<uint4*>(hi + c) = make_uint4(h[0], h[1], h[2], h[3]);
     }
-  } else if constexpr (KIND == KIND_Q8) {
+  } else if constexpr (KIND == KIND_Q8 || KIND == KIND_Q40) {
     // kp may be 32 short of KP: pieces past kp read the row's last 8 bytes
     // (their columns are >= K and come out zero).
-    const int8_t* qr = static_cast<const int8_t*>(t.p0) + (size_t)n * kp;
     const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
     uint2 q[4];
+    if constexpr (KIND == KIND_Q8) {
+      const int8_t* qr = static_cast<const int8_t*>(t.p0) + (size_t)n * kp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t c = c0 + 512 * i;
-      q[i] = *reinterpret_cast<const uint2*>(qr + (c < kp ? c : kp - 8));
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t c = c0 + 512 * i;
+        q[i] = *reinterpret_cast<const uint2*>(qr + (c < kp ? c : kp - 8));
+      }
+    } else {
+      // Q4_0: columns c .. c + 7 of a block are the low (c % 32 < 16) or high
+      // nibbles of bytes c % 16 .. + 7; each is widened to the int8 q - 8
+      // (q4_0.rs:89-93), so the rest is the Q8 decode.
+      const uint8_t* qr = static_cast<const uint8_t*>(t.p0) + (size_t)n * (kp / 2);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t c = c0 + 512 * i, cc = c < kp ? c : kp - 8;
+        const uint2 raw = *reinterpret_cast<const uint2*>(qr + (cc / 32) * 16 + cc % 16);
+        const uint32_t sh = (cc % 32) < 16 ? 0u : 4u;
+        q[i].x = ((((raw.x >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+        q[i].y = ((((raw.y >> sh) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+      }
     }
     float d[4] = {1.0f, 1.0f, 1.0f, 1.0f};
     if (qblock) {   // block scales as f32; blocks past the weights' own are zero
@@ -362,7 +377,7 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
       }
       float dm = 0.0f;
       for (uint32_t g = lane; g < kp / 32; g += 64) dm = fmaxf(dm, fabsf(f16_to_f32_exact(dp[g])));
-      s = row_scale(127.0f * wave_max(dm));
+      s = row_scale((KIND == KIND_Q8 ? 127.0f : 8.0f) * wave_max(dm));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -732,7 +747,8 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   pl.lib = lib;
   // The library multiplies plain f16 operands: Q8 then takes the hi/lo panel
   // (exact for q * d) instead of int8 values with block scales.
-  pl.wmode = t.kind == KIND_G64 ? kWPlain : (t.kind == KIND_Q8 && x_bf16 && !lib ? kWQBlock : kWHiLo);
+  pl.wmode = t.kind == KIND_G64 ? kWPlain
+                                : ((t.kind == KIND_Q8 || t.kind == KIND_Q40) && x_bf16 && !lib ? kWQBlock : kWHiLo);
   pl.kp = (t.cols + BK - 1) / BK * BK;
   const uint32_t ktiles = pl.kp / BK;
   pl.bm = m >= 256 ? 128 : 64;
@@ -917,7 +933,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
                       pl.kt_per_split, xe, s);
   } else if constexpr (KIND == KIND_G64) {
     e = launch_dense_m<kWPlain>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
-  } else if constexpr (KIND == KIND_Q8) {
+  } else if constexpr (KIND == KIND_Q8 || KIND == KIND_Q40) {
     if (pl.wmode == kWQBlock)
       e = launch_dense_m<kWQBlock>(p, ah, al, x_bf16, m, t.rows, y, y_bf16, pl, partial, xe, s);
     else
@@ -1059,6 +1075,7 @@ hipError_t launch_gemm(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
   switch (t.kind) {
     case KIND_G64: return gp::run<KIND_G64>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
     case KIND_Q8: return gp::run<KIND_Q8>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
+    case KIND_Q40: return gp::run<KIND_Q40>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
     case KIND_CB4: return gp::run<KIND_CB4>(t, x, x_bf16, m, y, y_bf16, rest, rest_bytes, xe, s, lib);
     default: return hipErrorInvalidValue;
   }

@@ -52,6 +52,11 @@ struct WChunk<KIND_CB4> {
   uint32_t sc;    // f16 scale bits
 };
 template <>
+struct WChunk<KIND_Q40> {
+  uint4 q;        // one block: byte j = column j (low nibble) | column j + 16 (high nibble)
+  uint32_t d;     // f16 scale bits
+};
+template <>
 struct WChunk<KIND_G64> {
   uint4 q;        // 32 nibbles
   uint4 lut;      // this lane's half of the group's 16-entry f16 table
@@ -69,6 +74,9 @@ __device__ __forceinline__ void load_chunk(const DevTensor& t, uint32_t row, uin
   } else if constexpr (KIND == KIND_CB4) {
     c.q = load_nt16(static_cast<const uint32_t*>(t.p0) + (size_t)row * (t.kp / 8) + k0 / 8);
     c.sc = t.p1[(size_t)row * (t.kp / 128) + k0 / 128];
+  } else if constexpr (KIND == KIND_Q40) {   // k0 is a block start (lanes take 32 columns)
+    c.q = load_nt16(static_cast<const uint8_t*>(t.p0) + (size_t)row * (t.kp / 2) + k0 / 2);
+    c.d = t.p1[(size_t)row * (t.kp / 32) + k0 / 32];
   } else {
     c.q = load_nt16(static_cast<const uint8_t*>(t.p0) + (size_t)row * (t.kp / 2) + k0 / 2);
     c.lut = load_nt16(t.p1 + ((size_t)row * (t.kp / 64) + g) * 16 + half * 8);
@@ -177,6 +185,21 @@ __device__ __forceinline__ void dequant_chunk(const WChunk<KIND>& c, uint32_t cb
     const uint32_t qa[8] = {c.a.x, c.a.y, c.a.z, c.a.w, c.b.x, c.b.y, c.b.z, c.b.w};
 #pragma unroll
     for (int j = 0; j < kChunk; ++j) w[j] = (float)(int8_t)((qa[j >> 2] >> ((j & 3) * 8)) & 0xffu);
+  } else if constexpr (KIND == KIND_Q40) {
+    // q - 8 of four nibbles at once as signed bytes: (n | 0x80) - 8 stays in
+    // its byte (no borrow), and ^ 0x80 turns 0x80 + (n - 8) into n - 8; the
+    // byte then converts with one sign-extending SDWA conversion.
+    const uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t lo = (((wd[i] & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+      const uint32_t hi = ((((wd[i] >> 4) & 0x0F0F0F0Fu) | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        w[4 * i + k] = (float)(int8_t)((lo >> (8 * k)) & 0xffu);        // column 4 i + k
+        w[16 + 4 * i + k] = (float)(int8_t)((hi >> (8 * k)) & 0xffu);   // column 16 + 4 i + k
+      }
+    }
   } else if constexpr (KIND == KIND_CB4) {
     const uint32_t wd[4] = {c.q.x, c.q.y, c.q.z, c.q.w};
     const uint32_t base = cbase;   // 64-byte aligned table for this row
@@ -498,7 +521,7 @@ __global__ __launch_bounds__(kWaves * 64) void gemv_kernel(DevTensor t, const vo
             p1 = __builtin_fmaf(w[j + 1], xm[j + 1], p1);
           }
           float p = p0 + p1;
-          if constexpr (KIND == KIND_Q8) {
+          if constexpr (KIND == KIND_Q8 || KIND == KIND_Q40) {
             p *= f16_to_f32(wc[s][r].d);
           } else if constexpr (KIND == KIND_CB4) {
             // codebook.rs:384-386: a zero scale skips the group.
@@ -873,10 +896,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_lds_kernel(DevTensor t, co
 // reading piece i touch 16 different 16-byte bank groups.  Products and the
 // order of the sums are those of the generic kernel (two fp32 chains per
 // lane, the block scale on their sum, steps in order, the wave sum).
-template <int RPW, int WAVES, int NS, bool XBF16 = false>
+// The same kernel serves Q4_0 weights (KB = KIND_Q40): 16 bytes of nibbles
+// and one scale per lane and block instead of 32 int8 values.
+template <int RPW, int WAVES, int NS, bool XBF16 = false, uint32_t KB = KIND_Q8>
 __global__ __launch_bounds__(WAVES * 64) void gemv_q8_m1_kernel(DevTensor t, const void* __restrict__ x,
                                                                  void* __restrict__ y, uint32_t y_bf16) {
   static_assert(NS >= 1 && NS <= 3, "K steps staged in LDS");
+  static_assert(KB == KIND_Q8 || KB == KIND_Q40, "block kinds");
   __shared__ __attribute__((aligned(16))) float s_x[NS * kStep];
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -897,13 +923,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_m1_kernel(DevTensor t, con
     const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);   // repeats write the same value
     xv[j] = __builtin_amdgcn_raw_buffer_load_b128(xr, p * 16u, 0, 0);
   }
-  WChunk<KIND_Q8> wc[NS][RPW];
+  WChunk<KB> wc[NS][RPW];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const uint32_t k0 = s * kStep + lane * kChunk;
     const uint32_t k0c = k0 < kp ? k0 : kp - kChunk;
 #pragma unroll
-    for (int r = 0; r < RPW; ++r) load_chunk<KIND_Q8>(t, std::min(row0 + r, rows - 1), k0c, 0, 0, wc[s][r]);
+    for (int r = 0; r < RPW; ++r) load_chunk<KB>(t, std::min(row0 + r, rows - 1), k0c, 0, 0, wc[s][r]);
   }
   // Nothing that uses a loaded value may be scheduled above the last load:
   // a conversion hoisted there makes the wave wait for the loads before it.
@@ -945,7 +971,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_m1_kernel(DevTensor t, con
 #pragma unroll
     for (int r = 0; r < RPW; ++r) {
       float w[kChunk];
-      dequant_chunk<KIND_Q8>(wc[s][r], 0, 0, lane, w);
+      dequant_chunk<KB>(wc[s][r], 0, 0, lane, w);
       float p0 = 0.0f, p1 = 0.0f;
 #pragma unroll
       for (int j = 0; j < kChunk; j += 2) {
@@ -1671,13 +1697,13 @@ hipError_t launch_cb4_m1_e(const DevTensor& t, const void* x, uint32_t outs, voi
 
 // Q8 x f32 activations, one token, staged through LDS (gemv_q8_m1_kernel).
 // Requires 16-byte aligned activations, cols % 4 == 0 and NS K steps.
-template <int RPW, int WAVES, int NS, bool XBF16 = false>
+template <int RPW, int WAVES, int NS, bool XBF16 = false, uint32_t KB = KIND_Q8>
 hipError_t launch_q8_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
   if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % (XBF16 ? 8 : 4) != 0 ||
       (t.kp + kStep - 1) / kStep != (uint32_t)NS)
     return hipErrorInvalidValue;
   const uint32_t per_block = WAVES * RPW;
-  hipLaunchKernelGGL((gemv_q8_m1_kernel<RPW, WAVES, NS, XBF16>), dim3((t.rows + per_block - 1) / per_block),
+  hipLaunchKernelGGL((gemv_q8_m1_kernel<RPW, WAVES, NS, XBF16, KB>), dim3((t.rows + per_block - 1) / per_block),
                      dim3(WAVES * 64), 0, s, t, x, y, (uint32_t)(y_bf16 ? 1u : 0u));
   return hipGetLastError();
 }
@@ -1848,17 +1874,17 @@ hipError_t launch_cb4_m1(const DevTensor& t, const void* x, void* y, bool y_bf16
 
 // One token of Q8 weights through the LDS-staged kernel: one row per wave and
 // eight waves per workgroup, four and four at >= 65536 rows (the LM head).
-template <bool XBF16>
+template <bool XBF16, uint32_t KB = KIND_Q8>
 hipError_t launch_q8_x1(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
   const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
   if (t.rows >= 65536) {
-    if (nsteps == 1) return launch_q8_m1_t<4, 4, 1, XBF16>(t, x, y, y_bf16, s);
-    if (nsteps == 2) return launch_q8_m1_t<4, 4, 2, XBF16>(t, x, y, y_bf16, s);
-    return launch_q8_m1_t<4, 4, 3, XBF16>(t, x, y, y_bf16, s);
+    if (nsteps == 1) return launch_q8_m1_t<4, 4, 1, XBF16, KB>(t, x, y, y_bf16, s);
+    if (nsteps == 2) return launch_q8_m1_t<4, 4, 2, XBF16, KB>(t, x, y, y_bf16, s);
+    return launch_q8_m1_t<4, 4, 3, XBF16, KB>(t, x, y, y_bf16, s);
   }
-  if (nsteps == 1) return launch_q8_m1_t<1, 8, 1, XBF16>(t, x, y, y_bf16, s);
-  if (nsteps == 2) return launch_q8_m1_t<1, 8, 2, XBF16>(t, x, y, y_bf16, s);
-  return launch_q8_m1_t<1, 8, 3, XBF16>(t, x, y, y_bf16, s);
+  if (nsteps == 1) return launch_q8_m1_t<1, 8, 1, XBF16, KB>(t, x, y, y_bf16, s);
+  if (nsteps == 2) return launch_q8_m1_t<1, 8, 2, XBF16, KB>(t, x, y, y_bf16, s);
+  return launch_q8_m1_t<1, 8, 3, XBF16, KB>(t, x, y, y_bf16, s);
 }
 
 // Rows per wave: more rows per wave (more bytes in flight per wave) once rows
@@ -1904,6 +1930,14 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
     const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
     if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
       return x_bf16 ? launch_q8_x1<true>(t, x, y, y_bf16, s) : launch_q8_x1<false>(t, x, y, y_bf16, s);
+  }
+  if constexpr (KIND == KIND_Q40) {
+    // One token: the LDS-staged block kernel with the nibble decode; the
+    // generic kernel takes the rest (4.5 bits per weight streamed either way).
+    const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
+    if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
+      return x_bf16 ? launch_q8_x1<true, KIND_Q40>(t, x, y, y_bf16, s)
+                    : launch_q8_x1<false, KIND_Q40>(t, x, y, y_bf16, s);
   }
   if constexpr (KIND == KIND_CB4) {
     // One token: the LDS-staged kernel (gemv_cb4_m1_kernel).  Measured against

@@ -477,25 +477,16 @@ void* vxt_hip_upload_q4_0(void* ctx, uint32_t rows, uint32_t cols, uint32_t padd
     if ((size_t)padded_cols != kb * 32u) fail(VXT_E_FORMAT, "invalid VXT Q4_0 padded_cols");
     if (n_scales != (size_t)rows * kb || n_words != (size_t)rows * kb * 4u)
       fail(VXT_E_FORMAT, "corrupt VXT Q4_0 plane lengths");
-    // The Q8_0 device layout with q - 8 in the int8 plane: (q - 8) * d is the
-    // same single f32 product decode_row forms (q4_0.rs:89-93).
+    // The planes as they are (the little-endian words are the block bytes in
+    // order): 16 nibble bytes per block, row after row, then the f16 scales.
     const uint32_t kp = (uint32_t)(kb * 32u);
-    const size_t qs_bytes = align256((size_t)rows * kp);
+    const size_t qs_bytes = align256((size_t)rows * kb * 16u);
     const size_t d_bytes = align256((size_t)rows * kb * 2u);
     std::vector<char> h(qs_bytes + d_bytes, 0);
-    int8_t* qs = reinterpret_cast<int8_t*>(h.data());
-    uint16_t* d = reinterpret_cast<uint16_t*>(h.data() + qs_bytes);
-    for (size_t blk = 0; blk < (size_t)rows * kb; ++blk) {
-      d[blk] = scales_f16[blk];
-      int8_t* dst = qs + blk * 32u;   // rows are kp = kb * 32 long: block blk starts at blk * 32
-      for (uint32_t j = 0; j < 16; ++j) {
-        const uint32_t byte = (qs_words[blk * 4u + j / 4u] >> (8u * (j % 4u))) & 0xffu;
-        dst[j] = (int8_t)((int32_t)(byte & 0x0fu) - 8);
-        dst[j + 16] = (int8_t)((int32_t)(byte >> 4) - 8);
-      }
-    }
+    std::memcpy(h.data(), qs_words, (size_t)rows * kb * 16u);
+    std::memcpy(h.data() + qs_bytes, scales_f16, (size_t)rows * kb * 2u);
     use_device(c);
-    Tensor* t = new_tensor(c, VXT_KIND_Q8_0, rows, cols, kp, h);
+    Tensor* t = new_tensor(c, VXT_KIND_Q4_0, rows, cols, kp, h);
     t->off_p0 = 0;
     t->off_p1 = qs_bytes;
     register_tensor(c, t);

@@ -49,7 +49,7 @@ DTYPE_F32, DTYPE_BF16 = 0, 1
 ACT_SILU, ACT_GELU_TANH = 0, 1
 NORM_PLAIN, NORM_GLU_SILU, NORM_GLU_GELU_TANH = 0, 1, 2
 GEMM_AUTO, GEMM_PANEL, GEMM_FUSED, GEMM_LIBRARY = 0, 1, 2, 3
-KIND_CB4, KIND_Q8_0, KIND_CB4_G64 = 2, 8, 9
+KIND_CB4, KIND_Q4_0, KIND_Q8_0, KIND_CB4_G64 = 2, 4, 8, 9
 
 ABI_SYMBOLS = (
     "vxt_hip_create", "vxt_hip_destroy", "vxt_hip_upload_cb4", "vxt_hip_upload_cb4_concat",

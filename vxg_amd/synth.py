@@ -13,13 +13,15 @@ as the benchmark configurations specify, with numpy's PCG64 generator:
   fp16 scales uniform in [0.002, 0.02], and ~0.74 % CSR outliers at ascending
   columns with f16(N(0, 0.02)) residuals (the reference encoder's outlier
   fraction, ``cb4_opt.rs:132``'s 0.0074 target).
+* Q4_0 (the secondary line at config 1's shape): nibbles uniform in 0..15
+  (values q - 8), one fp16 scale per block of 32 uniform in [0.002, 0.02].
 * Activations: f32 or bf16 N(0, 1).
 """
 from __future__ import annotations
 
 import numpy as np
 
-from .formats import (Cb4G64Matrix, CodebookMatrix, Q8Matrix, f32_to_bf16_bits,
+from .formats import (Cb4G64Matrix, CodebookMatrix, Q4_0Matrix, Q8Matrix, f32_to_bf16_bits,
                       f32_to_f16_bits, q8_from_planes)
 
 
@@ -35,6 +37,20 @@ def make_q8(rows: int, cols: int, seed: int = 0) -> Q8Matrix:
         qs[:, cols:] = 0
     d = f32_to_f16_bits(g.uniform(0.002, 0.02, size=rows * kb).astype(np.float32))
     return q8_from_planes(rows, cols, qs, d)
+
+
+def make_q40(rows: int, cols: int, seed: int = 3) -> Q4_0Matrix:
+    g = rng(seed)
+    kb = (cols + 31) // 32
+    words = g.integers(0, 2**32, size=rows * kb * 4, dtype=np.uint64).astype(np.uint32)
+    if kb * 32 != cols:
+        # padding columns carry q = 8 (value 0); x is zero there in every consumer
+        b = words.view(np.uint8).reshape(rows, kb * 16)
+        for c in range(cols, kb * 32):
+            j = (kb - 1) * 16 + (c % 32) % 16
+            b[:, j] = (b[:, j] & np.uint8(0xF0)) | np.uint8(8) if c % 32 < 16 else (b[:, j] & np.uint8(0x0F)) | np.uint8(0x80)
+    d = f32_to_f16_bits(g.uniform(0.002, 0.02, size=rows * kb).astype(np.float32))
+    return Q4_0Matrix(rows, cols, kb * 32, d, words)
 
 
 def make_g64(rows: int, cols: int, seed: int = 1) -> Cb4G64Matrix:
