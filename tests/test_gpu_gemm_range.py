@@ -114,3 +114,74 @@ def test_gemm_nonfinite_activation_row_propagates(eng):
     yref = oracle.gemm(m, Xq[keep], threads=THREADS)
     check(y[keep], yref, oracle.decode_rows(m), Xq[keep], False)
     t.free()
+
+
+def _inf_rows(M, cols, seed):
+    """Activations whose rows 3 and 7 each hold one Inf next to finite entries
+    far above the f16 range (1e10): the row's scale must come from its finite
+    entries so they stay finite, and the Inf must reach every product."""
+    X = synth.make_x_f32(M, cols, seed=seed)
+    X[3] *= np.float32(1e10)
+    X[3, 17] = np.inf
+    X[7] *= np.float32(-3e9)
+    X[7, cols - 5] = -np.inf
+    return X
+
+
+@pytest.mark.parametrize("kind,rows,M,path", [
+    ("g64", 192, 128, engine.GEMM_AUTO), ("g64", 192, 300, engine.GEMM_AUTO), ("g64", 192, 300, engine.GEMM_PANEL),
+    ("g64", 192, 128, engine.GEMM_FUSED), ("g64", 6144, 2048, engine.GEMM_PANEL),
+    ("q8", 192, 128, engine.GEMM_AUTO), ("q8", 192, 300, engine.GEMM_PANEL), ("q8", 2048, 2048, engine.GEMM_AUTO),
+    ("cb4", 192, 300, engine.GEMM_PANEL), ("cb4", 192, 2048, engine.GEMM_AUTO), ("cb4", 4096, 2048, engine.GEMM_AUTO)])
+def test_gemm_inf_with_large_finite_entries(eng, kind, rows, M, path):
+    """Rows holding an Inf and finite entries above 65504 give exactly the
+    oracle's pattern of +-Inf and NaN outputs (gemm_cpu: w * Inf is +-Inf, or
+    NaN where w = 0), and finite rows keep the bar.  The g64 tile path (M =
+    128..2047), the fused/tile pin, the dense kernels of the two-phase path
+    (plain, Q8 block and hi/lo, on both the 128 x 128 and the large-tile
+    kernel) are covered."""
+    cols = 544
+    m = make(kind, rows, cols, seed=21)
+    t = eng.upload_packed(m)
+    X = _inf_rows(M, cols, seed=22)
+    xb = f32_to_bf16_bits(X)
+    Xq = bf16_bits_to_f32(xb).reshape(M, cols)
+    sel = np.r_[0:9, M - 3:M]
+    with np.errstate(invalid="ignore", over="ignore"):
+        yref = oracle.gemm(m, Xq[sel], threads=THREADS)
+    eng.set_gemm_path(path)
+    try:
+        y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)[sel]
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
+    assert np.array_equal(np.isnan(y), np.isnan(yref))
+    assert np.array_equal(np.isinf(y), np.isinf(yref))
+    both = np.isinf(y) & np.isinf(yref)
+    assert np.array_equal(np.sign(y[both]), np.sign(yref[both]))
+    fin = np.all(np.isfinite(yref), axis=1)
+    assert fin.sum() == len(sel) - 2
+    check(y[fin], yref[fin], oracle.decode_rows(m), Xq[sel][fin], False)
+    t.free()
+
+
+def test_gemm_inf_rows_cb4_tile_path(eng):
+    """The cb4 decode-in-loop tile kernel multiplies a residual operand that
+    is zero off the residual columns, so an Inf activation gives NaN (not
+    +-Inf) across its row; that row is non-finite as in gemm_cpu, the others
+    keep the bar."""
+    rows, cols = 192, 544
+    m = make("cb4", rows, cols, seed=23)
+    t = eng.upload_packed(m)
+    M = 256
+    X = _inf_rows(M, cols, seed=24)
+    xb = f32_to_bf16_bits(X)
+    Xq = bf16_bits_to_f32(xb).reshape(M, cols)
+    eng.set_gemm_path(engine.GEMM_FUSED)
+    try:
+        y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
+    assert not np.isfinite(y[3]).any() and not np.isfinite(y[7]).any()
+    keep = np.r_[0:3, 4:7, 8:12]
+    check(y[keep], oracle.gemm(m, Xq[keep], threads=THREADS), oracle.decode_rows(m), Xq[keep], False)
+    t.free()

@@ -12,7 +12,7 @@ import pytest
 
 import oracle
 from vxg_amd import engine, synth
-from vxg_amd.formats import Cb4G64Matrix, bf16_bits_to_f32, f32_to_bf16_bits
+from vxg_amd.formats import Cb4G64Matrix, bf16_bits_to_f32, f32_to_bf16_bits, f32_to_f16_bits
 from parity_util import THREADS, assert_bf16_close, floor_scale, make, max_rel, run_dev
 
 pytestmark = pytest.mark.gpu
@@ -108,7 +108,7 @@ def test_dense_kernel_q8_block_scales_extreme(eng):
 
 # ---- the cb4 decode-in-loop tile kernel (GEMM_FUSED pins it for eligible
 # tensors: finite planes, each row's residual columns increasing, at most
-# 4096 residuals per 128-row block) -------------------------------------------
+# 16384 residuals per 128-row block) ------------------------------------------
 
 def check_parts(eng, parts, M, path, seed=0):
     """check() for a row-concatenated tensor of cb4 parts."""
@@ -203,3 +203,40 @@ def test_cb4_tile_kernel_on_auto_path(eng, M):
     c = check(eng, m, M, engine.GEMM_AUTO, seed=2)
     d = check(eng, m, M, engine.GEMM_PANEL, seed=2)
     assert np.array_equal(c.view(np.uint32), d.view(np.uint32))
+
+
+def _block_of_residuals(total, seed):
+    """128 x 6144 cb4 whose one 128-row block holds `total` residuals:
+    128 per row at increasing columns, the remainder on row 0."""
+    m = synth.make_cb4(128, 6144, seed=seed, outlier_frac=0.0)
+    g = np.random.default_rng(seed)
+    per = np.full(128, total // 128, np.int64)
+    per[0] += total - per.sum()
+    ents = []
+    for r in range(128):
+        cols = np.sort(g.choice(6144, size=int(per[r]), replace=False)).astype(np.uint32)
+        vals = f32_to_f16_bits(g.normal(0, 0.02, size=cols.size).astype(np.float32)).astype(np.uint32)
+        ents.append(cols | (vals << np.uint32(16)))
+    m.outliers_packed = np.concatenate(ents).astype(np.uint32)
+    m.outlier_row_ptr = np.r_[0, np.cumsum(per)].astype(np.uint32)
+    return m
+
+
+def test_cb4_tile_kernel_residual_cap(eng):
+    """Eligibility at the LDS cap: a block of exactly 16384 residuals takes
+    the tile kernel (on the automatic route at batch 200 its results are the
+    pinned kernel's bits, which differ from the two-phase path's summation),
+    one more residual makes the tensor take the two-phase path (automatic =
+    pinned panel bits).  Both at the bar."""
+    at_cap = _block_of_residuals(16384, seed=41)
+    over = _block_of_residuals(16385, seed=41)
+    a = check(eng, at_cap, 200, engine.GEMM_AUTO, seed=5)
+    b = check(eng, at_cap, 200, engine.GEMM_FUSED, seed=5)
+    p = check(eng, at_cap, 200, engine.GEMM_PANEL, seed=5)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert not np.array_equal(b.view(np.uint32), p.view(np.uint32))
+    c = check(eng, over, 200, engine.GEMM_AUTO, seed=5)
+    d = check(eng, over, 200, engine.GEMM_PANEL, seed=5)
+    e = check(eng, over, 200, engine.GEMM_FUSED, seed=5)   # pinned: falls back to the two-phase path too
+    assert np.array_equal(c.view(np.uint32), d.view(np.uint32))
+    assert np.array_equal(e.view(np.uint32), d.view(np.uint32))

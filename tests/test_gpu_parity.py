@@ -574,9 +574,12 @@ def test_cb4_zero_scale_group_with_nonfinite_x(eng, M):
 @pytest.mark.parametrize("rows,cols", [(7, 4100), (300, 6144), (65, 9000)])
 @pytest.mark.parametrize("xdt", ["bf16", "f32"])
 def test_gemv_split_k_shapes(eng, kind, rows, cols, xdt):
-    """M = 1 with K of two or more 2048-column steps and at most 4096 rows
-    takes the split-K kernel (the K steps of a row on separate waves, summed
-    in wave order): ragged K, a few rows, cb4 residuals anywhere in the row."""
+    """M = 1 with K of two or more 2048-column steps: 4100 and 9000 columns
+    (x rows not 16-byte multiples, and more than three steps) take the
+    split-K kernel where the kind allows it (the K steps of a row on separate
+    waves, summed in wave order); 6144 columns with aligned rows take the
+    one-token LDS-staged kernels (three K steps).  Ragged K, a few rows, cb4
+    residuals anywhere in the row."""
     m = make(kind, rows, cols, seed=rows + cols)
     t = eng.upload_packed(m)
     if xdt == "bf16":
@@ -591,3 +594,83 @@ def test_gemv_split_k_shapes(eng, kind, rows, cols, xdt):
     y2 = run_dev(eng, t, xh if xdt == "bf16" else X, engine.DTYPE_BF16 if xdt == "bf16" else engine.DTYPE_F32, 1,
                  engine.DTYPE_F32)
     assert_bits_equal(y2, y)   # deterministic: the waves' sums are added in a fixed order
+
+
+def _shuffled_duplicate_outliers(m, seed, every=3, extra=2):
+    """Rows r % every == 0 get their CSR entries shuffled plus `extra` more
+    residuals on columns they already hold (decode_row adds each in CSR
+    order, codebook.rs:316-333; the GEMV adds each f16(res) * x[col])."""
+    g = np.random.default_rng(seed)
+    rp, pk = m.outlier_row_ptr, m.outliers_packed
+    rows = []
+    for r in range(m.rows):
+        e = pk[rp[r]:rp[r + 1]].copy()
+        if r % every == 0 and e.size:
+            g.shuffle(e)
+            add = (e[:extra] & np.uint32(0xFFFF)) | (np.uint32(f16b(0.0625)) << np.uint32(16))
+            e = np.concatenate([e, add])
+        rows.append(e)
+    m.outliers_packed = np.concatenate(rows).astype(np.uint32)
+    m.outlier_row_ptr = np.r_[0, np.cumsum([len(e) for e in rows])].astype(np.uint32)
+    return m
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8])
+@pytest.mark.parametrize("xdt", ["bf16", "f32"])
+def test_gemv_cb4_unsorted_and_duplicate_outliers(eng, M, xdt):
+    """The decode GEMV at every batch size on CSR rows in any order with
+    repeated columns (llm_gpu_cpu_parity.rs:678-690's case at scale): the
+    one-token LDS-staged kernel (aligned rows, 2304 columns) and the generic
+    kernels add every entry, in any order, at the GEMV bar."""
+    m = _shuffled_duplicate_outliers(synth.make_cb4(130, 2304, seed=31, outlier_frac=0.03), seed=31)
+    t = eng.upload_packed(m)
+    if xdt == "bf16":
+        xh = synth.make_x_bf16(M, m.cols, seed=M)
+        X = bf16_bits_to_f32(xh).reshape(M, m.cols)
+        xd = engine.DTYPE_BF16
+    else:
+        X = synth.make_x_f32(M, m.cols, seed=M)
+        xh, xd = X, engine.DTYPE_F32
+    W = oracle.decode_rows(m)
+    y = run_dev(eng, t, xh, xd, M, engine.DTYPE_F32)
+    assert max_rel(y, gemv_ref(m, X), floor_scale(W, X)) <= 1e-3
+    t.free()
+
+
+@pytest.mark.parametrize("rows", [1, 5, 17])
+@pytest.mark.parametrize("cols", [129, 513])
+@pytest.mark.parametrize("M", [1, 2, 8])
+def test_gemv_duplicate_column_fixture(eng, rows, cols, M):
+    """The duplicate-column fixture of llm_gpu_cpu_parity.rs:680-688 (two
+    residuals on column 0, one on the last column, every row) through the
+    GEMV, against the oracle's gemv_cpu."""
+    m = closed_form(rows, cols, lambda c: [f16b(0.25) << 16, f16b(-0.125) << 16,
+                                           (f16b(0.5) << 16) | (c - 1)])
+    t = eng.upload_packed(m)
+    X = synth.make_x_f32(M, cols, seed=cols)
+    y = run_dev(eng, t, X, engine.DTYPE_F32, M, engine.DTYPE_F32)
+    assert max_rel(y, gemv_ref(m, X), floor_scale(oracle.decode_rows(m), X)) <= 1e-3
+    t.free()
+
+
+@pytest.mark.parametrize("M", [1, 2, 8])
+def test_gemv_cb4_sink_row(eng, M):
+    """A "sink" row holding thousands of residuals (the reference's encoder
+    puts most of a tensor's outliers on a few rows, reports/cb4-v2-2026-11-08.md)
+    next to ordinary rows: every lane walks many entries of that row."""
+    m = synth.make_cb4(300, 6144, seed=33)
+    g = np.random.default_rng(33)
+    sink = np.sort(g.choice(6144, size=5000, replace=False)).astype(np.uint32)
+    vals = f32_to_f16_bits(g.normal(0, 0.02, size=5000).astype(np.float32)).astype(np.uint32)
+    rp, pk = m.outlier_row_ptr, m.outliers_packed
+    r = 123
+    m.outliers_packed = np.concatenate([pk[:rp[r]], sink | (vals << np.uint32(16)), pk[rp[r + 1]:]]).astype(np.uint32)
+    cnt = np.diff(rp.astype(np.int64))
+    cnt[r] = 5000
+    m.outlier_row_ptr = np.r_[0, np.cumsum(cnt)].astype(np.uint32)
+    t = eng.upload_packed(m)
+    xh = synth.make_x_bf16(M, 6144, seed=M + 3)
+    X = bf16_bits_to_f32(xh).reshape(M, 6144)
+    y = run_dev(eng, t, xh, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+    assert max_rel(y, gemv_ref(m, X), floor_scale(oracle.decode_rows(m), X)) <= 1e-3
+    t.free()

@@ -112,6 +112,14 @@ __device__ __forceinline__ uint32_t bf16x2_pack(float lo, float hi) {
 }
 __device__ __forceinline__ uint16_t f32_to_bf16(float v) { return (uint16_t)bf16x2_pack(v, 0.0f); }
 
+// A hi/lo pair of GEMM accumulators, acc + accl * 2^-11.  An Inf activation
+// x puts hi * x = +-Inf in acc -- the sign of w * x, as hi carries w's sign
+// -- and lo * x in accl, which is NaN where lo = 0 and may be an Inf of the
+// other sign; gemm_cpu gives acc's Inf, so an infinite acc is the result.
+__device__ __forceinline__ float hilo_combine(float acc, float accl) {
+  return __builtin_isinf(acc) ? acc : __builtin_fmaf(accl, 1.0f / 2048.0f, acc);
+}
+
 // Inputs of a GEMV whose activations are an RMSNorm of the residual stream
 // (batch 1): x = bf16(rms_norm(cur [+ delta]) * w).
 struct NormIn {

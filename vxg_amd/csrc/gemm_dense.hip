@@ -316,7 +316,7 @@ __global__ __launch_bounds__(NT, occupancy<MODE>()) void dense2_kernel(const uin
   auto row_of = [&](int ii, int r) { return (uint32_t)(wm * 64 + ii * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
   auto value = [&](int ii, int j, int r) {
     float v = acc[ii][j][r];
-    if constexpr (LO) v = __builtin_fmaf(accl[ii][j][r], kLoInv, v);
+    if constexpr (LO) v = hilo_combine(v, accl[ii][j][r]);
     return v;
   };
   if (rows_fast) {

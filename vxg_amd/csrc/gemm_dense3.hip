@@ -65,7 +65,6 @@ namespace vxt {
 namespace g3 {
 
 constexpr int BK = 32, NT = 256;
-constexpr float kLoInv = 1.0f / 2048.0f;
 enum : int { kPlain = 0, kHiLo = 1, kQBlock = 2 };
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -389,7 +388,7 @@ __global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uin
   const bool to_partial = gridDim.y > 1;
   auto value = [&](int i, int j, int r) {
     float v = acc[i][j][r];
-    if constexpr (LO) v = __builtin_fmaf(accl[i][j][r], kLoInv, v);
+    if constexpr (LO) v = hilo_combine(v, accl[i][j][r]);
     return v;
   };
   auto row_of = [&](int i, int r) { return (uint32_t)(wm * 32 * WM + i * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };

@@ -64,6 +64,12 @@ constexpr int BK = 64;
 constexpr int LDK = BK + 8;   // padded LDS row (halves): conflict-light fragment reads
 constexpr int THREADS = 256;
 constexpr float kLoScale = 2048.0f;
+
+// The lo half (v - hi) * 2^11 of a hi/lo split; 0 for Inf / NaN v, whose hi
+// half carries it whole (Inf - Inf would turn an Inf product into NaN).
+__device__ __forceinline__ float lo_part(float v, float hi) {
+  return fabsf(v) <= 3.4028234663852886e38f ? (v - hi) * kLoScale : 0.0f;
+}
 constexpr float kLoInv = 1.0f / 2048.0f;
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -101,15 +107,16 @@ __device__ __forceinline__ void split_write(float w, float s, uint16_t* hi, uint
   const float ws = w * s;                              // exact: s is a power of two
   const _Float16 h = (_Float16)ws;
   hi[i] = __builtin_bit_cast(uint16_t, h);
-  lo[i] = __builtin_bit_cast(uint16_t, (_Float16)((ws - (float)h) * kLoScale));
+  lo[i] = __builtin_bit_cast(uint16_t, (_Float16)lo_part(ws, (float)h));
 }
 
 // ---- phase 1: activations and panel -----------------------------------------
 
 // Activation conversion, run by the first `blocks` workgroups of the panel
 // launch, one activation row per workgroup at a time: the row's largest
-// magnitude first (its exponent xe[m] puts it in [2^14, 2^15): 0 for a row
-// that is all zero or holds Inf / NaN), then X[m] * 2^xe[m] -> A [M][kp] f16,
+// finite magnitude first (its exponent xe[m] puts it in [2^14, 2^15): 0 for
+// a row with none; Inf / NaN entries pass as they are), then X[m] * 2^xe[m]
+// -> A [M][kp] f16,
 // zero for k >= K; f32 X also gets the lo plane (x - hi) * 2^11.  One thread
 // per 8 columns.
 struct XConv {
@@ -154,15 +161,18 @@ __device__ __forceinline__ void load8(const void* __restrict__ x, uint32_t K, ui
   }
 }
 
-// Exponent that puts `b` (a row's largest magnitude; Inf for non-finite
-// rows) in [2^14, 2^15), or 0.
+// Exponent that puts `b` (a row's largest finite magnitude) in [2^14, 2^15),
+// or 0 when the row has no non-zero finite entry.
 __device__ __forceinline__ int row_exponent(float b) {
   return (b > 0.0f && b <= 3.4028234663852886e38f) ? 14 - ilogbf(b) : 0;
 }
 
-__device__ __forceinline__ float abs_or_inf(float v) {
+// |v| of a finite v, 0 for Inf / NaN: a row's exponent comes from its largest
+// finite magnitude, and its Inf / NaN entries stay Inf / NaN when scaled and
+// converted, so they reach the products as gemm_cpu sees them.
+__device__ __forceinline__ float finite_abs(float v) {
   const float a = fabsf(v);
-  return a != a ? __builtin_inff() : a;   // NaN counts as non-finite
+  return a <= 3.4028234663852886e38f ? a : 0.0f;
 }
 
 template <bool XBF16>
@@ -178,7 +188,7 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
       float v[8];
       load8<XBF16>(x, K, x_vec, m, k, v);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, finite_abs(v[j]));
     }
     mx = lane_reduce<64, true>(mx);
     if ((threadIdx.x & 63) == 0) s_max[threadIdx.x >> 6] = mx;
@@ -200,7 +210,7 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
         const _Float16 h0 = (_Float16)v[2 * j], h1 = (_Float16)v[2 * j + 1];
         h[j] = pack_h2(h0, h1);
         if constexpr (!XBF16)
-          l[j] = pack_h2((_Float16)((v[2 * j] - (float)h0) * kLoScale), (_Float16)((v[2 * j + 1] - (float)h1) * kLoScale));
+          l[j] = pack_h2((_Float16)lo_part(v[2 * j], (float)h0), (_Float16)lo_part(v[2 * j + 1], (float)h1));
       }
       *reinterpret_cast<uint4*>(ah + (size_t)m * kp + k) = make_uint4(h[0], h[1], h[2], h[3]);
       if constexpr (!XBF16) *reinterpret_cast<uint4*>(al + (size_t)m * kp + k) = make_uint4(l[0], l[1], l[2], l[3]);
@@ -211,10 +221,11 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
 __device__ __forceinline__ float wave_max(float v) { return lane_reduce<64, true>(v); }
 __device__ __forceinline__ float wave_add(float v) { return lane_reduce<64>(v); }
 
-// Per activation row m: xe[m] such that the row's largest magnitude times
-// 2^xe[m] lies in [2^14, 2^15), so the f16 operands neither overflow nor
-// (for bf16 X) round; 0 for a row that is all zero or holds Inf or NaN (those
-// propagate as in the reference's f32 arithmetic).  One wave per row.
+// Per activation row m: xe[m] such that the row's largest finite magnitude
+// times 2^xe[m] lies in [2^14, 2^15), so the f16 operands neither overflow
+// nor (for bf16 X) round; 0 for a row with no non-zero finite entry.  Inf and
+// NaN entries stay Inf and NaN and propagate as in the reference's f32
+// arithmetic.  One wave per row.
 template <bool XBF16>
 __global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict__ x, uint32_t M, uint32_t K,
                                                          uint32_t x_vec, int32_t* __restrict__ xe) {
@@ -239,10 +250,10 @@ __global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict_
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           if constexpr (XBF16) {
-            mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] << 16)));
-            mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j] & 0xffff0000u)));
+            mx = fmaxf(mx, finite_abs(__uint_as_float(w[j] << 16)));
+            mx = fmaxf(mx, finite_abs(__uint_as_float(w[j] & 0xffff0000u)));
           } else {
-            mx = fmaxf(mx, abs_or_inf(__uint_as_float(w[j])));
+            mx = fmaxf(mx, finite_abs(__uint_as_float(w[j])));
           }
         }
       }
@@ -251,7 +262,7 @@ __global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict_
     for (uint32_t k = lane; k < K; k += 64) {
       const float v = XBF16 ? bf16_to_f32(static_cast<const uint16_t*>(x)[(size_t)m * K + k])
                             : static_cast<const float*>(x)[(size_t)m * K + k];
-      mx = fmaxf(mx, abs_or_inf(v));
+      mx = fmaxf(mx, finite_abs(v));
     }
   }
   mx = lane_reduce<64, true>(mx);
@@ -267,7 +278,7 @@ __device__ __forceinline__ void store8(const float (&w)[8], float s, uint16_t* h
     const float a = w[2 * j] * s, b = w[2 * j + 1] * s;   // exact: s is a power of two
     const _Float16 ha = (_Float16)a, hb = (_Float16)b;
     h[j] = pack_h2(ha, hb);
-    if constexpr (SPLIT) l[j] = pack_h2((_Float16)((a - (float)ha) * kLoScale), (_Float16)((b - (float)hb) * kLoScale));
+    if constexpr (SPLIT) l[j] = pack_h2((_Float16)lo_part(a, (float)ha), (_Float16)lo_part(b, (float)hb));
   }
   *reinterpret_cast<uint4*>(hi + c) = make_uint4(h[0], h[1], h[2], h[3]);
   if constexpr (SPLIT) *reinterpret_cast<uint4*>(lo + c) = make_uint4(l[0], l[1], l[2], l[3]);
@@ -653,7 +664,7 @@ __global__ __launch_bounds__(THREADS) void dense_kernel(Panel p, const uint16_t*
         const uint32_t m = m0 + wm * (BM / 2) + i * 32 + (lane >> 5) * 4 + 8 * (r >> 2) + (r & 3);
         if (m >= M) continue;
         float v = acc[i][j][r];
-        if constexpr (SPLIT || SPLIT_A) v = __builtin_fmaf(accl[i][j][r], kLoInv, v);   // not in block mode
+        if constexpr (SPLIT || SPLIT_A) v = hilo_combine(v, accl[i][j][r]);   // not in block mode
         if (to_partial) {
           partial[((size_t)blockIdx.y * M + m) * N + n] = v;
         } else {

@@ -8,8 +8,9 @@
 //
 // Two launches (plus the split-K reduction when K is split):
 //   1. xprep_kernel: per activation row, the power-of-two exponent xe[m]
-//      that puts the row's largest magnitude in [2^14, 2^15) (0 for rows that
-//      are all zero or hold Inf/NaN), then X[m] * 2^xe[m] as f16 (exact for
+//      that puts the row's largest finite magnitude in [2^14, 2^15) (0 for
+//      rows with no non-zero finite entry; Inf and NaN entries stay Inf and
+//      NaN), then X[m] * 2^xe[m] as f16 (exact for
 //      bf16 X within 2^28 of the row's largest), padded with zeros to kp and
 //      stored with each aligned group of 8 columns in the order
 //      0 2 4 6 1 3 5 7 -- the order in which the weight decode below
@@ -68,9 +69,12 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 
 // ---- activation preparation --------------------------------------------------
 
-__device__ __forceinline__ float abs_or_inf(float v) {
+// |v| of a finite v, 0 for Inf / NaN: a row's exponent comes from its largest
+// finite magnitude, and its Inf / NaN entries stay Inf / NaN when scaled and
+// converted, so they reach the products as gemm_cpu sees them.
+__device__ __forceinline__ float finite_abs(float v) {
   const float a = fabsf(v);
-  return a != a ? __builtin_inff() : a;   // NaN counts as non-finite
+  return a <= 3.4028234663852886e38f ? a : 0.0f;
 }
 
 __device__ __forceinline__ int row_exponent(float b) {
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__
 #pragma unroll
     for (int i = 0; i < NPT; ++i)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[i][j]));
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, finite_abs(v[i][j]));
     const int e = row_exponent(row_max(mx));
     if (tid == 0) xe[m] = e;
 #pragma unroll
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(256) void xprep_kernel(const uint16_t* __restrict__
       float v[8];
       piece(pc, v);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, abs_or_inf(v[j]));
+      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, finite_abs(v[j]));
     }
     const int e = row_exponent(row_max(mx));
     if (tid == 0) xe[m] = e;
@@ -972,7 +976,7 @@ __global__ __launch_bounds__(NT, 1) void tile_cb4_kernel(DevTensor t, const uint
   // per output).
   const uint32_t nl = wave * 32 + l32, ncol = n0 + nl;
   auto row_of = [&](int f, int r) { return (uint32_t)(f * 32 + h * 4 + 8 * (r >> 2) + (r & 3)); };
-  auto value = [&](int f, int r) { return __builtin_fmaf(accl[f][r], 1.0f / 2048.0f, acc[f][r]); };
+  auto value = [&](int f, int r) { return hilo_combine(acc[f][r], accl[f][r]); };
   auto load_xs = [&](int f, int (&xs)[16]) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
