@@ -35,6 +35,29 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, s), s
 
 
+def _needed(path):
+    """DT_NEEDED entries of an ELF shared library built here (readelf -d)."""
+    import subprocess
+    out = subprocess.run(["readelf", "-d", path], capture_output=True, text=True, check=True).stdout
+    return re.findall(r"\(NEEDED\)\s+Shared library: \[([^\]]+)\]", out)
+
+
+def test_vendor_gemm_library_is_a_separate_plugin():
+    # The matmul library does not link hipBLASLt; the pinned comparison
+    # path's plugin beside it does, and exports what blas_plugin.cpp looks up.
+    lib_dir = os.path.join(ROOT, "vxg_amd")
+    main = os.path.join(lib_dir, "libvxt_hip.so")
+    plugin = os.path.join(lib_dir, "libvxt_hip_blas.so")
+    engine.load_library()
+    assert not any("hipblaslt" in n for n in _needed(main)), _needed(main)
+    assert any("hipblaslt" in n for n in _needed(plugin))
+    import subprocess
+    syms = subprocess.run(["nm", "-D", "--defined-only", plugin], capture_output=True, text=True,
+                          check=True).stdout
+    for s in ("vxt_blas_gemm_f16_tn", "vxt_blas_release_device"):
+        assert re.search(rf"\bT {s}$", syms, re.M), s
+
+
 def test_no_cpu_fallback_without_device():
     # Construction must raise (no silent host path) when no GPU is visible.
     try:

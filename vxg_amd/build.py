@@ -1,4 +1,6 @@
-"""Build the HIP library ``vxg_amd/libvxt_hip.so`` for gfx950 with hipcc.
+"""Build the HIP library ``vxg_amd/libvxt_hip.so`` for gfx950 with hipcc,
+and beside it ``libvxt_hip_blas.so``, the hipBLASLt plugin that only the
+pinned library GEMM path opens.
 
 Run ``python -m vxg_amd.build`` (or ``__graft_entry__.build()``).  hipcc
 cross-compiles for gfx950 without a GPU present.
@@ -14,10 +16,14 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvxt_hip.so")
 SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_q40.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip", "gemm_tile.hip", "gemm_dense.hip", "gemm_dense3.hip",
-           "gemm_blas.cpp", "dequant.hip", "greedy.hip", "probe.hip", "ffn.hip", "attn.hip", "archive.cpp"]
+           "blas_plugin.cpp", "dequant.hip", "greedy.hip", "probe.hip", "ffn.hip", "attn.hip", "archive.cpp"]
+LIBS = ["-ldl"]
 
-# hipBLASLt runs the dense phase of large-batch prefill GEMMs (gemm_blas.cpp).
-LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
+# The pinned comparison path's dense phase on hipBLASLt (gemm_blas.cpp), a
+# library of its own that libvxt_hip.so opens on first use (blas_plugin.cpp).
+BLAS_LIB = os.path.join(HERE, "libvxt_hip_blas.so")
+BLAS_SOURCES = ["gemm_blas.cpp"]
+BLAS_LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -45,23 +51,30 @@ def _compile(src: str, obj: str, verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> str:
-    """Compile every source to an object in parallel, then link the library."""
-    from concurrent.futures import ThreadPoolExecutor
-    os.makedirs(OBJ_DIR, exist_ok=True)
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in SOURCES]
-    jobs = jobs or min(len(srcs), os.cpu_count() or 1)
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(lambda so: _compile(so[0], so[1], verbose), zip(srcs, objs)))
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, *LIBS, "-o", tmp]
+def _link(objs: list[str], libs: list[str], out: str, verbose: bool) -> None:
+    tmp = out + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *objs, *libs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError(f"link failed ({r.returncode}):\n{r.stderr}")
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {os.path.basename(out)} failed ({r.returncode}):\n{r.stderr}")
+    os.replace(tmp, out)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compile every source to an object in parallel, then link the library
+    and the hipBLASLt plugin."""
+    from concurrent.futures import ThreadPoolExecutor
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    names = SOURCES + BLAS_SOURCES
+    srcs = [os.path.join(CSRC, s) for s in names]
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in names]
+    jobs = jobs or min(len(srcs), os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(lambda so: _compile(so[0], so[1], verbose), zip(srcs, objs)))
+    _link(objs[:len(SOURCES)], LIBS, LIB, verbose)
+    _link(objs[len(SOURCES):], BLAS_LIBS, BLAS_LIB, verbose)
     return LIB
 
 

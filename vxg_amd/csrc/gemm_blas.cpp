@@ -1,5 +1,10 @@
 // gemm_blas.cpp -- the dense phase of the two-phase prefill GEMM on
-// hipBLASLt, for large batches.
+// hipBLASLt, for the pinned comparison path only.
+//
+// Built as its own shared library (libvxt_hip_blas.so, next to
+// libvxt_hip.so), which libvxt_hip.so opens the first time a caller runs the
+// pinned library path (blas_plugin.cpp): the matmul library itself does not
+// link or load hipBLASLt.
 //
 // Once the weights are decoded into an f16 panel (gemm_panel.hip), what is
 // left is a plain f16 x f16 -> f32 GEMM, D[M][N] = alpha * A[M][K] * B[N][K]^T
@@ -34,7 +39,6 @@ using Key = std::tuple<int, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, ui
 std::mutex g_mu;
 std::map<int, hipblasLtHandle_t> g_handles;
 std::map<Key, Entry> g_entries;
-std::map<int, int> g_users;   // contexts alive per device
 constexpr size_t kMaxEntries = 512;
 
 void destroy_entry(Entry& en) {
@@ -115,19 +119,14 @@ hipError_t entry_for(int dev, uint32_t M, uint32_t N, uint32_t K, uint32_t lda, 
 
 }  // namespace
 
-// The library handle and cached descriptors of a device live while a
-// context on that device does: contexts register here, and the last one to
-// go releases them (the handle is shared by the device's contexts).
-void blas_acquire_device(int dev) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  ++g_users[dev];
-}
+}  // namespace vxt
 
-void blas_release_device(int dev) {
+// Releases the library handle and cached descriptors of a device; called by
+// libvxt_hip.so when the last context on that device is destroyed (the
+// handle is shared by the device's contexts).
+extern "C" __attribute__((visibility("default"))) void vxt_blas_release_device(int dev) {
+  using namespace vxt;
   std::lock_guard<std::mutex> lk(g_mu);
-  auto u = g_users.find(dev);
-  if (u == g_users.end() || --u->second > 0) return;
-  g_users.erase(u);
   for (auto it = g_entries.begin(); it != g_entries.end();) {
     if (std::get<0>(it->first) == dev) {
       destroy_entry(it->second);
@@ -150,8 +149,10 @@ void blas_release_device(int dev) {
 // D_b[M][N] (f32, row-major; block b at D + b * M * N) = alpha * A_b[M][K] *
 // B_b[N][K]^T + beta * D_b for b < batch, where A_b and B_b are the columns
 // [b K, (b + 1) K) of A and B (f16 row-major, row strides lda, ldb elements).
-hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N,
-                            uint32_t K, uint32_t batch, float alpha, float beta, float* D, hipStream_t s) {
+extern "C" __attribute__((visibility("default"))) hipError_t vxt_blas_gemm_f16_tn(
+    const uint16_t* A, uint32_t lda, const uint16_t* B, uint32_t ldb, uint32_t M, uint32_t N, uint32_t K,
+    uint32_t batch, float alpha, float beta, float* D, hipStream_t s) {
+  using namespace vxt;
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -162,5 +163,3 @@ hipError_t blas_gemm_f16_tn(const uint16_t* A, uint32_t lda, const uint16_t* B, 
   return status(hipblasLtMatmul(h, en->op, &alpha, B, en->la, A, en->lb, &beta, D, en->ld, D, en->ld, &en->algo,
                                 nullptr, 0, s));
 }
-
-}  // namespace vxt
