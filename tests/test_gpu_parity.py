@@ -185,18 +185,26 @@ def test_gemv_small_batch_f32_x(eng, kind, M):
         assert max_rel(y, gemv_ref(m, X), floor_scale(oracle.decode_rows(m), X)) <= 1e-3, (rows, cols)
 
 
-@pytest.mark.parametrize("cols", [100, 2048])
+@pytest.mark.parametrize("cols", [100, 2048, 2050, 4096])
 def test_gemv_q8_many_rows_small_batch(eng, cols):
-    """Row counts >= 65536 with M = 2..8 take the LDS-staged persistent kernel."""
+    """Row counts >= 65536 with M = 2..8: the persistent MFMA kernel where
+    kp is a multiple of 512 (2048; 4096 on two staged K steps), the
+    LDS-staged persistent dot2 kernel otherwise (100 -> kp 128, 2050 -> kp
+    2080).  The last row tile is partial (65541 rows)."""
     m = synth.make_q8(65541, cols, seed=cols)
     t = eng.upload_packed(m)
-    for M in (2, 3, 4, 8):
+    for M in (2, 3, 4, 5, 6, 7, 8):
         xb = synth.make_x_bf16(M, cols, seed=M)
         X = bf16_bits_to_f32(xb).reshape(M, cols)
         y = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
         for i in range(M):
             yref = oracle.gemv(m, X[i], threads=THREADS)
-            assert max_rel(y[i], yref, q8_floor(m, X[i])) <= 1e-3, (M, i)
+            fl = q8_floor(m, X[i])
+            assert max_rel(y[i], yref, fl) <= 1e-3, (M, i)
+            assert_bf16_close(yb[i], yref, fl)
+        y2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        assert np.array_equal(y.view(np.uint32), y2.view(np.uint32)), "run-to-run bits"
 
 
 @pytest.mark.parametrize("M", [5, 6, 7, 8])

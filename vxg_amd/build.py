@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libvxt_hip.so")
-SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_q40.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip", "gemm_tile.hip", "gemm_dense.hip", "gemm_dense3.hip",
+SOURCES = ["vxt_hip.hip", "gemv.hip", "gemv_q8.hip", "gemv_q8p.hip", "gemv_q40.hip", "gemv_cb4.hip", "gemv_g64.hip", "gemm_panel.hip", "gemm_fused.hip", "gemm_tile.hip", "gemm_dense.hip", "gemm_dense3.hip",
            "blas_plugin.cpp", "dequant.hip", "greedy.hip", "probe.hip", "ffn.hip", "attn.hip", "archive.cpp"]
 LIBS = ["-ldl"]
 
@@ -39,8 +39,13 @@ FLAGS = [
 ]
 
 
+# Per-source flags: gemv_q8p.hip keeps MFMA results in VGPRs (its reason is
+# at the top of that file).
+FILE_FLAGS = {"gemv_q8p.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str, obj: str, verbose: bool) -> None:
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)

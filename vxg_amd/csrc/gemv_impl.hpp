@@ -1717,6 +1717,11 @@ hipError_t launch_q8_mfma_t(const DevTensor& t, const void* x, uint32_t m, void*
   return hipGetLastError();
 }
 
+// Q8 x bf16 activations, 3..8 tokens, >= 65536 rows: the persistent MFMA
+// kernel of gemv_q8p.hip (its own translation unit, compiled with MFMA
+// results in VGPRs).  hipErrorInvalidValue when the shape does not fit it.
+hipError_t launch_q8_lm(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s);
+
 // Grid for the persistent kernel: enough workgroups to fill every CU at the
 // occupancy the LDS footprint allows, never more than there are row blocks.
 template <int MT, int RPW, int WAVES, int NS>
@@ -1900,6 +1905,15 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
     // 3.22 / 4.95 / 5.26 / 63.0; M = 4 4.95 / 7.82 / 8.75 / 84.6 -> 3.81 /
     // 5.92 / 6.64 / 80.1; M = 8 only at 2048 x 2048, 6.25 -> 4.98 (the MFMA
     // and persistent kernels keep the others).
+    // 3..8 tokens over >= 65536 rows (the LM head): the persistent MFMA
+    // kernel, one wave per SIMD (measured best of 1..3 per SIMD and of
+    // 4 or 8 pairs per batch, 2 to 6 batches in flight).  151936 x 2048,
+    // graph-timed: M = 4 89.4 -> 64.4 us (gemv_q8_mt_kernel before), M = 8
+    // 101.4 -> 68.1 (gemv_q8_mfma_kernel); M = 2 stays on the LDS-staged
+    // dot2 kernel (64.2 against 66-68).
+    if (x_bf16 && m >= 3 && m <= 8 && t.rows >= 65536 && t.kp % 512 == 0 && t.kp <= 2 * kStep &&
+        t.cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0)
+      return launch_q8_lm(t, x, m, y, y_bf16, s);
     if (x_bf16 && m >= 2 && m <= 8) {
       const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
       if (nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % 8 == 0) {
