@@ -365,6 +365,47 @@ def bench_step(eng, kind: str, head_m, tokens: int, layers: int = 24, hidden: in
             "ms_per_token": ms_tok, "launches_per_token": launches, "last_token": tok, "nonfinite": bad}
 
 
+def bench_runner(eng, kind: str, head_m, prompt: int, tokens: int, layers: int = 24, hidden: int = 2048,
+                 ffn: int = 6144, n_head: int = 16, hd: int = 128, seed: int = 40):
+    """The C-level decode-step runner (``vxt_hip_runner_*``) on config 4's
+    weights with real attention: per layer RMSNorm, [q;k;v] (16 heads x 128,
+    16 kv heads), q / k RMSNorm + RoPE + K/V into the layer's Q8_0 cache +
+    attention, o, add + RMSNorm, [gate;up] + SwiGLU, down; final norm, tied Q8
+    LM head, greedy.  A ``prompt``-token prefill (one batched step), then
+    ``tokens`` greedy decode steps on the device (one graph launch each),
+    timed host-side around each call."""
+    import numpy as np
+    from vxg_amd import engine
+    lw, _ = _stack_layers(eng, kind, layers, hidden, ffn, seed)
+    head = eng.upload_packed(head_m)
+    rng = np.random.default_rng(seed)
+    bufs = [eng.to_device((1 + 0.1 * rng.standard_normal(hidden)).astype(np.float32))
+            for _ in range(2 * layers + 1)]
+    qk = [eng.to_device((1 + 0.1 * rng.standard_normal(hd)).astype(np.float32)) for _ in range(2)]
+    rl = [engine.RunnerLayer(L.qkv.handle, L.o.handle, L.gate_up.handle, L.down.handle, bufs[2 * i].ptr,
+                             bufs[2 * i + 1].ptr, qk[0].ptr, qk[1].ptr) for i, L in enumerate(lw)]
+    cfg = engine.RunnerConfig(layers, hidden, n_head, n_head, hd, ffn, head_m.rows, 0, hd, 1, engine.ACT_SILU,
+                              prompt + tokens + 8, prompt, 1e6, 1e-6, 1.0)
+    r = eng.runner(cfg, rl, bufs[-1].ptr, head, head)
+    ids = rng.integers(0, head_m.rows, size=prompt).astype(np.uint32)
+    r.step(ids, 0)                       # warm: the batched path's workspace
+    r.generate(1, prompt, 4)
+    t0 = time.perf_counter()
+    logits = r.step(ids, 0)
+    t_prefill = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    out, flags = r.generate(int(np.argmax(logits)), prompt, tokens)
+    t_decode = time.perf_counter() - t0
+    r.free()
+    for b in bufs + qk:
+        b.free()
+    _free_layers(lw)
+    head.free()
+    return {"prefill_tokens_per_s": prompt / t_prefill, "prefill_ms": t_prefill * 1e3,
+            "decode_tokens_per_s": tokens / t_decode, "ms_per_token": t_decode * 1e3 / tokens,
+            "nonfinite_steps": int(flags.sum())}
+
+
 def bench_attn(eng, seq: int, n_head: int, n_kv: int, hd: int, calls: int = 200, seed: int = 6,
                eager: bool = False):
     """Decode attention over a Q8_0 KV cache of ``seq`` positions: one
@@ -440,15 +481,16 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline only, no secondary configs")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--configs", default="f,0,r,q,g,2,3,4,s,a",
+    ap.add_argument("--configs", default="f,0,r,q,g,2,3,4,s,t,a",
                     help="secondary configurations to run (f: HBM streaming floor at the configs' sizes, "
-                         "s: whole decode step on config 4's weights, a: KV-Q8 decode attention, "
+                         "s: whole decode step on config 4's weights, t: the decode-step runner with KV-cache "
+                         "attention on config 4's weights, a: KV-Q8 decode attention, "
                          "c: config 3's cb4 lines on the pinned decode-in-loop tile kernel, q: Q4_0 GEMV at config 1's shape)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--eager", action="store_true",
                     help="time with plain launches instead of graph replays (for profilers: rocprofv3's kernel "
-                         "tracer has crashed inside hipGraphLaunch after many GEMM graphs; `value` is then not "
-                         "the graph-timed number)")
+                         "tracer has crashed inside hipGraphLaunch on this image, a cause not shown to be in this "
+                         "library; `value` is then not the graph-timed number)")
     args = ap.parse_args()
 
     global EAGER
@@ -606,6 +648,24 @@ def main():
                               "launches_per_token": rw["launches_per_token"]})
             log(f"  {rw['tokens_per_s']:.1f} tok/s ({rw['ms_per_token']*1e3:.1f} us/token, "
                 f"{rw['launches_per_token']} launches)")
+        del head_m
+    if "t" in run:
+        head_m = synth.make_q8(151936, 2048, seed=5)
+        prompt, gen = 512, max(32, min(256, args.steps // 2))
+        log(f"runner: 24 layers g64 with Q8_0-cache attention (16 heads x 128), tied Q8 head; prefill {prompt}, "
+            f"then {gen} greedy steps")
+        rr = bench_runner(eng, "g64", head_m, prompt, gen)
+        secondary.append({"config": f"decode-step runner (vxt_hip_runner_*): 24 x {{norm,[q;k;v],q/k norm+RoPE+"
+                                    f"Q8_0 KV cache+attention,o,add+norm,[gate;up]+swiglu,down}} g64 + norm + tied "
+                                    f"q8 head + greedy; {prompt}-token prefill, then {gen} greedy steps at "
+                                    f"positions {prompt}..{prompt + gen - 1}",
+                          "prefill_tokens_per_s": round(rr["prefill_tokens_per_s"], 1),
+                          "prefill_ms": round(rr["prefill_ms"], 2),
+                          "decode_tokens_per_s": round(rr["decode_tokens_per_s"], 1),
+                          "ms_per_token": round(rr["ms_per_token"], 4),
+                          "nonfinite_steps": rr["nonfinite_steps"]})
+        log(f"  prefill {rr['prefill_tokens_per_s']:.0f} tok/s ({rr['prefill_ms']:.1f} ms), decode "
+            f"{rr['decode_tokens_per_s']:.1f} tok/s ({rr['ms_per_token']*1e3:.1f} us/token)")
         del head_m
     if "a" in run:
         for seq, nh, nkv in ((4096, 16, 16), (32768, 16, 16), (32768, 16, 4), (131072, 16, 4)):

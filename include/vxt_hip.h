@@ -353,6 +353,77 @@ VXT_API int vxt_hip_attn_step_q8_dev(void* ctx, const VxtKvQ8Cache* cache, const
                                      uint32_t kv_stride, uint32_t batch_m, uint32_t pos, uint32_t rope_pos,
                                      float* out, void* stream, char* err, size_t err_cap);
 
+/* ---- Decode-step runner ----------------------------------------------------
+ * A whole forward pass of a decoder with full (grouped-query) attention over
+ * a Q8_0 KV cache, held on the device: the host side of the reference's
+ * device runner, vxt_metal_cb4_fast_{create, state_create, step_batch,
+ * enqueue_async, wait_cmd, destroy} (metal_cb4_fast_ffi.rs:134-206; the pass
+ * itself metal_cb4_fast_run.mm:94-434), for models whose layers are all
+ * full-attention layers (the reference's recurrent DeltaNet layers are not
+ * part of this library).  Per layer, as the CPU step (llm_cpu.rs:395-482):
+ *   normed = rms_norm(cur [+= delta], attn_norm)          (bf16)
+ *   qkv    = w_in . normed                                 (f32: [q | gate per head]; k; v)
+ *   attn   = step_full_gqa_q8(qkv, cache, pos)             (vxt_hip_attn_step_q8_dev)
+ *   delta  = w_out . attn                                  (f32)
+ *   normed = rms_norm(cur += delta, post_attn_norm)        (bf16)
+ *   act    = act(gate . normed) * (up . normed)            (vxt_hip_ffn_glu_dev, bf16)
+ *   delta  = w_ffn_dn . act                                (f32)
+ * then normed = rms_norm(cur += delta, output_norm), logits = lm_head .
+ * normed (f32), and for generation the greedy id (vxt_hip_greedy_dev) whose
+ * embedding row (vxt_hip_embed_dev, times embed_scale) starts the next step.
+ * Every piece is the entry point named beside it; the runner adds the
+ * buffers, one KV cache per layer (max_seq rows) and, for single tokens, one
+ * captured HIP graph whose attention reads the position from device memory,
+ * so a decode step is one graph launch with no per-token host work. */
+typedef struct VxtRunnerLayer {
+    void* w_in;                   /* (q_rows + 2 * n_kv * head_dim) x hidden */
+    void* w_out;                  /* hidden x (n_head * head_dim)            */
+    void* w_ffn_gu;               /* (2 * ffn) x hidden, [gate; up]          */
+    void* w_ffn_dn;               /* hidden x ffn                            */
+    const float* attn_norm;       /* device [hidden]                         */
+    const float* post_attn_norm;  /* device [hidden]                         */
+    const float* q_norm;          /* device [head_dim] or NULL               */
+    const float* k_norm;          /* device [head_dim] or NULL               */
+} VxtRunnerLayer;
+
+/* q_rows = n_head * head_dim * (gated_q ? 2 : 1); the rope and norm fields
+ * as in VxtGqaParams; activation VXT_ACT_*; embed_scale as in
+ * vxt_hip_embed_dev.  max_batch bounds the tokens of one vxt_hip_runner_step. */
+typedef struct VxtRunnerConfig {
+    uint32_t n_layers, hidden, n_head, n_kv, head_dim, ffn, vocab;
+    uint32_t gated_q, rope_dim, rope_neox, activation;
+    uint32_t max_seq, max_batch;
+    float rope_freq_base, eps, embed_scale;
+} VxtRunnerConfig;
+
+/* Checks every shape against the config (tensors of this context, norms
+ * non-null), allocates the buffers and the KV caches, and captures the
+ * single-token step.  The tensors and norm buffers must outlive the runner;
+ * vxt_hip_destroy of the context also releases it. */
+VXT_API void* vxt_hip_runner_create(void* ctx, const VxtRunnerConfig* cfg, const VxtRunnerLayer* layers,
+                                    const float* output_norm, void* lm_head, void* embed, char* err,
+                                    size_t err_cap);
+
+/* vxt_metal_cb4_fast_step_batch (metal_cb4_fast_run.mm:440-481): batch_m
+ * tokens (host ids, each < vocab) at positions pos_base .. pos_base +
+ * batch_m - 1 (rope positions the same), causal over the cache rows below;
+ * their K and V enter the cache.  logits_out (NULL or [vocab]) receives the
+ * last token's logits.  batch_m 1 replays the captured step; larger batches
+ * run the batched GEMM path.  Synchronous. */
+VXT_API int vxt_hip_runner_step(void* runner, const uint32_t* tok_ids, uint32_t batch_m, uint32_t pos_base,
+                                float* logits_out, char* err, size_t err_cap);
+
+/* Greedy generation on the device, the reference's ring of enqueue_async /
+ * wait_cmd (metal_cb4_fast_ffi.rs:191-206): starting from `token` at
+ * pos_base, n_steps single-token steps, each feeding the greedy id of the
+ * previous one; tokens_out[i] is the id chosen after step i and flags_out
+ * (NULL or [n_steps]) is 1 where that step's logits held NaN or +-inf.
+ * n_steps graph launches, one copy back.  Synchronous. */
+VXT_API int vxt_hip_runner_generate(void* runner, uint32_t token, uint32_t pos_base, uint32_t n_steps,
+                                    uint32_t* tokens_out, uint32_t* flags_out, char* err, size_t err_cap);
+
+VXT_API void vxt_hip_runner_destroy(void* runner);
+
 /* ---- Weight containers ----------------------------------------------------
  * Readers over bytes the caller holds (e.g. a mapped file); they keep no
  * pointer after returning.  Offsets below are byte offsets into those bytes. */

@@ -132,6 +132,29 @@ def test_gemv_baseline_shapes_bf16(eng, kind, K, N, M):
     assert_bf16_close(yb, yref, fl)
 
 
+@pytest.mark.parametrize("rows,cols", [(6144, 2048), (12288, 2048), (2048, 6144), (300, 2052), (77, 4100),
+                                       (5, 130)])
+def test_gemv_g64_one_token_f32_x(eng, rows, cols):
+    """g64 at M = 1 with f32 activations (an attention output): the one-token
+    LDS-staged kernel stages them as they are (cols % 4 == 0; one, two and
+    three K steps, one and two rows per wave), the generic kernel otherwise
+    (130 columns).  Against the oracle, and bit-equal to the bf16-activation
+    call on the same (bf16-representable) values: both stage f32 in LDS and
+    sum in one order."""
+    m = make("g64", rows, cols, seed=rows + cols)
+    t = eng.upload_packed(m)
+    xb = synth.make_x_bf16(1, cols, seed=cols)
+    X = bf16_bits_to_f32(xb).reshape(1, cols)
+    yf = run_dev(eng, t, np.ascontiguousarray(X, dtype=np.float32), engine.DTYPE_F32, 1, engine.DTYPE_F32)
+    yb = run_dev(eng, t, np.ascontiguousarray(X, dtype=np.float32), engine.DTYPE_F32, 1, engine.DTYPE_BF16)
+    ref = gemv_ref(m, X)
+    fl = floor_scale(oracle.decode_rows(m), X)
+    assert max_rel(yf, ref, fl) <= 1e-3
+    assert_bf16_close(yb, ref, fl)
+    if cols % 8 == 0:
+        assert_bits_equal(run_dev(eng, t, xb, engine.DTYPE_BF16, 1, engine.DTYPE_F32), yf)
+
+
 def test_gemv_q8_config0_f32(eng):
     """Config 0: Q8, M=1, K=N=4096, x f32 N(0,1), y f32, seed 0."""
     m = synth.make_q8(4096, 4096, seed=0)

@@ -297,6 +297,9 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t slot = lane / LPT, sub = lane % LPT;
   const uint32_t kvh = blockIdx.x, ck = blockIdx.y;
+  if constexpr (PREP) {
+    if (pp.dpos) seq0 = min(pp.dpos[0], c.max_seq - 1u) + 1u;   // device position (one token)
+  }
   const uint32_t seq_len = seq0 + blockIdx.z;             // token z sees positions [0, seq0 + z)
   const uint32_t t0 = ck * CH;
   if (t0 >= seq_len) return;                              // a chunk past this token's positions
@@ -386,7 +389,7 @@ __global__ __launch_bounds__(kThreads) void attn_chunk_kernel(KvQ8Dev c, const f
     // sine and cosine of pair i by thread 64 + i (waves 1 and 2), beside the
     // norms and the V quantisation
     if (tid >= 64u && tid - 64u < pp.half) {
-      const float th = (float)pp.rope_pos * fr;
+      const float th = (float)(pp.dpos ? pp.dpos[1] : pp.rope_pos) * fr;
       double sd, cd;
       sincos((double)th, &sd, &cd);
       s_cs[2u * (tid - 64u)] = (float)sd;
@@ -574,13 +577,15 @@ __global__ __launch_bounds__(W * 64) void attn_merge_kernel(const float* __restr
                                                             uint32_t chunk_stride, uint32_t chunk, uint32_t seq0,
                                                             const float* __restrict__ gate, uint32_t gate_stride,
                                                             const float* __restrict__ gate_bias,
-                                                            float* __restrict__ out) {
+                                                            float* __restrict__ out,
+                                                            const uint32_t* __restrict__ dpos) {
 #pragma clang fp contract(off)
   __shared__ float s_m[W], s_acc[W][64], s_l[W];
   const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t d = blockIdx.y * 64u + lane;
   const uint32_t z = blockIdx.z, n_head = gridDim.x;
-  const uint32_t n_chunks = (seq0 + z + chunk - 1u) / chunk;   // token z's chunks
+  if (dpos) seq0 = dpos[0] + 1u;   // device position (one token); clamped below like the chunks
+  const uint32_t n_chunks = min((seq0 + z + chunk - 1u) / chunk, chunk_stride);   // token z's chunks
   const size_t stride = hd + 2;
   const float* ph = part + ((size_t)z * n_head + h) * chunk_stride * stride;
   if (gate) gate += (size_t)z * n_head * gate_stride;
@@ -990,17 +995,17 @@ const RopeFreq& rope_table(uint32_t rope_dim, float freq_base, uint32_t hd, uint
 // already gives every CU workgroups (prefill: a token has few chunks).
 hipError_t launch_merge(const float* part, uint32_t hd, uint32_t n_head, uint32_t batch, uint32_t n_chunks,
                         uint32_t chunk, uint32_t seq0, const float* gate, uint32_t gate_stride,
-                        const float* gate_bias, float* out, hipStream_t s) {
+                        const float* gate_bias, float* out, hipStream_t s, const uint32_t* dpos = nullptr) {
   const dim3 grid(n_head, (hd + 63) / 64, batch);
   if ((size_t)grid.x * grid.y * grid.z < 512u)
     hipLaunchKernelGGL(attn_merge_kernel<16>, grid, dim3(16 * 64), 0, s, part, hd, n_chunks, chunk, seq0, gate,
-                       gate_stride, gate_bias, out);
+                       gate_stride, gate_bias, out, dpos);
   else if (n_chunks >= 8)
     hipLaunchKernelGGL(attn_merge_kernel<4>, grid, dim3(4 * 64), 0, s, part, hd, n_chunks, chunk, seq0, gate,
-                       gate_stride, gate_bias, out);
+                       gate_stride, gate_bias, out, dpos);
   else
     hipLaunchKernelGGL(attn_merge_kernel<1>, grid, dim3(64), 0, s, part, hd, n_chunks, chunk, seq0, gate,
-                       gate_stride, gate_bias, out);
+                       gate_stride, gate_bias, out, dpos);
   return hipGetLastError();
 }
 
@@ -1102,13 +1107,16 @@ hipError_t launch_attn_prefill(const KvQ8Dev& c, const float* q, const float* ga
 // One decode step (a single token at row pp.pos, rope position pp.rope_pos)
 // in two launches: the chunk kernel with the prep folded in, then the merge
 // (the gate read from q_raw's gate halves).  ws holds
-// attn_workspace_bytes(n_head, pp.pos + 1, n_kv, hd, 1).
+// attn_workspace_bytes(n_head, pp.pos + 1, n_kv, hd, 1).  With pp.dpos the
+// position is read on the device: the grids cover the whole cache (chunks
+// past the position return at once) and ws holds
+// attn_workspace_bytes(n_head, max_seq, n_kv, hd, 1).
 hipError_t launch_attn_step(const KvQ8Dev& c, GqaPrep pp, uint32_t rope_dim, float freq_base, float* out, void* ws,
                             hipStream_t s) {
   const uint32_t group = pp.n_head / c.n_kv;
   if (group == 0 || group > kMaxGroup) return hipErrorInvalidValue;
   const RopeFreq& tab = rope_table(rope_dim, freq_base, c.hd, &pp.half);
-  const uint32_t chunk = chunk_of(c.hd), seq0 = pp.pos + 1u;
+  const uint32_t chunk = chunk_of(c.hd), seq0 = pp.dpos ? c.max_seq : pp.pos + 1u;
   const uint32_t n_chunks = (seq0 + chunk - 1) / chunk;
   if (n_chunks > 65535u) return hipErrorInvalidValue;
   float* part = static_cast<float*>(ws);
@@ -1116,7 +1124,8 @@ hipError_t launch_attn_step(const KvQ8Dev& c, GqaPrep pp, uint32_t rope_dim, flo
   if (e != hipSuccess) return e;
   const float* gate = pp.gated ? pp.q_raw + c.hd : nullptr;
   const float* gate_bias = pp.gated && pp.q_bias ? pp.q_bias + c.hd : nullptr;
-  return launch_merge(part, c.hd, pp.n_head, 1, n_chunks, chunk, seq0, gate, 2u * c.hd, gate_bias, out, s);
+  return launch_merge(part, c.hd, pp.n_head, 1, n_chunks, chunk, seq0, gate, 2u * c.hd, gate_bias, out, s,
+                      pp.dpos);
 }
 
 }  // namespace vxt

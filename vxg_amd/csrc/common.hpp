@@ -156,6 +156,10 @@ struct GqaPrep {
   float* gate_out;       // gated only
   uint32_t q_stride, kv_stride, n_head, gated, half, neox, pos, rope_pos;
   float eps;
+  // Decode step only: null, or device words {pos, rope_pos} read by the
+  // kernels in place of pos / rope_pos (pos clamped to the cache), so one
+  // captured graph serves every position.
+  const uint32_t* dpos;
 };
 
 // Workgroup barrier that orders LDS traffic only.  __syncthreads() also

@@ -1004,14 +1004,14 @@ __device__ __forceinline__ void opaque4(uint4& v) {
 }
 
 // ---------------------------------------------------------------------------
-// cb4-g64 weights x bf16 activations, one token, 1..3 K steps: the structure
-// of gemv_q8_m1_kernel (activations staged once per workgroup, widened to f32
-// in swizzled LDS; every load unconditional; RPW rows per wave) with the g64
-// decode of gemv_kernel (each wave's transposed table blocks in LDS, one
-// v_perm_b32 address per lookup).  Products and summation order are those of
-// gemv_kernel.
-template <int RPW, int WAVES, int NS>
-__global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, const uint16_t* __restrict__ x,
+// cb4-g64 weights x bf16 (or f32) activations, one token, 1..3 K steps: the
+// structure of gemv_q8_m1_kernel (activations staged once per workgroup,
+// widened to f32 in swizzled LDS; every load unconditional; RPW rows per
+// wave) with the g64 decode of gemv_kernel (each wave's transposed table
+// blocks in LDS, one v_perm_b32 address per lookup).  Products and summation
+// order are those of gemv_kernel.
+template <int RPW, int WAVES, int NS, bool XBF16 = true>
+__global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, const void* __restrict__ x,
                                                                 void* __restrict__ y, uint32_t y_bf16) {
   static_assert(NS >= 1 && NS <= 3, "K steps staged in LDS");
   constexpr int NB = (RPW + 1) / 2;   // table blocks per wave
@@ -1026,10 +1026,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, co
   const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
   const uint32_t row0 = (blockIdx.x * WAVES + wave) * RPW;
 
-  constexpr uint32_t kPieces = NS * kStep / 8;   // 16-byte pieces of bf16 activations
+  constexpr uint32_t kXB = XBF16 ? 2u : 4u;                 // bytes per activation
+  constexpr uint32_t kPieces = NS * kStep * kXB / 16u;      // 16-byte pieces of activations
   constexpr uint32_t kPer = (kPieces + WAVES * 64 - 1) / (WAVES * 64);
   const __amdgpu_buffer_rsrc_t xr =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(x), (short)0, (int)(cols * 2u), 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(x), (short)0, (int)(cols * kXB), 0x00020000);
   u32x4 xv[kPer];
 #pragma unroll
   for (uint32_t j = 0; j < kPer; ++j) {
@@ -1057,8 +1058,12 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_g64_m1_kernel(DevTensor t, co
   for (uint32_t j = 0; j < kPer; ++j) {
     const uint32_t p = std::min(tid + WAVES * 64 * j, kPieces - 1);
     const u32x4 v = xv[j];
-    put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
-    put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
+    if constexpr (XBF16) {
+      put(2 * p, u32x4{v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u});
+      put(2 * p + 1, u32x4{v.z << 16, v.z & 0xffff0000u, v.w << 16, v.w & 0xffff0000u});
+    } else {
+      put(p, v);
+    }
   }
   __syncthreads();
   __builtin_amdgcn_sched_barrier(0);   // the barrier waits for the activations only
@@ -1656,15 +1661,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma_kernel(DevTensor t, c
 // 2307 for the 151936-row LM head, level at 2048 x 2048; behind at M = 4
 // (the MFMA cost does not shrink with M) and at K = 6144 x N = 2048, where
 // 128 row tiles leave most CUs idle (987 vs 1089 GB/s on 4 waves, 1023 on 8).
-// cb4-g64 x bf16, one token, staged through LDS (gemv_g64_m1_kernel).
-// Requires 16-byte aligned activations, cols % 8 == 0 and NS K steps.
-template <int RPW, int WAVES, int NS>
+// cb4-g64 x bf16 (or f32), one token, staged through LDS (gemv_g64_m1_kernel).
+// Requires 16-byte aligned activations, 16-byte pieces wholly inside or
+// outside the row, and NS K steps.
+template <int RPW, int WAVES, int NS, bool XBF16 = true>
 hipError_t launch_g64_m1_t(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s) {
-  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % 8 != 0 || (t.kp + kStep - 1) / kStep != (uint32_t)NS)
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.cols % (XBF16 ? 8 : 4) != 0 ||
+      (t.kp + kStep - 1) / kStep != (uint32_t)NS)
     return hipErrorInvalidValue;
   const uint32_t per_block = WAVES * RPW;
-  hipLaunchKernelGGL((gemv_g64_m1_kernel<RPW, WAVES, NS>), dim3((t.rows + per_block - 1) / per_block),
-                     dim3(WAVES * 64), 0, s, t, static_cast<const uint16_t*>(x), y, (uint32_t)(y_bf16 ? 1u : 0u));
+  hipLaunchKernelGGL((gemv_g64_m1_kernel<RPW, WAVES, NS, XBF16>), dim3((t.rows + per_block - 1) / per_block),
+                     dim3(WAVES * 64), 0, s, t, x, y, (uint32_t)(y_bf16 ? 1u : 0u));
   return hipGetLastError();
 }
 
@@ -1862,6 +1869,20 @@ hipError_t launch_q8_mt(const DevTensor& t, const void* x, uint32_t m, void* y, 
   return launch_q8_mt_t<MT, 1, 4, 3>(t, x, m, y, y_bf16, s);
 }
 
+// One token of g64 weights through the LDS-staged kernel: one row per wave up
+// to 8192 rows, two above; four waves per workgroup.
+template <bool XBF16>
+hipError_t launch_g64_m1(const DevTensor& t, const void* x, void* y, bool y_bf16, hipStream_t s, uint32_t nsteps) {
+  if (t.rows > 8192) {
+    if (nsteps == 1) return launch_g64_m1_t<2, 4, 1, XBF16>(t, x, y, y_bf16, s);
+    if (nsteps == 2) return launch_g64_m1_t<2, 4, 2, XBF16>(t, x, y, y_bf16, s);
+    return launch_g64_m1_t<2, 4, 3, XBF16>(t, x, y, y_bf16, s);
+  }
+  if (nsteps == 1) return launch_g64_m1_t<1, 4, 1, XBF16>(t, x, y, y_bf16, s);
+  if (nsteps == 2) return launch_g64_m1_t<1, 4, 2, XBF16>(t, x, y, y_bf16, s);
+  return launch_g64_m1_t<1, 4, 3, XBF16>(t, x, y, y_bf16, s);
+}
+
 // One token of cb4 weights through the LDS-staged kernel: one row per wave
 // up to 8192 rows, two above; eight waves per workgroup.
 template <bool XBF16>
@@ -1970,17 +1991,11 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
     // before) 5.61 -> 5.33 with one row per wave; 12288 x 2048 7.71 -> 6.85,
     // 24576 x 2048 12.32 -> 11.59, 151936 x 2048 59.6 -> 52.4 with two; four
     // waves per workgroup throughout.
+    // f32 activations (an attention output) take the same kernel, staged as
+    // they are.
     const uint32_t nsteps = (t.kp + kStep - 1) / kStep;
-    if (m == 1 && x_bf16 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % 8 == 0) {
-      if (t.rows > 8192) {
-        if (nsteps == 1) return launch_g64_m1_t<2, 4, 1>(t, x, y, y_bf16, s);
-        if (nsteps == 2) return launch_g64_m1_t<2, 4, 2>(t, x, y, y_bf16, s);
-        return launch_g64_m1_t<2, 4, 3>(t, x, y, y_bf16, s);
-      }
-      if (nsteps == 1) return launch_g64_m1_t<1, 4, 1>(t, x, y, y_bf16, s);
-      if (nsteps == 2) return launch_g64_m1_t<1, 4, 2>(t, x, y, y_bf16, s);
-      return launch_g64_m1_t<1, 4, 3>(t, x, y, y_bf16, s);
-    }
+    if (m == 1 && nsteps <= 3 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.cols % (x_bf16 ? 8 : 4) == 0)
+      return x_bf16 ? launch_g64_m1<true>(t, x, y, y_bf16, s, nsteps) : launch_g64_m1<false>(t, x, y, y_bf16, s, nsteps);
   }
   if (m == 1 && split_k_enabled()) {
     hipError_t e = hipSuccess;

@@ -11,6 +11,7 @@
 #include <algorithm>
 #include <cmath>
 #include <limits>
+#include <memory>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -109,6 +110,8 @@ struct Tensor {
 };
 
 struct Graph;
+struct Runner;
+void release_runner(Runner* r);   // with the context's lock held, or unneeded
 
 struct Ctx {
   int device = 0;
@@ -129,6 +132,7 @@ struct Ctx {
   std::set<Tensor*> tensors;
   std::set<void*> buffers;
   std::set<Graph*> graphs;
+  std::set<Runner*> runners;
   bool capturing = false;
 };
 
@@ -404,6 +408,11 @@ void vxt_hip_destroy(void* ctx) {
     // Everything the context handed out goes with it; those handles become
     // stale (their release calls are then no-ops).
     std::lock_guard<std::mutex> g(c->mu);
+    for (Runner* r : c->runners) {
+      reg_take(r);
+      release_runner(r);
+    }
+    c->runners.clear();
     for (Graph* gr : c->graphs) {
       reg_take(gr);
       release_graph(gr);
@@ -1330,5 +1339,354 @@ int vxt_hip_set_gemm_path(void* ctx, uint32_t path) {
   return VXT_OK;
 }
 
+
+// ============================================================================
+// Decode-step runner (see include/vxt_hip.h): the layer sequence of
+// llm_cpu.rs:395-482 over the entry points above, one KV cache per layer,
+// and a captured single-token step whose attention reads the position from
+// device memory.
+
+// After a captured step: the greedy id and its flag into the history row of
+// the step's position, then the position (and rope position) advanced.  One
+// thread; the host keeps the position below max_seq.
+__global__ void runner_advance_kernel(uint32_t* __restrict__ dpos, const uint32_t* __restrict__ tok,
+                                      uint32_t* __restrict__ hist, uint32_t max_seq) {
+  if (threadIdx.x != 0) return;
+  const uint32_t p = dpos[0];
+  if (p < max_seq) {
+    hist[2u * p] = tok[0];
+    hist[2u * p + 1u] = tok[1];
+  }
+  dpos[0] = p + 1u;
+  dpos[1] = dpos[1] + 1u;
+}
+
+namespace {
+
+struct Runner {
+  Ctx* ctx = nullptr;
+  VxtRunnerConfig cfg{};
+  std::vector<VxtRunnerLayer> layers;
+  const float* out_norm = nullptr;
+  void* head = nullptr;
+  void* embed = nullptr;
+  void* arena = nullptr;
+  float* cur = nullptr;        // [max_batch][hidden] residual stream
+  float* delta = nullptr;      // [max_batch][hidden]
+  uint16_t* normed = nullptr;  // [max_batch][hidden] bf16
+  float* qkv = nullptr;        // [max_batch][qkv_rows]
+  float* attn = nullptr;       // [max_batch][n_head * head_dim]
+  uint16_t* act = nullptr;     // [max_batch][ffn] bf16
+  float* logits = nullptr;     // [vocab]
+  uint32_t* tok_in = nullptr;  // [max_batch] ids of a batched step
+  uint32_t* tok = nullptr;     // [2] greedy id and flag; the single-token step embeds tok[0]
+  uint32_t* dpos = nullptr;    // [2] position, rope position of the single-token step
+  uint32_t* hist = nullptr;    // [max_seq][2] greedy id and flag per position
+  std::vector<VxtKvQ8Cache> caches;
+  uint32_t q_rows = 0, kvd = 0, qkv_rows = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  uint32_t seed[4] = {};       // host words copied into tok / dpos before a step
+};
+
+// A failed entry point call inside the runner: its code and message.
+void call_ok(int rc, const char* what, const char* err) {
+  if (rc != VXT_OK) fail(rc, std::string(what) + ": " + err);
+}
+
+VxtGqaParams runner_params(const Runner& r, uint32_t layer) {
+  VxtGqaParams p{};
+  p.q_norm = r.layers[layer].q_norm;
+  p.k_norm = r.layers[layer].k_norm;
+  p.n_head = r.cfg.n_head;
+  p.gated_q = r.cfg.gated_q;
+  p.rope_dim = r.cfg.rope_dim;
+  p.rope_neox = r.cfg.rope_neox;
+  p.rope_freq_base = r.cfg.rope_freq_base;
+  p.eps = r.cfg.eps;
+  return p;
+}
+
+// The layers and the head for m tokens whose embeddings are in cur; the
+// attention at host position pos (m tokens) or, with dpos, at the device
+// position (m == 1).  logits of the last token.
+void runner_layers(Runner& r, uint32_t m, uint32_t pos, bool device_pos, hipStream_t s) {
+  Ctx* c = r.ctx;
+  void* ctx = c;
+  const VxtRunnerConfig& g = r.cfg;
+  char e[256];
+  const size_t H = g.hidden;
+  for (uint32_t l = 0; l < g.n_layers; ++l) {
+    const VxtRunnerLayer& L = r.layers[l];
+    call_ok(vxt_hip_rms_norm_dev(ctx, r.cur, l ? r.delta : nullptr, L.attn_norm, r.normed, VXT_DTYPE_BF16, g.hidden,
+                                 g.hidden, m, g.eps, s, e, sizeof e),
+            "attention norm", e);
+    call_ok(vxt_hip_matmul_dev(ctx, L.w_in, r.normed, VXT_DTYPE_BF16, m, r.qkv, VXT_DTYPE_F32, s, e, sizeof e),
+            "qkv projection", e);
+    const VxtGqaParams p = runner_params(r, l);
+    const float* k = r.qkv + r.q_rows;
+    const float* v = r.qkv + r.q_rows + r.kvd;
+    if (device_pos) {
+      const vxt::KvQ8Dev kc = kv_cache_dev(&r.caches[l]);
+      vxt::GqaPrep a = gqa_prep_args(kc, &p, r.qkv, r.qkv_rows, k, v, r.qkv_rows, 1, 0, 0);
+      a.dpos = r.dpos;
+      const hipError_t he = vxt::launch_attn_step(kc, a, p.rope_dim, p.rope_freq_base, r.attn, c->ws, s);
+      if (he != hipSuccess) fail(VXT_E_DEVICE, std::string("attention step launch failed: ") + hipGetErrorString(he));
+    } else {
+      call_ok(vxt_hip_attn_step_q8_dev(ctx, &r.caches[l], &p, r.qkv, r.qkv_rows, k, v, r.qkv_rows, m, pos, pos,
+                                       r.attn, s, e, sizeof e),
+              "attention", e);
+    }
+    call_ok(vxt_hip_matmul_dev(ctx, L.w_out, r.attn, VXT_DTYPE_F32, m, r.delta, VXT_DTYPE_F32, s, e, sizeof e),
+            "output projection", e);
+    call_ok(vxt_hip_rms_norm_dev(ctx, r.cur, r.delta, L.post_attn_norm, r.normed, VXT_DTYPE_BF16, g.hidden, g.hidden,
+                                 m, g.eps, s, e, sizeof e),
+            "post-attention norm", e);
+    call_ok(vxt_hip_ffn_glu_dev(ctx, L.w_ffn_gu, r.normed, VXT_DTYPE_BF16, m, r.act, VXT_DTYPE_BF16, g.ffn,
+                                g.activation, s, e, sizeof e),
+            "gated FFN", e);
+    call_ok(vxt_hip_matmul_dev(ctx, L.w_ffn_dn, r.act, VXT_DTYPE_BF16, m, r.delta, VXT_DTYPE_F32, s, e, sizeof e),
+            "down projection", e);
+  }
+  // the last token only: its final norm and the head
+  float* cur_last = r.cur + (size_t)(m - 1) * H;
+  const float* delta_last = r.delta + (size_t)(m - 1) * H;
+  uint16_t* normed_last = r.normed + (size_t)(m - 1) * H;
+  call_ok(vxt_hip_rms_norm_dev(ctx, cur_last, g.n_layers ? delta_last : nullptr, r.out_norm, normed_last,
+                               VXT_DTYPE_BF16, g.hidden, g.hidden, 1, g.eps, s, e, sizeof e),
+          "output norm", e);
+  call_ok(vxt_hip_matmul_dev(ctx, r.head, normed_last, VXT_DTYPE_BF16, 1, r.logits, VXT_DTYPE_F32, s, e, sizeof e),
+          "head", e);
+}
+
+// The single-token step as captured: embedding of tok[0], the layers at the
+// device position, the head, the greedy id into tok, the history row and the
+// position advanced.
+void runner_enqueue_token(Runner& r, hipStream_t s) {
+  char e[256];
+  call_ok(vxt_hip_embed_dev(r.ctx, r.embed, r.tok, 1, r.cfg.embed_scale, r.cur, r.cfg.hidden, s, e, sizeof e),
+          "embedding", e);
+  runner_layers(r, 1, 0, true, s);
+  call_ok(vxt_hip_greedy_dev(r.ctx, r.logits, r.cfg.vocab, r.tok, s, e, sizeof e), "greedy", e);
+  hipLaunchKernelGGL(runner_advance_kernel, dim3(1), dim3(64), 0, s, r.dpos, r.tok, r.hist, r.cfg.max_seq);
+  const hipError_t he = hipGetLastError();
+  if (he != hipSuccess) fail(VXT_E_DEVICE, std::string("runner advance launch failed: ") + hipGetErrorString(he));
+}
+
+void release_runner(Runner* r) {
+  (void)hipSetDevice(r->ctx->device);
+  (void)hipStreamSynchronize(r->ctx->stream);
+  if (r->exec) (void)hipGraphExecDestroy(r->exec);
+  if (r->graph) (void)hipGraphDestroy(r->graph);
+  if (r->arena) (void)hipFree(r->arena);
+  delete r;
+}
+
+Runner* as_runner(void* p) {
+  if (!p) fail(VXT_E_ARG, "null runner handle");
+  if (!reg_live(p)) fail(VXT_E_ARG, "destroyed or unknown runner handle");
+  return static_cast<Runner*>(p);
+}
+
+// Puts the host position into dpos (both words) and the token into tok[0].
+void runner_seed(Runner& r, uint32_t token, uint32_t pos) {
+  r.seed[0] = token;
+  r.seed[1] = 0u;
+  r.seed[2] = pos;
+  r.seed[3] = pos;
+  VXT_HIP_CHECK(hipMemcpyAsync(r.tok, r.seed, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, r.ctx->stream));
+  VXT_HIP_CHECK(hipMemcpyAsync(r.dpos, r.seed + 2, 2 * sizeof(uint32_t), hipMemcpyHostToDevice, r.ctx->stream));
+}
+
+}  // namespace
+
+void* vxt_hip_runner_create(void* ctx, const VxtRunnerConfig* cfg, const VxtRunnerLayer* layers,
+                            const float* output_norm, void* lm_head, void* embed, char* err, size_t err_cap) {
+  Runner* out = nullptr;
+  guarded(err, err_cap, [&] {
+    Ctx* c = as_ctx(ctx);
+    if (!cfg || (!layers && cfg->n_layers)) fail(VXT_E_ARG, "null config or layers");
+    if (!output_norm) fail(VXT_E_ARG, "null output norm");
+    const VxtRunnerConfig g = *cfg;
+    if (g.hidden == 0 || g.n_head == 0 || g.n_kv == 0 || g.ffn == 0 || g.vocab == 0 || g.max_seq == 0 ||
+        g.max_batch == 0)
+      fail(VXT_E_SHAPE, "hidden, n_head, n_kv, ffn, vocab, max_seq and max_batch must be positive");
+    if (g.head_dim != 32 && g.head_dim != 64 && g.head_dim != 128 && g.head_dim != 256)
+      fail(VXT_E_UNSUPPORTED, "head_dim must be 32, 64, 128 or 256");
+    if (g.n_head % g.n_kv != 0) fail(VXT_E_SHAPE, "n_head must be a multiple of n_kv");
+    if (g.n_head / g.n_kv > 8) fail(VXT_E_UNSUPPORTED, "at most 8 query heads per kv head");
+    if (g.gated_q > 1 || g.rope_neox > 1 || g.activation > VXT_ACT_GELU_TANH)
+      fail(VXT_E_ARG, "gated_q, rope_neox or activation out of range");
+    if (g.max_batch > 65535 || g.max_seq > (1u << 24)) fail(VXT_E_SHAPE, "max_batch or max_seq too large");
+    if (!(g.eps >= 0.0f) || !std::isfinite(g.rope_freq_base) || !std::isfinite(g.embed_scale))
+      fail(VXT_E_ARG, "eps, rope_freq_base or embed_scale out of range");
+    auto shape = [&](void* h, uint32_t rows, uint32_t cols, const char* what) {
+      Tensor* t = as_tensor(h);
+      if (t->ctx != c) fail(VXT_E_ARG, std::string(what) + " belongs to another context");
+      if (t->rows != rows || t->cols != cols) fail(VXT_E_SHAPE, std::string(what) + " has the wrong shape");
+    };
+    const uint32_t q_rows = g.n_head * g.head_dim * (g.gated_q ? 2u : 1u);
+    const uint32_t kvd = g.n_kv * g.head_dim, attn_w = g.n_head * g.head_dim;
+    for (uint32_t l = 0; l < g.n_layers; ++l) {
+      const VxtRunnerLayer& L = layers[l];
+      shape(L.w_in, q_rows + 2u * kvd, g.hidden, "w_in");
+      shape(L.w_out, g.hidden, attn_w, "w_out");
+      shape(L.w_ffn_gu, 2u * g.ffn, g.hidden, "w_ffn_gu");
+      shape(L.w_ffn_dn, g.hidden, g.ffn, "w_ffn_dn");
+      if (!L.attn_norm || !L.post_attn_norm) fail(VXT_E_ARG, "null layer norm");
+    }
+    shape(lm_head, g.vocab, g.hidden, "lm_head");
+    {
+      Tensor* t = as_tensor(embed);
+      if (t->ctx != c) fail(VXT_E_ARG, "embed belongs to another context");
+      if (t->cols != g.hidden) fail(VXT_E_SHAPE, "embed width != hidden");
+    }
+    use_device(c);
+    std::unique_ptr<Runner> r(new Runner());
+    r->ctx = c;
+    r->cfg = g;
+    r->layers.assign(layers, layers + g.n_layers);
+    r->out_norm = output_norm;
+    r->head = lm_head;
+    r->embed = embed;
+    r->q_rows = q_rows;
+    r->kvd = kvd;
+    r->qkv_rows = q_rows + 2u * kvd;
+    // One arena: activations, ids, then per layer K / V values and scales.
+    const size_t B = g.max_batch;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      const size_t o = off;
+      off += align256(bytes);
+      return o;
+    };
+    const size_t o_cur = take(B * g.hidden * 4), o_delta = take(B * g.hidden * 4), o_normed = take(B * g.hidden * 2);
+    const size_t o_qkv = take(B * r->qkv_rows * 4), o_attn = take(B * attn_w * 4), o_act = take(B * g.ffn * 2);
+    const size_t o_logits = take((size_t)g.vocab * 4), o_tin = take(B * 4), o_tok = take(8), o_dpos = take(8);
+    const size_t o_hist = take((size_t)g.max_seq * 8);
+    std::vector<size_t> o_kv(4 * (size_t)g.n_layers);
+    for (uint32_t l = 0; l < g.n_layers; ++l) {
+      o_kv[4 * l] = take((size_t)g.max_seq * kvd);
+      o_kv[4 * l + 1] = take((size_t)g.max_seq * (kvd / 32) * 2);
+      o_kv[4 * l + 2] = take((size_t)g.max_seq * kvd);
+      o_kv[4 * l + 3] = take((size_t)g.max_seq * (kvd / 32) * 2);
+    }
+    VXT_HIP_CHECK(hipMalloc(&r->arena, off));
+    VXT_HIP_CHECK(hipMemsetAsync(r->arena, 0, off, c->stream));
+    char* base = static_cast<char*>(r->arena);
+    r->cur = reinterpret_cast<float*>(base + o_cur);
+    r->delta = reinterpret_cast<float*>(base + o_delta);
+    r->normed = reinterpret_cast<uint16_t*>(base + o_normed);
+    r->qkv = reinterpret_cast<float*>(base + o_qkv);
+    r->attn = reinterpret_cast<float*>(base + o_attn);
+    r->act = reinterpret_cast<uint16_t*>(base + o_act);
+    r->logits = reinterpret_cast<float*>(base + o_logits);
+    r->tok_in = reinterpret_cast<uint32_t*>(base + o_tin);
+    r->tok = reinterpret_cast<uint32_t*>(base + o_tok);
+    r->dpos = reinterpret_cast<uint32_t*>(base + o_dpos);
+    r->hist = reinterpret_cast<uint32_t*>(base + o_hist);
+    for (uint32_t l = 0; l < g.n_layers; ++l)
+      r->caches.push_back(VxtKvQ8Cache{base + o_kv[4 * l], base + o_kv[4 * l + 1], base + o_kv[4 * l + 2],
+                                       base + o_kv[4 * l + 3], g.max_seq, g.n_kv, g.head_dim, 0});
+    // The single-token step's attention partial sums for the whole cache,
+    // then the capture (nothing in it allocates).
+    ensure_ws(c, vxt::attn_workspace_bytes(g.n_head, g.max_seq, g.n_kv, g.head_dim, 1), c->stream);
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+    if (c->capturing) fail(VXT_E_ARG, "a capture is in progress on this context");
+    VXT_HIP_CHECK(hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+    c->capturing = true;
+    try {
+      runner_enqueue_token(*r, c->stream);
+    } catch (...) {
+      c->capturing = false;
+      hipGraph_t junk = nullptr;
+      (void)hipStreamEndCapture(c->stream, &junk);
+      if (junk) (void)hipGraphDestroy(junk);
+      (void)hipFree(r->arena);
+      r->arena = nullptr;
+      throw;
+    }
+    c->capturing = false;
+    VXT_HIP_CHECK(hipStreamEndCapture(c->stream, &r->graph));
+    const hipError_t ie = hipGraphInstantiate(&r->exec, r->graph, nullptr, nullptr, 0);
+    if (ie != hipSuccess) {
+      (void)hipGraphDestroy(r->graph);
+      (void)hipFree(r->arena);
+      fail(VXT_E_DEVICE, std::string("hipGraphInstantiate failed: ") + hipGetErrorString(ie));
+    }
+    out = r.release();
+    {
+      std::lock_guard<std::mutex> lk(c->mu);
+      c->runners.insert(out);
+    }
+    reg_add(out);
+  });
+  return out;
+}
+
+int vxt_hip_runner_step(void* runner, const uint32_t* tok_ids, uint32_t batch_m, uint32_t pos_base,
+                        float* logits_out, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Runner* r = as_runner(runner);
+    Ctx* c = r->ctx;
+    const VxtRunnerConfig& g = r->cfg;
+    if (!tok_ids) fail(VXT_E_ARG, "null token ids");
+    if (batch_m == 0 || batch_m > g.max_batch) fail(VXT_E_SHAPE, "need 1 <= batch_m <= max_batch");
+    if (pos_base >= g.max_seq || batch_m > g.max_seq - pos_base) fail(VXT_E_SHAPE, "pos_base + batch_m > max_seq");
+    for (uint32_t i = 0; i < batch_m; ++i)
+      if (tok_ids[i] >= g.vocab) fail(VXT_E_ARG, "token id out of vocabulary range");
+    if (c->capturing) fail(VXT_E_ARG, "a capture is in progress on this context");
+    use_device(c);
+    if (batch_m == 1) {
+      runner_seed(*r, tok_ids[0], pos_base);
+      VXT_HIP_CHECK(hipGraphLaunch(r->exec, c->stream));
+    } else {
+      char e[256];
+      VXT_HIP_CHECK(hipMemcpyAsync(r->tok_in, tok_ids, (size_t)batch_m * 4, hipMemcpyHostToDevice, c->stream));
+      call_ok(vxt_hip_embed_dev(c, r->embed, r->tok_in, batch_m, g.embed_scale, r->cur, g.hidden, c->stream, e,
+                                sizeof e),
+              "embedding", e);
+      runner_layers(*r, batch_m, pos_base, false, c->stream);
+    }
+    if (logits_out)
+      VXT_HIP_CHECK(hipMemcpyAsync(logits_out, r->logits, (size_t)g.vocab * 4, hipMemcpyDeviceToHost, c->stream));
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+  });
+}
+
+int vxt_hip_runner_generate(void* runner, uint32_t token, uint32_t pos_base, uint32_t n_steps, uint32_t* tokens_out,
+                            uint32_t* flags_out, char* err, size_t err_cap) {
+  return guarded(err, err_cap, [&] {
+    Runner* r = as_runner(runner);
+    Ctx* c = r->ctx;
+    const VxtRunnerConfig& g = r->cfg;
+    if (n_steps == 0) return;
+    if (!tokens_out) fail(VXT_E_ARG, "null tokens_out");
+    if (token >= g.vocab) fail(VXT_E_ARG, "token id out of vocabulary range");
+    if (pos_base >= g.max_seq || n_steps > g.max_seq - pos_base) fail(VXT_E_SHAPE, "pos_base + n_steps > max_seq");
+    if (c->capturing) fail(VXT_E_ARG, "a capture is in progress on this context");
+    use_device(c);
+    runner_seed(*r, token, pos_base);
+    for (uint32_t i = 0; i < n_steps; ++i) VXT_HIP_CHECK(hipGraphLaunch(r->exec, c->stream));
+    std::vector<uint32_t> h(2 * (size_t)n_steps);
+    VXT_HIP_CHECK(hipMemcpyAsync(h.data(), r->hist + 2 * (size_t)pos_base, h.size() * 4, hipMemcpyDeviceToHost,
+                                 c->stream));
+    VXT_HIP_CHECK(hipStreamSynchronize(c->stream));
+    for (uint32_t i = 0; i < n_steps; ++i) {
+      tokens_out[i] = h[2 * i];
+      if (flags_out) flags_out[i] = h[2 * i + 1];
+    }
+  });
+}
+
+void vxt_hip_runner_destroy(void* runner) {
+  if (!runner || !reg_take(runner)) return;   // released already (or with its context)
+  Runner* r = static_cast<Runner*>(runner);
+  {
+    std::lock_guard<std::mutex> lk(r->ctx->mu);
+    r->ctx->runners.erase(r);
+  }
+  release_runner(r);
+}
 
 }  // extern "C"

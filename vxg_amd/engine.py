@@ -63,6 +63,7 @@ ABI_SYMBOLS = (
     "vxt_hip_matmul_noalloc_dev", "vxt_hip_read_probe_dev", "vxt_hip_last_kernel_ms", "vxt_hip_set_gemm_path", "vxt_hip_device_alloc", "vxt_hip_device_free", "vxt_hip_memcpy",
     "vxt_hip_stream", "vxt_hip_synchronize", "vxt_hip_capture_begin", "vxt_hip_capture_end",
     "vxt_hip_graph_launch", "vxt_hip_graph_free",
+    "vxt_hip_runner_create", "vxt_hip_runner_step", "vxt_hip_runner_generate", "vxt_hip_runner_destroy",
 )
 
 
@@ -121,6 +122,23 @@ class GqaParams(C.Structure):
     _fields_ = [("q_norm", C.c_void_p), ("k_norm", C.c_void_p), ("q_bias", C.c_void_p), ("k_bias", C.c_void_p),
                 ("v_bias", C.c_void_p), ("n_head", C.c_uint32), ("gated_q", C.c_uint32), ("rope_dim", C.c_uint32),
                 ("rope_neox", C.c_uint32), ("rope_freq_base", C.c_float), ("eps", C.c_float)]
+
+
+class RunnerLayer(C.Structure):
+    """``VxtRunnerLayer``: one decoder layer's tensors (handles) and device
+    norm weights (0 = none for q_norm / k_norm)."""
+    _fields_ = [("w_in", C.c_void_p), ("w_out", C.c_void_p), ("w_ffn_gu", C.c_void_p), ("w_ffn_dn", C.c_void_p),
+                ("attn_norm", C.c_void_p), ("post_attn_norm", C.c_void_p), ("q_norm", C.c_void_p),
+                ("k_norm", C.c_void_p)]
+
+
+class RunnerConfig(C.Structure):
+    """``VxtRunnerConfig``."""
+    _fields_ = [("n_layers", C.c_uint32), ("hidden", C.c_uint32), ("n_head", C.c_uint32), ("n_kv", C.c_uint32),
+                ("head_dim", C.c_uint32), ("ffn", C.c_uint32), ("vocab", C.c_uint32), ("gated_q", C.c_uint32),
+                ("rope_dim", C.c_uint32), ("rope_neox", C.c_uint32), ("activation", C.c_uint32),
+                ("max_seq", C.c_uint32), ("max_batch", C.c_uint32), ("rope_freq_base", C.c_float),
+                ("eps", C.c_float), ("embed_scale", C.c_float)]
 
 
 class HipJob(C.Structure):
@@ -230,6 +248,14 @@ def load_library(path: str = LIB_PATH):
     L.vxt_hip_graph_launch.argtypes = [vp, vp, u32, C.POINTER(C.c_double), cp, sz]
     L.vxt_hip_graph_free.restype = None
     L.vxt_hip_graph_free.argtypes = [vp]
+    L.vxt_hip_runner_create.restype = vp
+    L.vxt_hip_runner_create.argtypes = [vp, C.POINTER(RunnerConfig), C.POINTER(RunnerLayer), vp, vp, vp, cp, sz]
+    L.vxt_hip_runner_step.restype = C.c_int
+    L.vxt_hip_runner_step.argtypes = [vp, C.POINTER(u32), u32, u32, vp, cp, sz]
+    L.vxt_hip_runner_generate.restype = C.c_int
+    L.vxt_hip_runner_generate.argtypes = [vp, u32, u32, u32, C.POINTER(u32), C.POINTER(u32), cp, sz]
+    L.vxt_hip_runner_destroy.restype = None
+    L.vxt_hip_runner_destroy.argtypes = [vp]
     _lib = L
     return L
 
@@ -420,6 +446,45 @@ class Graph:
         self.handle = None
 
 
+class DecodeRunner:
+    """A device-resident decoder (``vxt_hip_runner_*``), the reference's
+    device runner (metal_cb4_fast_ffi.rs:134-206): ``step`` is step_batch,
+    ``generate`` the ring of enqueue_async / wait_cmd."""
+
+    def __init__(self, engine: "HipEngine", handle: int, cfg: RunnerConfig):
+        self._engine = engine
+        self.handle = handle
+        self.cfg = cfg
+
+    def step(self, tokens, pos_base: int, want_logits: bool = True):
+        """Feed ``tokens`` at positions ``pos_base..``; the last token's
+        logits (f32 [vocab]) or None."""
+        ids = np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32).reshape(-1))
+        logits = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        buf = _errbuf()
+        _check(load_library().vxt_hip_runner_step(
+            self.handle, ids.ctypes.data_as(C.POINTER(C.c_uint32)), len(ids), int(pos_base),
+            logits.ctypes.data if logits is not None else None, buf, len(buf)), buf)
+        return logits
+
+    def generate(self, token: int, pos_base: int, n_steps: int):
+        """Greedy ids of ``n_steps`` single-token steps from ``token`` at
+        ``pos_base``, and the per-step non-finite-logits flags."""
+        ids = np.zeros(n_steps, np.uint32)
+        flags = np.zeros(n_steps, np.uint32)
+        buf = _errbuf()
+        _check(load_library().vxt_hip_runner_generate(
+            self.handle, int(token), int(pos_base), int(n_steps), ids.ctypes.data_as(C.POINTER(C.c_uint32)),
+            flags.ctypes.data_as(C.POINTER(C.c_uint32)), buf, len(buf)), buf)
+        return ids, flags
+
+    def free(self) -> None:
+        """Release the runner (a no-op once its engine is closed)."""
+        if self.handle and self._engine.ctx:
+            load_library().vxt_hip_runner_destroy(self.handle)
+        self.handle = None
+
+
 class HipEngine:
     """HIP compute engine for fused compressed-domain GEMV / GEMM (one GPU)."""
 
@@ -604,6 +669,17 @@ class HipEngine:
 
     def kv_q8_cache(self, max_seq: int, n_kv: int, head_dim: int) -> KvQ8Cache:
         return KvQ8Cache(self, max_seq, n_kv, head_dim)
+
+    def runner(self, cfg: RunnerConfig, layers: Sequence[RunnerLayer], output_norm: int,
+               lm_head: GpuPackedTensor, embed: GpuPackedTensor) -> DecodeRunner:
+        """``vxt_hip_runner_create`` over uploaded tensors and device norms."""
+        arr = (RunnerLayer * max(1, len(layers)))(*layers)
+        buf = _errbuf()
+        h = load_library().vxt_hip_runner_create(self.ctx, C.byref(cfg), arr, output_norm, lm_head.handle,
+                                                 embed.handle, buf, len(buf))
+        if not h:
+            _upload_failed(buf)
+        return DecodeRunner(self, h, cfg)
 
     # -- device-pointer calls (asynchronous on `stream`) ----------------------
     def matmul_dev(self, t: GpuPackedTensor, x_ptr: int, x_dtype: int, batch_m: int, y_ptr: int,
