@@ -7,11 +7,12 @@ metal_cb4_fast_run.mm:94-434 behind metal_cb4_fast_ffi.rs:134-206).
 
 Bars:
 * against the eager composition of the entry points it is built from (the
-  same kernels in the same order, attention at host positions, separate KV
-  caches): last-token logits bit-equal after a batched prefill and after every
-  single-token step, and ``generate`` ids equal to the eager greedy loop --
-  the captured step with the position in device memory computes what the
-  entry points compute;
+  same kernels in the same order -- a single token with each layer's norms
+  inside the projections that read them --, attention at host positions,
+  separate KV caches): last-token logits bit-equal after a batched prefill
+  and after every single-token step, and ``generate`` ids equal to the eager
+  greedy loop -- the captured step with the position in device memory
+  computes what the entry points compute;
 * against the oracle's whole forward (oracle.embed_rows, rms_norm, gemv per
   weight kind, GqaStep.step, glu, the projections' inputs rounded to bf16 as
   the device stores them): |logits - ref| <= 5e-3 max|ref| per step (fp32 sums
@@ -122,6 +123,7 @@ class Eager:
         B = MAX_BATCH
         self.caches = [eng.kv_q8_cache(MAX_SEQ, NKV, HD) for _ in model.kinds]
         self.cur, self.delta = eng.alloc(B * H * 4), eng.alloc(B * H * 4)
+        self.cur2 = eng.alloc(H * 4)
         self.normed = eng.alloc(B * H * 2)
         self.qkv_rows = model.q_rows + 2 * model.kvd
         self.qkv = eng.alloc(B * self.qkv_rows * 4)
@@ -132,6 +134,8 @@ class Eager:
         self.g = eng.alloc(8)
 
     def forward(self, tokens, pos):
+        if len(tokens) == 1:
+            return self.forward_one(tokens[0], pos)
         e, m, s = self.eng, self.m, self.eng.stream
         bf, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
         n = len(tokens)
@@ -157,6 +161,35 @@ class Eager:
         e.synchronize()
         return self.logits.download(np.float32, (VOCAB,))
 
+    def forward_one(self, token, pos):
+        """One token: the two norms of a layer inside the projections that
+        read them (vxt_hip_norm_matmul_dev), the residual stream alternating
+        between two buffers."""
+        e, m, s = self.eng, self.m, self.eng.stream
+        bf, f32 = engine.DTYPE_BF16, engine.DTYPE_F32
+        self.tok.upload(np.asarray([token], np.uint32))
+        e.embed_dev(m.embed, self.tok.ptr, 1, self.cur.ptr, H, 1.0, s)
+        res, c = (self.cur.ptr, self.cur2.ptr), 0
+        glu = engine.NORM_GLU_GELU_TANH if m.act == engine.ACT_GELU_TANH else engine.NORM_GLU_SILU
+        for i, L in enumerate(m.layers):
+            e.norm_matmul_dev(m.tensors_by_handle[L.w_in], res[c], self.delta.ptr if i else 0, L.attn_norm, EPS,
+                              res[1 - c] if i else 0, engine.NORM_PLAIN, self.qkv.ptr, f32, self.qkv_rows, s)
+            if i:
+                c = 1 - c
+            k = self.qkv.ptr + m.q_rows * 4
+            v = self.qkv.ptr + (m.q_rows + m.kvd) * 4
+            self.caches[i].step(m.params[i], self.qkv.ptr, k, v, pos, pos, self.attn.ptr, batch_m=1,
+                                q_stride=self.qkv_rows, kv_stride=self.qkv_rows, stream=s)
+            e.matmul_dev(m.tensors_by_handle[L.w_out], self.attn.ptr, f32, 1, self.delta.ptr, f32, s)
+            e.norm_matmul_dev(m.tensors_by_handle[L.w_ffn_gu], res[c], self.delta.ptr, L.post_attn_norm, EPS,
+                              res[1 - c], glu, self.act.ptr, bf, FFN, s)
+            c = 1 - c
+            e.matmul_dev(m.tensors_by_handle[L.w_ffn_dn], self.act.ptr, bf, 1, self.delta.ptr, f32, s)
+        e.rms_norm_dev(res[c], self.delta.ptr, m.out_norm_dev.ptr, self.normed.ptr, bf, H, H, 1, EPS, s)
+        e.matmul_dev(m.head, self.normed.ptr, bf, 1, self.logits.ptr, f32, s)
+        e.synchronize()
+        return self.logits.download(np.float32, (VOCAB,))
+
     def greedy(self):
         self.eng.greedy_dev(self.logits.ptr, VOCAB, self.g.ptr, self.eng.stream)
         self.eng.synchronize()
@@ -166,7 +199,8 @@ class Eager:
     def free(self):
         for c in self.caches:
             c.free()
-        for b in (self.cur, self.delta, self.normed, self.qkv, self.attn, self.act, self.logits, self.tok, self.g):
+        for b in (self.cur, self.cur2, self.delta, self.normed, self.qkv, self.attn, self.act, self.logits, self.tok,
+                  self.g):
             b.free()
 
 

@@ -1372,6 +1372,7 @@ struct Runner {
   void* embed = nullptr;
   void* arena = nullptr;
   float* cur = nullptr;        // [max_batch][hidden] residual stream
+  float* cur2 = nullptr;       // [hidden] its other buffer in the single-token step (norms inside GEMVs)
   float* delta = nullptr;      // [max_batch][hidden]
   uint16_t* normed = nullptr;  // [max_batch][hidden] bf16
   float* qkv = nullptr;        // [max_batch][qkv_rows]
@@ -1407,6 +1408,11 @@ VxtGqaParams runner_params(const Runner& r, uint32_t layer) {
   return p;
 }
 
+// Whether the single-token step builds its two norms per layer inside the
+// projections that read them (vxt_hip_norm_matmul_dev: one launch fewer
+// each, the residual stream alternating between cur and cur2).
+bool runner_fused_norms(const Runner& r) { return r.cfg.hidden <= 4096; }
+
 // The layers and the head for m tokens whose embeddings are in cur; the
 // attention at host position pos (m tokens) or, with dpos, at the device
 // position (m == 1).  logits of the last token.
@@ -1416,13 +1422,24 @@ void runner_layers(Runner& r, uint32_t m, uint32_t pos, bool device_pos, hipStre
   const VxtRunnerConfig& g = r.cfg;
   char e[256];
   const size_t H = g.hidden;
+  const bool fused = m == 1 && runner_fused_norms(r);
+  float* res[2] = {r.cur, r.cur2};   // fused: the residual stream, ping-pong
+  int rc = 0;
   for (uint32_t l = 0; l < g.n_layers; ++l) {
     const VxtRunnerLayer& L = r.layers[l];
-    call_ok(vxt_hip_rms_norm_dev(ctx, r.cur, l ? r.delta : nullptr, L.attn_norm, r.normed, VXT_DTYPE_BF16, g.hidden,
-                                 g.hidden, m, g.eps, s, e, sizeof e),
-            "attention norm", e);
-    call_ok(vxt_hip_matmul_dev(ctx, L.w_in, r.normed, VXT_DTYPE_BF16, m, r.qkv, VXT_DTYPE_F32, s, e, sizeof e),
-            "qkv projection", e);
+    if (fused) {
+      call_ok(vxt_hip_norm_matmul_dev(ctx, L.w_in, res[rc], l ? r.delta : nullptr, L.attn_norm, g.eps,
+                                      l ? res[rc ^ 1] : nullptr, VXT_NORM_PLAIN, r.qkv, VXT_DTYPE_F32, r.qkv_rows, s,
+                                      e, sizeof e),
+              "attention norm + qkv projection", e);
+      if (l) rc ^= 1;
+    } else {
+      call_ok(vxt_hip_rms_norm_dev(ctx, r.cur, l ? r.delta : nullptr, L.attn_norm, r.normed, VXT_DTYPE_BF16,
+                                   g.hidden, g.hidden, m, g.eps, s, e, sizeof e),
+              "attention norm", e);
+      call_ok(vxt_hip_matmul_dev(ctx, L.w_in, r.normed, VXT_DTYPE_BF16, m, r.qkv, VXT_DTYPE_F32, s, e, sizeof e),
+              "qkv projection", e);
+    }
     const VxtGqaParams p = runner_params(r, l);
     const float* k = r.qkv + r.q_rows;
     const float* v = r.qkv + r.q_rows + r.kvd;
@@ -1439,17 +1456,25 @@ void runner_layers(Runner& r, uint32_t m, uint32_t pos, bool device_pos, hipStre
     }
     call_ok(vxt_hip_matmul_dev(ctx, L.w_out, r.attn, VXT_DTYPE_F32, m, r.delta, VXT_DTYPE_F32, s, e, sizeof e),
             "output projection", e);
-    call_ok(vxt_hip_rms_norm_dev(ctx, r.cur, r.delta, L.post_attn_norm, r.normed, VXT_DTYPE_BF16, g.hidden, g.hidden,
-                                 m, g.eps, s, e, sizeof e),
-            "post-attention norm", e);
-    call_ok(vxt_hip_ffn_glu_dev(ctx, L.w_ffn_gu, r.normed, VXT_DTYPE_BF16, m, r.act, VXT_DTYPE_BF16, g.ffn,
-                                g.activation, s, e, sizeof e),
-            "gated FFN", e);
+    if (fused) {
+      const uint32_t mode = g.activation == VXT_ACT_GELU_TANH ? VXT_NORM_GLU_GELU_TANH : VXT_NORM_GLU_SILU;
+      call_ok(vxt_hip_norm_matmul_dev(ctx, L.w_ffn_gu, res[rc], r.delta, L.post_attn_norm, g.eps, res[rc ^ 1], mode,
+                                      r.act, VXT_DTYPE_BF16, g.ffn, s, e, sizeof e),
+              "post-attention norm + gated FFN", e);
+      rc ^= 1;
+    } else {
+      call_ok(vxt_hip_rms_norm_dev(ctx, r.cur, r.delta, L.post_attn_norm, r.normed, VXT_DTYPE_BF16, g.hidden,
+                                   g.hidden, m, g.eps, s, e, sizeof e),
+              "post-attention norm", e);
+      call_ok(vxt_hip_ffn_glu_dev(ctx, L.w_ffn_gu, r.normed, VXT_DTYPE_BF16, m, r.act, VXT_DTYPE_BF16, g.ffn,
+                                  g.activation, s, e, sizeof e),
+              "gated FFN", e);
+    }
     call_ok(vxt_hip_matmul_dev(ctx, L.w_ffn_dn, r.act, VXT_DTYPE_BF16, m, r.delta, VXT_DTYPE_F32, s, e, sizeof e),
             "down projection", e);
   }
   // the last token only: its final norm and the head
-  float* cur_last = r.cur + (size_t)(m - 1) * H;
+  float* cur_last = fused ? res[rc] : r.cur + (size_t)(m - 1) * H;
   const float* delta_last = r.delta + (size_t)(m - 1) * H;
   uint16_t* normed_last = r.normed + (size_t)(m - 1) * H;
   call_ok(vxt_hip_rms_norm_dev(ctx, cur_last, g.n_layers ? delta_last : nullptr, r.out_norm, normed_last,
@@ -1560,7 +1585,8 @@ void* vxt_hip_runner_create(void* ctx, const VxtRunnerConfig* cfg, const VxtRunn
       off += align256(bytes);
       return o;
     };
-    const size_t o_cur = take(B * g.hidden * 4), o_delta = take(B * g.hidden * 4), o_normed = take(B * g.hidden * 2);
+    const size_t o_cur = take(B * g.hidden * 4), o_cur2 = take((size_t)g.hidden * 4);
+    const size_t o_delta = take(B * g.hidden * 4), o_normed = take(B * g.hidden * 2);
     const size_t o_qkv = take(B * r->qkv_rows * 4), o_attn = take(B * attn_w * 4), o_act = take(B * g.ffn * 2);
     const size_t o_logits = take((size_t)g.vocab * 4), o_tin = take(B * 4), o_tok = take(8), o_dpos = take(8);
     const size_t o_hist = take((size_t)g.max_seq * 8);
@@ -1575,6 +1601,7 @@ void* vxt_hip_runner_create(void* ctx, const VxtRunnerConfig* cfg, const VxtRunn
     VXT_HIP_CHECK(hipMemsetAsync(r->arena, 0, off, c->stream));
     char* base = static_cast<char*>(r->arena);
     r->cur = reinterpret_cast<float*>(base + o_cur);
+    r->cur2 = reinterpret_cast<float*>(base + o_cur2);
     r->delta = reinterpret_cast<float*>(base + o_delta);
     r->normed = reinterpret_cast<uint16_t*>(base + o_normed);
     r->qkv = reinterpret_cast<float*>(base + o_qkv);
