@@ -39,9 +39,13 @@ FLAGS = [
 ]
 
 
-# Per-source flags: gemv_q8p.hip keeps MFMA results in VGPRs (its reason is
-# at the top of that file).
-FILE_FLAGS = {"gemv_q8p.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+# Per-source flags: MFMA results in VGPRs where the VALU scales each fresh
+# fragment right after its MFMAs (in AGPRs every element needs a
+# v_accvgpr_read first): the persistent Q8 GEMV (gemv_q8p.hip) and the fused
+# Q8 GEMM (gemm_fused.hip; Q8 M = 128 graph-timed 102 -> 114 and 106 -> 119
+# TFLOP/s on the same box, the g64 instantiations unchanged).
+_VGPR_MFMA = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
+FILE_FLAGS = {"gemv_q8p.hip": _VGPR_MFMA, "gemm_fused.hip": _VGPR_MFMA}
 
 
 def _compile(src: str, obj: str, verbose: bool) -> None:
