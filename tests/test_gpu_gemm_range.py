@@ -185,3 +185,53 @@ def test_gemm_inf_rows_cb4_tile_path(eng):
     keep = np.r_[0:3, 4:7, 8:12]
     check(y[keep], oracle.gemm(m, Xq[keep], threads=THREADS), oracle.decode_rows(m), Xq[keep], False)
     t.free()
+
+
+# g64 tile-path grids with one K-way: 100 x 300 x 1576 splits K in 5 slices
+# with a partial activation tile, a partial weight tile and columns past K
+# inside the last K tile; 128 x 2048 x 2048 splits K in 8 slices; 2048 x
+# 3072 x 512 has one slice per tile over 384 tiles (bf16 rows written
+# through LDS).
+TILE_SLICES = [(100, 300, 1576), (128, 2048, 2048), (2048, 3072, 512)]
+
+
+@pytest.mark.parametrize("M,rows,cols", TILE_SLICES)
+def test_gemm_tile_slices_any_magnitude(eng, M, rows, cols):
+    print(f"gemm tile slices range M={M} rows={rows} cols={cols}", flush=True)
+    m = make("g64", rows, cols, seed=M + cols)
+    t = eng.upload_packed(m)
+    xb = f32_to_bf16_bits(ranged_rows(M, cols, -30, 100, seed=M).astype(np.float32))
+    X = bf16_bits_to_f32(xb).reshape(M, cols)
+    sel = np.unique(np.r_[0:4, M // 2, M - 4:M, np.random.default_rng(M).choice(M, 8, replace=False)])
+    yref = oracle.gemm(m, X[sel], threads=THREADS)
+    W = oracle.decode_rows(m)
+    check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)[sel], yref, W, X[sel], False)
+    check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)[sel], yref, W, X[sel], True)
+    t.free()
+
+
+@pytest.mark.parametrize("M,rows,cols", TILE_SLICES)
+def test_gemm_tile_slices_inf_with_large_finite_entries(eng, M, rows, cols):
+    """The Inf / NaN pattern of test_gemm_inf_with_large_finite_entries on the
+    tile grids above, split K included: the row scale comes from the finite
+    entries, and an Inf reaches the partial sums of its slice."""
+    print(f"gemm tile slices inf M={M} rows={rows} cols={cols}", flush=True)
+    m = make("g64", rows, cols, seed=31)
+    t = eng.upload_packed(m)
+    X = _inf_rows(M, cols, seed=32)
+    xb = f32_to_bf16_bits(X)
+    Xq = bf16_bits_to_f32(xb).reshape(M, cols)
+    sel = np.r_[0:9, M - 3:M]
+    with np.errstate(invalid="ignore", over="ignore"):
+        yref = oracle.gemm(m, Xq[sel], threads=THREADS)
+    for ydt in (engine.DTYPE_F32, engine.DTYPE_BF16):
+        yraw = run_dev(eng, t, xb, engine.DTYPE_BF16, M, ydt)[sel]
+        y = yraw if ydt == engine.DTYPE_F32 else bf16_bits_to_f32(yraw).reshape(yraw.shape)
+        assert np.array_equal(np.isnan(y), np.isnan(yref))
+        assert np.array_equal(np.isinf(y), np.isinf(yref))
+        both = np.isinf(y) & np.isinf(yref)
+        assert np.array_equal(np.sign(y[both]), np.sign(yref[both]))
+        fin = np.all(np.isfinite(yref), axis=1)
+        assert fin.sum() == len(sel) - 2
+        check(yraw[fin], yref[fin], oracle.decode_rows(m), Xq[sel][fin], ydt == engine.DTYPE_BF16)
+    t.free()
