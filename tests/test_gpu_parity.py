@@ -251,6 +251,29 @@ def test_gemv_q8_mfma_batch_edges(eng, M):
         assert np.array_equal(yf.view(np.uint32), yf2.view(np.uint32)), "run-to-run bits"
 
 
+@pytest.mark.parametrize("M", [5, 6, 7, 8])
+def test_gemv_q8_mfma8_batch_edges(eng, M):
+    """Q8 x bf16 at M = 5..8 with K > 4096 and <= 4096 rows (the 8-row MFMA
+    kernel): row counts off the 8-row tile, cols off the 32-column block
+    (pieces past cols read as zero), odd block counts (a pair without its
+    second block) and the longest rows it takes (K = 8192, 256 blocks)."""
+    for rows, cols in [(1, 4104), (13, 6144), (37, 5000), (2049, 6152), (4096, 8192)]:
+        print(f"q8 mfma8 edges M={M} rows={rows} cols={cols}", flush=True)
+        m = synth.make_q8(rows, cols, seed=rows + cols + M)
+        t = eng.upload_packed(m)
+        xb = synth.make_x_bf16(M, cols, seed=cols + 7 * M)
+        X = bf16_bits_to_f32(xb).reshape(M, cols)
+        yf = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        yb = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)
+        yref = gemv_ref(m, X)
+        fl = floor_scale(oracle.decode_rows(m), X)
+        assert max_rel(yf, yref, fl) <= 1e-3, (rows, cols)
+        assert_bf16_close(yb, yref, fl)
+        yf2 = run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)
+        assert np.array_equal(yf.view(np.uint32), yf2.view(np.uint32)), "run-to-run bits"
+        t.free()
+
+
 def test_gemv_deterministic_and_grouping_invariant(eng):
     for kind in ("cb4", "g64", "q8"):
         m = make(kind, 17, 513, seed=3)

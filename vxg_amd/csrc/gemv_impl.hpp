@@ -1729,6 +1729,11 @@ hipError_t launch_q8_mfma_t(const DevTensor& t, const void* x, uint32_t m, void*
 // results in VGPRs).  hipErrorInvalidValue when the shape does not fit it.
 hipError_t launch_q8_lm(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s);
 
+// Q8 x bf16 activations, 5..8 tokens, 8 rows per workgroup
+// (gemv_q8_mfma8_kernel in gemv_q8p.hip), kp / 32 <= kQ8M8MaxNb.
+constexpr uint32_t kQ8M8MaxNb = 256;
+hipError_t launch_q8_m8(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s);
+
 // Grid for the persistent kernel: enough workgroups to fill every CU at the
 // occupancy the LDS footprint allows, never more than there are row blocks.
 template <int MT, int RPW, int WAVES, int NS>
@@ -1946,6 +1951,15 @@ hipError_t launch_kind(const DevTensor& t, const void* x, bool x_bf16, uint32_t 
       if (m == 2) return launch_q8_dot2_m<2>(t, x, m, y, y_bf16, s);
       if (m > 4 && t.cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.kp / 32 <= kQ8MfmaMaxNb<4, 4>)
         return launch_q8_mfma_t<4, 4>(t, x, m, y, y_bf16, s);
+      // Rows longer than two K steps at 5..8 tokens: the 8-row MFMA kernel,
+      // twice the row tiles of the 16-row one.  Graph-timed against dot2, M =
+      // 5 / 8, K = 6144: 2048 rows 11.3 / 11.8 -> 9.6 / 10.1 us, 1024 rows
+      // 11.0 / 11.4 -> 9.2 / 9.8, 4096 rows 17.8 / 18.5 -> 14.0 / 15.5 (8
+      // waves, 6 pairs per batch; 4 waves or 12 pairs per batch were slower);
+      // level at K = 4096, so not taken there.
+      if (m > 4 && t.cols % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 && t.kp > 2 * kStep &&
+          t.kp / 32 <= kQ8M8MaxNb && t.rows <= 4096)
+        return launch_q8_m8(t, x, m, y, y_bf16, s);
       if (m <= 4) return launch_q8_dot2_m<4>(t, x, m, y, y_bf16, s);
       if (m <= 8) return launch_q8_dot2_m<8>(t, x, m, y, y_bf16, s);
       return hipErrorInvalidValue;

@@ -170,6 +170,141 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma_p_kernel(DevTensor t,
   }
 }
 
+// Q8 x bf16 activations, 5..8 tokens, 8 weight rows per workgroup: twice
+// the row tiles of gemv_q8_mfma_kernel (16 rows), for matrices whose row
+// count leaves CUs idle at 16.  One v_mfma_f32_16x16x32_bf16 multiplies
+// both 32-column blocks of a 64-column pair for 8 rows: operand rows
+// (tokens) 0-7 and columns (weight rows) 0-7 carry the pair's first block,
+// operand rows and columns 8-15 its second, so the two diagonal 8 x 8
+// quarters of the result are the two blocks' partial dot products and the
+// off-diagonal quarters (blocks mixed) are dropped.  A result element's
+// block scale depends only on its column, so each lane applies one scale
+// per pair.  Half of each MFMA is kept, as in gemv_q8_mfma_kernel, whose
+// masked operands give the same ratio.  The waves of a workgroup split the
+// pairs (PB pairs of loads in flight per batch); the diagonal quarters of
+// every wave are added through LDS in wave order.
+// Requires cols % 8 == 0, 16-byte aligned activations and kp / 32 <=
+// kQ8M8MaxNb.
+
+template <int WAVES, int PB>
+__global__ __launch_bounds__(WAVES * 64) void gemv_q8_mfma8_kernel(DevTensor t, const uint16_t* __restrict__ x,
+                                                                  void* __restrict__ y, uint32_t M_rt,
+                                                                  uint32_t y_bf16) {
+  constexpr uint32_t kDi = (8 * kQ8M8MaxNb + WAVES * 64 - 1) / (WAVES * 64);   // scale loads per thread
+  __shared__ uint16_t s_d[8 * kQ8M8MaxNb];
+  __shared__ f32x4_t s_red[WAVES][64];
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t rows = t.rows, cols = t.cols, kp = t.kp;
+  const uint32_t nb = kp / 32, np = (nb + 1) / 2;
+  const uint32_t row0 = blockIdx.x * 8;
+  // Lane (c16, grp): operand row / column c16, K elements 8 grp .. 8 grp + 7
+  // of its block; hi = second block of the pair.
+  const uint32_t c16 = lane & 15, grp = lane >> 4, hi = c16 >> 3, r8 = c16 & 7;
+
+  // The tile's scales (rows row0 .., contiguous in the plane), clamped loads.
+  const uint32_t dn = 8 * nb;
+  const size_t dlast = (size_t)rows * nb - 1;
+  uint16_t dv[kDi];
+#pragma unroll
+  for (uint32_t i = 0; i < kDi; ++i) {
+    const size_t idx = (size_t)row0 * nb + tid + i * (WAVES * 64);
+    dv[i] = t.p1[idx < dlast ? idx : dlast];
+  }
+
+  const uint32_t row = row0 + r8 < rows ? row0 + r8 : rows - 1;   // rows past the matrix are never stored
+  const bool tok_live = r8 < M_rt;                                  // operand row c16 is token r8
+  const uint16_t* xr = x + (size_t)(tok_live ? r8 : 0) * cols;
+  const uint8_t* wr = static_cast<const uint8_t*>(t.p0) + (size_t)row * kp;
+  const uint32_t koff = 32 * hi + 8 * grp;   // the lane's columns inside a pair
+  const uint32_t p_begin = wave * np / WAVES, p_end = (wave + 1) * np / WAVES;   // uniform per wave
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  const f32x4_t zero = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc = zero;
+  bool staged = false;
+  for (uint32_t p0 = p_begin; p0 < p_end; p0 += PB) {
+    uint2 wv[PB];
+    u32x4 xv[PB];
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {   // clamped, unconditional loads
+      const uint32_t p = p0 + i < p_end ? p0 + i : p_end - 1;
+      const uint32_t k = p * 64 + koff;
+      // A second block past the row (odd nb) re-reads the first block's
+      // bytes; its activations are past cols (zero) and its scale is 0.
+      wv[i] = *reinterpret_cast<const uint2*>(wr + (k < kp ? k : k - 32));
+      xv[i] = *reinterpret_cast<const u32x4*>(xr + (k < cols ? k : cols - 8));
+    }
+    if (!staged) {   // first batch only (uniform): scales to LDS behind the loads above
+#pragma unroll
+      for (uint32_t i = 0; i < kDi; ++i) {
+        const uint32_t j = tid + i * (WAVES * 64);
+        if (j < dn) s_d[j] = dv[i];
+      }
+      lds_barrier();
+      staged = true;
+    }
+#pragma unroll
+    for (int i = 0; i < PB; ++i) {
+      const uint32_t p = p0 + i;
+      if (p >= p_end) continue;   // uniform
+      const uint32_t k = p * 64 + koff, blk = 2 * p + hi;
+      const bf16x8_t a = __builtin_bit_cast(bf16x8_t, tok_live && k < cols ? xv[i] : z);
+      const f32x4_t c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, q8_bf16x8(wv[i].x, wv[i].y), zero, 0, 0, 0);
+      const float d = blk < nb ? f16_to_f32(s_d[r8 * nb + blk]) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[j] += d * c[j];
+    }
+  }
+  if (!staged) {   // a wave with no pairs still takes part in the staging barrier
+#pragma unroll
+    for (uint32_t i = 0; i < kDi; ++i) {
+      const uint32_t j = tid + i * (WAVES * 64);
+      if (j < dn) s_d[j] = dv[i];
+    }
+    lds_barrier();
+  }
+  // Lane (c16, grp) holds result rows 4 grp .. 4 grp + 3 of column c16: the
+  // first block's quarter in lanes c16 < 8, grp < 2 (tokens 4 grp + j, weight
+  // row c16), the second block's in lanes c16 >= 8, grp >= 2, 40 lanes on.
+  s_red[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && grp < 2 && c16 < 8) {
+    f32x4_t v = zero;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) {
+      const f32x4_t a = s_red[w][lane], b = s_red[w][lane + 40];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) v[j] += a[j] + b[j];
+    }
+    const uint32_t n = row0 + c16;
+    if (n < rows) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t m = 4 * grp + j;
+        if (m < M_rt) {
+          if (y_bf16)
+            static_cast<uint16_t*>(y)[(size_t)m * rows + n] = f32_to_bf16(v[j]);
+          else
+            static_cast<float*>(y)[(size_t)m * rows + n] = v[j];
+        }
+      }
+    }
+  }
+}
+
+template <int WAVES, int PB>
+hipError_t launch_q8_mfma8_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  if (m > 8 || t.cols % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || t.kp / 32 > kQ8M8MaxNb)
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL((gemv_q8_mfma8_kernel<WAVES, PB>), dim3((t.rows + 7) / 8), dim3(WAVES * 64), 0, s, t,
+                     static_cast<const uint16_t*>(x), y, m, (uint32_t)(y_bf16 ? 1u : 0u));
+  return hipGetLastError();
+}
+
+hipError_t launch_q8_m8(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s) {
+  return launch_q8_mfma8_t<8, 6>(t, x, m, y, y_bf16, s);
+}
+
 template <int WAVES, int NS, int PB, int NBUF>
 hipError_t launch_q8_mfma_p_t(const DevTensor& t, const void* x, uint32_t m, void* y, bool y_bf16, hipStream_t s,
                               uint32_t per_cu) {
