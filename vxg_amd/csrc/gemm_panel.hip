@@ -218,6 +218,59 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
   }
 }
 
+// bf16 rows of 16-byte aligned pieces (x_vec) up to NPT * THREADS * 8
+// columns: each row is read once into registers (NPT pieces of 8 columns per
+// thread, all loads in flight together, unconditional from clamped
+// addresses), its maximum combined through LDS, then converted from the
+// registers.  xconv_blocks reads every row twice; this halves the activation
+// reads and takes one memory round trip per row off the launch's tail.
+template <int NPT>
+__device__ __forceinline__ void xconv_rows_bf16(const XConv& c, uint32_t kp) {
+  __shared__ float s_max[THREADS / 64];
+  const uint32_t K = c.cols, np = K / 8, npk = kp / 8, tid = threadIdx.x;
+  for (uint32_t m = blockIdx.x; m < c.m; m += c.blocks) {
+    const uint4* row = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(c.x) + (size_t)m * K);
+    uint4 u[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) u[i] = row[std::min(i * THREADS + tid, np - 1)];
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      if (i * THREADS + tid >= np) continue;
+      const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        mx = fmaxf(mx, finite_abs(__uint_as_float(w[j] << 16)));
+        mx = fmaxf(mx, finite_abs(__uint_as_float(w[j] & 0xffff0000u)));
+      }
+    }
+    mx = lane_reduce<64, true>(mx);
+    if ((tid & 63) == 0) s_max[tid >> 6] = mx;
+    __syncthreads();
+    float b = s_max[0];
+#pragma unroll
+    for (int w = 1; w < THREADS / 64; ++w) b = fmaxf(b, s_max[w]);
+    const int e = row_exponent(b);
+    if (tid == 0) c.xe[m] = e;
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+      const uint32_t pc = i * THREADS + tid;
+      if (pc >= npk) continue;
+      const bool in = pc < np;   // pieces past K are zero
+      const uint32_t w[4] = {u[i].x, u[i].y, u[i].z, u[i].w};
+      uint32_t h[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float a = in ? ldexpf(__uint_as_float(w[j] << 16), e) : 0.0f;   // exact (a power of two)
+        const float bb = in ? ldexpf(__uint_as_float(w[j] & 0xffff0000u), e) : 0.0f;
+        h[j] = pack_h2((_Float16)a, (_Float16)bb);
+      }
+      *reinterpret_cast<uint4*>(c.ah + (size_t)m * kp + pc * 8) = make_uint4(h[0], h[1], h[2], h[3]);
+    }
+    __syncthreads();   // s_max is reused by the next row
+  }
+}
+
 __device__ __forceinline__ float wave_max(float v) { return lane_reduce<64, true>(v); }
 __device__ __forceinline__ float wave_add(float v) { return lane_reduce<64>(v); }
 
@@ -298,7 +351,14 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
   __shared__ __attribute__((aligned(64))) uint32_t s_tab[KIND == KIND_G64 ? 4 * 32 * kTab / 4 : 1];
   __shared__ __attribute__((aligned(64))) float s_cent[48];
   if (blockIdx.x < xc.blocks) {   // uniform per workgroup: the activation conversion's share
-    if (xc.x_bf16)
+    const uint32_t npt = (p.kp / 8 + THREADS - 1) / THREADS;   // 8-column pieces per thread
+    if (xc.x_bf16 && xc.x_vec && npt <= 1)
+      xconv_rows_bf16<1>(xc, p.kp);
+    else if (xc.x_bf16 && xc.x_vec && npt <= 2)
+      xconv_rows_bf16<2>(xc, p.kp);
+    else if (xc.x_bf16 && xc.x_vec && npt <= 4)
+      xconv_rows_bf16<4>(xc, p.kp);
+    else if (xc.x_bf16)
       xconv_blocks<true>(xc, p.kp);
     else
       xconv_blocks<false>(xc, p.kp);
@@ -922,7 +982,11 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   const uint32_t x_vec = (reinterpret_cast<uintptr_t>(x) % 16 == 0) && ((size_t)t.cols * esz) % 16 == 0;
   // One launch: the activation conversion's workgroups first, then one
   // wave per (weight row, 2048-column segment) of the panel decode.
-  XConv xc{x, ah, al, const_cast<int32_t*>(xe), m, t.cols, (uint32_t)x_bf16, x_vec, std::min<uint32_t>(m, 1024u)};
+  // The register-resident conversion takes one row per workgroup (up to
+  // 4096 workgroups); the two-pass one walks rows over at most 1024.
+  const bool xreg = x_bf16 && x_vec && p.kp <= 4u * THREADS * 8u;
+  XConv xc{x, ah, al, const_cast<int32_t*>(xe), m, t.cols, (uint32_t)x_bf16, x_vec,
+           std::min<uint32_t>(m, xreg ? 4096u : 1024u)};
   const uint32_t nseg = (p.kp + 64 * 32 - 1) / (64 * 32);
   const uint32_t pgrid = (uint32_t)(((size_t)t.rows * nseg + 3) / 4);
   hipLaunchKernelGGL((panel_kernel<KIND>), dim3(xc.blocks + pgrid), dim3(THREADS), 0, s, t, p,
