@@ -841,16 +841,21 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   // 2048 x 6144 -> 2048 59 us (128 x 128, no split) against 58-59 us
   // (dense2_kernel, two K slices and the reduction).
   //
-  // Q8 block mode where 128 x 128 tiles alone fill both workgroup slots of
-  // every CU: each block's scale FMAs run while the other workgroup's MFMAs
-  // keep the matrix pipe busy.  Measured (whole call, graph-timed): M = 2048
-  // x 2048 -> 6144 480 vs 444 TFLOP/s on dense2_kernel's block mode, 6144 ->
-  // 2048 level; with fewer tiles the K slices its grid needs cost more
-  // (M = 512 x 6144 -> 2048 239 vs 273), so dense2_kernel keeps those.
+  // Q8 block and hi/lo panels (cb4) from 192 tiles of 128 x 128: the
+  // 128 x 128 large-tile kernel (two workgroups per CU, so one block's scale
+  // FMAs run while the other workgroup's MFMAs keep the matrix pipe busy),
+  // one K range per workgroup.  Measured (whole call, graph-timed, against
+  // dense2_kernel unless stated): Q8 M = 2048 x 2048 -> 6144 480 vs 444
+  // TFLOP/s; Q8 M = 512 x 2048 -> 6144 287 vs 227 and cb4 230 vs 204; Q8
+  // M = 2048 x 6144 -> 2048 434 vs 409 with two K slices on the same kernel
+  // (one slice was better at 192 and 256 tiles for both panels).  At 64
+  // tiles (M = 512 x 6144 -> 2048) the K slices the grid needs cost more
+  // (Q8 258 vs 268, cb4 217 vs 223), so dense2_kernel keeps those.
   //
-  // hi/lo panels (cb4) at large batches of the wide projections: 256 x 128
-  // tiles (lab, dense phase alone, M = 2048 x 2048 -> 6144: 122.6 vs 128.4
-  // us; M = 4096: 226 vs 278 us).
+  // hi/lo panels at large batches: 256 x 128 tiles (lab, dense phase alone,
+  // M = 2048 x 2048 -> 6144: 122.6 vs 128.4 us; M = 4096: 226 vs 278 us);
+  // also at 2048 x 2048 outputs, in two K slices (389 vs 371 TFLOP/s whole
+  // call at M = 2048 x 6144 -> 2048, 381 for 128 x 128 tiles).
   pl.d3cfg = -1;
   pl.d3mode = 0;
   const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
@@ -858,22 +863,28 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
     const uint32_t t192 = ((m + 255) / 256) * (t.rows / 192);
     if (t.rows % 192 == 0 && t192 >= 224) pl.d3cfg = 1;
     else if (t128 >= 224) pl.d3cfg = 3;
-  } else if (x_bf16 && !lib && pl.wmode == kWQBlock && t128 >= 256) {
+  } else if (x_bf16 && !lib && pl.wmode == kWQBlock && t128 >= 192) {
     pl.d3cfg = 3;
     pl.d3mode = 2;
-  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && m >= 2048 && t.rows >= 4096) {
+  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && m >= 2048 && (t.rows >= 4096 || t128 >= 256)) {
     pl.d3cfg = 2;
+    pl.d3mode = 1;
+  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && t128 >= 192) {
+    pl.d3cfg = 3;
     pl.d3mode = 1;
   }
   if (pl.d3cfg >= 0) {
     // K slices until the grid fills the CUs (one workgroup per CU at 256 x
-    // 192, two at 128 x 128), each slice at least 8 tiles of 32 columns
+    // 192 and 256 x 128, two at 128 x 128), each slice at least 8 tiles of
+    // 32 columns; none for the Q8 block and hi/lo panels on 128 x 128 tiles
+    // (measured above).
     const uint32_t bm = pl.d3cfg == 3 ? 128 : 256, bn = pl.d3cfg == 1 ? 192 : 128;
     const uint32_t slots = pl.d3cfg == 3 ? 512 : 256;
     const uint32_t tiles3 = ((m + bm - 1) / bm) * ((t.rows + bn - 1) / bn);
     const uint32_t kt32 = pl.kp / 32;
     uint32_t sp = 1;
-    while (tiles3 * sp * 2 <= slots && kt32 / (sp * 2) >= 8) sp *= 2;
+    const bool one_slice = pl.d3cfg == 3 && pl.d3mode != 0;
+    while (!one_slice && tiles3 * sp * 2 <= slots && kt32 / (sp * 2) >= 8) sp *= 2;
     pl.kt_per_split = (kt32 + sp - 1) / sp;
     pl.splits = (kt32 + pl.kt_per_split - 1) / pl.kt_per_split;
   }
