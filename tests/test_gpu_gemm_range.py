@@ -132,7 +132,8 @@ def _inf_rows(M, cols, seed):
     ("g64", 192, 128, engine.GEMM_AUTO), ("g64", 192, 300, engine.GEMM_AUTO), ("g64", 192, 300, engine.GEMM_PANEL),
     ("g64", 192, 128, engine.GEMM_FUSED), ("g64", 6144, 2048, engine.GEMM_PANEL),
     ("q8", 192, 128, engine.GEMM_AUTO), ("q8", 192, 300, engine.GEMM_PANEL), ("q8", 2048, 2048, engine.GEMM_AUTO),
-    ("cb4", 192, 300, engine.GEMM_PANEL), ("cb4", 192, 2048, engine.GEMM_AUTO), ("cb4", 4096, 2048, engine.GEMM_AUTO)])
+    ("cb4", 192, 300, engine.GEMM_PANEL), ("cb4", 192, 2048, engine.GEMM_AUTO), ("cb4", 4096, 2048, engine.GEMM_AUTO),
+    ("cb4", 4096, 1024, engine.GEMM_AUTO), ("cb4", 2048, 2048, engine.GEMM_AUTO), ("q8", 6144, 512, engine.GEMM_AUTO)])
 def test_gemm_inf_with_large_finite_entries(eng, kind, rows, M, path):
     """Rows holding an Inf and finite entries above 65504 give exactly the
     oracle's pattern of +-Inf and NaN outputs (gemm_cpu: w * Inf is +-Inf, or

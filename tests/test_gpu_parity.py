@@ -406,9 +406,10 @@ def test_gemm_matches_per_token_gemv_96x256x11(eng):
 
 @pytest.mark.parametrize("kind", ["cb4", "g64", "q8"])
 @pytest.mark.parametrize("K,N", [(2048, 6144), (6144, 2048)])
-@pytest.mark.parametrize("M", [128, 512, 2048])
+@pytest.mark.parametrize("M", [128, 512, 1024, 2048])
 def test_gemm_prefill_shapes_bf16(eng, kind, K, N, M):
-    """Config 3: bf16 activations, fp32 accumulate, bf16 output (and f32)."""
+    """Config 3: bf16 activations, fp32 accumulate, bf16 output (and f32);
+    M = 1024 is between the config's batches (the planner's thresholds)."""
     m = make(kind, N, K, seed=K + M)
     t = eng.upload_packed(m)
     xb = synth.make_x_bf16(M, K, seed=M)

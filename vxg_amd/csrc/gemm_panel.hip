@@ -853,9 +853,14 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   // (Q8 258 vs 268, cb4 217 vs 223), so dense2_kernel keeps those.
   //
   // hi/lo panels at large batches: 256 x 128 tiles (lab, dense phase alone,
-  // M = 2048 x 2048 -> 6144: 122.6 vs 128.4 us; M = 4096: 226 vs 278 us);
-  // also at 2048 x 2048 outputs, in two K slices (389 vs 371 TFLOP/s whole
-  // call at M = 2048 x 6144 -> 2048, 381 for 128 x 128 tiles).
+  // M = 2048 x 2048 -> 6144: 122.6 vs 128.4 us; M = 4096: 226 vs 278 us;
+  // whole call at M = 1024 x 2048 -> 6144: 347 vs 305 TFLOP/s on 128 x 128
+  // tiles); also at 2048 x 2048 outputs, in two K slices (389 vs 371 whole
+  // call at M = 2048 x 6144 -> 2048, 381 for 128 x 128 tiles).  Measured and
+  // not taken: g64 at M = 1024 x 2048 -> 6144 on 256 x 128 tiles (509 vs 458
+  // for the tile kernel) needs the tile / two-phase split moved for every
+  // M = 1024..2047 shape, and g64 M = 2048 x 6144 -> 2048 on 128 x 128 tiles
+  // was level with the tile kernel (600 vs 589).
   pl.d3cfg = -1;
   pl.d3mode = 0;
   const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
@@ -866,7 +871,7 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   } else if (x_bf16 && !lib && pl.wmode == kWQBlock && t128 >= 192) {
     pl.d3cfg = 3;
     pl.d3mode = 2;
-  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && m >= 2048 && (t.rows >= 4096 || t128 >= 256)) {
+  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && ((m >= 1024 && t.rows >= 4096) || (m >= 2048 && t128 >= 256))) {
     pl.d3cfg = 2;
     pl.d3mode = 1;
   } else if (x_bf16 && !lib && pl.wmode == kWHiLo && t128 >= 192) {
