@@ -48,6 +48,7 @@ namespace vxt {
 
 namespace fz {
 
+
 constexpr int BN = 128;      // weight rows per workgroup
 constexpr int BK = 64;       // K tile
 constexpr int KC = 4;        // K tiles per chunk
@@ -78,8 +79,8 @@ constexpr int a_bytes() { return KC * FI * 4 * FRAG; }
 template <uint32_t KIND, int KW>
 constexpr size_t slot_bytes() { return KIND == KIND_G64 ? (size_t)4 * KW * 64 * SLOT : 0; }
 
-// LDS: two activation buffers (reused for the K-way sums at the end), then
-// the g64 table slots.
+// LDS: two activation buffers (the first reused for the K-way sums at the
+// end), then the g64 table slots.
 template <uint32_t KIND, int FI, int KW>
 constexpr size_t lds_bytes() {
   const size_t a = 2 * (size_t)a_bytes<FI>();
@@ -94,32 +95,48 @@ constexpr size_t lds_bytes() {
 // repeat row M-1 (never stored); columns past K are zero.
 template <uint32_t KIND, int FI, int KW>
 __device__ __forceinline__ void issue_a(const uint16_t* __restrict__ x, uint32_t M, uint32_t K, uint32_t x_vec,
-                                        uint32_t m0, uint32_t kt0, uint32_t KT, uint32_t a_lds, char* abuf,
-                                        uint32_t wn, uint32_t wk, uint32_t lane) {
+                                        uint32_t m0, uint32_t kt0, uint32_t KT, char* abuf, uint32_t wn,
+                                        uint32_t wk, uint32_t lane) {
   const uint32_t h = lane >> 5;
+  // Every tile of the chunk inside the rows (uniform): all blocks by DMA,
+  // with no LDS store beside them -- an LDS store after a DMA into the same
+  // buffer would make the compiler wait for the DMA first, one round trip
+  // per block.  The DMA targets are formed from the buffer's own pointer, so
+  // the compiler can tell them from the other buffer's fragment reads.
+  const uint32_t kt_last = std::min(kt0 + KC, KT) - 1;
+  if (x_vec && (kt_last + 1) * BK <= K) {
+#pragma unroll
+    for (int j = 0; j < KC * FI / KW; ++j) {
+      const uint32_t kg = wk + KW * j;   // kl * FI + g
+      const uint32_t kl = kg / FI, g = kg % FI;
+      const uint32_t kt = kt0 + kl;
+      if (kt >= KT) continue;   // uniform
+      const uint32_t col = kt * BK + col8<KIND>(wn, h);
+      const uint32_t row = std::min(m0 + g * 32 + (lane & 31), M - 1);
+      const uint32_t blk = (kg * 4 + wn) * FRAG;
+      __builtin_amdgcn_global_load_lds(x + (size_t)row * K + col, (lds_ptr)(abuf + blk), 16, 0, 0);
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < KC * FI / KW; ++j) {
-    const uint32_t kg = wk + KW * j;   // kl * FI + g
+    const uint32_t kg = wk + KW * j;
     const uint32_t kl = kg / FI, g = kg % FI;
     const uint32_t kt = kt0 + kl;
     if (kt >= KT) continue;   // uniform
     const uint32_t col = kt * BK + col8<KIND>(wn, h);
     const uint32_t row = std::min(m0 + g * 32 + (lane & 31), M - 1);
     const uint32_t blk = (kg * 4 + wn) * FRAG;
-    if (x_vec && (kt + 1) * BK <= K) {   // uniform: the whole tile lies inside the rows
-      __builtin_amdgcn_global_load_lds(x + (size_t)row * K + col, (lds_ptr)(size_t)(a_lds + blk), 16, 0, 0);
-    } else {
-      // element loads from clamped (always valid) addresses, masked after
-      const uint16_t* rowp = x + (size_t)row * K;
-      uint32_t e[8];
+    // element loads from clamped (always valid) addresses, masked after
+    const uint16_t* rowp = x + (size_t)row * K;
+    uint32_t e[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = rowp[std::min(col + i, K - 1)];
-      uint32_t w[4];
+    for (int i = 0; i < 8; ++i) e[i] = rowp[std::min(col + i, K - 1)];
+    uint32_t w[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        w[i] = (col + 2 * i < K ? e[2 * i] : 0u) | ((col + 2 * i + 1 < K ? e[2 * i + 1] : 0u) << 16);
-      *reinterpret_cast<u32x4*>(abuf + blk + lane * 16) = u32x4{w[0], w[1], w[2], w[3]};
-    }
+    for (int i = 0; i < 4; ++i)
+      w[i] = (col + 2 * i < K ? e[2 * i] : 0u) | ((col + 2 * i + 1 < K ? e[2 * i + 1] : 0u) << 16);
+    *reinterpret_cast<u32x4*>(abuf + blk + lane * 16) = u32x4{w[0], w[1], w[2], w[3]};
   }
 }
 
@@ -170,8 +187,7 @@ struct BTile<KIND_G64> {
 template <>
 struct BTile<KIND_Q8> {
   u32x4 q[2];    // int8 values of block b: columns kb + 32b + 16h .. +16
-  uint32_t d0;   // f16 scale of block 0
-  uint32_t d1;   // f16 scale of block 1 (a repeat of block 0's when the row ends first)
+  u32x4 dch;     // (tile 0 of a chunk only) the row's f16 scales of the chunk's 8 blocks
 };
 
 template <uint32_t KIND>
@@ -186,27 +202,36 @@ __device__ __forceinline__ void load_b(const DevTensor& t, uint32_t n, uint32_t 
     // its scale is taken as zero where it is used.  No value is combined
     // here, so every load of the chunk is in flight before the first wait.
     const int8_t* qs = static_cast<const int8_t*>(t.p0) + (size_t)n * kp;
-    const uint16_t* dp = t.p1 + (size_t)n * (kp / 32);
     const uint32_t b1 = kb + 32 < kp ? kb + 32 : kb;
     b.q[0] = *reinterpret_cast<const u32x4*>(qs + kb + 16 * h);
     b.q[1] = *reinterpret_cast<const u32x4*>(qs + b1 + 16 * h);
-    b.d0 = dp[kb / 32];
-    b.d1 = dp[b1 / 32];
   }
 }
 
 // Loads of one chunk for wave (wn, wk): activation blocks into the LDS buffer
-// at abuf (LDS address a_lds), and this lane's packed weights of tiles
+// at abuf, and this lane's packed weights of tiles
 // wk, wk + KW, ... into b.  Tiles past the row repeat its last one (loaded,
 // never used).
 template <uint32_t KIND, int FI, int KW>
 __device__ __forceinline__ void issue_chunk(const DevTensor& t, const uint16_t* __restrict__ x, uint32_t M,
                                             uint32_t x_vec, uint32_t m0, uint32_t n, uint32_t kt0, uint32_t KT,
-                                            uint32_t a_lds, char* abuf, uint32_t wn, uint32_t wk, uint32_t lane,
+                                            char* abuf, uint32_t wn, uint32_t wk, uint32_t lane,
                                             BTile<KIND> (&b)[KC / KW]) {
-  issue_a<KIND, FI, KW>(x, M, t.cols, x_vec, m0, kt0, KT, a_lds, abuf, wn, wk, lane);
+  issue_a<KIND, FI, KW>(x, M, t.cols, x_vec, m0, kt0, KT, abuf, wn, wk, lane);
 #pragma unroll
   for (int j = 0; j < KC / KW; ++j) load_b<KIND>(t, n, std::min(kt0 + wk + KW * j, KT - 1), lane >> 5, b[j]);
+  if constexpr (KIND == KIND_Q8) {
+    // The row's scales of the chunk's 2 * KC blocks, one 16-byte load: the
+    // plane holds kp / 32 scales per row and chunks start at multiples of
+    // 2 * KC blocks, so the load is 4-byte aligned, and the upload keeps 16
+    // bytes after the plane's last scale, so it stays inside the allocation
+    // (scales past the row belong to the next row or the padding; blocks
+    // past the row are never applied).
+    const uint32_t nb = t.kp / 32;
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(t.p1), (short)0, (int)(t.rows * nb * 2u + 16u), 0x00020000);
+    b[0].dch = __builtin_amdgcn_raw_buffer_load_b128(rd, (n * nb + 2u * kt0) * 2u, 0, 0);
+  }
 }
 
 // Decode and multiply this wave's tiles of one chunk (activations at abuf).
@@ -268,7 +293,9 @@ __device__ __forceinline__ void compute_chunk(const DevTensor& t, const char* ab
       }
       if constexpr (KIND == KIND_Q8) {
         if (s & 1) {
-          const float d = s >> 1 ? (kb + 32 < t.kp ? f16_to_f32(b[j].d1) : 0.0f) : f16_to_f32(b[j].d0);
+          const uint32_t e = 2u * kl + (uint32_t)(s >> 1);   // block of the chunk
+          const uint32_t dbits = (b[0].dch[e >> 1] >> (16u * (e & 1u))) & 0xffffu;
+          const float d = (s >> 1) && !(kb + 32 < t.kp) ? 0.0f : f16_to_f32(dbits);
 #pragma unroll
           for (int i = 0; i < FI; ++i)
 #pragma unroll
@@ -291,7 +318,14 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
   constexpr uint32_t BM = 32 * FI;
   constexpr uint32_t AB = a_bytes<FI>();
   constexpr int NT = KC / KW;
-  extern __shared__ __attribute__((aligned(1024))) char smem[];
+  // Two activation buffers and the g64 table slots, each its own array:
+  // the compiler then knows that a DMA into one buffer does not write what
+  // the fragment reads of the other read, and does not wait for it.
+  constexpr size_t SB = slot_bytes<KIND, KW>();
+  __shared__ __attribute__((aligned(1024))) char s_buf0[AB];
+  __shared__ __attribute__((aligned(1024))) char s_buf1[AB];
+  __shared__ __attribute__((aligned(16))) char s_slot[SB > 0 ? SB : 16];
+  static_assert((size_t)(KW - 1) * 4 * FI * 16 * 64 * 4 <= AB, "K-way sums fit in one buffer");
   const uint32_t lane = threadIdx.x & 63, h = lane >> 5;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t wn = wave & 3, wk = wave >> 2;
@@ -303,11 +337,10 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
   const uint32_t c0 = blockIdx.y * chunks_per_split;
   const uint32_t c1 = std::min(nchunks, c0 + chunks_per_split);
   const uint32_t n = std::min(n0 + wn * 32 + (lane & 31), N - 1);
-  const uint32_t lds0 = (uint32_t)(size_t)(lds_ptr)smem;
-  char* const buf0 = smem;
-  char* const buf1 = smem + AB;
+  char* const buf0 = s_buf0;
+  char* const buf1 = s_buf1;
   // g64: this row's two table slots in this wave's region
-  char* slot = smem + (lds_bytes<KIND, FI, KW>() - slot_bytes<KIND, KW>()) + (wave * 64 + (lane & 31)) * SLOT;
+  char* slot = s_slot + (wave * 64 + (lane & 31)) * SLOT;
 
   float16v acc[FI];
 #pragma unroll
@@ -316,7 +349,7 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
     for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 
   BTile<KIND> b0[NT], b1[NT];
-  if (c0 < c1) issue_chunk<KIND, FI, KW>(t, x, M, x_vec, m0, n, c0 * KC, KT, lds0, buf0, wn, wk, lane, b0);
+  if (c0 < c1) issue_chunk<KIND, FI, KW>(t, x, M, x_vec, m0, n, c0 * KC, KT, buf0, wn, wk, lane, b0);
   for (uint32_t c = c0; c < c1; c += 2) {
     wait_vm0();        // chunk c has landed (nothing else is in flight)
     __syncthreads();   // ... for every wave; and the other buffer is free
@@ -325,7 +358,7 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
       __syncthreads();
     }
     if (c + 1 < c1)
-      issue_chunk<KIND, FI, KW>(t, x, M, x_vec, m0, n, (c + 1) * KC, KT, lds0 + AB, buf1, wn, wk, lane, b1);
+      issue_chunk<KIND, FI, KW>(t, x, M, x_vec, m0, n, (c + 1) * KC, KT, buf1, wn, wk, lane, b1);
     compute_chunk<KIND, FI, KW>(t, buf0, slot, b0, c * KC, KT, wk, lane, acc);
     if (c + 1 >= c1) break;
     wait_vm0();
@@ -335,14 +368,14 @@ __global__ __launch_bounds__(256 * KW) void fused_kernel(DevTensor t, const uint
       __syncthreads();
     }
     if (c + 2 < c1)
-      issue_chunk<KIND, FI, KW>(t, x, M, x_vec, m0, n, (c + 2) * KC, KT, lds0, buf0, wn, wk, lane, b0);
+      issue_chunk<KIND, FI, KW>(t, x, M, x_vec, m0, n, (c + 2) * KC, KT, buf0, wn, wk, lane, b0);
     compute_chunk<KIND, FI, KW>(t, buf1, slot, b1, (c + 1) * KC, KT, wk, lane, acc);
   }
 
   // K ways 1.. hand their sums to K way 0 through LDS; added in ascending wk.
   if constexpr (KW > 1) {
     __syncthreads();   // every wave is done with the activation buffers
-    float* red = reinterpret_cast<float*>(smem);
+    float* red = reinterpret_cast<float*>(s_buf0);
     if (wk > 0) {
 #pragma unroll
       for (int i = 0; i < FI; ++i)
@@ -438,12 +471,8 @@ inline Plan plan(const DevTensor& t, uint32_t m) {
 template <uint32_t KIND, int FI, int KW>
 hipError_t launch(const DevTensor& t, const uint16_t* x, uint32_t m, uint32_t x_vec, void* y, bool y_bf16,
                   const Plan& p, float* partial, const int32_t* xe, hipStream_t s) {
-  constexpr size_t lds = lds_bytes<KIND, FI, KW>();
-  static_assert(lds <= 160 * 1024, "LDS budget");
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&fused_kernel<KIND, FI, KW>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((fused_kernel<KIND, FI, KW>), dim3(p.tiles_m * p.tiles_n, p.splits), dim3(256 * KW), lds, s,
+  static_assert(lds_bytes<KIND, FI, KW>() <= 160 * 1024, "LDS budget");   // static arrays in the kernel
+  hipLaunchKernelGGL((fused_kernel<KIND, FI, KW>), dim3(p.tiles_m * p.tiles_n, p.splits), dim3(256 * KW), 0, s,
                      t, x, m, x_vec, y, (uint32_t)y_bf16, partial, p.cps, p.tiles_m, xe);
   return hipGetLastError();
 }
@@ -490,3 +519,4 @@ hipError_t launch_gemm_fused(const DevTensor& t, const uint16_t* x, uint32_t m, 
 }
 
 }  // namespace vxt
+

@@ -452,8 +452,11 @@ void* vxt_hip_upload_q8_0(void* ctx, uint32_t rows, uint32_t cols, const uint8_t
     const uint32_t kp = (uint32_t)(kb * 32u);
     // Split each 34-byte block into an int8 plane and an f16 scale plane so
     // every lane's 16-byte load is aligned and contiguous.
+    // The scale plane keeps 16 bytes after its last scale (zero), so a
+    // 16-byte load of 8 scales that starts at any scale stays inside the
+    // allocation (the fused GEMM reads a chunk's 8 scales per row at once).
     const size_t qs_bytes = align256((size_t)rows * kp);
-    const size_t d_bytes = align256((size_t)rows * kb * 2u);
+    const size_t d_bytes = align256((size_t)rows * kb * 2u + 16u);
     std::vector<char> h(qs_bytes + d_bytes, 0);
     int8_t* qs = reinterpret_cast<int8_t*>(h.data());
     uint16_t* d = reinterpret_cast<uint16_t*>(h.data() + qs_bytes);
