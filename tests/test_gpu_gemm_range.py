@@ -138,7 +138,7 @@ def test_gemm_inf_with_large_finite_entries(eng, kind, rows, M, path):
     """Rows holding an Inf and finite entries above 65504 give exactly the
     oracle's pattern of +-Inf and NaN outputs (gemm_cpu: w * Inf is +-Inf, or
     NaN where w = 0), and finite rows keep the bar.  The g64 tile path (M =
-    128..2047), the fused/tile pin, the dense kernels of the two-phase path
+    128..767), the fused/tile pin, the dense kernels of the two-phase path
     (plain, Q8 block and hi/lo, on both the 128 x 128 and the large-tile
     kernel) are covered."""
     cols = 544
@@ -188,11 +188,11 @@ def test_gemm_inf_rows_cb4_tile_path(eng):
     t.free()
 
 
-# g64 tile-path grids with one K-way: 100 x 300 x 1576 splits K in 5 slices
-# with a partial activation tile, a partial weight tile and columns past K
-# inside the last K tile; 128 x 2048 x 2048 splits K in 8 slices; 2048 x
-# 3072 x 512 has one slice per tile over 384 tiles (bf16 rows written
-# through LDS).
+# g64 tile-kernel grids (GEMM_FUSED pins the tile kernel above batch 64)
+# with one K-way: 100 x 300 x 1576 splits K in 5 slices with a partial
+# activation tile, a partial weight tile and columns past K inside the last K
+# tile; 128 x 2048 x 2048 splits K in 8 slices; 2048 x 3072 x 512 has one
+# slice per tile over 384 tiles (bf16 rows written through LDS).
 TILE_SLICES = [(100, 300, 1576), (128, 2048, 2048), (2048, 3072, 512)]
 
 
@@ -206,8 +206,12 @@ def test_gemm_tile_slices_any_magnitude(eng, M, rows, cols):
     sel = np.unique(np.r_[0:4, M // 2, M - 4:M, np.random.default_rng(M).choice(M, 8, replace=False)])
     yref = oracle.gemm(m, X[sel], threads=THREADS)
     W = oracle.decode_rows(m)
-    check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)[sel], yref, W, X[sel], False)
-    check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)[sel], yref, W, X[sel], True)
+    eng.set_gemm_path(engine.GEMM_FUSED)
+    try:
+        check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_F32)[sel], yref, W, X[sel], False)
+        check(run_dev(eng, t, xb, engine.DTYPE_BF16, M, engine.DTYPE_BF16)[sel], yref, W, X[sel], True)
+    finally:
+        eng.set_gemm_path(engine.GEMM_AUTO)
     t.free()
 
 
@@ -226,7 +230,11 @@ def test_gemm_tile_slices_inf_with_large_finite_entries(eng, M, rows, cols):
     with np.errstate(invalid="ignore", over="ignore"):
         yref = oracle.gemm(m, Xq[sel], threads=THREADS)
     for ydt in (engine.DTYPE_F32, engine.DTYPE_BF16):
-        yraw = run_dev(eng, t, xb, engine.DTYPE_BF16, M, ydt)[sel]
+        eng.set_gemm_path(engine.GEMM_FUSED)
+        try:
+            yraw = run_dev(eng, t, xb, engine.DTYPE_BF16, M, ydt)[sel]
+        finally:
+            eng.set_gemm_path(engine.GEMM_AUTO)
         y = yraw if ydt == engine.DTYPE_F32 else bf16_bits_to_f32(yraw).reshape(yraw.shape)
         assert np.array_equal(np.isnan(y), np.isnan(yref))
         assert np.array_equal(np.isinf(y), np.isinf(yref))

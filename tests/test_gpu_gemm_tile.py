@@ -95,6 +95,21 @@ def test_dense_kernel_modes(eng, kind, M, N, K):
     check(eng, make(kind, N, K, seed=M + K), M, engine.GEMM_PANEL, seed=N)
 
 
+# The large-tile dense kernel (gemm_dense3.hip) streams both operands from
+# planes of 1 KB pieces (16 rows x 32 columns, rows padded to 16): batch and
+# weight row counts that are not multiples of 16, K short of a whole piece,
+# every wave tile and weight mode the planner gives it (plain on 256 x 192,
+# 256 x 128 and 128 x 128; Q8 block on 128 x 128; hi/lo on 128 x 128 and
+# 256 x 128), 128 x 128 in one K range and in two.
+@pytest.mark.parametrize("kind,M,N,K", [("g64", 1800, 5376, 512), ("g64", 1030, 6600, 256),
+                                        ("g64", 1100, 3100, 1000), ("g64", 1000, 1500, 1000),
+                                        ("q8", 1000, 3000, 1000), ("q8", 1000, 1500, 1000),
+                                        ("cb4", 1000, 3000, 1000), ("cb4", 1000, 1500, 1000),
+                                        ("cb4", 4100, 400, 256)])
+def test_large_tile_kernel_ragged(eng, kind, M, N, K):
+    check(eng, make(kind, N, K, seed=M + N), M, engine.GEMM_PANEL, seed=K)
+
+
 def test_dense_kernel_q8_block_scales_extreme(eng):
     """Block scales spanning subnormal to 2^15 in one row (each block's
     fragment is scaled on its own)."""

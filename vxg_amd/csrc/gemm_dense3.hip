@@ -1,6 +1,9 @@
 // gemm_dense3.hip -- large-tile dense phase of the two-phase prefill GEMM:
 // Y = A * W^T with A the row-scaled f16 activations [M][kp] and W the f16
-// weight panel [N][kp] (gemm_panel.hip writes both).
+// weight panel [N][kp] (gemm_panel.hip writes both), each stored in 1 KB
+// pieces of 16 rows x 32 columns: piece (r / 16, k / 32) at byte
+// ((r / 16) * kp / 32 + k / 32) * 1024, row r % 16 at 64 (r % 16) inside,
+// rows padded to a multiple of 16.
 //
 // Reference behaviour: the dense tile product of PackedTensor::gemm_cpu
 // (llm_prefill.rs:156-255) over decoded weights; MFMA products are exact in
@@ -16,7 +19,10 @@
 // Operands move global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 // round trip, no ds_write).  A K tile is 32 columns (64 bytes per row); the
 // hardware writes lane l's 16 bytes at LDS base + 16 l, so one instruction
-// fills 16 rows and the bank swizzle is applied on the global side: lane l
+// fills 16 rows from one contiguous 1 KB piece (eight whole 128-byte lines;
+// row-major planes, 16 half lines at the row stride, measured 28 % slower
+// over the whole Q8 M = 2048 call), and the bank swizzle is applied on the
+// global side: lane l
 // fetches logical chunk (l % 4) ^ ((l >> 4) & 3) of row l / 4, i.e. chunk c
 // of row r sits at position c ^ ((r >> 2) & 3).  Fragment reads (16 lanes =
 // 16 consecutive rows at one logical chunk) then hit 16 distinct 16-byte
@@ -197,34 +203,30 @@ __global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uin
   const uint32_t kt1 = std::min(KTT, kt0 + kt_per_split);
   const uint32_t KT = kt1 - kt0;   // >= 1
 
-  const __amdgpu_buffer_rsrc_t ra = rsrc(ah, (size_t)M * kp * 2);
-  const __amdgpu_buffer_rsrc_t rb = rsrc(bh, (size_t)N * kp * 2);
-  const __amdgpu_buffer_rsrc_t rl = rsrc(LO ? bl : bh, (size_t)N * kp * 2);
+  const size_t pa = (size_t)((M + 15u) & ~15u) * kp * 2, pb = (size_t)((N + 15u) & ~15u) * kp * 2;   // padded planes
+  const __amdgpu_buffer_rsrc_t ra = rsrc(ah, pa);
+  const __amdgpu_buffer_rsrc_t rb = rsrc(bh, pb);
+  const __amdgpu_buffer_rsrc_t rl = rsrc(LO ? bl : bh, pb);
   const uint32_t nblk = kp / BK;   // Q8 block scales per weight row
   const __amdgpu_buffer_rsrc_t rd = rsrc(QB ? (const void*)dsc : (const void*)bh, QB ? (size_t)N * nblk * 4 : 16);
 
   // Per-lane byte offsets of the load instructions (tile 0 of the slice):
-  // instruction j of this wave fills rows 16 (wave + 4 j) .. + 15.
+  // instruction j of this wave fills rows 16 (wave + 4 j) .. + 15, one piece.
   uint32_t va[C::NA], vb[C::NB], vd = 0;
   if constexpr (QB)   // wave w loads the scales of weight rows 64 (w % 2) .. + 63 (waves 2, 3 repeat 0, 1)
     vd = std::min(n0 + 64 * (wave & 1) + lane, N - 1) * nblk * 4 + kt0 * 4;
   {
     const uint32_t r16 = lane >> 2, chunk = (lane & 3) ^ ((lane >> 4) & 3);
+    auto off = [&](uint32_t g) { return (g >> 4) * KTT * 1024u + (g & 15u) * 64u + chunk * 16u + kt0 * 1024u; };
 #pragma unroll
-    for (int j = 0; j < C::NA; ++j) {
-      const uint32_t g = std::min(m0 + 16 * (wave + 4 * j) + r16, M - 1);
-      va[j] = g * kp * 2 + chunk * 16 + kt0 * (BK * 2);
-    }
+    for (int j = 0; j < C::NA; ++j) va[j] = off(std::min(m0 + 16 * (wave + 4 * j) + r16, M - 1));
 #pragma unroll
-    for (int j = 0; j < C::NB; ++j) {
-      const uint32_t g = std::min(n0 + 16 * (wave + 4 * j) + r16, N - 1);
-      vb[j] = g * kp * 2 + chunk * 16 + kt0 * (BK * 2);
-    }
+    for (int j = 0; j < C::NB; ++j) vb[j] = off(std::min(n0 + 16 * (wave + 4 * j) + r16, N - 1));
   }
   // Load piece j (A pieces, then W, then W's lo plane) of slice tile t into
   // stage k.
   auto load_piece = [&](auto k_, int j, uint32_t t) {
-    const uint32_t so = t * (BK * 2);
+    const uint32_t so = t * 1024u;   // the next piece of the same 16 rows
     if (QB && j == C::NLD - 1) {
       dma4(rd, stD(k_) + 256 * (wave & 1), vd, t * 4);
     } else if (j < C::NA) {
@@ -492,8 +494,9 @@ hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, co
 // 0 = 4 x 4 (workgroup tile 256 x 256), 1 = 4 x 3 (256 x 192), 2 = 4 x 2
 // (256 x 128), 3 = 2 x 2 (128 x 128).  wmode 0 = plain f16 panel, 1 = hi/lo
 // panel (bh + bl * 2^-11; cfg 2 and 3), 2 = Q8 block (int8 values as f16 in
-// bh, f32 scales dsc [n][kp / 32]; cfg 3).  kt_per_split counts 32-column K
-// tiles; kp % 32 == 0.
+// bh, f32 scales dsc [n][kp / 32]; cfg 3).  ah, bh and bl are planes of 1 KB
+// pieces (16 rows x 32 columns, rows padded to 16).  kt_per_split counts
+// 32-column K tiles; kp % 32 == 0.
 hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl,
                          const float* dsc, const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
                          float* partial, uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {

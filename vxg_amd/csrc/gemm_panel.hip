@@ -81,6 +81,7 @@ struct Panel {
   float* inv;       // [N] 1 / s
   float* dsc;       // [N][kp/32] block scales (Q8 block mode)
   uint32_t kp;      // K rounded up to BK
+  uint32_t tiled;   // hi / lo in 1 KB pieces (plane_off), else row-major
 };
 
 // How a panel represents the weights.
@@ -91,6 +92,17 @@ enum WMode : int {
 };
 
 __host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~size_t(255); }
+
+// Element offset of (row, col) in an f16 plane of kp columns: row-major, or
+// (tiled) in 1 KB pieces of 16 rows x 32 columns, piece (row / 16, col / 32)
+// at element ((row / 16) * kp / 32 + col / 32) * 512 and row row % 16 at
+// 32 (row % 16) inside it.  The large-tile dense kernel (gemm_dense3.hip)
+// loads one whole piece per wave instruction; a tiled plane holds its rows
+// rounded up to 16.  8 columns from a multiple of 8 stay contiguous.
+__device__ __forceinline__ size_t plane_off(uint32_t row, uint32_t col, uint32_t kp, uint32_t tiled) {
+  return tiled ? ((size_t)(row >> 4) * (kp >> 5) + (col >> 5)) * 512u + (row & 15u) * 32u + (col & 31u)
+               : (size_t)row * kp + col;
+}
 
 __device__ __forceinline__ uint32_t pack_h2(_Float16 a, _Float16 b) {
   return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
@@ -125,6 +137,7 @@ struct XConv {
   uint16_t* al;
   int32_t* xe;   // per-row exponent, written here
   uint32_t m, cols, x_bf16, x_vec, blocks;
+  uint32_t tiled;   // A (and its lo plane) in the panel's piece layout (plane_off)
 };
 
 // 8 activations at column k of row m (zero past K).
@@ -212,8 +225,9 @@ __device__ __forceinline__ void xconv_blocks(const XConv& c, uint32_t kp) {
         if constexpr (!XBF16)
           l[j] = pack_h2((_Float16)lo_part(v[2 * j], (float)h0), (_Float16)lo_part(v[2 * j + 1], (float)h1));
       }
-      *reinterpret_cast<uint4*>(ah + (size_t)m * kp + k) = make_uint4(h[0], h[1], h[2], h[3]);
-      if constexpr (!XBF16) *reinterpret_cast<uint4*>(al + (size_t)m * kp + k) = make_uint4(l[0], l[1], l[2], l[3]);
+      const size_t o = plane_off(m, k, kp, c.tiled);
+      *reinterpret_cast<uint4*>(ah + o) = make_uint4(h[0], h[1], h[2], h[3]);
+      if constexpr (!XBF16) *reinterpret_cast<uint4*>(al + o) = make_uint4(l[0], l[1], l[2], l[3]);
     }
   }
 }
@@ -265,7 +279,7 @@ __device__ __forceinline__ void xconv_rows_bf16(const XConv& c, uint32_t kp) {
         const float bb = in ? ldexpf(__uint_as_float(w[j] & 0xffff0000u), e) : 0.0f;
         h[j] = pack_h2((_Float16)a, (_Float16)bb);
       }
-      *reinterpret_cast<uint4*>(c.ah + (size_t)m * kp + pc * 8) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(c.ah + plane_off(m, pc * 8, kp, c.tiled)) = make_uint4(h[0], h[1], h[2], h[3]);
     }
     __syncthreads();   // s_max is reused by the next row
   }
@@ -322,9 +336,9 @@ __global__ __launch_bounds__(THREADS) void xscale_kernel(const void* __restrict_
   if (lane == 0) xe[m] = row_exponent(mx);
 }
 
-// 8 consecutive f32 weights -> hi (and lo) f16 pieces at column c of the row.
+// 8 consecutive f32 weights -> hi (and lo) f16 pieces at element offset c.
 template <bool SPLIT>
-__device__ __forceinline__ void store8(const float (&w)[8], float s, uint16_t* hi, uint16_t* lo, uint32_t c) {
+__device__ __forceinline__ void store8(const float (&w)[8], float s, uint16_t* hi, uint16_t* lo, size_t c) {
   uint32_t h[4], l[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -376,8 +390,9 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
   // Piece i starts at column c0 + 512 i; KP % 64 == 0, so a piece is wholly
   // inside or outside the panel row.
   const uint32_t c0 = seg + 8 * lane;
-  uint16_t* hi = p.hi + (size_t)n * KP;
-  uint16_t* lo = p.lo + (size_t)n * KP;
+  uint16_t* hi = p.hi;
+  uint16_t* lo = p.lo;
+  auto at = [&](uint32_t c) { return plane_off(n, c, KP, p.tiled); };   // column c of row n
   float s = 1.0f;
   if constexpr (KIND == KIND_G64) {
     // KP <= kp here (kp is a multiple of 64 and at least K).  The segment's
@@ -407,7 +422,7 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
         const uint32_t e1 = c + 2 * j + 1 < K ? tab[(wd[i] >> (8 * j + 4)) & 0xfu] : 0u;
         h[j] = e0 | (e1 << 16);
       }
-      *reinterpret_cast<uint4*>(hi + c) = make_uint4(h[0], h[1], h[2], h[3]);
+      *reinterpret_cast<uint4*>(hi + at(c)) = make_uint4(h[0], h[1], h[2], h[3]);
     }
   } else if constexpr (KIND == KIND_Q8 || KIND == KIND_Q40) {
     // kp may be 32 short of KP: pieces past kp read the row's last 8 bytes
@@ -460,9 +475,9 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
       for (int j = 0; j < 8; ++j)   // gguf.rs:223-229
         w[j] = c + j < K ? (float)(int8_t)((wd[j >> 2] >> ((j & 3) * 8)) & 0xffu) * d[i] : 0.0f;
       if (qblock)   // the int8 value itself, exact in f16
-        store8<false>(w, 1.0f, hi, lo, c);
+        store8<false>(w, 1.0f, hi, lo, at(c));
       else
-        store8<true>(w, s, hi, lo, c);
+        store8<true>(w, s, hi, lo, at(c));
     }
   } else {
     // KP <= kp here (kp is a multiple of 128 and at least K).
@@ -491,7 +506,7 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
       float w[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) w[j] = c + j < K ? sc[i] * cent[(wd[i] >> (4 * j)) & 0xfu] : 0.0f;
-      store8<true>(w, s, hi, lo, c);
+      store8<true>(w, s, hi, lo, at(c));
     }
     // CSR residuals of this segment's columns (codebook.rs:316-333): the lane
     // holding a column's first entry rebuilds the column from sc * cent[q] and
@@ -524,7 +539,7 @@ __global__ __launch_bounds__(THREADS) void panel_kernel(DevTensor t, Panel p, ui
             if ((pk & 0xffffu) == c) v += f16_to_f32_exact(pk >> 16);
           }
         }
-        split_write(v, s, hi, lo, c);
+        split_write(v, s, hi, lo, at(c));
       }
     }
   }
@@ -833,70 +848,62 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   while (tiles * splits < 512 && ktiles / (splits * 2) >= 16) splits *= 2;
   pl.kt_per_split = (ktiles + splits - 1) / splits;
   pl.splits = (ktiles + pl.kt_per_split - 1) / pl.kt_per_split;
-  // Large batches of bf16 activations over a plain f16 panel: the
-  // large-tile kernel, one K range per workgroup.  256 x 192 tiles where the
-  // rows divide (at 2048 x 6144 outputs, one tile per CU), 128 x 128
-  // otherwise.  Measured (lab, graph-free, realistic operands), dense phase
-  // alone: 2048 x 2048 -> 6144 51-61 us against 60-63 us for dense2_kernel;
-  // 2048 x 6144 -> 2048 59 us (128 x 128, no split) against 58-59 us
-  // (dense2_kernel, two K slices and the reduction).
-  //
-  // Q8 block and hi/lo panels (cb4) from 192 tiles of 128 x 128: the
-  // 128 x 128 large-tile kernel (two workgroups per CU, so one block's scale
-  // FMAs run while the other workgroup's MFMAs keep the matrix pipe busy),
-  // one K range per workgroup.  Measured (whole call, graph-timed, against
-  // dense2_kernel unless stated): Q8 M = 2048 x 2048 -> 6144 480 vs 444
-  // TFLOP/s; Q8 M = 512 x 2048 -> 6144 287 vs 227 and cb4 230 vs 204; Q8
-  // M = 2048 x 6144 -> 2048 434 vs 409 with two K slices on the same kernel
-  // (one slice was better at 192 and 256 tiles for both panels).  At 64
-  // tiles (M = 512 x 6144 -> 2048) the K slices the grid needs cost more
-  // (Q8 258 vs 268, cb4 217 vs 223), so dense2_kernel keeps those.
-  //
-  // hi/lo panels at large batches: 256 x 128 tiles (lab, dense phase alone,
-  // M = 2048 x 2048 -> 6144: 122.6 vs 128.4 us; M = 4096: 226 vs 278 us;
-  // whole call at M = 1024 x 2048 -> 6144: 347 vs 305 TFLOP/s on 128 x 128
-  // tiles); also at 2048 x 2048 outputs, in two K slices (389 vs 371 whole
-  // call at M = 2048 x 6144 -> 2048, 381 for 128 x 128 tiles).  Measured and
-  // not taken: g64 at M = 1024 x 2048 -> 6144 on 256 x 128 tiles (509 vs 458
-  // for the tile kernel) needs the tile / two-phase split moved for every
-  // M = 1024..2047 shape, and g64 M = 2048 x 6144 -> 2048 on 128 x 128 tiles
-  // was level with the tile kernel (600 vs 589).
+  // bf16 activations from 96 output tiles of 128 x 128: the large-tile
+  // kernel (gemm_dense3.hip) on the piece-layout planes.  Wave tile and K
+  // slices as measured best (whole call, graph-timed, TFLOP/s; lab sweeps of
+  // every tile and 1-4 slices, K x N = 2048 x 6144 / 6144 x 2048):
+  //   * plain (g64): 256 x 192 from 192 such tiles (M = 1536: 640 vs 580 /
+  //     591 for 256 x 128 / 128 x 128; M = 2048: 781 vs 697 / 705), else
+  //     256 x 128 from 256 tiles (M = 4096 x 6144 -> 2048: 858 vs 815), else
+  //     128 x 128 (M = 768: 457; M = 2048 x 6144 -> 2048: 675 vs 600 for
+  //     256 x 128);
+  //   * Q8 block and hi/lo (cb4) panels: 128 x 128 (two workgroups per CU,
+  //     so one block's scale FMAs run while the other workgroup's MFMAs keep
+  //     the matrix pipe busy; cb4 M = 2048: 467 / 457 vs 426 / 411 for
+  //     256 x 128), hi/lo on 256 x 128 from M = 4096 (532 vs 515 at
+  //     6144 -> 2048, level at 2048 -> 6144);
+  //   * K slices: 128 x 128 tiles take two below 192 tiles and one from 192
+  //     (g64 M = 2048 x 6144 -> 2048, 256 tiles: 675 vs 606 in two; Q8 /
+  //     cb4 M = 1024 x 6144 -> 2048, 128 tiles: 363 / 324 vs 292 / 296 in
+  //     one and 313 / 288 on dense2_kernel); the 256-row tiles split while
+  //     the grid stays within one workgroup per CU and a slice keeps >= 8
+  //     K tiles (cb4 M = 2048 x 6144 -> 2048 on 256 x 128: 411 vs 372).
+  // Below 96 tiles dense2_kernel: at Q8 / cb4 M = 512 x 6144 -> 2048 (64
+  // tiles) the slices the large-tile grid needs cost as much as they give
+  // (258 / 221 vs 259 / 227 in four).
   pl.d3cfg = -1;
   pl.d3mode = 0;
   const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
-  if (x_bf16 && !lib && pl.wmode == kWPlain && m >= 1024) {
-    const uint32_t t192 = ((m + 255) / 256) * (t.rows / 192);
-    if (t.rows % 192 == 0 && t192 >= 224) pl.d3cfg = 1;
-    else if (t128 >= 224) pl.d3cfg = 3;
-  } else if (x_bf16 && !lib && pl.wmode == kWQBlock && t128 >= 192) {
-    pl.d3cfg = 3;
-    pl.d3mode = 2;
-  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && ((m >= 1024 && t.rows >= 4096) || (m >= 2048 && t128 >= 256))) {
-    pl.d3cfg = 2;
-    pl.d3mode = 1;
-  } else if (x_bf16 && !lib && pl.wmode == kWHiLo && t128 >= 192) {
-    pl.d3cfg = 3;
-    pl.d3mode = 1;
+  if (x_bf16 && !lib && t128 >= 96) {
+    pl.d3mode = pl.wmode == kWPlain ? 0 : pl.wmode == kWHiLo ? 1 : 2;
+    const uint32_t m256 = (m + 255) / 256;
+    if (pl.wmode == kWPlain && t.rows % 192 == 0 && m256 * (t.rows / 192) >= 192)
+      pl.d3cfg = 1;
+    else if ((pl.wmode == kWPlain && m256 * ((t.rows + 127) / 128) >= 256) || (pl.wmode == kWHiLo && m >= 4096))
+      pl.d3cfg = 2;
+    else
+      pl.d3cfg = 3;
   }
   if (pl.d3cfg >= 0) {
-    // K slices until the grid fills the CUs (one workgroup per CU at 256 x
-    // 192 and 256 x 128, two at 128 x 128), each slice at least 8 tiles of
-    // 32 columns; none for the Q8 block and hi/lo panels on 128 x 128 tiles
-    // (measured above).
     const uint32_t bm = pl.d3cfg == 3 ? 128 : 256, bn = pl.d3cfg == 1 ? 192 : 128;
-    const uint32_t slots = pl.d3cfg == 3 ? 512 : 256;
     const uint32_t tiles3 = ((m + bm - 1) / bm) * ((t.rows + bn - 1) / bn);
     const uint32_t kt32 = pl.kp / 32;
     uint32_t sp = 1;
-    const bool one_slice = pl.d3cfg == 3 && pl.d3mode != 0;
-    while (!one_slice && tiles3 * sp * 2 <= slots && kt32 / (sp * 2) >= 8) sp *= 2;
+    if (pl.d3cfg == 3)
+      sp = tiles3 < 192 && kt32 >= 16 ? 2 : 1;
+    else
+      while (tiles3 * sp * 2 <= 256 && kt32 / (sp * 2) >= 8) sp *= 2;
     pl.kt_per_split = (kt32 + sp - 1) / sp;
     pl.splits = (kt32 + pl.kt_per_split - 1) / pl.kt_per_split;
   }
-  pl.panel_plane = al256((size_t)t.rows * pl.kp * 2);
+  // The large-tile kernel reads both planes in 1 KB pieces (plane_off):
+  // rows rounded up to 16.
+  const bool tiled = pl.d3cfg >= 0;
+  const size_t prow = tiled ? (t.rows + 15u) & ~15u : t.rows, arow = tiled ? (m + 15u) & ~15u : m;
+  pl.panel_plane = al256(prow * pl.kp * 2);
   pl.dsc_bytes = pl.wmode == kWQBlock ? al256((size_t)t.rows * (pl.kp / 32) * 4) : 0;
   pl.panel_bytes = pl.panel_plane * (pl.wmode == kWHiLo ? 2 : 1) + pl.dsc_bytes + al256((size_t)t.rows * 4);
-  pl.a_plane = al256((size_t)m * pl.kp * 2);
+  pl.a_plane = al256(arow * pl.kp * 2);
   pl.a_bytes = pl.a_plane * (x_bf16 ? 1 : 2);
   pl.partial_bytes = pl.splits > 1 ? al256((size_t)pl.splits * m * t.rows * 4) : 0;
   // Library: for products of fewer than 128 output tiles of 128 x 128, K
@@ -990,6 +997,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   p.dsc = reinterpret_cast<float*>(base + pl.panel_plane * (hilo ? 2 : 1));
   p.inv = reinterpret_cast<float*>(base + pl.panel_plane * (hilo ? 2 : 1) + pl.dsc_bytes);
   p.kp = pl.kp;
+  p.tiled = pl.d3cfg >= 0;
   uint16_t* ah = reinterpret_cast<uint16_t*>(base + pl.panel_bytes);
   uint16_t* al = reinterpret_cast<uint16_t*>(base + pl.panel_bytes + (x_bf16 ? 0 : pl.a_plane));
   float* partial = reinterpret_cast<float*>(base + pl.panel_bytes + pl.a_bytes);
@@ -1002,7 +1010,7 @@ hipError_t run(const DevTensor& t, const void* x, bool x_bf16, uint32_t m, void*
   // 4096 workgroups); the two-pass one walks rows over at most 1024.
   const bool xreg = x_bf16 && x_vec && p.kp <= 4u * THREADS * 8u;
   XConv xc{x, ah, al, const_cast<int32_t*>(xe), m, t.cols, (uint32_t)x_bf16, x_vec,
-           std::min<uint32_t>(m, xreg ? 4096u : 1024u)};
+           std::min<uint32_t>(m, xreg ? 4096u : 1024u), p.tiled};
   const uint32_t nseg = (p.kp + 64 * 32 - 1) / (64 * 32);
   const uint32_t pgrid = (uint32_t)(((size_t)t.rows * nseg + 3) / 4);
   hipLaunchKernelGGL((panel_kernel<KIND>), dim3(xc.blocks + pgrid), dim3(THREADS), 0, s, t, p,
@@ -1076,8 +1084,8 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 
 // Path choice, unless the caller pins one (every path runs every kind):
 //   * g64 weights, bf16 activations: the fused kernel up to batch 64; the
-//     decode-in-registers tile kernel (gemm_tile.hip) from batch 128 to
-//     2047, and beyond when K > N; the two-phase path otherwise;
+//     decode-in-registers tile kernel (gemm_tile.hip) from batch 128 to 767
+//     (to 1023 when K > N); the two-phase path otherwise;
 //   * cb4 weights, bf16 activations, within the tile kernel's limits
 //     (gemm_tile_cb4_supported): its decode-in-loop tile kernel from batch
 //     128 to 511 (M = 128 / 256: 96 / 84 and 137 / 145 TFLOP/s against the
@@ -1090,14 +1098,18 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 // K x N = 2048 x 6144 / 6144 x 2048):
 //   g64 M = 64: fused 73 / 61, two-phase 68 / 61; M = 96: tile 82, two-phase
 //   89 (2048 x 6144); M = 128: tile 134 / 118, two-phase 115 / 107; M = 512:
-//   tile 407 / 350, two-phase 300 / 325; M = 2048: tile 636 / 637, two-phase
-//   671 / 581; M = 4096: 673 / 761 (2048 x 6144);
+//   tile 407 / 350, two-phase 300 / 325; with the two-phase planes in 1 KB
+//   pieces: M = 512: tile 409 / 358, two-phase 418 / 321; M = 768: tile
+//   378 / 396, two-phase 457 / 384; M = 1024: tile 484 / 463, two-phase
+//   554 / 465; M = 1536: tile 513 / 517, two-phase 640 / 555; M = 4096: tile
+//   693 (6144 x 2048), two-phase 858;
 //   Q8 M = 64: fused 81 / 71, two-phase 61 / 54; M = 256: fused 125 / 161,
 //   two-phase 132 / 163.
 constexpr uint32_t kFusedMaxM = 128;
 constexpr uint32_t kG64FusedMaxM = 64;
 constexpr uint32_t kTileMinM = 128;
-constexpr uint32_t kTileMaxM = 2048;   // exclusive, unless K > N
+constexpr uint32_t kTileMaxM = 768;        // exclusive
+constexpr uint32_t kTileMaxMTall = 1024;   // exclusive, K > N
 constexpr uint32_t kCb4TileMaxM = 512;  // exclusive
 
 enum class Path { Fused, Tile, TileCb4, Panel };
@@ -1115,7 +1127,7 @@ static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
     return Path::TileCb4;
   if (t.kind == KIND_G64 && x_bf16) {
     if (fused_ok && m <= kG64FusedMaxM) return Path::Fused;
-    if (tile_ok && m >= kTileMinM && (m < kTileMaxM || t.cols > t.rows)) return Path::Tile;
+    if (tile_ok && m >= kTileMinM && m < (t.cols > t.rows ? kTileMaxMTall : kTileMaxM)) return Path::Tile;
     return Path::Panel;
   }
   if (fused_ok && m <= kFusedMaxM) return Path::Fused;
