@@ -99,26 +99,28 @@ def test_dense_kernel_modes(eng, kind, M, N, K):
 # planes of 1 KB pieces (16 rows x 32 columns, rows padded to 16): batch and
 # weight row counts that are not multiples of 16, K short of a whole piece,
 # every wave tile and weight mode the planner gives it (plain on 256 x 192,
-# 256 x 128 and 128 x 128; Q8 block on 128 x 128; hi/lo on 128 x 128 and
-# 256 x 128), 128 x 128 in one K range and in two.
+# 256 x 128 and 128 x 128 of 4 waves; Q8 block and hi/lo on 128 x 128 of 4
+# waves and 256 x 128 of 8 waves), 128 x 128 in one K range and in two.
 @pytest.mark.parametrize("kind,M,N,K", [("g64", 1800, 5376, 512), ("g64", 1030, 6600, 256),
                                         ("g64", 1100, 3100, 1000), ("g64", 1000, 1500, 1000),
                                         ("q8", 1000, 3000, 1000), ("q8", 1000, 1500, 1000),
-                                        ("cb4", 1000, 3000, 1000), ("cb4", 1000, 1500, 1000),
-                                        ("cb4", 4100, 400, 256)])
+                                        ("q8", 1000, 6100, 256), ("cb4", 1000, 3000, 1000),
+                                        ("cb4", 1000, 1500, 1000), ("cb4", 1000, 6100, 256)])
 def test_large_tile_kernel_ragged(eng, kind, M, N, K):
     check(eng, make(kind, N, K, seed=M + N), M, engine.GEMM_PANEL, seed=K)
 
 
-def test_dense_kernel_q8_block_scales_extreme(eng):
+@pytest.mark.parametrize("rows,K,M", [(300, 2048, 512), (3000, 1024, 1000), (6144, 256, 1024)])
+def test_dense_kernel_q8_block_scales_extreme(eng, rows, K, M):
     """Block scales spanning subnormal to 2^15 in one row (each block's
-    fragment is scaled on its own)."""
-    q = synth.make_q8(300, 2048, seed=7)
+    fragment is scaled on its own), on the interleaved kernel and on the
+    large-tile kernel's 4-wave and 8-wave tiles."""
+    q = synth.make_q8(rows, K, seed=7)
     b = q.blocks.copy().reshape(-1, 34)
     b[0::5, 0:2] = np.array([0x7800], np.uint16).view(np.uint8)   # d = 32768
     b[1::7, 0:2] = np.array([0x0001], np.uint16).view(np.uint8)   # subnormal d
     q.blocks = b.reshape(-1)
-    check(eng, q, 512, engine.GEMM_PANEL)
+    check(eng, q, M, engine.GEMM_PANEL)
 
 
 # ---- the cb4 decode-in-loop tile kernel (GEMM_FUSED pins it for eligible

@@ -9,12 +9,14 @@
 // (llm_prefill.rs:156-255) over decoded weights; MFMA products are exact in
 // the fp32 accumulators.
 //
-// Shape: a workgroup is 4 waves in 2 x 2; wave (wm, wn) owns WM x WN
-// fragments of v_mfma_f32_32x32x16_f16 (32·WM activation rows x 32·WN weight
-// rows), so the workgroup tile is 64·WM x 64·WN.  The wave tile is the
-// lever: every 16-deep step reads WM + WN fragments (1 KB each) from LDS for
-// WM·WN MFMAs, so 4 x 4 fragments need half the LDS reads per MFMA of the
-// 2 x 2 fragments of a 128 x 128 tile.
+// Shape: a workgroup is NW = 4 or 8 waves in NW / 2 x 2; wave (wm, wn) owns
+// WM x WN fragments of v_mfma_f32_32x32x16_f16 (32·WM activation rows x
+// 32·WN weight rows), so the workgroup tile is 16·NW·WM x 64·WN.  The wave
+// tile is the lever: every 16-deep step reads WM + WN fragments (1 KB each)
+// from LDS for WM·WN MFMAs, so 4 x 4 fragments need half the LDS reads per
+// MFMA of the 2 x 2 fragments of a 128 x 128 tile.  Eight waves of 2 x 2
+// fragments (256 x 128) keep two waves per SIMD, as two 4-wave 128 x 128
+// workgroups per CU do, with a quarter less L2 -> LDS traffic per output.
 //
 // Operands move global -> LDS with buffer_load_dwordx4 ... lds (no VGPR
 // round trip, no ds_write).  A K tile is 32 columns (64 bytes per row); the
@@ -52,10 +54,13 @@
 //     fresh fragment set, and acc += d * fragment (the lane's output column
 //     is fixed, so one scale per fragment) -- for tile t in tile t + 1's
 //     step 0, fragment q's sixteen FMAs just before the MFMA that restarts
-//     fragment q.  Two workgroups per CU (two waves per SIMD), so one wave's
-//     scale FMAs run in the VALU while the other wave's MFMAs keep the
-//     matrix pipe busy.  The tile's scales travel with it: a 4-byte-per-lane
-//     LDS load of the scales of the tile's weight rows.
+//     fragment q.  Two waves per SIMD (two 4-wave workgroups per CU, or one
+//     of 8 waves), so one wave's scale FMAs run in the VALU while the other
+//     wave's MFMAs keep the matrix pipe busy.  The tile's scales travel with
+//     it: a 4-byte-per-lane LDS load of the scales of the tile's weight rows
+//     (waves 0 and 1 fetch them, the others repeat the same loads so that
+//     every wave counts the same loads per tile).  The two scale register
+//     sets alternate with the stage parity, so the stage count is even.
 // With gridDim.y > 1 the workgroup writes fp32 partial sums of its K slice;
 // reduce_kernel adds them in slice order and applies the scales.
 #include <algorithm>
@@ -70,7 +75,7 @@ namespace vxt {
 
 namespace g3 {
 
-constexpr int BK = 32, NT = 256;
+constexpr int BK = 32;
 enum : int { kPlain = 0, kHiLo = 1, kQBlock = 2 };
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -87,19 +92,25 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_seq(f, std::make_integer_sequence<int, N>{});
 }
 
-// 128 x 128 tiles run two workgroups per CU (the LDS budget halves)
-constexpr int occupancy(int wm, int wn) { return (wm == 2 && wn == 2) ? 2 : 1; }
+// 4-wave workgroups of 2 x 2-fragment waves (128 x 128 tiles) run two per
+// CU (the LDS budget halves); every other shape one per CU.
+constexpr int occupancy(int wm, int wn, int nw) { return (nw == 4 && wm == 2 && wn == 2) ? 2 : 1; }
 
-template <int WM, int WN, int MODE>
+// NW waves per workgroup in NW / 2 x 2 (wave rows x wave columns).
+template <int WM, int WN, int MODE, int NW = 4>
 struct Cfg {
-  static constexpr int BM = 64 * WM, BN = 64 * WN;
+  static constexpr int NT = 64 * NW;
+  static constexpr int BM = 32 * WM * (NW / 2), BN = 64 * WN;
   static constexpr bool LO = MODE == kHiLo, QB = MODE == kQBlock;
   static constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64;   // one stage of one operand
   static constexpr int D_BYTES = QB ? BN * 4 : 16;             // Q8 block: the tile's scales
   static constexpr int STAGE = A_BYTES + B_BYTES * (LO ? 2 : 1) + (QB ? D_BYTES : 0);
-  static constexpr int OCC = occupancy(WM, WN);
-  static constexpr int NS = std::min(5, (160 * 1024 / OCC - 2048) / STAGE);
-  static constexpr int NA = BM / 64, NB = BN / 64, NL = LO ? NB : 0;   // 1 KB loads per wave per tile
+  static constexpr int OCC = occupancy(WM, WN, NW);
+  // Q8 block mode alternates two scale register sets by stage parity (tile t
+  // uses set t & 1 from stage t mod NS), which needs an even stage count.
+  static constexpr int NS0 = std::min(5, (160 * 1024 / OCC - 2048) / STAGE);
+  static constexpr int NS = QB ? NS0 & ~1 : NS0;
+  static constexpr int NA = BM / (16 * NW), NB = BN / (16 * NW), NL = LO ? NB : 0;   // 1 KB loads per wave per tile
   static constexpr int ND = QB ? 1 : 0;   // one 4-byte-per-lane scale load per wave per tile
   static constexpr int NLD = NA + NB + NL + ND;
   static constexpr int NR = WM + WN + (LO ? WN : 0);   // fragment reads per step
@@ -107,8 +118,13 @@ struct Cfg {
   static_assert(NS >= 3, "stages");
   static constexpr int LPS = (NLD + NM - 1) / NM;   // loads per MFMA slice of step 1
   static_assert(NR <= NM && LPS <= 2, "one read and at most two loads per MFMA slice");
-  static_assert(32 * (32 * WN + 8) * 2 <= A_BYTES, "epilogue transpose region");
-  static_assert(!QB || (BN == 128 && OCC == 2), "Q8 block mode: 128 x 128 tiles");
+  static_assert(NA * 16 * NW == BM && NB * 16 * NW == BN, "whole 16-row pieces per wave");
+  // epilogue: a transpose region per wave, RPA per stage A array, then RPB
+  // per stage W array
+  static constexpr int REGION = 32 * (32 * WN + 8) * 2, RPA = A_BYTES / REGION, RPB = B_BYTES / REGION;
+  static_assert(NW <= NS * (RPA + RPB), "epilogue transpose regions");
+  // Q8 block: two waves per SIMD (one wave's scale FMAs beside the other's MFMAs)
+  static_assert(!QB || (WM == 2 && WN == 2 && NW * OCC == 8), "Q8 block mode: 2 x 2-fragment waves, two per SIMD");
 };
 
 // 16 bytes per lane from buffer `r` at voff + soff into LDS at lds + 16 lane
@@ -137,15 +153,15 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((V & 15) | ((V >> 4) << 14) | (7 << 4));
 }
 
-template <int WM, int WN, int MODE>
-__global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uint16_t* __restrict__ ah, const uint16_t* __restrict__ bh,
+template <int WM, int WN, int MODE, int NW>
+__global__ __launch_bounds__(64 * NW, occupancy(WM, WN, NW)) void dense3_kernel(const uint16_t* __restrict__ ah, const uint16_t* __restrict__ bh,
                                                       const uint16_t* __restrict__ bl, const float* __restrict__ dsc,
                                                       const float* __restrict__ inv,
                                                       uint32_t M, uint32_t N, uint32_t kp, void* __restrict__ y,
                                                       uint32_t y_bf16, float* __restrict__ partial,
                                                       uint32_t kt_per_split, uint32_t tiles_m,
                                                       const int32_t* __restrict__ xe) {
-  using C = Cfg<WM, WN, MODE>;
+  using C = Cfg<WM, WN, MODE, NW>;
   constexpr int BM = C::BM, BN = C::BN, NS = C::NS;
   constexpr bool LO = C::LO, QB = C::QB;
 #define VXT_STAGE(k)                                                                  \
@@ -211,17 +227,17 @@ __global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uin
   const __amdgpu_buffer_rsrc_t rd = rsrc(QB ? (const void*)dsc : (const void*)bh, QB ? (size_t)N * nblk * 4 : 16);
 
   // Per-lane byte offsets of the load instructions (tile 0 of the slice):
-  // instruction j of this wave fills rows 16 (wave + 4 j) .. + 15, one piece.
+  // instruction j of this wave fills rows 16 (wave + NW j) .. + 15, one piece.
   uint32_t va[C::NA], vb[C::NB], vd = 0;
-  if constexpr (QB)   // wave w loads the scales of weight rows 64 (w % 2) .. + 63 (waves 2, 3 repeat 0, 1)
+  if constexpr (QB)   // wave w loads the scales of weight rows 64 (w % 2) .. + 63 (the other waves repeat waves 0, 1)
     vd = std::min(n0 + 64 * (wave & 1) + lane, N - 1) * nblk * 4 + kt0 * 4;
   {
     const uint32_t r16 = lane >> 2, chunk = (lane & 3) ^ ((lane >> 4) & 3);
     auto off = [&](uint32_t g) { return (g >> 4) * KTT * 1024u + (g & 15u) * 64u + chunk * 16u + kt0 * 1024u; };
 #pragma unroll
-    for (int j = 0; j < C::NA; ++j) va[j] = off(std::min(m0 + 16 * (wave + 4 * j) + r16, M - 1));
+    for (int j = 0; j < C::NA; ++j) va[j] = off(std::min(m0 + 16 * (wave + NW * j) + r16, M - 1));
 #pragma unroll
-    for (int j = 0; j < C::NB; ++j) vb[j] = off(std::min(n0 + 16 * (wave + 4 * j) + r16, N - 1));
+    for (int j = 0; j < C::NB; ++j) vb[j] = off(std::min(n0 + 16 * (wave + NW * j) + r16, N - 1));
   }
   // Load piece j (A pieces, then W, then W's lo plane) of slice tile t into
   // stage k.
@@ -230,13 +246,13 @@ __global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uin
     if (QB && j == C::NLD - 1) {
       dma4(rd, stD(k_) + 256 * (wave & 1), vd, t * 4);
     } else if (j < C::NA) {
-      dma16(ra, stA(k_) + 1024 * (wave + 4 * j), va[j], so);
+      dma16(ra, stA(k_) + 1024 * (wave + NW * j), va[j], so);
     } else if (j < C::NA + C::NB) {
       const int q = j - C::NA;
-      dma16(rb, stB(k_) + 1024 * (wave + 4 * q), vb[q], so);
+      dma16(rb, stB(k_) + 1024 * (wave + NW * q), vb[q], so);
     } else {
       const int q = j - C::NA - C::NB;
-      dma16(rl, stL(k_) + 1024 * (wave + 4 * q), vb[q], so);
+      dma16(rl, stL(k_) + 1024 * (wave + NW * q), vb[q], so);
     }
   };
 
@@ -398,14 +414,22 @@ __global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uin
                          reinterpret_cast<uintptr_t>(y) % 16 == 0;
   if (rows_fast) {
     // Each wave transposes its 32·WM x 32·WN block through its own LDS
-    // region (stage wave's A array; with three stages wave 3 takes stage 0's
-    // W array), 32 rows at a time, and writes whole-row 16-byte pieces.  Rows
+    // region (the stages' A arrays first, then their W arrays), 32 rows at a
+    // time, and writes whole-row 16-byte pieces.  Rows
     // r and r + 1 of a lane are converted as one pair (one v_cvt_pk_bf16_f32)
     // and stored as the pair's two halves.
     constexpr uint32_t LDO = 32 * WN + 8;   // bf16 elements per LDS row
-    static_assert(NS >= 4 || 32 * LDO * 2 <= C::B_BYTES, "epilogue region of wave 3");
-    char* const reg3 = NS >= 4 ? sA3 : sB0;
-    uint16_t* reg = reinterpret_cast<uint16_t*>(wave == 0 ? sA0 : wave == 1 ? sA1 : wave == 2 ? sA2 : reg3);
+    auto pick = [](uint32_t k, char* a0, char* a1, char* a2, char* a3, char* a4) {
+      return k == 0 ? a0 : k == 1 ? a1 : k == 2 ? a2 : k == 3 ? a3 : a4;
+    };
+    char* rbase;
+    if (C::RPA > 0 && wave < (uint32_t)(NS * C::RPA)) {
+      rbase = pick(wave / C::RPA, sA0, sA1, sA2, sA3, sA4) + (wave % C::RPA) * C::REGION;
+    } else {
+      const uint32_t w = wave - NS * C::RPA;
+      rbase = pick(w / C::RPB, sB0, sB1, sB2, sB3, sB4) + (w % C::RPB) * C::REGION;
+    }
+    uint16_t* reg = reinterpret_cast<uint16_t*>(rbase);
     float sc[WN];
 #pragma unroll
     for (int j = 0; j < WN; ++j) sc[j] = inv[n0 + wn * 32 * WN + j * 32 + l32];
@@ -477,40 +501,42 @@ __global__ __launch_bounds__(NT, occupancy(WM, WN)) void dense3_kernel(const uin
   }
 }
 
-template <int WM, int WN, int MODE>
+template <int WM, int WN, int MODE, int NW = 4>
 hipError_t launch(const uint16_t* ah, const uint16_t* bh, const uint16_t* bl, const float* dsc, const float* inv, uint32_t m,
                   uint32_t n, uint32_t kp, void* y, bool y_bf16, float* partial, uint32_t splits,
                   uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
-  using C = Cfg<WM, WN, MODE>;
+  using C = Cfg<WM, WN, MODE, NW>;
   const uint32_t tiles_m = (m + C::BM - 1) / C::BM;
-  hipLaunchKernelGGL((dense3_kernel<WM, WN, MODE>), dim3(tiles_m * ((n + C::BN - 1) / C::BN), splits), dim3(NT), 0,
+  hipLaunchKernelGGL((dense3_kernel<WM, WN, MODE, NW>), dim3(tiles_m * ((n + C::BN - 1) / C::BN), splits), dim3(C::NT), 0,
                      s, ah, bh, bl, dsc, inv, m, n, kp, y, (uint32_t)y_bf16, partial, kt_per_split, tiles_m, xe);
   return hipGetLastError();
 }
 
 }  // namespace g3
 
-// Large-tile dense phase.  cfg selects the wave tile (WM x WN fragments):
-// 0 = 4 x 4 (workgroup tile 256 x 256), 1 = 4 x 3 (256 x 192), 2 = 4 x 2
-// (256 x 128), 3 = 2 x 2 (128 x 128).  wmode 0 = plain f16 panel, 1 = hi/lo
-// panel (bh + bl * 2^-11; cfg 2 and 3), 2 = Q8 block (int8 values as f16 in
-// bh, f32 scales dsc [n][kp / 32]; cfg 3).  ah, bh and bl are planes of 1 KB
+// Large-tile dense phase.  cfg selects the wave tile (WM x WN fragments) and
+// the waves per workgroup: 0 = 4 x 4, 4 waves (workgroup tile 256 x 256),
+// 1 = 4 x 3, 4 waves (256 x 192), 2 = 4 x 2, 4 waves (256 x 128), 3 = 2 x 2,
+// 4 waves (128 x 128), 4 = 2 x 2, 8 waves (256 x 128).  wmode 0 = plain f16
+// panel (cfg 0-3), 1 = hi/lo panel (bh + bl * 2^-11; cfg 3 and 4), 2 = Q8
+// block (int8 values as f16 in bh, f32 scales dsc [n][kp / 32]; cfg 3 and 4).  ah, bh and bl are planes of 1 KB
 // pieces (16 rows x 32 columns, rows padded to 16).  kt_per_split counts
 // 32-column K tiles; kp % 32 == 0.
 hipError_t launch_dense3(int cfg, int wmode, const uint16_t* ah, const uint16_t* bh, const uint16_t* bl,
                          const float* dsc, const float* inv, uint32_t m, uint32_t n, uint32_t kp, void* y, bool y_bf16,
                          float* partial, uint32_t splits, uint32_t kt_per_split, const int32_t* xe, hipStream_t s) {
   if (kp % g3::BK != 0 || xe == nullptr || m == 0 || n == 0 || kt_per_split == 0) return hipErrorInvalidValue;
-#define VXT_D3(WM, WN, MODE) \
-  return g3::launch<WM, WN, MODE>(ah, bh, bl, dsc, inv, m, n, kp, y, y_bf16, partial, splits, kt_per_split, xe, s)
+#define VXT_D3(WM, WN, MODE, NW) \
+  return g3::launch<WM, WN, MODE, NW>(ah, bh, bl, dsc, inv, m, n, kp, y, y_bf16, partial, splits, kt_per_split, xe, s)
   switch (wmode * 16 + cfg) {
-    case g3::kPlain * 16 + 0: VXT_D3(4, 4, g3::kPlain);
-    case g3::kPlain * 16 + 1: VXT_D3(4, 3, g3::kPlain);
-    case g3::kPlain * 16 + 2: VXT_D3(4, 2, g3::kPlain);
-    case g3::kPlain * 16 + 3: VXT_D3(2, 2, g3::kPlain);
-    case g3::kHiLo * 16 + 2: VXT_D3(4, 2, g3::kHiLo);
-    case g3::kHiLo * 16 + 3: VXT_D3(2, 2, g3::kHiLo);
-    case g3::kQBlock * 16 + 3: VXT_D3(2, 2, g3::kQBlock);
+    case g3::kPlain * 16 + 0: VXT_D3(4, 4, g3::kPlain, 4);
+    case g3::kPlain * 16 + 1: VXT_D3(4, 3, g3::kPlain, 4);
+    case g3::kPlain * 16 + 2: VXT_D3(4, 2, g3::kPlain, 4);
+    case g3::kPlain * 16 + 3: VXT_D3(2, 2, g3::kPlain, 4);
+    case g3::kHiLo * 16 + 3: VXT_D3(2, 2, g3::kHiLo, 4);
+    case g3::kHiLo * 16 + 4: VXT_D3(2, 2, g3::kHiLo, 8);
+    case g3::kQBlock * 16 + 3: VXT_D3(2, 2, g3::kQBlock, 4);
+    case g3::kQBlock * 16 + 4: VXT_D3(2, 2, g3::kQBlock, 8);
     default: return hipErrorInvalidValue;
   }
 #undef VXT_D3

@@ -823,8 +823,8 @@ struct Plan {
   bool lib;   // dense phase on the vendor library (gemm_blas.cpp)
   uint32_t kp, splits, kt_per_split;
   uint32_t lib_splits;   // K slices of the library call (one strided batch)
-  int d3cfg;             // >= 0: the dense phase on dense3_kernel (gemm_dense3.hip) with this wave tile
-  int d3mode;            // its weight mode (0 plain, 2 Q8 block)
+  int d3cfg;             // >= 0: the dense phase on dense3_kernel (gemm_dense3.hip) in this shape (launch_dense3)
+  int d3mode;            // its weight mode (0 plain, 1 hi/lo, 2 Q8 block)
   size_t panel_plane, dsc_bytes, panel_bytes, a_plane, a_bytes, partial_bytes;
 };
 
@@ -857,11 +857,14 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   //     256 x 128 from 256 tiles (M = 4096 x 6144 -> 2048: 858 vs 815), else
   //     128 x 128 (M = 768: 457; M = 2048 x 6144 -> 2048: 675 vs 600 for
   //     256 x 128);
-  //   * Q8 block and hi/lo (cb4) panels: 128 x 128 (two workgroups per CU,
-  //     so one block's scale FMAs run while the other workgroup's MFMAs keep
-  //     the matrix pipe busy; cb4 M = 2048: 467 / 457 vs 426 / 411 for
-  //     256 x 128), hi/lo on 256 x 128 from M = 4096 (532 vs 515 at
-  //     6144 -> 2048, level at 2048 -> 6144);
+  //   * Q8 block and hi/lo (cb4) panels: waves of 2 x 2 fragments, two per
+  //     SIMD (one wave's scale FMAs beside the other's MFMAs), as 256 x 128
+  //     tiles of 8 waves where those number 192-256 or >= 512 (Q8 / cb4
+  //     M = 1024 x 2048 -> 6144: 429 / 354 vs 404 / 338; M = 4096: 683 / 529
+  //     and 654 / 529 vs 594 / 520 and 568 / 511), else 128 x 128 tiles of 4
+  //     waves, two workgroups per CU (M = 2048 x 2048 -> 6144, 384 of the
+  //     larger tiles: cb4 456 vs 429; fewer than 192: Q8 M = 2048 x 6144 ->
+  //     2048 502 vs 391);
   //   * K slices: 128 x 128 tiles take two below 192 tiles and one from 192
   //     (g64 M = 2048 x 6144 -> 2048, 256 tiles: 675 vs 606 in two; Q8 /
   //     cb4 M = 1024 x 6144 -> 2048, 128 tiles: 363 / 324 vs 292 / 296 in
@@ -876,11 +879,13 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
   if (x_bf16 && !lib && t128 >= 96) {
     pl.d3mode = pl.wmode == kWPlain ? 0 : pl.wmode == kWHiLo ? 1 : 2;
-    const uint32_t m256 = (m + 255) / 256;
+    const uint32_t m256 = (m + 255) / 256, t256 = m256 * ((t.rows + 127) / 128);
     if (pl.wmode == kWPlain && t.rows % 192 == 0 && m256 * (t.rows / 192) >= 192)
       pl.d3cfg = 1;
-    else if ((pl.wmode == kWPlain && m256 * ((t.rows + 127) / 128) >= 256) || (pl.wmode == kWHiLo && m >= 4096))
+    else if (pl.wmode == kWPlain && t256 >= 256)
       pl.d3cfg = 2;
+    else if (pl.wmode != kWPlain && t256 >= 192 && (t256 <= 256 || t256 >= 512))
+      pl.d3cfg = 4;
     else
       pl.d3cfg = 3;
   }
