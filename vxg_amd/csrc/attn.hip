@@ -631,10 +631,11 @@ __global__ __launch_bounds__(W * 64) void attn_merge_kernel(const float* __restr
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      if (c0 + W * u >= n_chunks) break;   // uniform across the wave
-      const float e = expf(mc[u] - m);
-      l += lc[u] * e;
-      acc += ac[u] * e;
+      if (c0 + W * u < n_chunks) {   // uniform across the wave; the valid chunks are a prefix
+        const float e = expf(mc[u] - m);
+        l += lc[u] * e;
+        acc += ac[u] * e;
+      }
     }
   }
   s_acc[wave][lane] = acc;

@@ -47,7 +47,6 @@ namespace gd {
 
 constexpr int BM = 128, BN = 128, BK = 64, NT = 256;
 constexpr uint32_t kOpBytes = 128 * 128;   // one operand of one stage
-constexpr float kLoInv = 1.0f / 2048.0f;
 
 enum : int { kPlain = 0, kHiLo = 1, kQBlock = 2 };
 

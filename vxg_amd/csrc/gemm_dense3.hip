@@ -314,8 +314,8 @@ __global__ __launch_bounds__(64 * NW, occupancy(WM, WN, NW)) void dense3_kernel(
       af[set][i] = *reinterpret_cast<const half8*>(stA(k_) + i * 2048 + offA[s]);
     }
   };
-  auto mma = [&](auto set_, auto q_, auto par_) {
-    constexpr int set = decltype(set_)::value, q = decltype(q_)::value, par = decltype(par_)::value;
+  auto mma = [&](auto set_, auto q_) {
+    constexpr int set = decltype(set_)::value, q = decltype(q_)::value;
     constexpr int p = LO ? q / 2 : q;
     constexpr int i = p / WN, j = p % WN;
     if constexpr (LO && q % 2 == 1)
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(64 * NW, occupancy(WM, WN, NW)) void dense3_kernel(
     static_for<C::NM>([&](auto q_) {
       constexpr int q = decltype(q_)::value;
       if constexpr (QB) scale(PPAR{}, q_);   // the previous block's fragment q, before the MFMA restarts it
-      mma(I0{}, q_, PAR{});
+      mma(I0{}, q_);
       if constexpr (q < C::NR) read(k_, I1{}, I1{}, q_);
       if constexpr (QB && q < WN)   // this tile's scales, before its stage is released
         dreg[PAR::value][q] = *reinterpret_cast<const float*>(stD(k_) + 4 * (wn * (32 * WN) + q * 32 + l32));
@@ -373,7 +373,7 @@ __global__ __launch_bounds__(64 * NW, occupancy(WM, WN, NW)) void dense3_kernel(
     const uint32_t tl = std::min(t + NS, KT - 1);
     static_for<C::NM>([&](auto q_) {
       constexpr int q = decltype(q_)::value;
-      mma(I1{}, q_, PAR{});
+      mma(I1{}, q_);
       if constexpr (q < C::NR) read(KN{}, I0{}, I0{}, q_);
       static_for<C::LPS>([&](auto u_) {
         constexpr int j = q * C::LPS + decltype(u_)::value;
