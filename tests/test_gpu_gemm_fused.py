@@ -73,7 +73,8 @@ def test_fused_tail_shapes(eng, kind, rows, cols, M):
 
 
 @pytest.mark.parametrize("kind", ["g64", "q8"])
-@pytest.mark.parametrize("M,N,K", [(16, 64, 4096), (40, 300, 3000), (128, 2048, 6144), (96, 6144, 2048)])
+@pytest.mark.parametrize("M,N,K", [(16, 64, 4096), (40, 300, 3000), (128, 2048, 6144), (96, 6144, 2048),
+                                   (300, 1500, 3000), (384, 2048, 6144)])
 def test_fused_split_k_deterministic(eng, kind, M, N, K):
     """K split across workgroups: fixed-order partial sums, identical across runs."""
     m = make(kind, N, K, seed=M + N)

@@ -1096,7 +1096,11 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 //     128 to 511 (M = 128 / 256: 96 / 84 and 137 / 145 TFLOP/s against the
 //     two-phase path's 81 / 77 and 121 / 131; at M = 64 and 512 the
 //     two-phase path is ahead);
-//   * Q8 weights, bf16 activations: the fused kernel up to batch 128;
+//   * Q8 weights, bf16 activations: the fused kernel up to batch 128, and
+//     up to 511 when K >= N (M = 256 / 384: 196 / 212 TFLOP/s against
+//     171 / 182 two-phase at 6144 -> 2048, 91 / 126 against 81 / 106 at
+//     2048 -> 2048; level at 512; behind at 2048 -> 6144, 154 / 177 against
+//     179 / 195);
 //   * everything else: the two-phase path with the own dense kernel.
 // The vendor dense GEMM runs only when pinned (kGemmLibrary), as a
 // comparison.  Measured on MI355X (whole call, graph of 100 calls, TFLOP/s,
@@ -1111,6 +1115,7 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 //   Q8 M = 64: fused 81 / 71, two-phase 61 / 54; M = 256: fused 125 / 161,
 //   two-phase 132 / 163.
 constexpr uint32_t kFusedMaxM = 128;
+constexpr uint32_t kQ8FusedMaxMTall = 512;   // exclusive, K >= N
 constexpr uint32_t kG64FusedMaxM = 64;
 constexpr uint32_t kTileMinM = 128;
 constexpr uint32_t kTileMaxM = 768;        // exclusive
@@ -1135,7 +1140,8 @@ static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
     if (tile_ok && m >= kTileMinM && m < (t.cols > t.rows ? kTileMaxMTall : kTileMaxM)) return Path::Tile;
     return Path::Panel;
   }
-  if (fused_ok && m <= kFusedMaxM) return Path::Fused;
+  if (fused_ok && (m <= kFusedMaxM || (t.kind == KIND_Q8 && t.cols >= t.rows && m < kQ8FusedMaxMTall)))
+    return Path::Fused;
   return Path::Panel;
 }
 
