@@ -205,8 +205,9 @@ def test_cb4_tile_kernel_ineligible_tensor(eng):
 
 @pytest.mark.parametrize("M", [128, 300])
 def test_cb4_tile_kernel_on_auto_path(eng, M):
-    """From batch 128 to 511 the automatic choice takes the cb4 tile kernel
-    for an eligible tensor: the same bits as the pinned kernel, and the
+    """From batch 128 to 511 (K >= N here; to 255 when K < N) the automatic
+    choice takes the cb4 tile kernel for an eligible tensor: the same bits
+    as the pinned kernel, and the
     oracle bar; an ineligible tensor keeps the two-phase path there."""
     m = synth.make_cb4(640, 2048, seed=M)
     a = check(eng, m, M, engine.GEMM_AUTO, seed=1)

@@ -1093,9 +1093,11 @@ hipError_t launch_gemm_tile_cb4(const DevTensor& t, const uint16_t* x, uint32_t 
 //     (to 1023 when K > N); the two-phase path otherwise;
 //   * cb4 weights, bf16 activations, within the tile kernel's limits
 //     (gemm_tile_cb4_supported): its decode-in-loop tile kernel from batch
-//     128 to 511 (M = 128 / 256: 96 / 84 and 137 / 145 TFLOP/s against the
-//     two-phase path's 81 / 77 and 121 / 131; at M = 64 and 512 the
-//     two-phase path is ahead);
+//     128 to 511, to 255 when K < N (M = 128 / 256: 96 / 84 and 137 / 145
+//     TFLOP/s against the two-phase path's 81 / 77 and 121 / 131; at M = 64
+//     and 512 the two-phase path is ahead; with the two-phase planes in 1 KB
+//     pieces, at 2048 -> 6144 M = 256 / 384: 133 / 146 against 149 / 172,
+//     at 6144 -> 2048 148 / 169 against 143 / 160);
 //   * Q8 weights, bf16 activations: the fused kernel up to batch 128, and
 //     up to 511 when K >= N (M = 256 / 384: 196 / 212 TFLOP/s against
 //     171 / 182 two-phase at 6144 -> 2048, 91 / 126 against 81 / 106 at
@@ -1120,7 +1122,8 @@ constexpr uint32_t kG64FusedMaxM = 64;
 constexpr uint32_t kTileMinM = 128;
 constexpr uint32_t kTileMaxM = 768;        // exclusive
 constexpr uint32_t kTileMaxMTall = 1024;   // exclusive, K > N
-constexpr uint32_t kCb4TileMaxM = 512;  // exclusive
+constexpr uint32_t kCb4TileMaxM = 512;      // exclusive
+constexpr uint32_t kCb4TileMaxMWide = 256;  // exclusive, K < N
 
 enum class Path { Fused, Tile, TileCb4, Panel };
 
@@ -1133,7 +1136,8 @@ static Path choose_path(const DevTensor& t, uint32_t m, bool x_bf16, int mode) {
     if (tile_ok && m > kG64FusedMaxM) return Path::Tile;
     return fused_ok ? Path::Fused : Path::Panel;
   }
-  if (t.kind == KIND_CB4 && m >= kTileMinM && m < kCb4TileMaxM && gemm_tile_cb4_supported(t, x_bf16))
+  if (t.kind == KIND_CB4 && m >= kTileMinM && m < (t.cols < t.rows ? kCb4TileMaxMWide : kCb4TileMaxM) &&
+      gemm_tile_cb4_supported(t, x_bf16))
     return Path::TileCb4;
   if (t.kind == KIND_G64 && x_bf16) {
     if (fused_ok && m <= kG64FusedMaxM) return Path::Fused;
