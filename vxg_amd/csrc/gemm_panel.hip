@@ -877,7 +877,13 @@ inline Plan plan(const DevTensor& t, uint32_t m, bool x_bf16, bool lib) {
   pl.d3cfg = -1;
   pl.d3mode = 0;
   const uint32_t t128 = ((m + 127) / 128) * ((t.rows + 127) / 128);
-  if (x_bf16 && !lib && t128 >= 96) {
+  // The large-tile kernel reads each plane through a buffer resource of at
+  // most 2^31 - 16 bytes (and 32-bit lane offsets): larger planes take
+  // dense2_kernel, whose addresses are 64-bit.
+  const size_t kRsrcMax = 0x7ffffff0u;
+  const bool fits = (size_t)((m + 15u) & ~15u) * pl.kp * 2 <= kRsrcMax &&
+                    (size_t)((t.rows + 15u) & ~15u) * pl.kp * 2 <= kRsrcMax;
+  if (x_bf16 && !lib && t128 >= 96 && fits) {
     pl.d3mode = pl.wmode == kWPlain ? 0 : pl.wmode == kWHiLo ? 1 : 2;
     const uint32_t m256 = (m + 255) / 256, t256 = m256 * ((t.rows + 127) / 128);
     if (pl.wmode == kWPlain && t.rows % 192 == 0 && m256 * (t.rows / 192) >= 192)
