@@ -459,25 +459,34 @@ inline Plan plan(const DevTensor& t, uint32_t m) {
   const uint32_t nchunks = (kt + KC - 1) / KC;
   // Activation tiles of 32·fi rows; K split across workgroups until about
   // one workgroup per CU.
-  auto shape = [&](int fi, uint32_t& tiles_m, uint32_t& cps, uint32_t& splits) {
+  // fit: the slice length grows until the grid is at most 256 workgroups
+  // (one 8-wave workgroup per CU).
+  auto shape = [&](int fi, uint32_t& tiles_m, uint32_t& cps, uint32_t& splits, bool fit) {
     tiles_m = (m + 32 * fi - 1) / (32 * fi);
     const uint32_t tiles = tiles_m * p.tiles_n;
     cps = std::max<uint32_t>(1u, (uint32_t)(((uint64_t)nchunks * tiles + 255) / 256));
     cps = std::min(cps, nchunks);
     splits = (nchunks + cps - 1) / cps;
+    while (fit && tiles * splits > 256 && cps < nchunks) {
+      ++cps;
+      splits = (nchunks + cps - 1) / cps;
+    }
     return tiles * splits;   // workgroups
   };
   p.fi = m <= 32 ? 1 : (m <= 64 ? 2 : 4);
   uint32_t tm, cps, sp;
   // Q8 at 65..128 rows: 64-row tiles (two per 128 rows, 8 waves per
-  // workgroup) where those fill up to 256 workgroups and 128-row tiles leave
-  // some idle.  Measured (whole call, TFLOP/s, M = 128 / 96, 128-row vs
-  // 64-row tiles): 6144 -> 2048 123 / 97 vs 142 / 111, 2048 -> 2048 59 / 49
-  // vs 68 / 58; kept at 128 rows: 2048 -> 6144 (64-row tiles overfill the
-  // CUs) 118 / 97 vs 110 / 87, 12288 -> 2048 (128-row tiles already fill
-  // them) 191 / 155 vs 182 / 144.
-  if (t.kind == KIND_Q8 && p.fi == 4 && shape(4, tm, cps, sp) < 256 && shape(2, tm, cps, sp) <= 256) p.fi = 2;
-  shape(p.fi, p.tiles_m, p.cps, p.splits);
+  // workgroup) where 128-row tiles leave some of the CUs idle, with K slices
+  // long enough that the grid fits one workgroup per CU.  Measured (whole
+  // call, TFLOP/s, M = 128 / 96, 128-row vs 64-row tiles): 6144 -> 2048
+  // 123 / 97 vs 142 / 111, 2048 -> 2048 59 / 49 vs 68 / 58, 2048 -> 6144
+  // 116 vs 126 (two K slices; 110 in three, 288 workgroups); kept at 128
+  // rows: 12288 -> 2048 (128-row tiles already fill the CUs) 191 / 155 vs
+  // 182 / 144.
+  const bool fi2 = t.kind == KIND_Q8 && p.fi == 4 && shape(4, tm, cps, sp, false) < 256 &&
+                   shape(2, tm, cps, sp, true) <= 256;
+  if (fi2) p.fi = 2;
+  shape(p.fi, p.tiles_m, p.cps, p.splits, fi2);
   p.partial_bytes = p.splits > 1 ? ((size_t)p.splits * m * t.rows * 4 + 255) / 256 * 256 : 0;
   return p;
 }
